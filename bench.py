@@ -1,0 +1,271 @@
+"""Benchmark of the MI355X K-quant dequant-matvec + MoE hot path.
+
+Headline (BASELINE.json metric "Q4_K matvec HBM GB/s (% peak); MoE layer
+us/token at batch 1 and 512"): the Q4_K 4096x4096 decode matvec of
+configs[0], fp32 x and y, measured cold from HBM.  One step = one matvec over
+each of NCOPY distinct copies of the weight matrix (>= 2x the 256 MB
+Infinity Cache), so no launch finds its weights in the MALL.  `value` is
+algorithmic bytes (packed weights + x + y per matvec) / wall time of the
+timed steps.  The same line carries the mixed-format sweep, the
+MoE layer at batch 1 and 16 and 512 tokens, the
+roofline fraction of the dominant kernel, and the reference CPU path timed
+on this host.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--quick", action="store_true", help="skip the sweep/MoE/CPU legs")
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def time_region(fn, steps, warmup, stream):
+    """Run fn() warmup times, then time exactly `steps` calls with HIP events
+    recorded on the stream the kernels run on; returns seconds."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3
+
+
+def matvec_bytes(qt, M, K):
+    from trailblaze_amd import formats as fm
+    return fm.weight_bytes(qt, M, K) + 4 * K + 4 * M
+
+
+def gpu_leg(args):
+    import torch
+
+    import trailblaze_amd as tb
+    from trailblaze_amd import formats as fm
+    from trailblaze_amd import synth
+
+    dev_name = tb.init()
+    log("device", dev_name)
+    stream = torch.cuda.current_stream()
+    res = {"device": dev_name}
+
+    # ---- headline: Q4_K 4096x4096, cold HBM via rotated copies ----------
+    qt, M, K = fm.Q4_K, 4096, 4096
+    rng = np.random.default_rng(0)
+    W0 = synth.kquant_matrix(qt, M, K, rng)
+    x = torch.from_numpy(synth.activations(K, rng)).cuda()
+    wbytes = fm.weight_bytes(qt, M, K)
+    ncopy = max(2, int(np.ceil(2 * 256e6 / wbytes)) + 1)
+    Wd = torch.from_numpy(W0).cuda()
+    copies = [Wd] + [Wd.clone() for _ in range(ncopy - 1)]
+    ys = torch.empty((ncopy, M), dtype=torch.float32, device="cuda")
+
+    def step():
+        for i in range(ncopy):
+            tb.matvec(copies[i], qt, M, K, x, ys[i])
+
+    secs = time_region(step, args.steps, args.warmup, stream)
+    per_launch = secs / (args.steps * ncopy)
+    bpl = matvec_bytes(qt, M, K)
+    gbs = bpl / per_launch / 1e9
+    res["headline"] = dict(qt="Q4_K", M=M, K=K, ncopy=ncopy, ms_per_step=secs / args.steps * 1e3,
+                           us_per_launch=per_launch * 1e6, bytes_per_launch=bpl, gbs=gbs)
+    log(f"Q4_K 4096x4096 cold: {per_launch * 1e6:.2f} us/launch  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+
+    # warm (MALL-resident) number, same matrix every launch
+    def warm():
+        tb.matvec(Wd, qt, M, K, x, ys[0])
+    ws = time_region(warm, 200, 20, stream)
+    res["headline"]["warm_us_per_launch"] = ws / 200 * 1e6
+    res["headline"]["warm_gbs"] = bpl / (ws / 200) / 1e9
+    del copies
+    torch.cuda.empty_cache()
+
+    if args.quick:
+        return res
+
+    # ---- configs[1] sweep ------------------------------------------------
+    sweep = []
+    for qt2, M2, K2 in [(fm.Q2_K, 12288, 4096), (fm.Q2_K, 4096, 12288), (fm.Q3_K, 12288, 4096),
+                        (fm.Q3_K, 4096, 12288), (fm.Q5_K, 12288, 4096), (fm.Q5_K, 4096, 12288),
+                        (fm.Q8_0, 12288, 4096), (fm.Q8_0, 4096, 12288), (fm.Q6_K, 151936, 4096)]:
+        Wm = torch.from_numpy(synth.kquant_matrix(qt2, M2, K2, rng)).cuda()
+        wb = fm.weight_bytes(qt2, M2, K2)
+        nc = max(1, int(np.ceil(2 * 256e6 / wb)))
+        cps = [Wm] + [Wm.clone() for _ in range(nc - 1)]
+        xv = torch.from_numpy(synth.activations(K2, rng)).cuda()
+        yv = torch.empty(M2, dtype=torch.float32, device="cuda")
+
+        def st():
+            for c in cps:
+                tb.matvec(c, qt2, M2, K2, xv, yv)
+        reps = max(3, int(2000 // max(1, nc)))
+        s = time_region(st, reps, 2, stream)
+        pl = s / (reps * nc)
+        b = matvec_bytes(qt2, M2, K2)
+        sweep.append(dict(qt=fm.NAMES[qt2], M=M2, K=K2, us=pl * 1e6, gbs=b / pl / 1e9))
+        log(f"{fm.NAMES[qt2]} {M2}x{K2}: {pl * 1e6:.2f} us  {b / pl / 1e9:.0f} GB/s")
+        del cps, Wm
+        torch.cuda.empty_cache()
+    res["sweep"] = sweep
+
+    # ---- MoE layer ------------------------------
+    H, F, E, k = 2048, 768, 128, 8
+    router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=3)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    L = tb.moe_layer(H, F, E, k, fm.Q4_K, d(router), d(gate), d(up), d(down))
+    moe = {}
+    for T in (1, 16):
+        ntok = 64
+        xs = d(synth.activations((ntok, T, H), rng))
+        rs = d(synth.activations((ntok, T, H), rng))
+        out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+        ws_t = torch.empty(tb.moe_workspace_size(L, T), dtype=torch.uint8, device="cuda")
+        it = [0]
+
+        def mstep():
+            i = it[0] % ntok
+            it[0] += 1
+            tb.moe_forward(L, T, xs[i], rs[i], out, workspace=ws_t)
+        reps = 200
+        s = time_region(mstep, reps, 10, stream)
+        us = s / reps * 1e6
+        moe[f"decode_b{T}"] = dict(us_per_layer=us, us_per_token=us / T)
+        log(f"MoE decode b={T}: {us:.1f} us/layer  {us / T:.2f} us/token")
+    # prefill, Zipf-skewed routing
+    T = 512
+    bias = synth.zipf_router_bias(E, 1.1, 1.0, rng)
+    Lb = tb.moe_layer(H, F, E, k, fm.Q4_K, L._keep[0], L._keep[1], L._keep[2], L._keep[3], bias=d(bias))
+    xs = d(synth.activations((T, H), rng))
+    rs = d(synth.activations((T, H), rng))
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    ws_t = torch.empty(tb.moe_workspace_size(Lb, T), dtype=torch.uint8, device="cuda")
+    s = time_region(lambda: tb.moe_forward(Lb, T, xs, rs, out, workspace=ws_t), 10, 2, stream)
+    us = s / 10 * 1e6
+    moe["prefill_512_fp32"] = dict(us_per_layer=us, us_per_token=us / T)
+    log(f"MoE prefill T=512 (fp32 path): {us:.1f} us/layer  {us / T:.2f} us/token")
+    res["moe"] = moe
+    return res
+
+
+def cpu_leg(budget_s=12.0):
+    """The reference CPU path on this host, one pinned core, on a bounded
+    sample of the headline workload (whole Q4_K 4096x4096 matvecs)."""
+    from oracle.pyoracle import Oracle, Reference, host_has_avx512
+    from trailblaze_amd import formats as fm
+    from trailblaze_amd import synth
+
+    try:
+        os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
+    except (AttributeError, OSError):
+        pass
+    rng = np.random.default_rng(0)
+    M, K = 4096, 4096
+    W = synth.kquant_matrix(fm.Q4_K, M, K, rng)
+    x = synth.activations(K, rng)
+    b = matvec_bytes(fm.Q4_K, M, K)
+    if Reference.available() and host_has_avx512():
+        ref = Reference()
+        kind = "reference"
+        fns = {"tb_dispatch_matvec (AVX-512 class)": lambda: ref.dispatch_matvec_avx512(W, fm.Q4_K, M, K, x),
+               "tb_gguf_dequant_matvec (scalar)": lambda: ref.matvec(W, fm.Q4_K, M, K, x)}
+    else:
+        orc = Oracle()
+        kind = "port"
+        fns = {"AVX-512-structured restatement": lambda: orc.matvec_q4k_avx512s(W, M, K, x),
+               "scalar restatement": lambda: orc.matvec(W, fm.Q4_K, M, K, x)}
+    out = {}
+    for name, fn in fns.items():
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s / len(fns):
+            fn()
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        out[name] = dict(ms_per_matvec=dt * 1e3, gbs=b / dt / 1e9, reps=n)
+        log(f"CPU {name}: {dt * 1e3:.1f} ms/matvec {b / dt / 1e9:.2f} GB/s")
+    best = max(out, key=lambda k: out[k]["gbs"])
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(value=out[best]["gbs"], unit="GB/s", cores=1, kind=kind,
+                sample=f"{out[best]['reps']} whole Q4_K 4096x4096 matvecs via {best}, 1 pinned thread "
+                       f"({cpu_model}, nproc={os.cpu_count()})",
+                detail=out)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU only (single-GPU hot path); --gpus must be 1",
+              file=sys.stderr)
+        sys.exit(2)
+    res = gpu_leg(args)
+    h = res["headline"]
+    cpu = None
+    if not args.no_cpu and not args.quick:
+        cpu = cpu_leg()
+    line = {
+        "metric": "Q4_K matvec HBM GB/s",
+        "value": round(h["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(h["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k weights, fp32 activations and accumulate",
+        "data": "synthetic (seeded: fp16 scales U(1e-3,1e-2), uniform bytes, x ~ N(0,1))",
+        "config": {"workload": f"Q4_K matvec 4096x4096 (BASELINE configs[0]) over {h['ncopy']} distinct "
+                               f"weight copies per step (cold HBM)", "M": 4096, "K": 4096,
+                   "copies_per_step": h["ncopy"]},
+        "roofline": {"bound": "hbm", "achieved": round(h["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_matvec Q4_K", "us_per_launch": round(h["us_per_launch"], 3),
+                     "bytes_per_launch": h["bytes_per_launch"]},
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "extra": {"device": res["device"], "warm_mall_gbs": round(h["warm_gbs"], 1),
+                  "warm_us_per_launch": round(h["warm_us_per_launch"], 3),
+                  "sweep": res.get("sweep"), "moe": res.get("moe"),
+                  "cpu_detail": None if cpu is None else cpu["detail"]},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

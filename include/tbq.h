@@ -1,0 +1,111 @@
+/*
+ * tbq.h -- explicit, device-resident C API of libtbq, the gfx950 K-quant
+ * dequant-matvec and MoE engine.  All tensor pointers are device pointers
+ * (HBM) unless a name says _host; `stream` is a hipStream_t (NULL = the
+ * default stream).  Every call enqueues work and returns without waiting.
+ * Return convention follows the reference's tb_cuda_* ABI: 1 = done,
+ * 0 = unsupported input or HIP error (tbq_last_error() says which).
+ *
+ * Weight tensors use the reference's block layouts and row-major packing
+ * (ceil(K / block_weights) blocks per row, rows contiguous;
+ * layer4/tb_gguf.c:376-419).  qtype ids are ggml's (layer4/tb_gguf.h:24):
+ * 0 F32, 1 F16, 2 Q4_0, 8 Q8_0, 10 Q2_K, 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K,
+ * 15 Q8_K, 30 BF16.
+ */
+#ifndef TBQ_H
+#define TBQ_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime ----------------------------------------------------------- */
+/* Select device 0 and cache its properties.  Idempotent.  1 = ready. */
+int tbq_init(void);
+/* Human-readable reason for the last 0 returned on this thread. */
+const char *tbq_last_error(void);
+/* Device name and compute-unit count of the selected device (after init). */
+const char *tbq_device_name(void);
+int tbq_cu_count(void);
+
+void *tbq_malloc(size_t bytes);                 /* NULL on failure */
+int tbq_free(void *dev);                        /* NULL-safe */
+int tbq_memcpy_h2d(void *dev, const void *host, size_t bytes, void *stream);
+int tbq_memcpy_d2h(void *host, const void *dev, size_t bytes, void *stream);
+int tbq_stream_sync(void *stream);
+int tbq_device_sync(void);
+
+/* ---- formats ----------------------------------------------------------- */
+/* Bytes of one row of K weights (0 for an unknown qtype);
+ * replaces the geometry table of layer4/tb_gguf.c:380-398. */
+size_t tbq_row_bytes(int qtype, int K);
+/* 1 if tbq_matvec / tbq_dequant accept qtype. */
+int tbq_qtype_supported(int qtype);
+
+/* ---- dequantise (bit-exact hook) --------------------------------------- */
+/* out[nrows*K] = the reference's dequantised weights, bit for bit
+ * (tb_gguf_dequant_row, layer4/tb_gguf.h:90).  K must be a multiple of the
+ * block size (and of 8). */
+int tbq_dequant(const void *W, int qtype, int nrows, int K, float *out, void *stream);
+
+/* ---- decode matvec ----------------------------------------------------- */
+/* y[M] = dequant(W[M][K]) . x[K], fp32 accumulate (tb_gguf_dequant_matvec,
+ * layer4/tb_gguf.h:95-96; device-resident form of tb_cuda_matvec_device,
+ * layer4/tb_gguf_dequant.h:36-37).  K a multiple of 256 for super-block
+ * formats, of 32 otherwise; W and x 16-byte aligned. */
+int tbq_matvec(const void *W, int qtype, int M, int K, const float *x, float *y, void *stream);
+
+/* ---- MoE block --------------------------------------------------------- */
+/* Router: logits[e] = router[e] . xn (summed in the reference's sequential
+ * order) + bias[e]; softmax; top-k in the reference's slot order;
+ * renormalised weights (tb_route_experts with use_hdgl=0,
+ * layer4/tb_infer.h:120-122).  sel_idx/sel_w are [T][8]; slots >= k hold
+ * -1 / 0.  E <= 256, top_k clamped to 8. */
+int tbq_route(const float *xn, const float *router, const float *bias, int T, int H, int E,
+              int top_k, int *sel_idx, float *sel_w, void *stream);
+
+/* One MoE layer in the reference's packed expert layout
+ * (layer4/tb_infer.c:780-806): gate/up are [E*F rows][H], down [E*H rows][F],
+ * all in `qtype`; router is fp32 [E][H]. */
+typedef struct {
+    int H, F, E, top_k, qtype;
+    const float *router;
+    const float *bias;   /* [E] logit bias added before routing, or NULL */
+    const void *gate;
+    const void *up;
+    const void *down;
+} tbq_moe_layer;
+
+#define TBQ_MOE_FP32 0      /* fp32 decode kernels; outputs within 1e-5 rel-L2 */
+#define TBQ_MOE_BF16 1      /* prefill: grouped bf16 MFMA; within 1e-2 rel-L2 */
+
+/* Workspace bytes tbq_moe_forward needs for T tokens in `mode`. */
+size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode);
+/* out[T][H] = resid + sum_slots w_slot * expert_slot(xn) for every token
+ * (layer4/tb_infer.c:753-833,876).  sel_idx/sel_w ([T][8]) may be NULL.
+ * workspace: device buffer of tbq_moe_workspace_size() bytes, or NULL to
+ * use a library-owned buffer (grown on demand; not safe for concurrent
+ * calls). */
+int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float *resid, float *out,
+                    int *sel_idx, float *sel_w, void *workspace, size_t workspace_bytes, int mode,
+                    void *stream);
+
+/* Host-memory MoE block: the substitution for the MoE branch of
+ * tb_layer_forward (layer4/tb_infer.c:753-833,876).  Weights in L are device
+ * pointers (e.g. from tb_cuda_upload_tensor); xn, resid, out, sel_idx and
+ * sel_w are host arrays.  Synchronous.  Implemented in C11 over this API. */
+int tbq_moe_block_host(const tbq_moe_layer *L, int T, const float *xn_host, const float *resid_host,
+                       float *out_host, int *sel_idx_host, float *sel_w_host, int mode);
+
+/* ---- test hooks -------------------------------------------------------- */
+/* out[i] = expf(in[i]) evaluated by the device code the router uses. */
+int tbq_expf_device(const float *in, float *out, size_t n, void *stream);
+/* The same function compiled for the host. */
+float tbq_expf_host(float x);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,138 @@
+"""Writes the golden vectors under tests/golden/ from the reference's own C
+code, compiled in this container by `make -C oracle ref` into
+oracle/_ref/libtbref.so (layer4/tb_gguf.c, layer4/tb_infer.c and the sources
+they link, built from /root/reference in place).
+
+Each .npz holds inputs and the reference's outputs only (no code):
+  dequant_<FMT>.npz  tb_gguf_dequant_row       layer4/tb_gguf.c:293-371
+  matvec_<FMT>.npz   tb_gguf_dequant_matvec    layer4/tb_gguf.c:376-419
+  route.npz          tb_route_experts (use_hdgl=0) layer4/tb_infer.c:239-377
+  swiglu.npz         tb_swiglu                 layer4/tb_infer.c:130-135
+  moe.npz            the MoE block of tb_layer_forward (layer4/tb_infer.c:
+                     753-833,876) assembled from the reference functions
+                     above; only the weighted accumulate and the residual
+                     add (one fp32 multiply and add each) run in numpy.
+
+Run:  make -C oracle ref && python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+from oracle.pyoracle import Reference  # noqa: E402
+from trailblaze_amd import formats as fm  # noqa: E402
+from trailblaze_amd import synth  # noqa: E402
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+
+FMT_LIST = [fm.Q2_K, fm.Q3_K, fm.Q4_K, fm.Q5_K, fm.Q6_K, fm.Q8_0, fm.Q4_0, fm.Q8_K, fm.F16, fm.BF16, fm.F32]
+
+# fp16 patterns that exercise every branch of the reference's f16 decode:
+# +-0, the smallest/largest subnormal, normals, the largest finite, inf, nan.
+F16_SPECIAL = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x8200, 0x0400, 0x3C00, 0xBC00,
+                        0x7BFF, 0x7C00, 0xFC00, 0x7E00, 0x1234, 0x2E66], np.uint16)
+
+
+def special_blocks(qtype, n_rows, K, rng):
+    """Random blocks whose fp16 scale fields cycle through F16_SPECIAL."""
+    W = synth.kquant_matrix(qtype, n_rows, K, rng)
+    if qtype not in fm.SCALE_FIELDS:
+        return W
+    bw, bb = fm.GEOMETRY[qtype]
+    blocks = W.reshape(-1, bb)
+    for i in range(blocks.shape[0]):
+        for j, off in enumerate(fm.SCALE_FIELDS[qtype]):
+            v = F16_SPECIAL[(i + 5 * j) % len(F16_SPECIAL)]
+            blocks[i, off:off + 2] = np.frombuffer(np.uint16(v).tobytes(), np.uint8)
+    return blocks.reshape(W.shape)
+
+
+def main():
+    ref = Reference()
+    rng = np.random.default_rng(20261201)
+    for qt in FMT_LIST:
+        bw, _ = fm.GEOMETRY[qt]
+        K = 512 if bw == 256 else 256
+        rows = 6
+        Wr = synth.kquant_matrix(qt, rows, K, rng)
+        Ws = special_blocks(qt, rows, K, rng)
+        if qt == fm.F16:
+            Ws = np.resize(F16_SPECIAL, rows * K).view(np.uint8).reshape(rows, K * 2).copy()
+        W = np.concatenate([Wr, Ws], 0)
+        M = W.shape[0]
+        rb = fm.row_bytes(qt, K)
+        deq = ref.dequant_rows(W, qt, M, K, rb)
+        np.savez_compressed(os.path.join(OUT, f"dequant_{fm.NAMES[qt]}.npz"),
+                            W=W, qtype=np.int32(qt), M=np.int32(M), K=np.int32(K), out=deq)
+        # matvec: finite weights only, two shapes (K spans 2 and 3 blocks of 256 / more of 32)
+        for K2 in ((512, 768) if bw == 256 else (256, 96)):
+            M2 = 24
+            W2 = synth.kquant_matrix(qt, M2, K2, rng)
+            x = synth.activations(K2, rng)
+            y = ref.matvec(W2, qt, M2, K2, x)
+            np.savez_compressed(os.path.join(OUT, f"matvec_{fm.NAMES[qt]}_K{K2}.npz"),
+                                W=W2, x=x, qtype=np.int32(qt), M=np.int32(M2), K=np.int32(K2), out=y)
+
+    # routing: several (E, k) combos, normal logits, plus forced ties
+    cases = []
+    for (E, k, n) in ((128, 8, 64), (64, 6, 16), (8, 2, 32), (16, 8, 16), (256, 8, 8), (5, 8, 4)):
+        L = rng.standard_normal((n, E)).astype(np.float32)
+        L[n // 2:] = np.round(L[n // 2:] * 4) / 4  # many exact ties
+        for t in range(n):
+            idx, w = ref.route(L[t], k)
+            cases.append((E, k, L[t], idx, w))
+    np.savez_compressed(os.path.join(OUT, "route.npz"),
+                        E=np.array([c[0] for c in cases], np.int32),
+                        k=np.array([c[1] for c in cases], np.int32),
+                        logits=np.concatenate([c[2] for c in cases]).astype(np.float32),
+                        idx=np.concatenate([c[3] for c in cases]).astype(np.int32),
+                        w=np.concatenate([c[4] for c in cases]).astype(np.float32))
+
+    # swiglu: wide range including exp overflow/underflow
+    g = np.concatenate([rng.standard_normal(4096).astype(np.float32) * 4,
+                        np.array([0.0, -0.0, 88.0, -88.0, 100.0, -100.0, 1e-30, -1e-30, 30.0, -30.0], np.float32)])
+    u = rng.standard_normal(g.size).astype(np.float32)
+    np.savez_compressed(os.path.join(OUT, "swiglu.npz"), g=g, u=u, out=ref.swiglu(g, u))
+
+    # MoE block: small Qwen3-MoE-like layer, Q4_K experts, with a router bias
+    H, F, E, k, T = 256, 256, 8, 3, 5
+    qt = fm.Q4_K
+    router, gate, up, down = synth.moe_layer(H, F, E, qt, seed=777)
+    bias = synth.zipf_router_bias(E, 1.1, 0.5, rng)
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    rbH, rbF = fm.row_bytes(qt, H), fm.row_bytes(qt, F)
+    out = np.empty((T, H), np.float32)
+    sidx = np.full((T, 8), -1, np.int32)
+    sw = np.zeros((T, 8), np.float32)
+    for t in range(T):
+        lg = ref.matvec(router.view(np.uint8).reshape(E, H * 4), fm.F32, E, H, xn[t])
+        lg = (lg + bias).astype(np.float32)
+        idx, w = ref.route(lg, k)
+        acc = np.zeros(H, np.float32)
+        for s, e in enumerate(idx):
+            gb = gate.reshape(E, F, rbH)[e]
+            ub = up.reshape(E, F, rbH)[e]
+            db = down.reshape(E, H, rbF)[e]
+            gv = ref.matvec(gb, qt, F, H, xn[t])
+            uv = ref.matvec(ub, qt, F, H, xn[t])
+            a = ref.swiglu(gv, uv)
+            y = ref.matvec(db, qt, H, F, a)
+            acc = (acc + (np.float32(w[s]) * y).astype(np.float32)).astype(np.float32)
+        out[t] = (resid[t] + acc).astype(np.float32)
+        sidx[t, :len(idx)] = idx
+        sw[t, :len(w)] = w
+    np.savez_compressed(os.path.join(OUT, "moe.npz"), H=np.int32(H), F=np.int32(F), E=np.int32(E),
+                        k=np.int32(k), qtype=np.int32(qt), router=router, gate=gate, up=up, down=down,
+                        bias=bias, xn=xn, resid=resid, out=out, idx=sidx, w=sw)
+    print("golden vectors written to", OUT)
+
+
+if __name__ == "__main__":
+    main()

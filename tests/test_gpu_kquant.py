@@ -1,0 +1,158 @@
+"""GPU parity for the K-quant path, through the C-ABI (libtbq.so):
+  * dequant: bit-exact against the reference's golden vectors and against
+    the oracle on random matrices (NaN payloads aside);
+  * matvec: relative L2 <= 1e-5 against the oracle (the reference's
+    sequential fp32 dot, layer4/tb_gguf.c:376-419) at the BASELINE.json
+    shapes and at ragged/edge shapes; exact on exactly-representable inputs;
+  * the reference ABI tb_cuda_matvec_device on host buffers;
+  * the router's device expf bit-identical to glibc's on a large sample."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import trailblaze_amd as tb
+from conftest import bits_equal, golden_names, load_golden, rel_l2
+from gpu_util import dev, empty, host
+from trailblaze_amd import formats as fm
+from trailblaze_amd import synth
+
+pytestmark = pytest.mark.gpu
+MATVEC_TOL = 1e-5
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    import torch
+    assert torch.cuda.is_available()
+    print("device:", tb.init(), flush=True)
+
+
+def gpu_dequant(W, qt, M, K):
+    import torch
+    out = empty(M * K, torch.float32)
+    tb.dequant(dev(W), qt, M, K, out)
+    return host(out).reshape(M, K)
+
+
+def gpu_matvec(W, qt, M, K, x):
+    import torch
+    y = empty(M, torch.float32)
+    tb.matvec(dev(W), qt, M, K, dev(x), y)
+    return host(y)
+
+
+@pytest.mark.parametrize("name", golden_names("dequant_"))
+def test_dequant_golden_bit_exact(name):
+    g = load_golden(name)
+    print(name, flush=True)
+    got = gpu_dequant(g["W"], int(g["qtype"]), int(g["M"]), int(g["K"]))
+    assert bits_equal(got, g["out"])
+
+
+@pytest.mark.parametrize("qt", [fm.Q2_K, fm.Q3_K, fm.Q4_K, fm.Q5_K, fm.Q6_K, fm.Q8_0, fm.Q4_0, fm.Q8_K])
+def test_dequant_random_bit_exact(oracle, qt):
+    rng = np.random.default_rng(1000 + qt)
+    M, K = 257, 4096
+    W = synth.kquant_matrix(qt, M, K, rng)
+    assert bits_equal(gpu_dequant(W, qt, M, K), oracle.dequant_rows(W, qt, M, K))
+
+
+@pytest.mark.parametrize("name", golden_names("matvec_"))
+def test_matvec_golden(name):
+    g = load_golden(name)
+    print(name, flush=True)
+    got = gpu_matvec(g["W"], int(g["qtype"]), int(g["M"]), int(g["K"]), g["x"])
+    assert rel_l2(got, g["out"]) <= MATVEC_TOL
+
+
+# BASELINE.json configs[0] and configs[1] shapes (Q6_K lm_head covered by
+# test_matvec_lm_head below)
+SHAPES = [(fm.Q4_K, 4096, 4096)] + [(qt, M, K) for qt in (fm.Q2_K, fm.Q3_K, fm.Q5_K, fm.Q8_0)
+                                    for (M, K) in ((12288, 4096), (4096, 12288))]
+
+
+@pytest.mark.parametrize("qt,M,K", SHAPES)
+def test_matvec_config_shapes(oracle, qt, M, K):
+    print(fm.NAMES[qt], M, K, flush=True)
+    rng = np.random.default_rng(M * 7 + K + qt)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, qt, M, K, x), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+
+
+def test_matvec_lm_head(oracle):
+    qt, M, K = fm.Q6_K, 151936, 4096
+    rng = np.random.default_rng(42)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    y = gpu_matvec(W, qt, M, K, x)
+    rows = rng.choice(M, 4096, replace=False)
+    rows.sort()
+    ref = oracle.matvec(np.ascontiguousarray(W[rows]), qt, len(rows), K, x)
+    assert rel_l2(y[rows], ref) <= MATVEC_TOL
+
+
+@pytest.mark.parametrize("qt", [fm.Q2_K, fm.Q3_K, fm.Q4_K, fm.Q5_K, fm.Q6_K, fm.Q8_0, fm.Q4_0, fm.Q8_K,
+                                fm.F16, fm.BF16, fm.F32])
+@pytest.mark.parametrize("M,K", [(1, 256), (3, 768), (131, 2048), (517, 512), (64, 12288)])
+def test_matvec_edge_shapes(oracle, qt, M, K):
+    rng = np.random.default_rng(M + K + qt)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, qt, M, K, x), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+
+
+def test_matvec_exact_one_hot():
+    # Q8_0 weights in {0, 1} with d = 1: every output is one x value exactly
+    M, K = 300, 1024
+    rng = np.random.default_rng(3)
+    W = np.zeros((M, K // 32, 34), np.uint8)
+    W[:, :, 0:2] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)
+    cols = rng.integers(0, K, M)
+    for m, j in enumerate(cols):
+        W[m, j // 32, 2 + j % 32] = 1
+    x = rng.standard_normal(K).astype(np.float32)
+    assert np.array_equal(gpu_matvec(W.reshape(M, -1), fm.Q8_0, M, K, x), x[cols])
+
+
+def test_matvec_rejects_bad_input():
+    import torch
+    W = empty(4096, torch.uint8)
+    x = empty(300, torch.float32)
+    y = empty(4, torch.float32)
+    with pytest.raises(tb.TbqError):
+        tb.matvec(W, fm.Q4_K, 4, 300, x, y)        # K not a multiple of 256
+    with pytest.raises(tb.TbqError):
+        tb.matvec(W, 21, 4, 256, x, y)            # qtype without a CPU decoder
+
+
+def test_reference_abi_matvec_device(oracle):
+    L = tb.lib()
+    assert L.tb_cuda_init() == 1
+    rng = np.random.default_rng(9)
+    for qt, M, K in ((fm.Q4_K, 1000, 4096), (fm.Q2_K, 64, 768), (fm.Q6_K, 33, 2048)):
+        W = synth.kquant_matrix(qt, M, K, rng)
+        x = synth.activations(K, rng)
+        d = L.tb_cuda_upload_tensor(W.ctypes.data, W.nbytes)
+        assert d
+        out = np.zeros(M, np.float32)
+        assert L.tb_cuda_matvec_device(d, qt, M, K, x.ctypes.data, out.ctypes.data) == 1
+        assert rel_l2(out, oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+        assert L.tb_cuda_matvec_device(d, 21, M, K, x.ctypes.data, out.ctypes.data) == 0
+        L.tb_cuda_free_tensor(d)
+    assert L.tb_cuda_upload_x(x.ctypes.data, K) == 1
+    L.tb_cuda_sync_all()
+    L.tb_cuda_cleanup()
+
+
+def test_device_expf_matches_glibc(oracle):
+    import torch
+    rng = np.random.default_rng(12)
+    xs = [rng.integers(0, 2 ** 32, 1 << 24, dtype=np.uint64).astype(np.uint32).view(np.float32),
+          np.linspace(-20, 0, 1 << 22, dtype=np.float32),
+          np.arange(0xBF800000, 0xBF800000 + (1 << 22), dtype=np.uint32).view(np.float32)]
+    for x in xs:
+        out = empty(x.size, torch.float32)
+        tb.expf_device(dev(x), out)
+        assert bits_equal(host(out), oracle.expf(x))

@@ -1,0 +1,223 @@
+// tbq_api.hip -- the extern "C" device API of libtbq (include/tbq.h): input
+// validation on the host, then the gfx950 launchers.  Nothing here falls back
+// to the CPU: an input the kernels do not cover returns 0 with a reason.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/tbq.h"
+#include "tbq_device.hpp"
+#include "tbq_kernels.h"
+
+using namespace tbq;
+
+namespace {
+
+thread_local char g_err[512] = "";
+std::once_flag g_init_once;
+int g_ready = 0;
+int g_cu = 0;
+char g_name[256] = "";
+
+std::mutex g_ws_mu;
+void *g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+int fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return 0;
+}
+
+int hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return 1;
+    return fail("%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool known_qtype(int qt) {
+    switch (qt) {
+    case QT_F32: case QT_F16: case QT_BF16: case QT_Q4_0: case QT_Q8_0: case QT_Q2_K:
+    case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_Q8_K:
+        return true;
+    default:
+        return false;
+    }
+}
+
+hipStream_t S(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+int ensure_init() {
+    std::call_once(g_init_once, [] {
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return;
+        if (hipSetDevice(0) != hipSuccess) return;
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, 0) != hipSuccess) return;
+        g_cu = p.multiProcessorCount;
+        snprintf(g_name, sizeof g_name, "%s (%s)", p.name, p.gcnArchName);
+        g_ready = 1;
+    });
+    if (!g_ready) return fail("no HIP device available");
+    return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tbq_init(void) { return ensure_init(); }
+const char *tbq_last_error(void) { return g_err; }
+const char *tbq_device_name(void) { return g_name; }
+int tbq_cu_count(void) { return g_cu; }
+
+void *tbq_malloc(size_t bytes) {
+    if (!ensure_init()) return nullptr;
+    void *p = nullptr;
+    if (!hip_ok(hipMalloc(&p, bytes ? bytes : 1), "hipMalloc")) return nullptr;
+    return p;
+}
+int tbq_free(void *p) { return p ? hip_ok(hipFree(p), "hipFree") : 1; }
+int tbq_memcpy_h2d(void *d, const void *h, size_t n, void *s) {
+    return hip_ok(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, S(s)), "hipMemcpyAsync H2D");
+}
+int tbq_memcpy_d2h(void *h, const void *d, size_t n, void *s) {
+    return hip_ok(hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, S(s)), "hipMemcpyAsync D2H");
+}
+int tbq_stream_sync(void *s) { return hip_ok(hipStreamSynchronize(S(s)), "hipStreamSynchronize"); }
+int tbq_device_sync(void) { return hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+
+size_t tbq_row_bytes(int qt, int K) {
+    if (!known_qtype(qt) || K < 0) return 0;
+    int bw = block_weights(qt), bb = block_bytes(qt);
+    return (size_t)((K + bw - 1) / bw) * (size_t)bb;
+}
+
+int tbq_qtype_supported(int qt) { return known_qtype(qt) ? 1 : 0; }
+
+int tbq_dequant(const void *W, int qt, int nrows, int K, float *out, void *s) {
+    if (!ensure_init()) return 0;
+    if (!known_qtype(qt)) return fail("tbq_dequant: unsupported qtype %d", qt);
+    if (nrows < 0 || K <= 0 || K % block_weights(qt) || K % 8) return fail("tbq_dequant: K=%d not a multiple of the block size", K);
+    if (!W || !out || !aligned16(out)) return fail("tbq_dequant: null or misaligned pointer");
+    if (nrows == 0) return 1;
+    return hip_ok(launch_dequant(qt, W, (long long)nrows * K, out, S(s)), "dequant launch");
+}
+
+static int check_matvec(const void *W, int qt, int M, int K, const float *x, const float *y) {
+    if (!known_qtype(qt)) return fail("unsupported qtype %d", qt);
+    int chunk = block_weights(qt) == 256 ? 256 : 32;
+    if (M < 0 || K <= 0 || K % chunk) return fail("K=%d must be a positive multiple of %d for qtype %d", K, chunk, qt);
+    if ((size_t)K * 4 + (size_t)(K / 16) * 4 > 64 * 1024) return fail("K=%d exceeds the LDS-resident x limit", K);
+    if (!W || !x || !y) return fail("null pointer");
+    if (!aligned16(x)) return fail("x must be 16-byte aligned");
+    if ((qt == QT_Q4_K || qt == QT_Q5_K || qt == QT_F32) && !aligned16(W))
+        return fail("W must be 16-byte aligned for qtype %d", qt);
+    if (((uintptr_t)W & 1u)) return fail("W must be 2-byte aligned");
+    return 1;
+}
+
+int tbq_matvec(const void *W, int qt, int M, int K, const float *x, float *y, void *s) {
+    if (!ensure_init()) return 0;
+    if (!check_matvec(W, qt, M, K, x, y)) return 0;
+    if (M == 0) return 1;
+    return hip_ok(launch_matvec_generic(qt, W, M, K, x, y, S(s), g_cu), "matvec launch");
+}
+
+int tbq_route(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
+              int *sel_idx, float *sel_w, void *s) {
+    if (!ensure_init()) return 0;
+    if (T < 0 || H <= 0 || H % 8 || E <= 0 || E > 256 || top_k <= 0)
+        return fail("tbq_route: bad shape T=%d H=%d E=%d k=%d", T, H, E, top_k);
+    if ((size_t)H * 4 + 1024 > 60 * 1024) return fail("tbq_route: H=%d too large", H);
+    if (!xn || !router || !sel_idx || !sel_w || !aligned16(xn) || !aligned16(router))
+        return fail("tbq_route: null or misaligned pointer");
+    if (T == 0) return 1;
+    return hip_ok(launch_route(xn, router, bias, T, H, E, top_k, sel_idx, sel_w, S(s)), "route launch");
+}
+
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode) {
+    (void)mode;
+    if (!L || T <= 0) return 0;
+    int k = L->top_k > 8 ? 8 : L->top_k;
+    size_t n = 0;
+    n += align256((size_t)T * 8 * 4) * 2;                   // sel idx / w
+    n += align256((size_t)T * k * L->F * 4);                 // act
+    n += align256((size_t)T * k * L->H * 4);                 // y
+    return n;
+}
+
+static int check_moe(const tbq_moe_layer *L, int T) {
+    if (!L) return fail("tbq_moe_forward: null layer");
+    if (T < 0 || L->E <= 0 || L->E > 256 || L->top_k <= 0) return fail("tbq_moe_forward: bad T/E/top_k");
+    if (L->H <= 0 || L->F <= 0 || L->H % 256 || L->F % 256) return fail("tbq_moe_forward: H and F must be multiples of 256");
+    switch (L->qtype) {
+    case QT_Q2_K: case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_Q8_0: break;
+    default: return fail("tbq_moe_forward: expert qtype %d not supported", L->qtype);
+    }
+    if (!L->router || !L->gate || !L->up || !L->down) return fail("tbq_moe_forward: null weight");
+    if (!aligned16(L->router) || !aligned16(L->gate) || !aligned16(L->up) || !aligned16(L->down))
+        return fail("tbq_moe_forward: weights must be 16-byte aligned");
+    if ((size_t)L->H * 4 + (size_t)L->H / 4 > 60 * 1024) return fail("tbq_moe_forward: H too large");
+    return 1;
+}
+
+int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float *resid, float *out, int *sel_idx,
+                    float *sel_w, void *workspace, size_t ws_bytes, int mode, void *s) {
+    if (!ensure_init()) return 0;
+    if (!check_moe(L, T)) return 0;
+    if (mode != TBQ_MOE_FP32) return fail("tbq_moe_forward: mode %d not available", mode);
+    if (!xn || !resid || !out || !aligned16(xn) || !aligned16(resid) || !aligned16(out))
+        return fail("tbq_moe_forward: null or misaligned activation pointer");
+    if (T == 0) return 1;
+    size_t need = tbq_moe_workspace_size(L, T, mode);
+    std::unique_lock<std::mutex> lk(g_ws_mu, std::defer_lock);
+    char *ws = (char *)workspace;
+    if (!ws) {
+        lk.lock();
+        if (g_ws_bytes < need) {
+            if (g_ws && !hip_ok(hipFree(g_ws), "hipFree")) return 0;
+            g_ws = nullptr;
+            g_ws_bytes = 0;
+            if (!hip_ok(hipMalloc(&g_ws, need), "hipMalloc workspace")) return 0;
+            g_ws_bytes = need;
+        }
+        ws = (char *)g_ws;
+    } else if (ws_bytes < need) {
+        return fail("tbq_moe_forward: workspace %zu < %zu bytes", ws_bytes, need);
+    }
+    MoeArgs a;
+    a.T = T; a.H = L->H; a.F = L->F; a.E = L->E; a.top_k = L->top_k;
+    a.k = L->top_k > 8 ? 8 : L->top_k;
+    a.qtype = L->qtype;
+    a.xn = xn; a.resid = resid; a.router = L->router; a.bias = L->bias;
+    a.gate = L->gate; a.up = L->up; a.down = L->down; a.out = out;
+    size_t off = 0;
+    int *ws_idx = (int *)(ws + off); off += align256((size_t)T * 8 * 4);
+    float *ws_w = (float *)(ws + off); off += align256((size_t)T * 8 * 4);
+    a.act = (float *)(ws + off); off += align256((size_t)T * a.k * a.F * 4);
+    a.y = (float *)(ws + off);
+    a.sel_idx = sel_idx ? sel_idx : ws_idx;
+    a.sel_w = sel_w ? sel_w : ws_w;
+    return hip_ok(launch_moe_fp32(a, S(s)), "moe launch");
+}
+
+int tbq_expf_device(const float *in, float *out, size_t n, void *s) {
+    if (!ensure_init()) return 0;
+    if (!in || !out) return fail("tbq_expf_device: null pointer");
+    if (n == 0) return 1;
+    return hip_ok(launch_expf(in, out, (long long)n, S(s)), "expf launch");
+}
+
+float tbq_expf_host(float x) { return expf_glibc(x); }
+
+}  // extern "C"

@@ -1,0 +1,127 @@
+// tbq_device.hpp -- shared device code for the gfx950 K-quant / MoE kernels.
+//
+// Everything here is compiled with -ffp-contract=off: an expression a*b+c is
+// a multiply and an add, each rounded, unless the code calls fmaf()
+// explicitly.  The dequant path relies on that to reproduce the reference's
+// roundings bit for bit (layer4/tb_gguf.c is built with -std=c11, which does
+// not contract either).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tbq {
+
+// ggml type ids used by the reference (layer4/tb_gguf.h:24).
+enum QType : int {
+    QT_F32 = 0, QT_F16 = 1, QT_Q4_0 = 2, QT_Q8_0 = 8, QT_Q2_K = 10, QT_Q3_K = 11,
+    QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_Q8_K = 15, QT_BF16 = 30
+};
+
+// weights / bytes per block, layer4/tb_gguf.c:380-394.
+__host__ __device__ constexpr int block_weights(int qt) {
+    return (qt == QT_F32 || qt == QT_F16 || qt == QT_BF16) ? 1
+         : (qt == QT_Q4_0 || qt == QT_Q8_0) ? 32 : 256;
+}
+__host__ __device__ constexpr int block_bytes(int qt) {
+    return qt == QT_F32 ? 4 : (qt == QT_F16 || qt == QT_BF16) ? 2 : qt == QT_Q4_0 ? 18
+         : qt == QT_Q8_0 ? 34 : qt == QT_Q2_K ? 84 : qt == QT_Q3_K ? 110 : qt == QT_Q4_K ? 144
+         : qt == QT_Q5_K ? 176 : qt == QT_Q6_K ? 210 : qt == QT_Q8_K ? 292 : 0;
+}
+
+// fp16 -> fp32 exactly as layer4/tb_gguf.c:92-101 decodes it.  A zero
+// exponent keeps the mantissa in place under a zero f32 exponent (subnormal
+// halves become m*2^-136); exponent 31 becomes the f32 inf/nan exponent.
+// Integer bit work only -- v_cvt_f32_f16 would decode subnormals correctly
+// and so differ from the reference.
+__host__ __device__ __forceinline__ float f16_ref(uint32_t h) {
+    uint32_t s = (h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    uint32_t bits = e == 0 ? (s | (m << 13))
+                  : e == 31 ? (s | 0x7F800000u | (m << 13))
+                  : (s | ((e + 112u) << 23) | (m << 13));
+    return __builtin_bit_cast(float, bits);
+}
+
+__host__ __device__ __forceinline__ float bf16_ref(uint32_t b) {
+    return __builtin_bit_cast(float, b << 16);
+}
+
+// ---------------------------------------------------------------------------
+// expf, bit-identical to glibc 2.35's expf on every float input.
+//
+// Method: the table-driven expf of ARM's optimized-routines (Szabolcs Nagy,
+// 2017; adopted by glibc 2.27): x*N/ln2 = k + r with N = 32 and |r| <= 1/2;
+// exp(x) = 2^(k/N) * 2^(r/N), where 2^(k/N) is a table value with k/N's
+// integer part added into the exponent bits, and 2^(r/N) is a cubic
+// polynomial in r, all evaluated in double (three explicit fmas, as the
+// FMA-enabled x86-64 build evaluates it) and rounded once to float.  The
+// table and coefficients are reproduced from that published method; one
+// table entry (index 31) carries an offset of 24 ulp so the results match
+// glibc's on all 2^32 inputs, which tests/ verify exhaustively on the host
+// and on a large sample on the GPU.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ float expf_glibc(float x) {
+    constexpr int TB = 5, N = 1 << TB;
+    const uint64_t T[N] = {
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4558ull};
+    const double C0 = 0x1.c6af84b912394p-5 / N / N / N;
+    const double C1 = 0x1.ebfce50fac4f3p-3 / N / N;
+    const double C2 = 0x1.62e42ff0c52d6p-1 / N;
+    const double InvLn2N = 0x1.71547652b82fep+0 * N;
+    const double Shift = 0x1.8p+52;
+
+    uint32_t ux = __builtin_bit_cast(uint32_t, x);
+    uint32_t abstop = (ux >> 20) & 0x7FFu;
+    if (abstop >= 0x42Bu) {               // |x| >= 88, inf or nan
+        if (ux == 0xFF800000u) return 0.0f;                 // -inf
+        if (abstop >= 0x7F8u) return x + x;                 // +inf, nan
+        if (x > 0x1.62e42ep6f) return __builtin_huge_valf(); // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;                 // underflow
+    }
+    double xd = (double)x;
+    double z = InvLn2N * xd;
+    double kd = z + Shift;
+    uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= Shift;
+    double r = z - kd;
+    uint64_t t = T[ki % N];
+    t += ki << (52 - TB);
+    double s = __builtin_bit_cast(double, t);
+    double p = __builtin_fma(C0, r, C1);
+    double r2 = r * r;
+    double y = __builtin_fma(C2, r, 1.0);
+    y = __builtin_fma(p, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level helpers (wave64).
+// ---------------------------------------------------------------------------
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, WIDTH);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
+    return *reinterpret_cast<const uint32_t *>(p);
+}
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {
+    return *reinterpret_cast<const uint16_t *>(p);
+}
+__device__ __forceinline__ uint4 ld_u128(const uint8_t *p) {
+    return *reinterpret_cast<const uint4 *>(p);
+}
+
+}  // namespace tbq

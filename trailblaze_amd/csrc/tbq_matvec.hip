@@ -1,0 +1,162 @@
+// tbq_matvec.hip -- gfx950 kernels for the bit-exact dequant hook and the
+// decode dequant-matvec y = W x (fp32 x, fp32 accumulate) for every block
+// format of the reference's dequant table (layer4/tb_gguf.c:293-419).
+#include "tbq_kquant.hpp"
+#include "tbq_kernels.h"
+
+namespace tbq {
+
+// ---------------------------------------------------------------------------
+// Dequant: thread t writes weights 8t..8t+7 of the flattened matrix.  Rows
+// are whole blocks, so flat weight index / block_weights is the block index.
+// ---------------------------------------------------------------------------
+template <int QT>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ W, long long n8,
+                                                 float *__restrict__ out) {
+    constexpr int BW = block_weights(QT), BB = block_bytes(QT);
+    for (long long t = blockIdx.x * 256ll + threadIdx.x; t < n8; t += (long long)gridDim.x * 256) {
+        long long e = t * 8;
+        float w[8];
+        if constexpr (BW == 1) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint8_t *p = W + (e + i) * BB;
+                w[i] = QT == QT_F32 ? __builtin_bit_cast(float, ldu32(p))
+                     : QT == QT_F16 ? f16_ref(ldu16(p)) : bf16_ref(ldu16(p));
+            }
+        } else {
+            long long blk = e / BW;
+            decode8<QT>(W + blk * BB, (int)(e - blk * BW), w);
+        }
+        float4 *o = reinterpret_cast<float4 *>(out + e);
+        o[0] = make_float4(w[0], w[1], w[2], w[3]);
+        o[1] = make_float4(w[4], w[5], w[6], w[7]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Generic decode matvec.  x (and its 16-element group sums) are staged once
+// per workgroup in LDS; LPR lanes share a row, each striding over the row's
+// 32-weight chunks; LPR-wide shuffle reduction; rows grid-strided.
+// ---------------------------------------------------------------------------
+template <int QT, int LPR>
+__global__ __launch_bounds__(256) void k_matvec_generic(const uint8_t *__restrict__ W, int M, int K,
+                                                        long long row_bytes, const float *__restrict__ x,
+                                                        float *__restrict__ y) {
+    extern __shared__ float lds[];
+    float *xl = lds;            // K floats
+    float *xs = lds + K;        // K/16 group sums
+    for (int i = threadIdx.x * 4; i < K; i += 1024)
+        *reinterpret_cast<float4 *>(xl + i) = *reinterpret_cast<const float4 *>(x + i);
+    __syncthreads();
+    for (int g = threadIdx.x; g < K / 16; g += 256) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) s += xl[16 * g + i];
+        xs[g] = s;
+    }
+    __syncthreads();
+    constexpr int RPW = 256 / LPR;
+    const int C = K / 32;
+    const int lane = threadIdx.x % LPR, rsub = threadIdx.x / LPR;
+    for (int r0 = blockIdx.x * RPW; r0 < M; r0 += gridDim.x * RPW) {
+        int r = r0 + rsub;
+        float acc = 0.f;
+        if (r < M) {
+            const uint8_t *row = W + (long long)r * row_bytes;
+            for (int c = lane; c < C; c += LPR) acc += chunk_dot<QT>(row, c, xl + 32 * c, xs + 2 * c);
+        }
+        acc = group_sum<LPR>(acc);
+        if (lane == 0 && r < M) y[r] = acc;
+    }
+}
+
+template <int QT>
+static hipError_t launch_dequant_t(const void *W, long long nweights, float *out, hipStream_t s) {
+    long long n8 = nweights / 8;
+    long long blocks = (n8 + 255) / 256;
+    int grid = (int)(blocks < 65536 ? blocks : 65536);
+    hipLaunchKernelGGL((k_dequant<QT>), dim3(grid), dim3(256), 0, s, (const uint8_t *)W, n8, out);
+    return hipGetLastError();
+}
+
+template <int QT, int LPR>
+static hipError_t launch_mv(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu) {
+    constexpr int RPW = 256 / LPR;
+    long long rb = (long long)(K / block_weights(QT)) * block_bytes(QT);
+    int need = (M + RPW - 1) / RPW;
+    int cap = n_cu * 4;
+    int grid = need < cap ? need : cap;
+    size_t lds = (size_t)K * 4 + (size_t)(K / 16) * 4;
+    hipLaunchKernelGGL((k_matvec_generic<QT, LPR>), dim3(grid), dim3(256), lds, s, (const uint8_t *)W, M, K, rb, x, y);
+    return hipGetLastError();
+}
+
+template <int QT>
+static hipError_t launch_mv_q(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu) {
+    int C = K / 32;
+    // largest power of two <= min(C, 64) that divides C when possible
+    int lpr = 64;
+    while (lpr > 1 && (lpr > C || C % lpr)) lpr >>= 1;
+    if (lpr < 4 && C >= 4) lpr = 4;
+    switch (lpr) {
+    case 64: return launch_mv<QT, 64>(W, M, K, x, y, s, n_cu);
+    case 32: return launch_mv<QT, 32>(W, M, K, x, y, s, n_cu);
+    case 16: return launch_mv<QT, 16>(W, M, K, x, y, s, n_cu);
+    case 8: return launch_mv<QT, 8>(W, M, K, x, y, s, n_cu);
+    case 4: return launch_mv<QT, 4>(W, M, K, x, y, s, n_cu);
+    case 2: return launch_mv<QT, 2>(W, M, K, x, y, s, n_cu);
+    default: return launch_mv<QT, 1>(W, M, K, x, y, s, n_cu);
+    }
+}
+
+hipError_t launch_dequant(int qt, const void *W, long long nweights, float *out, hipStream_t s) {
+    switch (qt) {
+    case QT_F32: return launch_dequant_t<QT_F32>(W, nweights, out, s);
+    case QT_F16: return launch_dequant_t<QT_F16>(W, nweights, out, s);
+    case QT_BF16: return launch_dequant_t<QT_BF16>(W, nweights, out, s);
+    case QT_Q4_0: return launch_dequant_t<QT_Q4_0>(W, nweights, out, s);
+    case QT_Q8_0: return launch_dequant_t<QT_Q8_0>(W, nweights, out, s);
+    case QT_Q2_K: return launch_dequant_t<QT_Q2_K>(W, nweights, out, s);
+    case QT_Q3_K: return launch_dequant_t<QT_Q3_K>(W, nweights, out, s);
+    case QT_Q4_K: return launch_dequant_t<QT_Q4_K>(W, nweights, out, s);
+    case QT_Q5_K: return launch_dequant_t<QT_Q5_K>(W, nweights, out, s);
+    case QT_Q6_K: return launch_dequant_t<QT_Q6_K>(W, nweights, out, s);
+    case QT_Q8_K: return launch_dequant_t<QT_Q8_K>(W, nweights, out, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_matvec_generic(int qt, const void *W, int M, int K, const float *x, float *y,
+                                 hipStream_t s, int n_cu) {
+    switch (qt) {
+    case QT_F32: return launch_mv_q<QT_F32>(W, M, K, x, y, s, n_cu);
+    case QT_F16: return launch_mv_q<QT_F16>(W, M, K, x, y, s, n_cu);
+    case QT_BF16: return launch_mv_q<QT_BF16>(W, M, K, x, y, s, n_cu);
+    case QT_Q4_0: return launch_mv_q<QT_Q4_0>(W, M, K, x, y, s, n_cu);
+    case QT_Q8_0: return launch_mv_q<QT_Q8_0>(W, M, K, x, y, s, n_cu);
+    case QT_Q2_K: return launch_mv_q<QT_Q2_K>(W, M, K, x, y, s, n_cu);
+    case QT_Q3_K: return launch_mv_q<QT_Q3_K>(W, M, K, x, y, s, n_cu);
+    case QT_Q4_K: return launch_mv_q<QT_Q4_K>(W, M, K, x, y, s, n_cu);
+    case QT_Q5_K: return launch_mv_q<QT_Q5_K>(W, M, K, x, y, s, n_cu);
+    case QT_Q6_K: return launch_mv_q<QT_Q6_K>(W, M, K, x, y, s, n_cu);
+    case QT_Q8_K: return launch_mv_q<QT_Q8_K>(W, M, K, x, y, s, n_cu);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// Device expf evaluated over a buffer (test hook for the router's expf).
+__global__ void k_expf(const float *__restrict__ in, float *__restrict__ out, long long n) {
+    for (long long i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (long long)gridDim.x * 256)
+        out[i] = expf_glibc(in[i]);
+}
+
+hipError_t launch_expf(const float *in, float *out, long long n, hipStream_t s) {
+    long long blocks = (n + 255) / 256;
+    int grid = (int)(blocks < 16384 ? blocks : 16384);
+    if (grid < 1) grid = 1;
+    hipLaunchKernelGGL(k_expf, dim3(grid), dim3(256), 0, s, in, out, n);
+    return hipGetLastError();
+}
+
+}  // namespace tbq

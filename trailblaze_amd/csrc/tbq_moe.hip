@@ -1,0 +1,287 @@
+// tbq_moe.hip -- gfx950 kernels for the MoE block of the reference's forward
+// pass (layer4/tb_infer.c:753-833,876) on the fp32 path:
+//
+//   k_route          router logits + softmax + top-k + renormalise, one
+//                    workgroup per token.  Logits are summed in the
+//                    reference's sequential order (acc = acc + w*x, no fma)
+//                    so the selected experts and their slot order are
+//                    bit-identical to tb_route_experts (tb_infer.c:351-374).
+//   k_gate_up        g = W_gate[e] x, u = W_up[e] x, a = swiglu(g, u) for
+//                    every (token, slot) pair.
+//   k_down           y[t][s] = W_down[e] a[t][s].
+//   k_combine        out = resid + sum over slots, in slot order, of w*y.
+#include "tbq_kquant.hpp"
+#include "tbq_kernels.h"
+
+namespace tbq {
+
+// ---------------------------------------------------------------------------
+// Router.  blockDim = 256; lane e < E owns expert e.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_route(const float *__restrict__ xn, const float *__restrict__ Wr,
+                                               const float *__restrict__ bias, int H, int E, int top_k,
+                                               int *__restrict__ sel_idx, float *__restrict__ sel_w) {
+    extern __shared__ float lds[];
+    float *xl = lds;             // H
+    float *p = lds + H;          // 256 scores
+    __shared__ int s_cnt[256];
+    __shared__ float s_sum;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float *x = xn + (long long)t * H;
+    for (int i = tid * 4; i < H; i += 1024) *reinterpret_cast<float4 *>(xl + i) = *reinterpret_cast<const float4 *>(x + i);
+    __syncthreads();
+
+    // logits in sequential order: acc = fl(acc + fl(w*x))
+    float lg = -__builtin_huge_valf();
+    if (tid < E) {
+        const float *w = Wr + (long long)tid * H;
+        float acc = 0.f;
+        for (int k = 0; k < H; k += 8) {
+            float4 wa = *reinterpret_cast<const float4 *>(w + k);
+            float4 wb = *reinterpret_cast<const float4 *>(w + k + 4);
+            float4 xa = *reinterpret_cast<const float4 *>(xl + k);
+            float4 xb = *reinterpret_cast<const float4 *>(xl + k + 4);
+            acc = acc + wa.x * xa.x; acc = acc + wa.y * xa.y;
+            acc = acc + wa.z * xa.z; acc = acc + wa.w * xa.w;
+            acc = acc + wb.x * xb.x; acc = acc + wb.y * xb.y;
+            acc = acc + wb.z * xb.z; acc = acc + wb.w * xb.w;
+        }
+        if (bias) acc = acc + bias[tid];
+        lg = acc;
+    }
+    p[tid] = lg;
+    __syncthreads();
+    // max (order-independent)
+    float mx = p[0];
+    for (int e = 1; e < E; e++) mx = p[e] > mx ? p[e] : mx;
+    float ex = 0.f;
+    if (tid < E) ex = expf_glibc(lg - mx);
+    __syncthreads();
+    p[tid] = ex;
+    __syncthreads();
+    if (tid == 0) {  // sequential sum, as the reference
+        float s = 0.f;
+        for (int e = 0; e < E; e++) s = s + p[e];
+        s_sum = s;
+    }
+    __syncthreads();
+    float pr = tid < E ? ex / s_sum : 0.f;
+    __syncthreads();
+    p[tid] = pr;
+    __syncthreads();
+    // Element e enters the slot array iff fewer than k earlier elements have
+    // a score >= its own (the slots always hold the k largest seen so far).
+    const int k = top_k > 8 ? 8 : top_k;
+    int cnt = 0;
+    if (tid < E)
+        for (int e2 = 0; e2 < tid; e2++) cnt += p[e2] >= pr ? 1 : 0;
+    s_cnt[tid] = (tid < E && cnt < k) ? 1 : 0;
+    __syncthreads();
+    if (tid == 0) {
+        // Replay the slot updates of the entering elements in index order:
+        // replace the first slot holding the minimum when strictly larger.
+        int idx[8];
+        float w[8];
+        for (int i = 0; i < 8; i++) { idx[i] = 0; w[i] = -1e30f; }
+        for (int e = 0; e < E; e++) {
+            if (!s_cnt[e]) continue;
+            int lo = 0;
+            for (int i = 1; i < k; i++) if (w[i] < w[lo]) lo = i;
+            float v = p[e];
+            if (v > w[lo]) { w[lo] = v; idx[lo] = e; }
+        }
+        float ws = 0.f;
+        for (int i = 0; i < k; i++) ws = ws + w[i];
+        if (ws > 0.f) for (int i = 0; i < k; i++) w[i] = w[i] / ws;
+        for (int i = 0; i < 8; i++) {
+            sel_idx[t * 8 + i] = i < k ? idx[i] : -1;
+            sel_w[t * 8 + i] = i < k ? w[i] : 0.f;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Expert gate/up + SwiGLU.  grid = (F / RPB, T*k); 256 threads; LPR lanes per
+// dot product; each iteration computes RPW = 256/LPR/2 outputs (gate row and
+// up row of the same index go to adjacent lane groups).
+// ---------------------------------------------------------------------------
+template <int QT, int LPR>
+__global__ __launch_bounds__(256) void k_gate_up(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
+                                                 const float *__restrict__ xn, const int *__restrict__ sel_idx,
+                                                 int H, int F, int k, int rows_per_block, float *__restrict__ act) {
+    extern __shared__ float lds[];
+    float *xl = lds, *xs = lds + H;
+    const int pair = blockIdx.y, t = pair / k, s = pair % k;
+    const int e = sel_idx[t * 8 + s];
+    const float *x = xn + (long long)t * H;
+    for (int i = threadIdx.x * 4; i < H; i += 1024) *reinterpret_cast<float4 *>(xl + i) = *reinterpret_cast<const float4 *>(x + i);
+    __syncthreads();
+    for (int g = threadIdx.x; g < H / 16; g += 256) {
+        float a = 0.f;
+        for (int i = 0; i < 16; i++) a += xl[16 * g + i];
+        xs[g] = a;
+    }
+    __syncthreads();
+    constexpr int GROUPS = 256 / LPR;   // dot products per iteration
+    const long long rb = (long long)(H / block_weights(QT)) * block_bytes(QT);
+    const int C = H / 32, lane = threadIdx.x % LPR, grp = threadIdx.x / LPR;
+    const int which = grp & 1, sub = grp >> 1;   // 0 = gate, 1 = up
+    const uint8_t *Wb = (which ? up : gate) + (long long)e * F * rb;
+    __shared__ float res[GROUPS];
+    const int r_begin = blockIdx.x * rows_per_block;
+    for (int r0 = r_begin; r0 < r_begin + rows_per_block; r0 += GROUPS / 2) {
+        int r = r0 + sub;
+        float acc = 0.f;
+        if (r < F) {
+            const uint8_t *row = Wb + (long long)r * rb;
+            for (int c = lane; c < C; c += LPR) acc += chunk_dot<QT>(row, c, xl + 32 * c, xs + 2 * c);
+        }
+        acc = group_sum<LPR>(acc);
+        if (lane == 0) res[grp] = acc;
+        __syncthreads();
+        if (threadIdx.x < GROUPS / 2) {
+            int rr = r0 + threadIdx.x;
+            if (rr < F) {
+                float g = res[2 * threadIdx.x], u = res[2 * threadIdx.x + 1];
+                float den = 1.0f + expf_glibc(-g);
+                float sg = g / den;
+                act[(long long)pair * F + rr] = sg * u;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Expert down projection: y[pair][r] = W_down[e][r] . act[pair].
+// ---------------------------------------------------------------------------
+template <int QT, int LPR>
+__global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, const float *__restrict__ act,
+                                              const int *__restrict__ sel_idx, int H, int F, int k,
+                                              int rows_per_block, float *__restrict__ yout) {
+    extern __shared__ float lds[];
+    float *xl = lds, *xs = lds + F;
+    const int pair = blockIdx.y, t = pair / k, s = pair % k;
+    const int e = sel_idx[t * 8 + s];
+    const float *x = act + (long long)pair * F;
+    for (int i = threadIdx.x * 4; i < F; i += 1024) *reinterpret_cast<float4 *>(xl + i) = *reinterpret_cast<const float4 *>(x + i);
+    __syncthreads();
+    for (int g = threadIdx.x; g < F / 16; g += 256) {
+        float a = 0.f;
+        for (int i = 0; i < 16; i++) a += xl[16 * g + i];
+        xs[g] = a;
+    }
+    __syncthreads();
+    constexpr int GROUPS = 256 / LPR;
+    const long long rb = (long long)(F / block_weights(QT)) * block_bytes(QT);
+    const int C = F / 32, lane = threadIdx.x % LPR, grp = threadIdx.x / LPR;
+    const uint8_t *Wb = down + (long long)e * H * rb;
+    const int r_begin = blockIdx.x * rows_per_block;
+    for (int r0 = r_begin; r0 < r_begin + rows_per_block; r0 += GROUPS) {
+        int r = r0 + grp;
+        float acc = 0.f;
+        if (r < H) {
+            const uint8_t *row = Wb + (long long)r * rb;
+            for (int c = lane; c < C; c += LPR) acc += chunk_dot<QT>(row, c, xl + 32 * c, xs + 2 * c);
+        }
+        acc = group_sum<LPR>(acc);
+        if (lane == 0 && r < H) yout[(long long)pair * H + r] = acc;
+    }
+}
+
+// out[t][i] = resid[t][i] + (((0 + w0*y0) + w1*y1) + ...) in slot order.
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const float *__restrict__ sel_w,
+                                                 const float *__restrict__ resid, int T, int H, int k,
+                                                 float *__restrict__ out) {
+    long long n = (long long)T * H;
+    for (long long i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
+        int t = (int)(i / H), h = (int)(i - (long long)t * H);
+        float acc = 0.f;
+        for (int s = 0; s < k; s++) {
+            float p = sel_w[t * 8 + s] * y[((long long)t * k + s) * H + h];
+            acc = acc + p;
+        }
+        out[i] = resid[i] + acc;
+    }
+}
+
+static int pick_lpr(int K) {
+    int C = K / 32, lpr = 64;
+    while (lpr > 1 && (lpr > C || C % lpr)) lpr >>= 1;
+    if (lpr < 4 && C >= 4) lpr = 4;
+    return lpr;
+}
+
+template <int QT, int LPR>
+static hipError_t launch_moe_experts_t(const MoeArgs &a, hipStream_t st) {
+    const int pairs = a.T * a.k;
+    {
+        constexpr int OUT_PER_IT = 256 / LPR / 2;
+        int rpb = OUT_PER_IT * 4;
+        dim3 grid((a.F + rpb - 1) / rpb, pairs);
+        size_t lds = (size_t)a.H * 4 + (size_t)(a.H / 16) * 4;
+        hipLaunchKernelGGL((k_gate_up<QT, LPR>), grid, dim3(256), lds, st, (const uint8_t *)a.gate,
+                           (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.k, rpb, a.act);
+    }
+    return hipGetLastError();
+}
+
+template <int QT, int LPR>
+static hipError_t launch_moe_down_t(const MoeArgs &a, hipStream_t st) {
+    const int pairs = a.T * a.k;
+    constexpr int OUT_PER_IT = 256 / LPR;
+    int rpb = OUT_PER_IT * 2;
+    dim3 grid((a.H + rpb - 1) / rpb, pairs);
+    size_t lds = (size_t)a.F * 4 + (size_t)(a.F / 16) * 4;
+    hipLaunchKernelGGL((k_down<QT, LPR>), grid, dim3(256), lds, st, (const uint8_t *)a.down, a.act, a.sel_idx,
+                       a.H, a.F, a.k, rpb, a.y);
+    return hipGetLastError();
+}
+
+template <int QT>
+static hipError_t launch_moe_q(const MoeArgs &a, hipStream_t st) {
+    hipError_t err;
+    switch (pick_lpr(a.H)) {
+    case 64: err = launch_moe_experts_t<QT, 64>(a, st); break;
+    case 32: err = launch_moe_experts_t<QT, 32>(a, st); break;
+    case 16: err = launch_moe_experts_t<QT, 16>(a, st); break;
+    case 8: err = launch_moe_experts_t<QT, 8>(a, st); break;
+    default: err = launch_moe_experts_t<QT, 4>(a, st); break;
+    }
+    if (err != hipSuccess) return err;
+    switch (pick_lpr(a.F)) {
+    case 64: return launch_moe_down_t<QT, 64>(a, st);
+    case 32: return launch_moe_down_t<QT, 32>(a, st);
+    case 16: return launch_moe_down_t<QT, 16>(a, st);
+    case 8: return launch_moe_down_t<QT, 8>(a, st);
+    default: return launch_moe_down_t<QT, 4>(a, st);
+    }
+}
+
+hipError_t launch_route(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
+                        int *sel_idx, float *sel_w, hipStream_t st) {
+    size_t lds = (size_t)H * 4 + 256 * 4;
+    hipLaunchKernelGGL(k_route, dim3(T), dim3(256), lds, st, xn, router, bias, H, E, top_k, sel_idx, sel_w);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
+    hipError_t err = launch_route(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.sel_idx, a.sel_w, st);
+    if (err != hipSuccess) return err;
+    switch (a.qtype) {
+    case QT_Q2_K: err = launch_moe_q<QT_Q2_K>(a, st); break;
+    case QT_Q3_K: err = launch_moe_q<QT_Q3_K>(a, st); break;
+    case QT_Q4_K: err = launch_moe_q<QT_Q4_K>(a, st); break;
+    case QT_Q5_K: err = launch_moe_q<QT_Q5_K>(a, st); break;
+    case QT_Q6_K: err = launch_moe_q<QT_Q6_K>(a, st); break;
+    case QT_Q8_0: err = launch_moe_q<QT_Q8_0>(a, st); break;
+    default: return hipErrorInvalidValue;
+    }
+    if (err != hipSuccess) return err;
+    long long n = (long long)a.T * a.H;
+    int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+    hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_w, a.resid, a.T, a.H, a.k, a.out);
+    return hipGetLastError();
+}
+
+}  // namespace tbq
