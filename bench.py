@@ -43,18 +43,30 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def time_region(fn, steps, warmup, stream):
-    """Run fn() warmup times, then time exactly `steps` calls with HIP events
-    recorded on the stream the kernels run on; returns seconds."""
+def time_region(fn, steps, warmup, stream, graph=True):
+    """Time exactly `steps` executions of fn() with HIP events recorded on the
+    stream the kernels run on; returns seconds.  With graph=True, fn's launches
+    are captured once into a HIP graph and the graph is replayed, so host-side
+    launch cost (Python + ctypes) is not in the measurement."""
     import torch
-    for _ in range(warmup):
+    for _ in range(max(1, warmup)):
         fn()
     torch.cuda.synchronize()
+    run = fn
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        run = g.replay
+        for _ in range(warmup):
+            run()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(steps):
-        fn()
+        run()
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / 1e3
@@ -102,10 +114,11 @@ def gpu_leg(args):
 
     # warm (MALL-resident) number, same matrix every launch
     def warm():
-        tb.matvec(Wd, qt, M, K, x, ys[0])
-    ws = time_region(warm, 200, 20, stream)
-    res["headline"]["warm_us_per_launch"] = ws / 200 * 1e6
-    res["headline"]["warm_gbs"] = bpl / (ws / 200) / 1e9
+        for _ in range(ncopy):
+            tb.matvec(Wd, qt, M, K, x, ys[0])
+    ws = time_region(warm, args.steps, args.warmup, stream)
+    res["headline"]["warm_us_per_launch"] = ws / (args.steps * ncopy) * 1e6
+    res["headline"]["warm_gbs"] = bpl / (ws / (args.steps * ncopy)) / 1e9
     del copies
     torch.cuda.empty_cache()
 
@@ -156,7 +169,7 @@ def gpu_leg(args):
             it[0] += 1
             tb.moe_forward(L, T, xs[i], rs[i], out, workspace=ws_t)
         reps = 200
-        s = time_region(mstep, reps, 10, stream)
+        s = time_region(mstep, reps, 10, stream, graph=False)
         us = s / reps * 1e6
         moe[f"decode_b{T}"] = dict(us_per_layer=us, us_per_token=us / T)
         log(f"MoE decode b={T}: {us:.1f} us/layer  {us / T:.2f} us/token")
@@ -168,7 +181,7 @@ def gpu_leg(args):
     rs = d(synth.activations((T, H), rng))
     out = torch.empty((T, H), dtype=torch.float32, device="cuda")
     ws_t = torch.empty(tb.moe_workspace_size(Lb, T), dtype=torch.uint8, device="cuda")
-    s = time_region(lambda: tb.moe_forward(Lb, T, xs, rs, out, workspace=ws_t), 10, 2, stream)
+    s = time_region(lambda: tb.moe_forward(Lb, T, xs, rs, out, workspace=ws_t), 10, 2, stream, graph=False)
     us = s / 10 * 1e6
     moe["prefill_512_fp32"] = dict(us_per_layer=us, us_per_token=us / T)
     log(f"MoE prefill T=512 (fp32 path): {us:.1f} us/layer  {us / T:.2f} us/token")

@@ -57,6 +57,16 @@ int tbq_dequant(const void *W, int qtype, int nrows, int K, float *out, void *st
  * formats, of 32 otherwise; W and x 16-byte aligned. */
 int tbq_matvec(const void *W, int qtype, int M, int K, const float *x, float *y, void *stream);
 
+/* Kernel choice for tbq_matvec (no counterpart in the reference: it has one
+ * CUDA kernel per format).  AUTO picks the fastest kernel for the shape;
+ * FMA is the byte->fp32 fma kernel every format has; INTDOT is the
+ * v_dot4-based kernel (Q4_K) and fails for shapes it does not cover. */
+#define TBQ_MV_AUTO 0
+#define TBQ_MV_FMA 1
+#define TBQ_MV_INTDOT 2
+int tbq_matvec_variant(const void *W, int qtype, int M, int K, const float *x, float *y, int variant,
+                       void *stream);
+
 /* ---- MoE block --------------------------------------------------------- */
 /* Router: logits[e] = router[e] . xn (summed in the reference's sequential
  * order) + bias[e]; softmax; top-k in the reference's slot order;

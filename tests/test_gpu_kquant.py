@@ -35,10 +35,10 @@ def gpu_dequant(W, qt, M, K):
     return host(out).reshape(M, K)
 
 
-def gpu_matvec(W, qt, M, K, x):
+def gpu_matvec(W, qt, M, K, x, variant=tb.TBQ_MV_AUTO):
     import torch
     y = empty(M, torch.float32)
-    tb.matvec(dev(W), qt, M, K, dev(x), y)
+    tb.matvec(dev(W), qt, M, K, dev(x), y, variant=variant)
     return host(y)
 
 
@@ -101,6 +101,33 @@ def test_matvec_edge_shapes(oracle, qt, M, K):
     W = synth.kquant_matrix(qt, M, K, rng)
     x = synth.activations(K, rng)
     assert rel_l2(gpu_matvec(W, qt, M, K, x), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+
+
+@pytest.mark.parametrize("variant", [tb.TBQ_MV_FMA, tb.TBQ_MV_INTDOT])
+@pytest.mark.parametrize("M,K", [(1, 256), (7, 512), (200, 768), (1000, 2048), (4096, 4096), (333, 8192),
+                                 (4096, 12288), (65, 16384)])
+def test_matvec_q4k_kernels(oracle, variant, M, K):
+    if variant == tb.TBQ_MV_FMA and K > 15360:
+        pytest.skip("x does not fit the fma kernel's LDS staging at this K")
+    rng = np.random.default_rng(M * 31 + K)
+    W = synth.kquant_matrix(fm.Q4_K, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, fm.Q4_K, M, K, x, variant), oracle.matvec(W, fm.Q4_K, M, K, x)) <= MATVEC_TOL
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-3, 1e3, 1e30])
+def test_matvec_q4k_activation_range(oracle, scale):
+    """Per-sub-block exponents keep the int-dot kernel in tolerance for tiny
+    and huge activations and for LLM-style outlier channels (1000x)."""
+    rng = np.random.default_rng(17)
+    M, K = 512, 4096
+    W = synth.kquant_matrix(fm.Q4_K, M, K, rng)
+    x = (synth.activations(K, rng) * np.float32(scale)).astype(np.float32)
+    x[rng.choice(K, 12, replace=False)] *= np.float32(1000.0)
+    ref = oracle.matvec(W, fm.Q4_K, M, K, x)
+    assert rel_l2(gpu_matvec(W, fm.Q4_K, M, K, x, tb.TBQ_MV_INTDOT), ref) <= MATVEC_TOL
+    x0 = np.zeros(K, np.float32)
+    assert np.all(gpu_matvec(W, fm.Q4_K, M, K, x0, tb.TBQ_MV_INTDOT) == 0.0)
 
 
 def test_matvec_exact_one_hot():

@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(HERE, "libtbq.so")
 
 TBQ_MOE_FP32 = 0
 TBQ_MOE_BF16 = 1
+TBQ_MV_AUTO, TBQ_MV_FMA, TBQ_MV_INTDOT = 0, 1, 2
 
 # (name, restype, argtypes) for every symbol declared in include/tbq.h and
 # include/tb_gguf_dequant.h.
@@ -41,6 +42,7 @@ SYMBOLS = {
     "tbq_qtype_supported": (_i, [_i]),
     "tbq_dequant": (_i, [_vp, _i, _i, _i, _vp, _vp]),
     "tbq_matvec": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
+    "tbq_matvec_variant": (_i, [_vp, _i, _i, _i, _vp, _vp, _i, _vp]),
     "tbq_route": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "tbq_moe_workspace_size": (_sz, [_vp, _i, _i]),
     "tbq_moe_forward": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _vp]),
@@ -114,9 +116,10 @@ def dequant(W, qtype: int, nrows: int, K: int, out, stream=None):
     return out
 
 
-def matvec(W, qtype: int, M: int, K: int, x, y, stream=None):
+def matvec(W, qtype: int, M: int, K: int, x, y, stream=None, variant: int = TBQ_MV_AUTO):
     """y[M] = dequant(W) . x on the device (all arguments device tensors)."""
-    _check(lib().tbq_matvec(_ptr(W), qtype, M, K, _ptr(x), _ptr(y), _stream(stream)), "tbq_matvec")
+    _check(lib().tbq_matvec_variant(_ptr(W), qtype, M, K, _ptr(x), _ptr(y), variant, _stream(stream)),
+           "tbq_matvec")
     return y
 
 

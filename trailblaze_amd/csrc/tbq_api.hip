@@ -115,7 +115,7 @@ static int check_matvec(const void *W, int qt, int M, int K, const float *x, con
     if (!known_qtype(qt)) return fail("unsupported qtype %d", qt);
     int chunk = block_weights(qt) == 256 ? 256 : 32;
     if (M < 0 || K <= 0 || K % chunk) return fail("K=%d must be a positive multiple of %d for qtype %d", K, chunk, qt);
-    if ((size_t)K * 4 + (size_t)(K / 16) * 4 > 64 * 1024) return fail("K=%d exceeds the LDS-resident x limit", K);
+    if (K > 16384) return fail("K=%d exceeds the LDS-resident x limit (16384)", K);
     if (!W || !x || !y) return fail("null pointer");
     if (!aligned16(x)) return fail("x must be 16-byte aligned");
     if ((qt == QT_Q4_K || qt == QT_Q5_K || qt == QT_F32) && !aligned16(W))
@@ -124,11 +124,23 @@ static int check_matvec(const void *W, int qt, int M, int K, const float *x, con
     return 1;
 }
 
-int tbq_matvec(const void *W, int qt, int M, int K, const float *x, float *y, void *s) {
+int tbq_matvec_variant(const void *W, int qt, int M, int K, const float *x, float *y, int variant, void *s) {
     if (!ensure_init()) return 0;
     if (!check_matvec(W, qt, M, K, x, y)) return 0;
+    if (variant < TBQ_MV_AUTO || variant > TBQ_MV_INTDOT) return fail("tbq_matvec_variant: unknown variant %d", variant);
     if (M == 0) return 1;
+    if (variant != TBQ_MV_FMA && qt == QT_Q4_K) {
+        hipError_t e = launch_matvec_q4k(W, M, K, x, y, S(s), g_cu);
+        if (e != hipErrorNotSupported) return hip_ok(e, "matvec launch (int-dot)");
+    }
+    if (variant == TBQ_MV_INTDOT) return fail("tbq_matvec_variant: no int-dot kernel for qtype %d K=%d", qt, K);
+    if ((size_t)K * 4 + (size_t)(K / 16) * 4 > 64 * 1024)
+        return fail("K=%d exceeds the LDS-resident x limit of the fma kernel", K);
     return hip_ok(launch_matvec_generic(qt, W, M, K, x, y, S(s), g_cu), "matvec launch");
+}
+
+int tbq_matvec(const void *W, int qt, int M, int K, const float *x, float *y, void *s) {
+    return tbq_matvec_variant(W, qt, M, K, x, y, TBQ_MV_AUTO, s);
 }
 
 int tbq_route(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
