@@ -36,6 +36,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--quick", action="store_true", help="skip the sweep/MoE/CPU legs")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--moe-only", action="store_true", help="only the MoE leg (profiling)")
     return p.parse_args()
 
 
@@ -125,6 +126,9 @@ def gpu_leg(args):
     if args.quick:
         return res
 
+    if args.moe_only:
+        res["moe"] = moe_leg(tb, fm, synth, torch, rng, stream)
+        return res
     # ---- configs[1] sweep ------------------------------------------------
     sweep = []
     for qt2, M2, K2 in [(fm.Q2_K, 12288, 4096), (fm.Q2_K, 4096, 12288), (fm.Q3_K, 12288, 4096),
@@ -150,27 +154,32 @@ def gpu_leg(args):
         torch.cuda.empty_cache()
     res["sweep"] = sweep
 
-    # ---- MoE layer ------------------------------
+    res["moe"] = moe_leg(tb, fm, synth, torch, rng, stream)
+    return res
+
+
+def moe_leg(tb, fm, synth, torch, rng, stream):
+    """MoE layer (configs[3] decode at batch 1 and 16, configs[4] prefill)."""
     H, F, E, k = 2048, 768, 128, 8
     router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=3)
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     L = tb.moe_layer(H, F, E, k, fm.Q4_K, d(router), d(gate), d(up), d(down))
     moe = {}
     for T in (1, 16):
+        # 64 different token batches per step, so consecutive layers route to
+        # different experts (the 340 MB of experts exceed the MALL)
         ntok = 64
         xs = d(synth.activations((ntok, T, H), rng))
         rs = d(synth.activations((ntok, T, H), rng))
         out = torch.empty((T, H), dtype=torch.float32, device="cuda")
-        ws_t = torch.empty(tb.moe_workspace_size(L, T), dtype=torch.uint8, device="cuda")
-        it = [0]
+        ws_t = torch.zeros(tb.moe_workspace_size(L, T), dtype=torch.uint8, device="cuda")
 
         def mstep():
-            i = it[0] % ntok
-            it[0] += 1
-            tb.moe_forward(L, T, xs[i], rs[i], out, workspace=ws_t)
-        reps = 200
-        s = time_region(mstep, reps, 10, stream, graph=False)
-        us = s / reps * 1e6
+            for i in range(ntok):
+                tb.moe_forward(L, T, xs[i], rs[i], out, workspace=ws_t)
+        reps = 20
+        s = time_region(mstep, reps, 2, stream)
+        us = s / (reps * ntok) * 1e6
         moe[f"decode_b{T}"] = dict(us_per_layer=us, us_per_token=us / T)
         log(f"MoE decode b={T}: {us:.1f} us/layer  {us / T:.2f} us/token")
     # prefill, Zipf-skewed routing
@@ -180,13 +189,12 @@ def gpu_leg(args):
     xs = d(synth.activations((T, H), rng))
     rs = d(synth.activations((T, H), rng))
     out = torch.empty((T, H), dtype=torch.float32, device="cuda")
-    ws_t = torch.empty(tb.moe_workspace_size(Lb, T), dtype=torch.uint8, device="cuda")
-    s = time_region(lambda: tb.moe_forward(Lb, T, xs, rs, out, workspace=ws_t), 10, 2, stream, graph=False)
+    ws_t = torch.zeros(tb.moe_workspace_size(Lb, T), dtype=torch.uint8, device="cuda")
+    s = time_region(lambda: tb.moe_forward(Lb, T, xs, rs, out, workspace=ws_t), 10, 2, stream)
     us = s / 10 * 1e6
     moe["prefill_512_fp32"] = dict(us_per_layer=us, us_per_token=us / T)
     log(f"MoE prefill T=512 (fp32 path): {us:.1f} us/layer  {us / T:.2f} us/token")
-    res["moe"] = moe
-    return res
+    return moe
 
 
 def cpu_leg(budget_s=12.0):

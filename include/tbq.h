@@ -91,13 +91,14 @@ typedef struct {
 #define TBQ_MOE_FP32 0      /* fp32 decode kernels; outputs within 1e-5 rel-L2 */
 #define TBQ_MOE_BF16 1      /* prefill: grouped bf16 MFMA; within 1e-2 rel-L2 */
 
-/* Workspace bytes tbq_moe_forward needs for T tokens in `mode`. */
+/* Workspace bytes tbq_moe_forward needs for T tokens in `mode` (T <= 65536). */
 size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode);
 /* out[T][H] = resid + sum_slots w_slot * expert_slot(xn) for every token
  * (layer4/tb_infer.c:753-833,876).  sel_idx/sel_w ([T][8]) may be NULL.
- * workspace: device buffer of tbq_moe_workspace_size() bytes, or NULL to
- * use a library-owned buffer (grown on demand; not safe for concurrent
- * calls). */
+ * workspace: device buffer of tbq_moe_workspace_size() bytes, zero-filled
+ * before its first use (its first 256 KiB hold router arrival counters that
+ * every call leaves at zero), or NULL to use a library-owned buffer (grown
+ * on demand).  Calls that share a workspace must not overlap. */
 int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float *resid, float *out,
                     int *sel_idx, float *sel_w, void *workspace, size_t workspace_bytes, int mode,
                     void *stream);

@@ -81,6 +81,13 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise TbqError(f"{LIB_PATH} is missing: build it with `python -m trailblaze_amd.build`")
+        # torch ships its own libamdhip64.so.7; loading torch first makes
+        # libtbq bind to that same HIP runtime (one runtime per process, so
+        # torch's device pointers and streams are valid in libtbq)
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(LIB_PATH)
         for name, (res, args) in SYMBOLS.items():
             fn = getattr(L, name)

@@ -25,6 +25,8 @@ char g_name[256] = "";
 std::mutex g_ws_mu;
 void *g_ws = nullptr;
 size_t g_ws_bytes = 0;
+void *g_route = nullptr;
+size_t g_route_bytes = 0;
 
 int fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 int fail(const char *fmt, ...) {
@@ -143,6 +145,12 @@ int tbq_matvec(const void *W, int qt, int M, int K, const float *x, float *y, vo
     return tbq_matvec_variant(W, qt, M, K, x, y, TBQ_MV_AUTO, s);
 }
 
+// Router arrival counters live at the start of every workspace, sized for
+// the largest T, so their position does not depend on T.  They are zero on
+// entry to every call and left zero on exit.
+constexpr int MAX_TOKENS = 65536;
+constexpr size_t COUNTER_BYTES = (size_t)MAX_TOKENS * 4;
+
 int tbq_route(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
               int *sel_idx, float *sel_w, void *s) {
     if (!ensure_init()) return 0;
@@ -152,17 +160,34 @@ int tbq_route(const float *xn, const float *router, const float *bias, int T, in
     if (!xn || !router || !sel_idx || !sel_w || !aligned16(xn) || !aligned16(router))
         return fail("tbq_route: null or misaligned pointer");
     if (T == 0) return 1;
-    return hip_ok(launch_route(xn, router, bias, T, H, E, top_k, sel_idx, sel_w, S(s)), "route launch");
+    if (T > MAX_TOKENS) return fail("tbq_route: T=%d above %d", T, MAX_TOKENS);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    const size_t need = COUNTER_BYTES + (size_t)T * E * 4;
+    if (g_route_bytes < need) {
+        if (g_route && !hip_ok(hipFree(g_route), "hipFree")) return 0;
+        g_route = nullptr;
+        g_route_bytes = 0;
+        if (!hip_ok(hipMalloc(&g_route, need), "hipMalloc router logits")) return 0;
+        if (!hip_ok(hipMemset(g_route, 0, COUNTER_BYTES), "hipMemset router counters")) return 0;
+        g_route_bytes = need;
+    }
+    unsigned *counters = (unsigned *)g_route;
+    float *logits = (float *)((char *)g_route + COUNTER_BYTES);
+    hipError_t e = launch_router(xn, router, bias, T, H, E, top_k, logits, counters, sel_idx, sel_w, S(s));
+    if (e == hipErrorNotSupported) e = launch_route(xn, router, bias, T, H, E, top_k, sel_idx, sel_w, S(s));
+    return hip_ok(e, "route launch");
 }
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
 
 size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode) {
     (void)mode;
     if (!L || T <= 0) return 0;
     int k = L->top_k > 8 ? 8 : L->top_k;
-    size_t n = 0;
+    size_t n = COUNTER_BYTES;
     n += align256((size_t)T * 8 * 4) * 2;                   // sel idx / w
+    n += align256((size_t)T * L->E * 4);                     // router logits
     n += align256((size_t)T * k * L->F * 4);                 // act
     n += align256((size_t)T * k * L->H * 4);                 // y
     return n;
@@ -170,7 +195,7 @@ size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode) {
 
 static int check_moe(const tbq_moe_layer *L, int T) {
     if (!L) return fail("tbq_moe_forward: null layer");
-    if (T < 0 || L->E <= 0 || L->E > 256 || L->top_k <= 0) return fail("tbq_moe_forward: bad T/E/top_k");
+    if (T < 0 || T > MAX_TOKENS || L->E <= 0 || L->E > 256 || L->top_k <= 0) return fail("tbq_moe_forward: bad T/E/top_k");
     if (L->H <= 0 || L->F <= 0 || L->H % 256 || L->F % 256) return fail("tbq_moe_forward: H and F must be multiples of 256");
     switch (L->qtype) {
     case QT_Q2_K: case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_Q8_0: break;
@@ -201,6 +226,7 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
             g_ws = nullptr;
             g_ws_bytes = 0;
             if (!hip_ok(hipMalloc(&g_ws, need), "hipMalloc workspace")) return 0;
+            if (!hip_ok(hipMemset(g_ws, 0, COUNTER_BYTES), "hipMemset workspace")) return 0;
             g_ws_bytes = need;
         }
         ws = (char *)g_ws;
@@ -214,8 +240,10 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     a.xn = xn; a.resid = resid; a.router = L->router; a.bias = L->bias;
     a.gate = L->gate; a.up = L->up; a.down = L->down; a.out = out;
     size_t off = 0;
+    a.counters = (unsigned *)(ws + off); off += COUNTER_BYTES;
     int *ws_idx = (int *)(ws + off); off += align256((size_t)T * 8 * 4);
     float *ws_w = (float *)(ws + off); off += align256((size_t)T * 8 * 4);
+    a.logits = (float *)(ws + off); off += align256((size_t)T * a.E * 4);
     a.act = (float *)(ws + off); off += align256((size_t)T * a.k * a.F * 4);
     a.y = (float *)(ws + off);
     a.sel_idx = sel_idx ? sel_idx : ws_idx;

@@ -11,6 +11,8 @@ struct MoeArgs {
     const float *xn, *resid, *router, *bias;
     const void *gate, *up, *down;
     float *out;
+    float *logits;     // [T][E]
+    unsigned *counters; // [T], zero between calls (router arrival counters)
     int *sel_idx;      // [T][8]
     float *sel_w;      // [T][8]
     float *act;        // [T*k][F]
@@ -25,5 +27,8 @@ hipError_t launch_expf(const float *in, float *out, long long n, hipStream_t s);
 hipError_t launch_route(const float *xn, const float *router, const float *bias, int T, int H, int E,
                         int top_k, int *sel_idx, float *sel_w, hipStream_t st);
 hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st);
+hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
+                         float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st);
+hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st);
 
 }  // namespace tbq

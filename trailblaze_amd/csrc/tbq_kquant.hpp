@@ -374,4 +374,30 @@ __device__ __forceinline__ float chunk_dot<QT_BF16>(const uint8_t *row, int c, c
     return a;
 }
 
+// ---------------------------------------------------------------------------
+// x staging for the fp32 chunk kernels.  x lives in LDS with float4 t of
+// chunk c (32 floats) at slot 8c + (t ^ (c & 7)): lanes that own
+// consecutive chunks then read distinct banks.  xs holds the fp32 sums of
+// x over 16-element groups.  NT = threads of the workgroup.
+// ---------------------------------------------------------------------------
+template <int NT>
+__device__ __forceinline__ void stage_x_swizzled(const float *__restrict__ x, int K, float *xl, float *xs) {
+    for (int i = threadIdx.x; i < K / 4; i += NT) {
+        const int c = i >> 3, t = i & 7;
+        *reinterpret_cast<float4 *>(xl + 4 * (8 * c + (t ^ (c & 7)))) = *reinterpret_cast<const float4 *>(x + 4 * i);
+    }
+    for (int g = threadIdx.x; g < K / 16; g += NT) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) a += x[16 * g + i];
+        xs[g] = a;
+    }
+}
+
+__device__ __forceinline__ void load_chunk_x(const float *xl, int c, float *xv) {
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+        *reinterpret_cast<float4 *>(xv + 4 * t) = *reinterpret_cast<const float4 *>(xl + 4 * (8 * c + (t ^ (c & 7))));
+}
+
 }  // namespace tbq

@@ -44,17 +44,9 @@ __global__ __launch_bounds__(256) void k_matvec_generic(const uint8_t *__restric
                                                         long long row_bytes, const float *__restrict__ x,
                                                         float *__restrict__ y) {
     extern __shared__ float lds[];
-    float *xl = lds;            // K floats
+    float *xl = lds;            // K floats (swizzled, see stage_x_swizzled)
     float *xs = lds + K;        // K/16 group sums
-    for (int i = threadIdx.x * 4; i < K; i += 1024)
-        *reinterpret_cast<float4 *>(xl + i) = *reinterpret_cast<const float4 *>(x + i);
-    __syncthreads();
-    for (int g = threadIdx.x; g < K / 16; g += 256) {
-        float s = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) s += xl[16 * g + i];
-        xs[g] = s;
-    }
+    stage_x_swizzled<256>(x, K, xl, xs);
     __syncthreads();
     constexpr int RPW = 256 / LPR;
     const int C = K / 32;
@@ -64,7 +56,11 @@ __global__ __launch_bounds__(256) void k_matvec_generic(const uint8_t *__restric
         float acc = 0.f;
         if (r < M) {
             const uint8_t *row = W + (long long)r * row_bytes;
-            for (int c = lane; c < C; c += LPR) acc += chunk_dot<QT>(row, c, xl + 32 * c, xs + 2 * c);
+            for (int c = lane; c < C; c += LPR) {
+                float xv[32];
+                load_chunk_x(xl, c, xv);
+                acc += chunk_dot<QT>(row, c, xv, xs + 2 * c);
+            }
         }
         acc = group_sum<LPR>(acc);
         if (lane == 0 && r < M) y[r] = acc;

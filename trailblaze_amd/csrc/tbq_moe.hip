@@ -113,14 +113,7 @@ __global__ __launch_bounds__(256) void k_gate_up(const uint8_t *__restrict__ gat
     float *xl = lds, *xs = lds + H;
     const int pair = blockIdx.y, t = pair / k, s = pair % k;
     const int e = sel_idx[t * 8 + s];
-    const float *x = xn + (long long)t * H;
-    for (int i = threadIdx.x * 4; i < H; i += 1024) *reinterpret_cast<float4 *>(xl + i) = *reinterpret_cast<const float4 *>(x + i);
-    __syncthreads();
-    for (int g = threadIdx.x; g < H / 16; g += 256) {
-        float a = 0.f;
-        for (int i = 0; i < 16; i++) a += xl[16 * g + i];
-        xs[g] = a;
-    }
+    stage_x_swizzled<256>(xn + (long long)t * H, H, xl, xs);
     __syncthreads();
     constexpr int GROUPS = 256 / LPR;   // dot products per iteration
     const long long rb = (long long)(H / block_weights(QT)) * block_bytes(QT);
@@ -134,7 +127,11 @@ __global__ __launch_bounds__(256) void k_gate_up(const uint8_t *__restrict__ gat
         float acc = 0.f;
         if (r < F) {
             const uint8_t *row = Wb + (long long)r * rb;
-            for (int c = lane; c < C; c += LPR) acc += chunk_dot<QT>(row, c, xl + 32 * c, xs + 2 * c);
+            for (int c = lane; c < C; c += LPR) {
+                float xv[32];
+                load_chunk_x(xl, c, xv);
+                acc += chunk_dot<QT>(row, c, xv, xs + 2 * c);
+            }
         }
         acc = group_sum<LPR>(acc);
         if (lane == 0) res[grp] = acc;
@@ -163,14 +160,7 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, 
     float *xl = lds, *xs = lds + F;
     const int pair = blockIdx.y, t = pair / k, s = pair % k;
     const int e = sel_idx[t * 8 + s];
-    const float *x = act + (long long)pair * F;
-    for (int i = threadIdx.x * 4; i < F; i += 1024) *reinterpret_cast<float4 *>(xl + i) = *reinterpret_cast<const float4 *>(x + i);
-    __syncthreads();
-    for (int g = threadIdx.x; g < F / 16; g += 256) {
-        float a = 0.f;
-        for (int i = 0; i < 16; i++) a += xl[16 * g + i];
-        xs[g] = a;
-    }
+    stage_x_swizzled<256>(act + (long long)pair * F, F, xl, xs);
     __syncthreads();
     constexpr int GROUPS = 256 / LPR;
     const long long rb = (long long)(F / block_weights(QT)) * block_bytes(QT);
@@ -182,7 +172,11 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, 
         float acc = 0.f;
         if (r < H) {
             const uint8_t *row = Wb + (long long)r * rb;
-            for (int c = lane; c < C; c += LPR) acc += chunk_dot<QT>(row, c, xl + 32 * c, xs + 2 * c);
+            for (int c = lane; c < C; c += LPR) {
+                float xv[32];
+                load_chunk_x(xl, c, xv);
+                acc += chunk_dot<QT>(row, c, xv, xs + 2 * c);
+            }
         }
         acc = group_sum<LPR>(acc);
         if (lane == 0 && r < H) yout[(long long)pair * H + r] = acc;
@@ -266,8 +260,15 @@ hipError_t launch_route(const float *xn, const float *router, const float *bias,
 }
 
 hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
-    hipError_t err = launch_route(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.sel_idx, a.sel_w, st);
+    hipError_t err = launch_router(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.logits, a.counters, a.sel_idx,
+                                   a.sel_w, st);
+    if (err == hipErrorNotSupported)
+        err = launch_route(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.sel_idx, a.sel_w, st);
     if (err != hipSuccess) return err;
+    if (a.qtype == QT_Q4_K) {
+        err = launch_moe_q4k_experts(a, st);
+        if (err != hipErrorNotSupported) return err;
+    }
     switch (a.qtype) {
     case QT_Q2_K: err = launch_moe_q<QT_Q2_K>(a, st); break;
     case QT_Q3_K: err = launch_moe_q<QT_Q3_K>(a, st); break;

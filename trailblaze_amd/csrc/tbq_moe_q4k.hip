@@ -1,0 +1,614 @@
+// tbq_moe_q4k.hip -- the MoE block's decode path on gfx950:
+//
+//   k_router_logits<EPB>  logits[t][e] = sum_k fl(W[e][k] * x[k]) summed in the
+//                         reference's order (acc = acc + p, k ascending).  The
+//                         sum is a dependent chain, so one lane owns one
+//                         expert; four loader waves form the products of the
+//                         next 32 KB tile in LDS while the chain wave adds
+//                         the current one (double-buffered).
+//   k_topk                softmax + top-k + renormalise per token, bit-exact
+//                         to tb_route_experts (layer4/tb_infer.c:351-374).
+//   k_gate_up_q4k         act[t][s] = swiglu(W_gate[e] x, W_up[e] x) with the
+//                         Q4_K int-dot units; a wave's two half-waves take
+//                         gate row r and up row r.
+//   k_down_combine_q4k    out[t][r] = resid[t][r] + sum_s w_s * (W_down[e_s] a_s)[r]
+//                         with the sum over slots in slot order, exactly as
+//                         the reference's weighted accumulate (tb_infer.c:
+//                         829-831) and residual add (:876).
+#include "tbq_kernels.h"
+#include "tbq_q4k.hpp"
+
+namespace tbq {
+
+// ---------------------------------------------------------------------------
+// Router logits.  grid = (T, ceil(E/EPB)); block = 64 (chain) + 256 (loaders).
+// ---------------------------------------------------------------------------
+constexpr int RT_LOADERS = 256;
+constexpr int RT_THREADS = 64 + RT_LOADERS;
+constexpr int RT_TILE_FLOATS = 4096;   // 16 KB of products per tile
+
+template <int EPB>
+__global__ __launch_bounds__(RT_THREADS) void k_router_logits(const float *__restrict__ xn, const float *__restrict__ Wr,
+                                                              const float *__restrict__ bias, int H, int E,
+                                                              float *__restrict__ logits) {
+    constexpr int KT = RT_TILE_FLOATS / EPB;        // k per tile (256 for EPB=16, 64 for EPB=64)
+    constexpr int F4 = KT / 4;                       // float4 per expert row of a tile
+    constexpr int SEGS = KT / 16;                    // 16-k segments per expert row
+    static_assert(EPB * SEGS == RT_LOADERS, "one 16-k segment per loader thread");
+    static_assert(F4 % 8 == 0, "swizzle needs 8 float4 per row");
+    extern __shared__ float lds[];
+    float *xl = lds;                                 // H floats
+    float *buf = lds + H;                            // 2 tiles of EPB x KT products
+    const int t = blockIdx.x, e0 = blockIdx.y * EPB, tid = threadIdx.x;
+    const float *x = xn + (long long)t * H;
+    const int ntiles = H / KT;
+
+    // loader role: expert ei, 16 consecutive k of each tile; W of tile i is
+    // held in register set i&1, two tiles ahead of the chain
+    const int lt = tid - 64, ei = lt / SEGS, seg = lt % SEGS;
+    const bool loader = tid >= 64, lvalid = loader && e0 + ei < E;
+    float4 wa[4], wb[4];
+    auto issue = [&](float4 *w, int tile) {
+        if (lvalid && tile < ntiles) {
+            const float4 *src = reinterpret_cast<const float4 *>(Wr + (long long)(e0 + ei) * H + tile * KT + 16 * seg);
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[i] = src[i];
+        }
+    };
+    auto produce = [&](const float4 *w, int tile) {
+        // float4 j of row ei goes to j ^ (ei & 7): chain lanes read distinct banks
+        float *dst = buf + (tile & 1) * RT_TILE_FLOATS + ei * KT;
+        const float *xk = xl + tile * KT + 16 * seg;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int j = 4 * seg + i;
+            float4 p;
+            p.x = lvalid ? w[i].x * xk[4 * i] : 0.f;
+            p.y = lvalid ? w[i].y * xk[4 * i + 1] : 0.f;
+            p.z = lvalid ? w[i].z * xk[4 * i + 2] : 0.f;
+            p.w = lvalid ? w[i].w * xk[4 * i + 3] : 0.f;
+            *reinterpret_cast<float4 *>(dst + 4 * (j ^ (ei & 7))) = p;
+        }
+    };
+    float acc = 0.f;
+    auto chain = [&](int tile) {
+        if (!loader && tid < EPB) {
+            // the next 8 float4 are read from LDS while the current 8 are added
+            const float *src = buf + (tile & 1) * RT_TILE_FLOATS + tid * KT;
+            float4 cur[8], nxt[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) cur[i] = *reinterpret_cast<const float4 *>(src + 4 * (i ^ (tid & 7)));
+#pragma unroll
+            for (int jb = 0; jb < F4; jb += 8) {
+                if (jb + 8 < F4) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+                        nxt[i] = *reinterpret_cast<const float4 *>(src + 4 * ((jb + 8 + i) ^ (tid & 7)));
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    acc = acc + cur[i].x;
+                    acc = acc + cur[i].y;
+                    acc = acc + cur[i].z;
+                    acc = acc + cur[i].w;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) cur[i] = nxt[i];
+            }
+        }
+    };
+    issue(wa, 0);
+    issue(wb, 1);
+    for (int i = tid * 4; i < H; i += RT_THREADS * 4) *reinterpret_cast<float4 *>(xl + i) = *reinterpret_cast<const float4 *>(x + i);
+    __syncthreads();
+    // step it: loaders form tile it, chain adds tile it-1; unrolled by two so
+    // the register sets are addressed statically
+    for (int it = 0; it <= ntiles; it += 2) {
+        if (loader && it < ntiles) { produce(wa, it); issue(wa, it + 2); }
+        if (it > 0) chain(it - 1);
+        __syncthreads();
+        if (it + 1 > ntiles) break;
+        if (loader && it + 1 < ntiles) { produce(wb, it + 1); issue(wb, it + 3); }
+        chain(it);
+        __syncthreads();
+    }
+    if (tid < EPB && e0 + tid < E) {
+        float lg = acc;
+        if (bias) lg = lg + bias[e0 + tid];
+        logits[(long long)t * E + e0 + tid] = lg;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode-size router: EPB_S experts per workgroup, the whole W slice loaded
+// at once (one load latency), products for all of H formed in LDS, then one
+// lane per expert runs the sequential chain.  grid = (T, ceil(E/EPB_S)).
+// ---------------------------------------------------------------------------
+constexpr int EPB_S = 4;
+constexpr int RS_THREADS = 256;
+
+template <int KPT>   // floats of W per thread: EPB_S * H / RS_THREADS
+__global__ __launch_bounds__(RS_THREADS) void k_router_logits_small(const float *__restrict__ xn,
+                                                                    const float *__restrict__ Wr,
+                                                                    const float *__restrict__ bias, int H, int E,
+                                                                    float *__restrict__ logits) {
+    extern __shared__ float prod[];                  // EPB_S rows of H products (float4-swizzled)
+    const int t = blockIdx.x, e0 = blockIdx.y * EPB_S, tid = threadIdx.x;
+    // thread -> expert ei, KPT consecutive k
+    const int tpe = RS_THREADS / EPB_S, ei = tid / tpe, k0 = (tid % tpe) * KPT;
+    const bool valid = e0 + ei < E;
+    float4 w[KPT / 4], xv[KPT / 4];
+    if (valid) {
+        const float4 *src = reinterpret_cast<const float4 *>(Wr + (long long)(e0 + ei) * H + k0);
+#pragma unroll
+        for (int i = 0; i < KPT / 4; i++) w[i] = src[i];
+    }
+    const float4 *xs = reinterpret_cast<const float4 *>(xn + (long long)t * H + k0);
+#pragma unroll
+    for (int i = 0; i < KPT / 4; i++) xv[i] = xs[i];
+    float *row = prod + ei * H;
+#pragma unroll
+    for (int i = 0; i < KPT / 4; i++) {
+        float4 p;
+        p.x = valid ? w[i].x * xv[i].x : 0.f;
+        p.y = valid ? w[i].y * xv[i].y : 0.f;
+        p.z = valid ? w[i].z * xv[i].z : 0.f;
+        p.w = valid ? w[i].w * xv[i].w : 0.f;
+        const int j = k0 / 4 + i;                    // float4 index within the row
+        *reinterpret_cast<float4 *>(row + 4 * (j ^ (ei & 3))) = p;
+    }
+    __syncthreads();
+    if (tid < EPB_S && valid) {
+        const float *src = prod + tid * H;
+        const int F4 = H / 4;
+        float acc = 0.f;
+        float4 cur[8], nxt[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) cur[i] = *reinterpret_cast<const float4 *>(src + 4 * (i ^ (tid & 3)));
+        for (int jb = 0; jb < F4; jb += 8) {
+            if (jb + 8 < F4) {
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    nxt[i] = *reinterpret_cast<const float4 *>(src + 4 * ((jb + 8 + i) ^ (tid & 3)));
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                acc = acc + cur[i].x;
+                acc = acc + cur[i].y;
+                acc = acc + cur[i].z;
+                acc = acc + cur[i].w;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) cur[i] = nxt[i];
+        }
+        if (bias) acc = acc + bias[e0 + tid];
+        logits[(long long)t * E + e0 + tid] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Softmax + top-k + renormalise for one token, by one wave (lane l holds
+// experts l + 64j, j < NJ).  lg points at the token's E logits.
+// Bit-exact to tb_route_experts (layer4/tb_infer.c:351-374): max, expf of
+// (s - max), sequential sum, division, then the slot scan that replaces the
+// first slot holding the minimum when a score is strictly larger, and the
+// sequential renormalisation over the k slots.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+__device__ __forceinline__ float rdlane(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+template <int NJ>
+__device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int t, float *P,
+                                          int *__restrict__ sel_idx, float *__restrict__ sel_w) {
+    const int lane = threadIdx.x & 63;
+    const float NEG = -__builtin_huge_valf();
+    float v[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? __builtin_nontemporal_load(lg + e) : NEG;
+    }
+    float m = v[0];
+#pragma unroll
+    for (int j = 1; j < NJ; j++) m = fmaxf(m, v[j]);
+    const float mx = wave_max(m);   // same value the reference's strict '>' scan keeps
+    float ex[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int e = lane + 64 * j;
+        ex[j] = e < E ? expf_glibc(v[j] - mx) : 0.f;
+        P[e] = ex[j];
+    }
+    if (lane < 16) P[64 * NJ + lane] = 0.f;
+    __syncthreads();
+    float ssum = 0.f;
+    if (lane == 0) {   // sequential sum in expert order
+        for (int e0 = 0; e0 < E; e0 += 16) {
+            float4 q[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) q[i] = *reinterpret_cast<const float4 *>(P + e0 + 4 * i);
+            const float qq[16] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w,
+                                  q[2].x, q[2].y, q[2].z, q[2].w, q[3].x, q[3].y, q[3].z, q[3].w};
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                if (e0 + i < E) ssum = ssum + qq[i];
+        }
+    }
+    ssum = rdlane(ssum, 0);
+    float pr[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) pr[j] = lane + 64 * j < E ? ex[j] / ssum : 0.f;
+    // slot scan: lanes 0..7 hold slot i; wl is the current minimum
+    const int k = top_k > 8 ? 8 : top_k;
+    float ws = -1e30f;
+    int wi = 0;
+    float wl = -1e30f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        // only experts already above the current minimum can enter; the
+        // minimum only grows, so the survivors are re-checked in order
+        unsigned long long cand = __ballot(lane + 64 * j < E && pr[j] > wl);
+        while (cand) {
+            const int l = __builtin_ctzll(cand);
+            cand &= cand - 1;
+            const float val = rdlane(pr[j], l);
+            if (val > wl) {   // wave-uniform
+                const unsigned long long at_min = __ballot(lane < k && ws == wl);
+                const int lo = __builtin_ctzll(at_min);
+                if (lane == lo) { ws = val; wi = 64 * j + l; }
+                float mn = lane < k ? ws : __builtin_huge_valf();
+                mn = fminf(mn, __shfl_xor(mn, 4));
+                mn = fminf(mn, __shfl_xor(mn, 2));
+                mn = fminf(mn, __shfl_xor(mn, 1));
+                wl = rdlane(mn, 0);
+            }
+        }
+    }
+    float wsum = 0.f;
+    for (int i = 0; i < k; i++) wsum = wsum + rdlane(ws, i);
+    if (lane < 8) {
+        float wo = 0.f;
+        int io = -1;
+        if (lane < k) {
+            wo = wsum > 0.f ? ws / wsum : ws;
+            io = wi;
+        }
+        sel_idx[t * 8 + lane] = io;
+        sel_w[t * 8 + lane] = wo;
+    }
+}
+
+template <int NJ>
+__global__ __launch_bounds__(64) void k_topk(const float *__restrict__ logits, int E, int top_k,
+                                             int *__restrict__ sel_idx, float *__restrict__ sel_w) {
+    __shared__ float P[64 * NJ + 16];
+    topk_wave<NJ>(logits + (long long)blockIdx.x * E, E, top_k, blockIdx.x, P, sel_idx, sel_w);
+}
+
+// ---------------------------------------------------------------------------
+// DPP router for H = 64*M.  A wave owns 4 experts, one per 16-lane row; lane
+// j of a row holds the products of k = 64m + 4j + c (m < M, c < 4) in
+// registers, and the row's last lane adds them in k order with
+// v_add_f32_dpp row_shr (one instruction per element, no LDS).  The last
+// workgroup of a token (per-token arrival counter, reset by that workgroup)
+// runs the softmax/top-k.  grid = (T, ceil(E/4)), 64 threads.
+// ---------------------------------------------------------------------------
+// One 64-element block of the chain: lane j of each 16-lane row holds w and
+// x for k = 4j..4j+3 of the block; the products are formed in place, then
+// the row's last lane (j = 15) adds the 64 products in k order, reading lane
+// j's registers with row_shr:(15-j).  s_nop 1 covers the VALU-write ->
+// DPP-read hazard.  IEEE fp32 add (commutative, round to nearest), no fma:
+// acc = fl(acc + fl(w*x)) exactly as the reference's sequential dot.
+#define TBQ_DPP_ADD(SH, R) "v_add_f32_dpp %0, %" #R ", %0 row_shr:" #SH " row_mask:0xf bank_mask:0xf bound_ctrl:1\n"
+#define TBQ_DPP_ADD4(SH) TBQ_DPP_ADD(SH, 1) TBQ_DPP_ADD(SH, 2) TBQ_DPP_ADD(SH, 3) TBQ_DPP_ADD(SH, 4)
+__device__ __forceinline__ float chain_block64(float acc, float4 w, float4 x) {
+    asm volatile(
+        "v_mul_f32 %1, %1, %5\n"
+        "v_mul_f32 %2, %2, %6\n"
+        "v_mul_f32 %3, %3, %7\n"
+        "v_mul_f32 %4, %4, %8\n"
+        "s_nop 1\n"
+        TBQ_DPP_ADD4(15) TBQ_DPP_ADD4(14) TBQ_DPP_ADD4(13) TBQ_DPP_ADD4(12) TBQ_DPP_ADD4(11)
+        TBQ_DPP_ADD4(10) TBQ_DPP_ADD4(9) TBQ_DPP_ADD4(8) TBQ_DPP_ADD4(7) TBQ_DPP_ADD4(6)
+        TBQ_DPP_ADD4(5) TBQ_DPP_ADD4(4) TBQ_DPP_ADD4(3) TBQ_DPP_ADD4(2) TBQ_DPP_ADD4(1)
+        "v_add_f32 %0, %1, %0\n"
+        "v_add_f32 %0, %2, %0\n"
+        "v_add_f32 %0, %3, %0\n"
+        "v_add_f32 %0, %4, %0\n"
+        : "+v"(acc), "+v"(w.x), "+v"(w.y), "+v"(w.z), "+v"(w.w)
+        : "v"(x.x), "v"(x.y), "v"(x.z), "v"(x.w));
+    return acc;
+}
+#undef TBQ_DPP_ADD4
+#undef TBQ_DPP_ADD
+
+// Chunks of 8 blocks (512 k) stream through two register slots: the loads
+// of chunk c+1 are issued before the chain of chunk c; sched_barrier keeps
+// the compiler from hoisting further.
+constexpr int RD_CH = 8;
+
+template <int C, int NC>
+__device__ __forceinline__ void router_dpp_chunks(const float4 *w4, const float4 *x4, int j, float4 (&wb)[2][RD_CH],
+                                                  float4 (&xb)[2][RD_CH], float &acc) {
+    if constexpr (C < NC) {
+        if constexpr (C + 1 < NC) {
+#pragma unroll
+            for (int i = 0; i < RD_CH; i++) {
+                wb[(C + 1) & 1][i] = w4[16 * (RD_CH * (C + 1) + i) + j];
+                xb[(C + 1) & 1][i] = x4[16 * (RD_CH * (C + 1) + i) + j];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RD_CH; i++) acc = chain_block64(acc, wb[C & 1][i], xb[C & 1][i]);
+        __builtin_amdgcn_sched_barrier(0);
+        router_dpp_chunks<C + 1, NC>(w4, x4, j, wb, xb, acc);
+    }
+}
+
+template <int M, int NJ>
+__global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn, const float *__restrict__ Wr,
+                                                   const float *__restrict__ bias, int E, int top_k,
+                                                   float *__restrict__ logits, unsigned *__restrict__ counters,
+                                                   int *__restrict__ sel_idx, float *__restrict__ sel_w) {
+    constexpr int H = 64 * M, NC = M / RD_CH;
+    static_assert(M % RD_CH == 0, "H must be a multiple of 512");
+    __shared__ float P[64 * NJ + 16];
+    const int t = blockIdx.x, lane = threadIdx.x, r = lane >> 4, j = lane & 15;
+    const int e = blockIdx.y * 4 + r;
+    const bool ev = e < E;
+    const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (long long)(ev ? e : 0) * H);
+    const float4 *x4 = reinterpret_cast<const float4 *>(xn + (long long)t * H);
+    float4 wb[2][RD_CH], xb[2][RD_CH];
+#pragma unroll
+    for (int i = 0; i < RD_CH; i++) {
+        wb[0][i] = w4[16 * i + j];
+        xb[0][i] = x4[16 * i + j];
+    }
+    float acc = 0.f;
+    router_dpp_chunks<0, NC>(w4, x4, j, wb, xb, acc);
+    if (j == 15 && ev) {
+        if (bias) acc = acc + bias[e];
+        logits[(long long)t * E + e] = acc;
+    }
+    // last arriving workgroup of this token does the top-k
+    __threadfence();
+    unsigned ticket = 0;
+    if (lane == 0) ticket = atomicAdd(counters + t, 1u);
+    ticket = (unsigned)__builtin_amdgcn_readfirstlane((int)ticket);
+    if (ticket != gridDim.y - 1) return;
+    __threadfence();
+    topk_wave<NJ>(logits + (long long)t * E, E, top_k, t, P, sel_idx, sel_w);
+    if (lane == 0) counters[t] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// gate/up + SwiGLU, Q4_K experts.  grid = (ceil(F / OUT_PER_WG), T*k); each
+// wave owns one output row per pass: lanes [0, 32) dot the gate row, lanes
+// [32, 64) the up row (LPR = 32 lanes hold one 64-weight unit each when
+// H = 2048; larger H loops units).
+// ---------------------------------------------------------------------------
+constexpr int GU_THREADS = 512;
+constexpr int GU_ROWS = 2;   // output rows per wave
+
+template <int UPL>
+__global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
+                                                            const float *__restrict__ xn, const int *__restrict__ sel_idx,
+                                                            int H, int F, int k, float *__restrict__ act) {
+    extern __shared__ uint32_t xd[];
+    constexpr int LPR = 32;
+    const int pair = blockIdx.y, t = pair / k, s = pair % k;
+    const int e = sel_idx[t * 8 + s];
+    const long long rb = (long long)(H / 256) * 144;
+    const int U = H / 64;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lr = lane & 31, half = lane >> 5;
+    const uint8_t *Wb = (half ? up : gate) + (long long)e * F * rb;
+    const int r0 = (blockIdx.x * (GU_THREADS / 64) + wave) * GU_ROWS;
+
+    Q4KUnit raw[GU_ROWS][UPL];
+#pragma unroll
+    for (int rr = 0; rr < GU_ROWS; rr++) {
+        const int r = r0 + rr;
+#pragma unroll
+        for (int i = 0; i < UPL; i++) {
+            const int u = lr + LPR * i;
+            if (r < F && u < U) q4k_load(Wb + (long long)r * rb, u, raw[rr][i]);
+        }
+    }
+    stage_x_digits_nibble<GU_THREADS>(xn + (long long)t * H, H, xd);
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < GU_ROWS; rr++) {
+        const int r = r0 + rr;
+        if (r >= F) break;   // wave-uniform
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < UPL; i++) {
+            const int u = lr + LPR * i;
+            if (u < U) acc = q4k_unit_dot(raw[rr][i], u, xd, acc);
+        }
+        acc = group_sum<32>(acc);
+        const float u_val = __shfl(acc, 32);
+        if (lane == 0) {
+            const float g = acc;
+            const float den = 1.0f + expf_glibc(-g);
+            const float sg = g / den;
+            act[(long long)pair * F + r] = sg * u_val;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// down + weighted combine + residual, Q4_K experts.  grid = (H / RB, T);
+// the workgroup owns RB output rows of one token for all k slots.  Each
+// (row, slot) dot uses LPR = 16 lanes (K = F = 768 gives 12 units; larger F
+// loops units).  Results meet in LDS and one lane per row adds them in slot
+// order.
+// ---------------------------------------------------------------------------
+constexpr int DC_THREADS = 512;
+constexpr int DC_ROWS = 8;   // rows per workgroup
+
+template <int UPL>
+__global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *__restrict__ down, const float *__restrict__ act,
+                                                                 const int *__restrict__ sel_idx, const float *__restrict__ sel_w,
+                                                                 const float *__restrict__ resid, int H, int F, int k,
+                                                                 float *__restrict__ out) {
+    extern __shared__ uint32_t xd[];                  // k act vectors' digits
+    __shared__ float yv[8][DC_ROWS];
+    constexpr int LPR = 16, RPP = 4;
+    const int t = blockIdx.y, r0 = blockIdx.x * DC_ROWS;
+    const long long rb = (long long)(F / 256) * 144;
+    const int U = F / 64, G = F / 32;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lr = lane & 15, rsub = lane >> 4;
+    // dot d = (row rd, slot sd), d < DC_ROWS * k; wave w pass p takes dots 4*(w + 8p) + rsub
+    constexpr int PASSES = (DC_ROWS * 8 + (DC_THREADS / 64) * RPP - 1) / ((DC_THREADS / 64) * RPP);
+    Q4KUnit raw[PASSES][UPL];
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int d = RPP * (wave + (DC_THREADS / 64) * p) + rsub;
+        if (d < DC_ROWS * k) {
+            const int rd = d / k, sd = d % k;
+            const int e = sel_idx[t * 8 + sd];
+            const uint8_t *row = down + ((long long)e * H + r0 + rd) * rb;
+#pragma unroll
+            for (int i = 0; i < UPL; i++) {
+                const int u = lr + LPR * i;
+                if (u < U) q4k_load(row, u, raw[p][i]);
+            }
+        }
+    }
+    stage_x_digits_nibble<DC_THREADS>(act + (long long)t * k * F, F, xd, k);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int d = RPP * (wave + (DC_THREADS / 64) * p) + rsub;
+        const bool dv = d < DC_ROWS * k;
+        const int rd = dv ? d / k : 0, sd = dv ? d % k : 0;
+        float acc = 0.f;
+        if (dv) {
+#pragma unroll
+            for (int i = 0; i < UPL; i++) {
+                const int u = lr + LPR * i;
+                if (u < U) acc = q4k_unit_dot(raw[p][i], u, xd + sd * G * XD_STRIDE, acc);
+            }
+        }
+        acc = group_sum<16>(acc);
+        if (dv && lr == 0) yv[sd][rd] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < DC_ROWS) {
+        const int rd = threadIdx.x, r = r0 + rd;
+        float a = 0.f;
+        for (int s = 0; s < k; s++) {
+            const float pr = sel_w[t * 8 + s] * yv[s][rd];
+            a = a + pr;
+        }
+        out[(long long)t * H + r] = resid[(long long)t * H + r] + a;
+    }
+}
+
+template <int NJ>
+static hipError_t launch_topk_t(const float *logits, int T, int E, int top_k, int *sel_idx, float *sel_w, hipStream_t st) {
+    hipLaunchKernelGGL((k_topk<NJ>), dim3(T), dim3(64), 0, st, logits, E, top_k, sel_idx, sel_w);
+    return hipGetLastError();
+}
+
+static hipError_t launch_topk(const float *logits, int T, int E, int top_k, int *sel_idx, float *sel_w, hipStream_t st) {
+    if (E <= 64) return launch_topk_t<1>(logits, T, E, top_k, sel_idx, sel_w, st);
+    if (E <= 128) return launch_topk_t<2>(logits, T, E, top_k, sel_idx, sel_w, st);
+    return launch_topk_t<4>(logits, T, E, top_k, sel_idx, sel_w, st);
+}
+
+template <int M, int NJ>
+static hipError_t launch_router_dpp_t(const float *xn, const float *router, const float *bias, int T, int E, int top_k,
+                                      float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st) {
+    dim3 grid(T, (E + 3) / 4);
+    hipLaunchKernelGGL((k_router_dpp<M, NJ>), grid, dim3(64), 0, st, xn, router, bias, E, top_k, logits, counters,
+                       sel_idx, sel_w);
+    return hipGetLastError();
+}
+
+template <int M>
+static hipError_t launch_router_dpp(const float *xn, const float *router, const float *bias, int T, int E, int top_k,
+                                    float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st) {
+    if (E <= 64) return launch_router_dpp_t<M, 1>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
+    if (E <= 128) return launch_router_dpp_t<M, 2>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
+    return launch_router_dpp_t<M, 4>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
+}
+
+// Router: logits then softmax/top-k.  With a counter buffer (T unsigned,
+// zero on entry, left zero on exit) and H in {512, 1024, 2048} the DPP
+// kernel does both in one launch; otherwise an LDS-tiled logits kernel and
+// a top-k kernel.  hipErrorNotSupported when H does not fit either tiling.
+hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
+                         float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st) {
+    if (counters) {
+        if (H == 2048) return launch_router_dpp<32>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
+        if (H == 1024) return launch_router_dpp<16>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
+        if (H == 512) return launch_router_dpp<8>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
+    }
+    const size_t lds = (size_t)H * 4 + 2 * RT_TILE_FLOATS * 4;
+    if (H > 8192) return hipErrorNotSupported;
+    if (T < 8 && (H == 1024 || H == 2048 || H == 4096)) {
+        dim3 grid(T, (E + EPB_S - 1) / EPB_S);
+        const size_t plds = (size_t)EPB_S * H * 4;
+        if (H == 1024)
+            hipLaunchKernelGGL((k_router_logits_small<16>), grid, dim3(RS_THREADS), plds, st, xn, router, bias, H, E, logits);
+        else if (H == 2048)
+            hipLaunchKernelGGL((k_router_logits_small<32>), grid, dim3(RS_THREADS), plds, st, xn, router, bias, H, E, logits);
+        else
+            hipLaunchKernelGGL((k_router_logits_small<64>), grid, dim3(RS_THREADS), plds, st, xn, router, bias, H, E, logits);
+    } else if (T < 8 && H % 256 == 0) {
+        constexpr int EPB = 16;
+        dim3 grid(T, (E + EPB - 1) / EPB);
+        hipLaunchKernelGGL((k_router_logits<EPB>), grid, dim3(RT_THREADS), lds, st, xn, router, bias, H, E, logits);
+    } else if (H % 64 == 0) {
+        constexpr int EPB = 64;
+        dim3 grid(T, (E + EPB - 1) / EPB);
+        hipLaunchKernelGGL((k_router_logits<EPB>), grid, dim3(RT_THREADS), lds, st, xn, router, bias, H, E, logits);
+    } else {
+        return hipErrorNotSupported;
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return launch_topk(logits, T, E, top_k, sel_idx, sel_w, st);
+}
+
+template <int UPL_GU, int UPL_DC>
+static hipError_t launch_experts_q4k(const MoeArgs &a, hipStream_t st) {
+    const int pairs = a.T * a.k;
+    {
+        const int out_per_wg = (GU_THREADS / 64) * GU_ROWS;
+        dim3 grid((a.F + out_per_wg - 1) / out_per_wg, pairs);
+        size_t lds = (size_t)(a.H / 32) * XD_STRIDE * 4;
+        hipLaunchKernelGGL((k_gate_up_q4k<UPL_GU>), grid, dim3(GU_THREADS), lds, st, (const uint8_t *)a.gate,
+                           (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.k, a.act);
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+    }
+    dim3 grid(a.H / DC_ROWS, a.T);
+    size_t lds = (size_t)a.k * (a.F / 32) * XD_STRIDE * 4;
+    hipLaunchKernelGGL((k_down_combine_q4k<UPL_DC>), grid, dim3(DC_THREADS), lds, st, (const uint8_t *)a.down, a.act,
+                       a.sel_idx, a.sel_w, a.resid, a.H, a.F, a.k, a.out);
+    return hipGetLastError();
+}
+
+// Expert kernels for Q4_K weights (routing already in a.sel_idx / a.sel_w);
+// hipErrorNotSupported outside H <= 4096, F <= 2048.
+hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st) {
+    const int ugu = (a.H / 64 + 31) / 32, udc = (a.F / 64 + 15) / 16;
+    if (ugu == 1 && udc == 1) return launch_experts_q4k<1, 1>(a, st);
+    if (ugu <= 2 && udc <= 1) return launch_experts_q4k<2, 1>(a, st);
+    if (ugu <= 2 && udc <= 2) return launch_experts_q4k<2, 2>(a, st);
+    return hipErrorNotSupported;
+}
+
+}  // namespace tbq
