@@ -182,7 +182,6 @@ static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 
 size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode) {
-    (void)mode;
     if (!L || T <= 0) return 0;
     int k = L->top_k > 8 ? 8 : L->top_k;
     size_t n = COUNTER_BYTES;
@@ -190,6 +189,7 @@ size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode) {
     n += align256((size_t)T * L->E * 4);                     // router logits
     n += align256((size_t)T * k * L->F * 4);                 // act
     n += align256((size_t)T * k * L->H * 4);                 // y
+    if (mode == TBQ_MOE_BF16) n += align256(prefill_workspace_bytes(T, k, L->E, L->H, L->F));
     return n;
 }
 
@@ -212,7 +212,9 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
                     float *sel_w, void *workspace, size_t ws_bytes, int mode, void *s) {
     if (!ensure_init()) return 0;
     if (!check_moe(L, T)) return 0;
-    if (mode != TBQ_MOE_FP32) return fail("tbq_moe_forward: mode %d not available", mode);
+    if (mode != TBQ_MOE_FP32 && mode != TBQ_MOE_BF16) return fail("tbq_moe_forward: unknown mode %d", mode);
+    if (mode == TBQ_MOE_BF16 && (L->qtype != QT_Q4_K || L->F % 128 || L->H % 128))
+        return fail("tbq_moe_forward: the bf16 MFMA path takes Q4_K experts with H, F multiples of 256");
     if (!xn || !resid || !out || !aligned16(xn) || !aligned16(resid) || !aligned16(out))
         return fail("tbq_moe_forward: null or misaligned activation pointer");
     if (T == 0) return 1;
@@ -245,9 +247,10 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     float *ws_w = (float *)(ws + off); off += align256((size_t)T * 8 * 4);
     a.logits = (float *)(ws + off); off += align256((size_t)T * a.E * 4);
     a.act = (float *)(ws + off); off += align256((size_t)T * a.k * a.F * 4);
-    a.y = (float *)(ws + off);
+    a.y = (float *)(ws + off); off += align256((size_t)T * a.k * a.H * 4);
     a.sel_idx = sel_idx ? sel_idx : ws_idx;
     a.sel_w = sel_w ? sel_w : ws_w;
+    if (mode == TBQ_MOE_BF16) return hip_ok(launch_moe_bf16(a, ws + off, S(s)), "moe launch (bf16 MFMA)");
     return hip_ok(launch_moe_fp32(a, S(s)), "moe launch");
 }
 

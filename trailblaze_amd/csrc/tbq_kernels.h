@@ -30,5 +30,8 @@ hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st);
 hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
                          float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st);
 hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st);
+size_t prefill_workspace_bytes(int T, int k, int E, int H, int F);
+hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t st);
+hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st);
 
 }  // namespace tbq

@@ -285,4 +285,20 @@ hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Prefill: exact routing, then grouped bf16-MFMA experts and the
+// slot-ordered combine.
+hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st) {
+    hipError_t err = launch_router(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.logits,
+                                   a.T >= 32 ? nullptr : a.counters, a.sel_idx, a.sel_w, st);
+    if (err == hipErrorNotSupported)
+        err = launch_route(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.sel_idx, a.sel_w, st);
+    if (err != hipSuccess) return err;
+    err = launch_moe_prefill_q4k(a, scratch, st);
+    if (err != hipSuccess) return err;
+    long long n = (long long)a.T * a.H;
+    int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+    hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_w, a.resid, a.T, a.H, a.k, a.out);
+    return hipGetLastError();
+}
+
 }  // namespace tbq

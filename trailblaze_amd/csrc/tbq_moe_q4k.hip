@@ -515,6 +515,45 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
     }
 }
 
+// ---------------------------------------------------------------------------
+// Batch router: one wave per (token, 64 experts), lane e owns expert e's
+// chain; x[k] is uniform across the wave (scalar loads into SGPRs), W[e][k]
+// streams into the lane's VGPRs 16 k at a time with the next block already
+// in flight.  Two VALU ops per element (mul, add), no LDS.
+// grid = (T, ceil(E/64)), 64 threads.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void k_router_lane(const float *__restrict__ xn, const float *__restrict__ Wr,
+                                                    const float *__restrict__ bias, int H, int E,
+                                                    float *__restrict__ logits) {
+    const int t = blockIdx.x, e = blockIdx.y * 64 + threadIdx.x;
+    const bool ev = e < E;
+    const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (long long)(ev ? e : 0) * H);
+    const float *x = xn + (long long)t * H;
+    float acc = 0.f;
+    float4 cur[4], nxt[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) cur[i] = w4[i];
+    for (int k0 = 0; k0 < H; k0 += 16) {
+        if (k0 + 16 < H) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) nxt[i] = w4[(k0 + 16) / 4 + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            acc = acc + cur[i].x * x[k0 + 4 * i];
+            acc = acc + cur[i].y * x[k0 + 4 * i + 1];
+            acc = acc + cur[i].z * x[k0 + 4 * i + 2];
+            acc = acc + cur[i].w * x[k0 + 4 * i + 3];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) cur[i] = nxt[i];
+    }
+    if (ev) {
+        if (bias) acc = acc + bias[e];
+        logits[(long long)t * E + e] = acc;
+    }
+}
+
 template <int NJ>
 static hipError_t launch_topk_t(const float *logits, int T, int E, int top_k, int *sel_idx, float *sel_w, hipStream_t st) {
     hipLaunchKernelGGL((k_topk<NJ>), dim3(T), dim3(64), 0, st, logits, E, top_k, sel_idx, sel_w);
@@ -550,12 +589,18 @@ static hipError_t launch_router_dpp(const float *xn, const float *router, const 
 // a top-k kernel.  hipErrorNotSupported when H does not fit either tiling.
 hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
                          float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st) {
-    if (counters) {
+    if (counters && T < 32) {
         if (H == 2048) return launch_router_dpp<32>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
         if (H == 1024) return launch_router_dpp<16>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
         if (H == 512) return launch_router_dpp<8>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
     }
     const size_t lds = (size_t)H * 4 + 2 * RT_TILE_FLOATS * 4;
+    if (T >= 32 && H % 16 == 0) {
+        hipLaunchKernelGGL(k_router_lane, dim3(T, (E + 63) / 64), dim3(64), 0, st, xn, router, bias, H, E, logits);
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        return launch_topk(logits, T, E, top_k, sel_idx, sel_w, st);
+    }
     if (H > 8192) return hipErrorNotSupported;
     if (T < 8 && (H == 1024 || H == 2048 || H == 4096)) {
         dim3 grid(T, (E + EPB_S - 1) / EPB_S);
