@@ -107,10 +107,43 @@ __host__ __device__ __forceinline__ float expf_glibc(float x) {
 // ---------------------------------------------------------------------------
 // Wave-level helpers (wave64).
 // ---------------------------------------------------------------------------
+// Cross-lane moves that stay in the VALU (no LDS crossbar round trip):
+// DPP quad_perm xor 1 / xor 2, row_half_mirror (lane i <-> 7-i within 8),
+// row_mirror (i <-> 15-i within 16); gfx950's permlane16/32 swaps pair
+// 16-lane rows 0<->1, 2<->3 and the two 32-lane halves.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_QXOR1 = 0xB1, DPP_QXOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
+// The swap builtins return both exchanged operands as a 2-vector.  Its
+// elements are copied into scalars before any bit cast: this clang lowers
+// __builtin_bit_cast of a vector element r[1] as a load from the vector's
+// first element.
+__device__ __forceinline__ float swap16_sum(float v) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float swap32_sum(float v) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+
+// Sum over aligned groups of WIDTH lanes (a power of two <= 64); every lane
+// of a group gets the same value.  The whole wave must be active.
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, WIDTH);
+    if constexpr (WIDTH >= 2) v += dpp_f32<DPP_QXOR1>(v);
+    if constexpr (WIDTH >= 4) v += dpp_f32<DPP_QXOR2>(v);
+    if constexpr (WIDTH >= 8) v += dpp_f32<DPP_HALF_MIRROR>(v);
+    if constexpr (WIDTH >= 16) v += dpp_f32<DPP_MIRROR>(v);
+    if constexpr (WIDTH >= 32) v = swap16_sum(v);
+    if constexpr (WIDTH >= 64) v = swap32_sum(v);
     return v;
 }
 

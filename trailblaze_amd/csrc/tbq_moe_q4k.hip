@@ -412,6 +412,8 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
     const uint8_t *Wb = (half ? up : gate) + (long long)e * F * rb;
     const int r0 = (blockIdx.x * (GU_THREADS / 64) + wave) * GU_ROWS;
 
+    XStager<GU_THREADS, 2> xs;   // H <= 8192
+    xs.load(xn + (long long)t * H, H);
     Q4KUnit raw[GU_ROWS][UPL];
 #pragma unroll
     for (int rr = 0; rr < GU_ROWS; rr++) {
@@ -422,7 +424,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
             if (r < F && u < U) q4k_load(Wb + (long long)r * rb, u, raw[rr][i]);
         }
     }
-    stage_x_digits_nibble<GU_THREADS>(xn + (long long)t * H, H, xd);
+    xs.store(xd, H);
     __syncthreads();
 #pragma unroll
     for (int rr = 0; rr < GU_ROWS; rr++) {
@@ -470,6 +472,8 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
     const int lr = lane & 15, rsub = lane >> 4;
     // dot d = (row rd, slot sd), d < DC_ROWS * k; wave w pass p takes dots 4*(w + 8p) + rsub
     constexpr int PASSES = (DC_ROWS * 8 + (DC_THREADS / 64) * RPP - 1) / ((DC_THREADS / 64) * RPP);
+    XStager<DC_THREADS, 2 * UPL> xs;   // k <= 8 vectors of F <= 1024 * UPL
+    xs.load(act + (long long)t * k * F, F, k);
     Q4KUnit raw[PASSES][UPL];
 #pragma unroll
     for (int p = 0; p < PASSES; p++) {
@@ -485,7 +489,7 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
             }
         }
     }
-    stage_x_digits_nibble<DC_THREADS>(act + (long long)t * k * F, F, xd, k);
+    xs.store(xd, F, k);
     __syncthreads();
 #pragma unroll
     for (int p = 0; p < PASSES; p++) {
@@ -497,7 +501,7 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
 #pragma unroll
             for (int i = 0; i < UPL; i++) {
                 const int u = lr + LPR * i;
-                if (u < U) acc = q4k_unit_dot(raw[p][i], u, xd + sd * G * XD_STRIDE, acc);
+                if (u < U) acc = q4k_unit_dot(raw[p][i], u, xd + sd * G * XD_PER_SB, acc);
             }
         }
         acc = group_sum<16>(acc);
@@ -633,14 +637,14 @@ static hipError_t launch_experts_q4k(const MoeArgs &a, hipStream_t st) {
     {
         const int out_per_wg = (GU_THREADS / 64) * GU_ROWS;
         dim3 grid((a.F + out_per_wg - 1) / out_per_wg, pairs);
-        size_t lds = (size_t)(a.H / 32) * XD_STRIDE * 4;
+        size_t lds = (size_t)(a.H / 32) * XD_PER_SB * 4;
         hipLaunchKernelGGL((k_gate_up_q4k<UPL_GU>), grid, dim3(GU_THREADS), lds, st, (const uint8_t *)a.gate,
                            (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.k, a.act);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
     dim3 grid(a.H / DC_ROWS, a.T);
-    size_t lds = (size_t)a.k * (a.F / 32) * XD_STRIDE * 4;
+    size_t lds = (size_t)a.k * (a.F / 32) * XD_PER_SB * 4;
     hipLaunchKernelGGL((k_down_combine_q4k<UPL_DC>), grid, dim3(DC_THREADS), lds, st, (const uint8_t *)a.down, a.act,
                        a.sel_idx, a.sel_w, a.resid, a.H, a.F, a.k, a.out);
     return hipGetLastError();

@@ -4,9 +4,9 @@
 // (Digit representation and its accuracy: tbq_q4k.hpp.)
 //
 // Work split: a 1024-thread workgroup (16 waves, one staging of x per CU)
-// stores x's digits in LDS (112 bytes per sub-block: 24 digit dwords,
-// sum(x), 2^-s, pad -- a stride that keeps ds_read_b128 free of bank
-// conflicts); each lane owns "units" of two consecutive sub-blocks of one
+// stores x's digits in LDS (XD_UNIT layout: 52 dwords per 64 elements, read
+// free of bank conflicts); x's loads are issued before the weight loads so
+// they do not queue behind them; each lane owns "units" of two consecutive sub-blocks of one
 // super-block (64 weights, 4 lanes per super-block), LPR lanes share a row,
 // and a wave issues its first row's loads before staging x and the next
 // row's loads before reducing the current one, so HBM latency overlaps the
@@ -17,6 +17,12 @@
 namespace tbq {
 
 constexpr int WG = 1024;        // threads per workgroup (16 waves share one x staging)
+#ifndef Q4K_XR_R
+#define Q4K_XR_R 1               // rows per lane of the register-x kernel
+#endif
+#ifndef Q4K_XR_NW
+#define Q4K_XR_NW 16             // waves per workgroup of the register-x kernel
+#endif
 
 // One pass of a wave covers RPP = 64/LPR rows; each lane owns UPL units of
 // its row.  Rows are grid-strided over all waves; the next pass's loads are
@@ -32,6 +38,8 @@ __global__ __launch_bounds__(WG) void k_mv_q4k(const uint8_t *__restrict__ W, in
     const int stride = gridDim.x * (WG / 64) * RPP;
     int row = (blockIdx.x * (WG / 64) + wave) * RPP + rsub;
 
+    XStager<WG, 2> xs;   // K <= 16384
+    xs.load(x, K);
     Q4KUnit cur[UPL], nxt[UPL];
     auto load = [&](Q4KUnit *dst, int r) {
 #pragma unroll
@@ -41,7 +49,7 @@ __global__ __launch_bounds__(WG) void k_mv_q4k(const uint8_t *__restrict__ W, in
         }
     };
     load(cur, row);
-    stage_x_digits_nibble<WG>(x, K, xd);
+    xs.store(xd, K);
     __syncthreads();
     // every lane of a wave runs the same number of passes: the bound uses the
     // wave's first row, so the shuffles below always see a full wave
@@ -68,6 +76,54 @@ __global__ __launch_bounds__(WG) void k_mv_q4k(const uint8_t *__restrict__ W, in
     }
 }
 
+// Rows of up to 64 units (K <= 4096): every lane keeps one unit index for
+// all its rows, so it reads that unit's digits from LDS once into registers
+// and reuses them for R rows (LDS traffic / R).  A wave covers R passes of
+// RPP = 64/LPR rows (rows wave_base + p*RPP + rsub); all R passes' weight
+// loads are in flight before x is staged.  No grid-stride loop: the grid
+// covers M exactly.
+template <int LPR, int R, int NW>
+__global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict__ W, int M, int K, long long rb,
+                                                      const float *__restrict__ x, float *__restrict__ y) {
+    extern __shared__ uint32_t xd[];
+    constexpr int NT = NW * 64, RPP = 64 / LPR;
+    const int U = K / 64;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lr = lane % LPR, rsub = lane / LPR;
+    const bool lv = lr < U;
+    XStager<NT, (4 * 128 + NT - 1) / NT> xs;   // K <= 4096
+    xs.load(x, K);
+    const int base = (blockIdx.x * NW + wave) * R * RPP + rsub;
+    Q4KUnit w[R];
+#pragma unroll
+    for (int p = 0; p < R; p++) {
+        const int r = base + p * RPP;
+        if (r < M && lv) q4k_load(W + (long long)r * rb, lr, w[p]);
+    }
+    xs.store(xd, K);
+    __syncthreads();
+    XUnit xu;
+    if (lv) xunit_load(xd, lr, xu);
+#pragma unroll
+    for (int p = 0; p < R; p++) {
+        const int r = base + p * RPP;
+        float acc = 0.f;
+        if (r < M && lv) acc = q4k_unit_dot(w[p], lr, xu, 0.f);
+        acc = group_sum<LPR>(acc);
+        if (lr == 0 && r < M) y[r] = acc;
+    }
+}
+
+template <int LPR, int R, int NW>
+static hipError_t launch_q4k_xr(const void *W, int M, int K, const float *x, float *y, hipStream_t s) {
+    constexpr int ROWS_PER_WG = NW * R * (64 / LPR);
+    const int grid = (M + ROWS_PER_WG - 1) / ROWS_PER_WG;
+    const long long rb = (long long)(K / 256) * 144;
+    const size_t lds = (size_t)(K / 32) * XD_PER_SB * 4;
+    hipLaunchKernelGGL((k_mv_q4k_xr<LPR, R, NW>), dim3(grid), dim3(NW * 64), lds, s, (const uint8_t *)W, M, K, rb, x, y);
+    return hipGetLastError();
+}
+
 template <int LPR, int UPL>
 static hipError_t launch_q4k_t(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu) {
     constexpr int ROWS_PER_WG = (WG / 64) * (64 / LPR);
@@ -75,7 +131,7 @@ static hipError_t launch_q4k_t(const void *W, int M, int K, const float *x, floa
     long long cap = 2ll * n_cu;
     int grid = (int)(need < cap ? need : cap);
     long long rb = (long long)(K / 256) * 144;
-    size_t lds = (size_t)(K / 32) * XD_STRIDE * 4;
+    size_t lds = (size_t)(K / 32) * XD_PER_SB * 4;
     hipLaunchKernelGGL((k_mv_q4k<LPR, UPL>), dim3(grid), dim3(WG), lds, s, (const uint8_t *)W, M, K, rb, x, y);
     return hipGetLastError();
 }
@@ -84,11 +140,11 @@ static hipError_t launch_q4k_t(const void *W, int M, int K, const float *x, floa
 hipError_t launch_matvec_q4k(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu) {
     const int U = K / 64;
     if (K % 256 || U < 4) return hipErrorNotSupported;
-    if (U <= 4) return launch_q4k_t<4, 1>(W, M, K, x, y, s, n_cu);
-    if (U <= 8) return launch_q4k_t<8, 1>(W, M, K, x, y, s, n_cu);
-    if (U <= 16) return launch_q4k_t<16, 1>(W, M, K, x, y, s, n_cu);
-    if (U <= 32) return launch_q4k_t<32, 1>(W, M, K, x, y, s, n_cu);
-    if (U <= 64) return launch_q4k_t<64, 1>(W, M, K, x, y, s, n_cu);
+    if (U <= 4) return launch_q4k_xr<4, Q4K_XR_R, Q4K_XR_NW>(W, M, K, x, y, s);
+    if (U <= 8) return launch_q4k_xr<8, Q4K_XR_R, Q4K_XR_NW>(W, M, K, x, y, s);
+    if (U <= 16) return launch_q4k_xr<16, Q4K_XR_R, Q4K_XR_NW>(W, M, K, x, y, s);
+    if (U <= 32) return launch_q4k_xr<32, Q4K_XR_R, Q4K_XR_NW>(W, M, K, x, y, s);
+    if (U <= 64) return launch_q4k_xr<64, Q4K_XR_R, Q4K_XR_NW>(W, M, K, x, y, s);
     if (U <= 128) return launch_q4k_t<64, 2>(W, M, K, x, y, s, n_cu);
     if (U <= 192) return launch_q4k_t<64, 3>(W, M, K, x, y, s, n_cu);
     if (U <= 256) return launch_q4k_t<64, 4>(W, M, K, x, y, s, n_cu);

@@ -18,74 +18,106 @@
 
 namespace tbq {
 
-constexpr int XD_STRIDE = 28;   // dwords of LDS per 32-element sub-block
+// LDS layout of the digits, per unit of two sub-blocks (64 elements, 52
+// dwords): digits of the even sub-block (24 dwords), digits of the odd one
+// (24), then {sum x_even, sum x_odd, 2^-s_even, 2^-s_odd}.  Lanes that own
+// consecutive units read at a 52-dword stride, which maps any 8 consecutive
+// lanes of a ds_read_b128 onto 8 disjoint 4-bank groups (52 = 20 mod 32).
+constexpr int XD_UNIT = 52;
+constexpr int XD_PER_SB = XD_UNIT / 2;   // LDS dwords per sub-block on average
 
-// Stage the digits of x (K elements) into LDS; all NT threads of the
-// workgroup participate.
-// Thread t handles 8 elements (group o = t%4 of sub-block g = t/4).  With
-// s_g from the sub-block's max |x|, X = rint(x * 2^s_g) fits 24 bits and its
-// little-endian bytes are the digits: l = byte0 and m = byte1 unsigned,
-// h = byte2 signed, X = 65536*h + 256*m + l.  Per 8-element group six dwords
-// are stored: {h, m, l} x {even elements (low nibbles), odd (high nibbles)}.
-// nvec > 1 stages nvec consecutive vectors of K elements (vector v's
-// sub-block g lands at sub-block v*K/32 + g), all threads sharing the work.
-template <int NT>
-__device__ __forceinline__ void stage_x_digits_nibble(const float *__restrict__ x, int K, uint32_t *xd,
-                                                      int nvec = 1) {
-    const int G = K / 32;
-    for (int t = threadIdx.x; t < 4 * G * nvec; t += NT) {
-        const int g = t >> 2, o = t & 3;   // g indexes sub-blocks across all vectors
-        const float4 *xp = reinterpret_cast<const float4 *>(x + 32 * g + 8 * o);
-        const float4 a = xp[0], b = xp[1];
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        float mx = 0.f, sm = 0.f;
+// Staging of x into digits, in two phases so that the loads of x can be
+// issued before a kernel's weight loads (x then does not queue behind them):
+// load() issues the global loads into registers, store() computes and writes
+// the digits.  All NT threads of the workgroup take part; each handles
+// ceil(4 * G * nvec / NT) <= MAXT tasks of 8 elements (task t: sub-block
+// g = t / 4, elements 8 * (t % 4) ..).  nvec > 1 stages nvec consecutive
+// vectors of K elements; vector v's sub-block g is staged as sub-block
+// v * K / 32 + g, so vector v's digits start at v * (K / 32) * XD_PER_SB.
+//
+// Per task: s_g from the sub-block's max |x|, X = rint(x * 2^s_g) fits 24
+// bits and its little-endian bytes are the digits: l = byte0 and m = byte1
+// unsigned, h = byte2 signed, X = 65536*h + 256*m + l.  Six dwords are
+// stored: {h, m, l} x {even elements (low nibbles), odd (high nibbles)}.
+template <int NT, int MAXT>
+struct XStager {
+    float4 v[MAXT][2];
+
+    __device__ __forceinline__ void load(const float *__restrict__ x, int K, int nvec = 1) {
+        const int ntask = 4 * (K / 32) * nvec;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            mx = fmaxf(mx, fabsf(v[i]));
-            sm += v[i];
+        for (int i = 0; i < MAXT; i++) {
+            const int t = threadIdx.x + i * NT;
+            if (t < ntask) {
+                const float4 *xp = reinterpret_cast<const float4 *>(x + 8 * t);
+                v[i][0] = xp[0];
+                v[i][1] = xp[1];
+            }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 1));
-        mx = fmaxf(mx, __shfl_xor(mx, 2));
-        sm += __shfl_xor(sm, 1);
-        sm += __shfl_xor(sm, 2);
-        int e = 0;
-        frexpf(mx, &e);
-        int s = mx > 0.f ? 22 - e : 0;
-        s = s > 126 ? 126 : (s < -126 ? -126 : s);
-        const float sc = ldexpf(1.f, s);
-        uint32_t X[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) X[i] = (uint32_t)(int)rintf(v[i] * sc);
-        uint32_t dig[6];
-#pragma unroll
-        for (int par = 0; par < 2; par++) {
-            // bytes 0,1 of X[par], X[par+2] and of X[par+4], X[par+6]
-            const uint32_t p01 = __builtin_amdgcn_perm(X[par + 2], X[par], 0x05010400u);
-            const uint32_t q01 = __builtin_amdgcn_perm(X[par + 6], X[par + 4], 0x05010400u);
-            const uint32_t p2 = __builtin_amdgcn_perm(X[par + 2], X[par], 0x07030602u);
-            const uint32_t q2 = __builtin_amdgcn_perm(X[par + 6], X[par + 4], 0x07030602u);
-            dig[4 + par] = __builtin_amdgcn_perm(q01, p01, 0x05040100u);   // l
-            dig[2 + par] = __builtin_amdgcn_perm(q01, p01, 0x07060302u);   // m
-            dig[0 + par] = __builtin_amdgcn_perm(q2, p2, 0x05040100u);     // h
-        }
-        uint32_t *dst = xd + g * XD_STRIDE + o * 6;
-        *reinterpret_cast<uint2 *>(dst) = make_uint2(dig[0], dig[1]);
-        *reinterpret_cast<uint2 *>(dst + 2) = make_uint2(dig[2], dig[3]);
-        *reinterpret_cast<uint2 *>(dst + 4) = make_uint2(dig[4], dig[5]);
-        if (o == 0)
-            *reinterpret_cast<float2 *>(xd + g * XD_STRIDE + 24) = make_float2(sm, ldexpf(1.f, -s));
     }
-}
+
+    __device__ __forceinline__ void store(uint32_t *xd, int K, int nvec = 1) const {
+        const int ntask = 4 * (K / 32) * nvec;
+#pragma unroll
+        for (int i = 0; i < MAXT; i++) {
+            const int t = threadIdx.x + i * NT;
+            if (t - (int)(threadIdx.x & 3) >= ntask) break;   // uniform over the task's 4 lanes
+            const int g = t >> 2, o = t & 3;
+            const float4 a = v[i][0], b = v[i][1];
+            const float e8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float mx = 0.f, sm = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                mx = fmaxf(mx, fabsf(e8[j]));
+                sm += e8[j];
+            }
+            // the task's 4 lanes form one DPP quad (active together)
+            mx = fmaxf(mx, dpp_f32<DPP_QXOR1>(mx));
+            mx = fmaxf(mx, dpp_f32<DPP_QXOR2>(mx));
+            sm += dpp_f32<DPP_QXOR1>(sm);
+            sm += dpp_f32<DPP_QXOR2>(sm);
+            int e = 0;
+            frexpf(mx, &e);
+            int s = mx > 0.f ? 22 - e : 0;
+            s = s > 126 ? 126 : (s < -126 ? -126 : s);
+            const float sc = ldexpf(1.f, s);
+            uint32_t X[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) X[j] = (uint32_t)(int)rintf(e8[j] * sc);
+            uint32_t dig[6];
+#pragma unroll
+            for (int par = 0; par < 2; par++) {
+                // bytes 0,1 of X[par], X[par+2] and of X[par+4], X[par+6]
+                const uint32_t p01 = __builtin_amdgcn_perm(X[par + 2], X[par], 0x05010400u);
+                const uint32_t q01 = __builtin_amdgcn_perm(X[par + 6], X[par + 4], 0x05010400u);
+                const uint32_t p2 = __builtin_amdgcn_perm(X[par + 2], X[par], 0x07030602u);
+                const uint32_t q2 = __builtin_amdgcn_perm(X[par + 6], X[par + 4], 0x07030602u);
+                dig[4 + par] = __builtin_amdgcn_perm(q01, p01, 0x05040100u);   // l
+                dig[2 + par] = __builtin_amdgcn_perm(q01, p01, 0x07060302u);   // m
+                dig[0 + par] = __builtin_amdgcn_perm(q2, p2, 0x05040100u);     // h
+            }
+            if (t < ntask) {
+                uint32_t *unit = xd + (g >> 1) * XD_UNIT;
+                uint32_t *dst = unit + (g & 1) * 24 + o * 6;
+                *reinterpret_cast<uint2 *>(dst) = make_uint2(dig[0], dig[1]);
+                *reinterpret_cast<uint2 *>(dst + 2) = make_uint2(dig[2], dig[3]);
+                *reinterpret_cast<uint2 *>(dst + 4) = make_uint2(dig[4], dig[5]);
+                if (o == 0) {
+                    unit[48 + (g & 1)] = __builtin_bit_cast(uint32_t, sm);
+                    unit[50 + (g & 1)] = __builtin_bit_cast(uint32_t, ldexpf(1.f, -s));
+                }
+            }
+        }
+    }
+};
 
 // sum q*x over one Q4_K sub-block whose 32 nibbles are packed in q (byte i =
-// weights 2i, 2i+1), times the sub-block scale S, minus M*sum(x), added to acc.
-__device__ __forceinline__ float q4_subblock(uint4 q, const uint32_t *xs, float S, float Mn, float acc) {
-    const uint4 *d4 = reinterpret_cast<const uint4 *>(xs);
-    uint4 D[6];
-#pragma unroll
-    for (int i = 0; i < 6; i++) D[i] = d4[i];
+// weights 2i, 2i+1), times the sub-block scale S, minus M*sum(x), added to
+// acc.  D holds the sub-block's 24 digit dwords, sx = sum of its x, isc =
+// 2^-s of its digits.
+__device__ __forceinline__ float q4_subblock(uint4 q, const uint4 *D, float sx, float isc, float S, float Mn,
+                                             float acc) {
     const uint32_t *D32 = reinterpret_cast<const uint32_t *>(D);
-    const float2 meta = *reinterpret_cast<const float2 *>(xs + 24);
     const uint32_t qv[4] = {q.x, q.y, q.z, q.w};
     int ah = 0;
     uint32_t am = 0, al = 0;
@@ -101,8 +133,22 @@ __device__ __forceinline__ float q4_subblock(uint4 q, const uint32_t *xs, float 
         al = __builtin_amdgcn_udot4(hi, D32[o * 6 + 5], al, false);
     }
     const float f = fmaf((float)ah, 65536.f, fmaf((float)am, 256.f, (float)al));
-    acc = fmaf(S * meta.y, f, acc);
-    return fmaf(-Mn, meta.x, acc);
+    acc = fmaf(S * isc, f, acc);
+    return fmaf(-Mn, sx, acc);
+}
+
+// One unit's digits (two sub-blocks) and {sum x_even, sum x_odd, 2^-s_even,
+// 2^-s_odd}, as laid out in LDS.
+struct XUnit {
+    uint4 d[12];
+    float4 meta;
+};
+
+__device__ __forceinline__ void xunit_load(const uint32_t *xd, int u, XUnit &x) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(xd + (size_t)u * XD_UNIT);
+#pragma unroll
+    for (int i = 0; i < 12; i++) x.d[i] = p[i];
+    x.meta = *reinterpret_cast<const float4 *>(p + 12);
 }
 
 struct Q4KUnit {
@@ -123,7 +169,7 @@ __device__ __forceinline__ void q4k_load(const uint8_t *row, int u, Q4KUnit &r) 
 // Reference scale/min selection (layer4/tb_gguf.c:163-168): sub-block j<4
 // takes scale byte 4+j and min byte 8+j; j>=4 takes scale byte 8+j and min
 // byte 12+j, i.e. the first four quant bytes.
-__device__ __forceinline__ float q4k_unit_dot(const Q4KUnit &r, int u, const uint32_t *xd, float acc) {
+__device__ __forceinline__ float q4k_unit_dot(const Q4KUnit &r, int u, const XUnit &x, float acc) {
     const int p = u & 3;
     const float d = f16_ref(r.hdr.x & 0xFFFFu), dmin = f16_ref(r.hdr.x >> 16);
     const uint32_t sw = p < 2 ? r.hdr.y : r.hdr.w;
@@ -131,9 +177,15 @@ __device__ __forceinline__ float q4k_unit_dot(const Q4KUnit &r, int u, const uin
     const int sh = 16 * (p & 1);
     const float S0 = d * (float)((sw >> sh) & 63), S1 = d * (float)((sw >> (sh + 8)) & 63);
     const float M0 = dmin * (float)((mw >> sh) & 63), M1 = dmin * (float)((mw >> (sh + 8)) & 63);
-    const uint32_t *xs = xd + (size_t)(2 * u) * XD_STRIDE;
-    acc = q4_subblock(r.q0, xs, S0, M0, acc);
-    return q4_subblock(r.q1, xs + XD_STRIDE, S1, M1, acc);
+    acc = q4_subblock(r.q0, x.d, x.meta.x, x.meta.z, S0, M0, acc);
+    return q4_subblock(r.q1, x.d + 6, x.meta.y, x.meta.w, S1, M1, acc);
+}
+
+// Same, with the unit's digits read from LDS.
+__device__ __forceinline__ float q4k_unit_dot(const Q4KUnit &r, int u, const uint32_t *xd, float acc) {
+    XUnit x;
+    xunit_load(xd, u, x);
+    return q4k_unit_dot(r, u, x, acc);
 }
 
 }  // namespace tbq
