@@ -134,6 +134,36 @@ __device__ __forceinline__ float swap32_sum(float v) {
     return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
 }
 
+__device__ __forceinline__ float swap16_max(float v) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+__device__ __forceinline__ float swap32_max(float v) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    const uint32_t r0 = r[0], r1 = r[1];
+    return fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+}
+
+// Max over the whole wave (all 64 lanes active); every lane gets it.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<DPP_QXOR1>(v));
+    v = fmaxf(v, dpp_f32<DPP_QXOR2>(v));
+    v = fmaxf(v, dpp_f32<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f32<DPP_MIRROR>(v));
+    v = swap16_max(v);
+    return swap32_max(v);
+}
+
+// Min over aligned groups of 8 lanes; every lane of a group gets it.
+__device__ __forceinline__ float group8_min(float v) {
+    v = fminf(v, dpp_f32<DPP_QXOR1>(v));
+    v = fminf(v, dpp_f32<DPP_QXOR2>(v));
+    return fminf(v, dpp_f32<DPP_HALF_MIRROR>(v));
+}
+
 // Sum over aligned groups of WIDTH lanes (a power of two <= 64); every lane
 // of a group gets the same value.  The whole wave must be active.
 template <int WIDTH>

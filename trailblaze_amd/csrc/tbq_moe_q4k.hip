@@ -194,12 +194,6 @@ __global__ __launch_bounds__(RS_THREADS) void k_router_logits_small(const float 
 // first slot holding the minimum when a score is strictly larger, and the
 // sequential renormalisation over the k slots.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
-
 __device__ __forceinline__ float rdlane(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
@@ -228,47 +222,62 @@ __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int
     }
     if (lane < 16) P[64 * NJ + lane] = 0.f;
     __syncthreads();
+    // sequential sum in expert order, by every lane from broadcast LDS reads;
+    // P is zero beyond E and adding +0 to the (non-negative) running sum is
+    // exact, so whole 32-blocks are added
     float ssum = 0.f;
-    if (lane == 0) {   // sequential sum in expert order
-        for (int e0 = 0; e0 < E; e0 += 16) {
-            float4 q[4];
+    {
+        const float4 *P4 = reinterpret_cast<const float4 *>(P);
+        float4 q[2][8];
 #pragma unroll
-            for (int i = 0; i < 4; i++) q[i] = *reinterpret_cast<const float4 *>(P + e0 + 4 * i);
-            const float qq[16] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w,
-                                  q[2].x, q[2].y, q[2].z, q[2].w, q[3].x, q[3].y, q[3].z, q[3].w};
+        for (int i = 0; i < 8; i++) q[0][i] = P4[i];
 #pragma unroll
-            for (int i = 0; i < 16; i++)
-                if (e0 + i < E) ssum = ssum + qq[i];
+        for (int b = 0; b < 2 * NJ; b++) {
+            if (32 * b >= E) break;
+            if (b + 1 < 2 * NJ && 32 * (b + 1) < E) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) q[(b + 1) & 1][i] = P4[8 * (b + 1) + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 c = q[b & 1][i];
+                ssum = ssum + c.x;
+                ssum = ssum + c.y;
+                ssum = ssum + c.z;
+                ssum = ssum + c.w;
+            }
         }
     }
-    ssum = rdlane(ssum, 0);
     float pr[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) pr[j] = lane + 64 * j < E ? ex[j] / ssum : 0.f;
-    // slot scan: lanes 0..7 hold slot i; wl is the current minimum
+    // Slot scan: lane i < k holds slot i (value ws, expert wi); lanes k..7
+    // hold +inf so they never count as the minimum.  wl is the current
+    // minimum over the k slots, which never decreases, and ms the first slot
+    // holding it.  Expert e enters iff pr[e] > wl at its turn (a float
+    // compare, so a NaN never enters): candidates are taken in expert order
+    // from a ballot that is re-filtered against the new minimum after every
+    // entry, so only entries cost a sequential step.
     const int k = top_k > 8 ? 8 : top_k;
-    float ws = -1e30f;
+    float ws = lane < k ? -1e30f : __builtin_huge_valf();
     int wi = 0;
     float wl = -1e30f;
+    int ms = 0;
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        // only experts already above the current minimum can enter; the
-        // minimum only grows, so the survivors are re-checked in order
-        unsigned long long cand = __ballot(lane + 64 * j < E && pr[j] > wl);
+        const bool valid = lane + 64 * j < E;
+        unsigned long long cand = __ballot(valid && pr[j] > wl);
         while (cand) {
             const int l = __builtin_ctzll(cand);
-            cand &= cand - 1;
             const float val = rdlane(pr[j], l);
-            if (val > wl) {   // wave-uniform
-                const unsigned long long at_min = __ballot(lane < k && ws == wl);
-                const int lo = __builtin_ctzll(at_min);
-                if (lane == lo) { ws = val; wi = 64 * j + l; }
-                float mn = lane < k ? ws : __builtin_huge_valf();
-                mn = fminf(mn, __shfl_xor(mn, 4));
-                mn = fminf(mn, __shfl_xor(mn, 2));
-                mn = fminf(mn, __shfl_xor(mn, 1));
-                wl = rdlane(mn, 0);
+            if (lane == ms) {
+                ws = val;
+                wi = 64 * j + l;
             }
+            wl = rdlane(group8_min(ws), 0);
+            ms = __builtin_ctzll(__ballot(lane < 8 && ws == wl));
+            cand &= cand - 1;
+            cand &= __ballot(valid && pr[j] > wl);
         }
     }
     float wsum = 0.f;
