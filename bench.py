@@ -27,6 +27,22 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+PMC_COPY_BYTES = 256 << 20
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "q4k_matvec_4096x4096_pmc.txt")
+
+
+def pmc_traffic():
+    """HBM bytes per launch of the headline kernel, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or
+    None when that summary is absent."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_launch:"):
+                    return int(float(ln.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def parse():
@@ -37,6 +53,9 @@ def parse():
     p.add_argument("--quick", action="store_true", help="skip the sweep/MoE/CPU legs")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--moe-only", action="store_true", help="only the MoE leg (profiling)")
+    p.add_argument("--pmc-calib", action="store_true",
+                   help="counter-collection run: the headline matvec as direct launches, then a plain "
+                        "copy of PMC_COPY_BYTES (the HBM-byte calibration of FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -105,6 +124,19 @@ def gpu_leg(args):
         for i in range(ncopy):
             tb.matvec(copies[i], qt, M, K, x, ys[i])
 
+    if args.pmc_calib:
+        # direct launches (no graph) so every dispatch carries its counters
+        for _ in range(3):
+            step()
+        src = torch.empty(PMC_COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"pmc calibration: {3 * ncopy} headline launches, 5 copies of {PMC_COPY_BYTES} B")
+        res["headline"] = None
+        return res
+
     secs = time_region(step, args.steps, args.warmup, stream)
     per_launch = secs / (args.steps * ncopy)
     bpl = matvec_bytes(qt, M, K)
@@ -125,6 +157,20 @@ def gpu_leg(args):
 
     if args.quick:
         return res
+
+    # the reference ABI (host x in, host y out, synchronous): PCIe-inclusive
+    # per-call time, never the headline value
+    xh = np.ascontiguousarray(synth.activations(K, rng))
+    yh = np.empty(M, np.float32)
+    fn = tb.lib().tb_cuda_matvec_device
+    for _ in range(20):
+        fn(Wd.data_ptr(), qt, M, K, xh.ctypes.data, yh.ctypes.data)
+    n_abi = 300
+    t0 = time.perf_counter()
+    for _ in range(n_abi):
+        fn(Wd.data_ptr(), qt, M, K, xh.ctypes.data, yh.ctypes.data)
+    res["abi_matvec_us"] = (time.perf_counter() - t0) / n_abi * 1e6
+    log(f"tb_cuda_matvec_device (host x/y, synchronous): {res['abi_matvec_us']:.1f} us/call")
 
     if args.moe_only:
         res["moe"] = moe_leg(tb, fm, synth, torch, rng, stream)
@@ -256,6 +302,8 @@ def main():
         sys.exit(2)
     res = gpu_leg(args)
     h = res["headline"]
+    if args.pmc_calib:
+        return
     cpu = None
     if not args.no_cpu and not args.quick:
         cpu = cpu_leg()
@@ -276,12 +324,13 @@ def main():
                                f"weight copies per step (cold HBM)", "M": 4096, "K": 4096,
                    "copies_per_step": h["ncopy"]},
         "roofline": {"bound": "hbm", "achieved": round(h["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_matvec Q4_K", "us_per_launch": round(h["us_per_launch"], 3),
+                     "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
+                     "kernel": "k_mv_q4k_xr (Q4_K int-dot)", "us_per_launch": round(h["us_per_launch"], 3),
                      "bytes_per_launch": h["bytes_per_launch"]},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "extra": {"device": res["device"], "warm_mall_gbs": round(h["warm_gbs"], 1),
                   "warm_us_per_launch": round(h["warm_us_per_launch"], 3),
+                  "abi_matvec_us": None if res.get("abi_matvec_us") is None else round(res["abi_matvec_us"], 2),
                   "sweep": res.get("sweep"), "moe": res.get("moe"),
                   "cpu_detail": None if cpu is None else cpu["detail"]},
     }
