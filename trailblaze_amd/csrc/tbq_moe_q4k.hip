@@ -529,39 +529,102 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
 }
 
 // ---------------------------------------------------------------------------
-// Batch router: one wave per (token, 64 experts), lane e owns expert e's
-// chain; x[k] is uniform across the wave (scalar loads into SGPRs), W[e][k]
-// streams into the lane's VGPRs 16 k at a time with the next block already
-// in flight.  Two VALU ops per element (mul, add), no LDS.
-// grid = (T, ceil(E/64)), 64 threads.
+// Batch router (T >= 32): a workgroup of 4 waves owns 4 tokens x 64 experts;
+// lane e of wave w runs token w's chain for expert e, acc = fl(acc +
+// fl(w*x)) over k ascending.  Each 64-k chunk of the 64 experts' W (16 KB)
+// and of the 4 tokens' x is loaded once per workgroup with coalesced 16-byte
+// loads and stored to LDS transposed ([k/4][expert] float4), so lane e's
+// ds_read_b128 is conflict-free and x is a broadcast read.  Global loads run
+// three chunks ahead through a 4-slot register ring (the loop is unrolled by
+// 4 so every slot index is static).  Requires H % 256 == 0.
+// grid = (ceil(T/4), ceil(E/64)), 256 threads.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void k_router_lane(const float *__restrict__ xn, const float *__restrict__ Wr,
-                                                    const float *__restrict__ bias, int H, int E,
-                                                    float *__restrict__ logits) {
-    const int t = blockIdx.x, e = blockIdx.y * 64 + threadIdx.x;
-    const bool ev = e < E;
-    const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (long long)(ev ? e : 0) * H);
-    const float *x = xn + (long long)t * H;
-    float acc = 0.f;
-    float4 cur[4], nxt[4];
+constexpr int RB_TOK = 4, RB_KC = 256, RB_THREADS = 64 * RB_TOK;
+constexpr int RB_Q = RB_KC / 4;                      // float4 per row per chunk
+constexpr int RB_WPT = 64 * RB_Q / RB_THREADS;       // W float4 per thread per chunk
+
+// Native 4-float vectors: HIP's float4 struct is copied with memcpy between
+// address spaces, which keeps a register array in scratch memory.
+typedef float rb_f4 __attribute__((ext_vector_type(4)));
+
+// wb[b][q][e ^ (q & 7)] holds W[e][4q..4q+3]: for a fixed q the 64 experts
+// are a permutation of one 1 KB row (lane e's ds_read_b128 is conflict-free),
+// and the loaders -- lane l stores q = l -- spread every 8-lane store phase
+// over 8 distinct bank groups.  xb holds the 4 tokens' x (broadcast reads).
+struct RbShared {
+    rb_f4 wb[2][RB_Q][64];        // [buffer][k/4][expert, swizzled]
+    rb_f4 xb[2][RB_TOK][RB_Q];    // [buffer][token][k/4]
+};
+
+// Sum one chunk from LDS, 16 k at a time; the empty asm statements (tied to
+// acc) keep the compiler from hoisting the whole chunk's LDS reads ahead of
+// the arithmetic, which would push the in-flight global loads to scratch.
+__device__ __forceinline__ float rb_chunk(const RbShared &sh, int b, int lane, int wave, float acc) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) cur[i] = w4[i];
-    for (int k0 = 0; k0 < H; k0 += 16) {
-        if (k0 + 16 < H) {
+    for (int q0 = 0; q0 < RB_Q; q0 += 4) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) nxt[i] = w4[(k0 + 16) / 4 + i];
+        for (int q = q0; q < q0 + 4; q++) {
+            const rb_f4 w = sh.wb[b][q][lane ^ (q & 7)];
+            const rb_f4 xv = sh.xb[b][wave][q];
+            acc = acc + w.x * xv.x;
+            acc = acc + w.y * xv.y;
+            acc = acc + w.z * xv.z;
+            acc = acc + w.w * xv.w;
         }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            acc = acc + cur[i].x * x[k0 + 4 * i];
-            acc = acc + cur[i].y * x[k0 + 4 * i + 1];
-            acc = acc + cur[i].z * x[k0 + 4 * i + 2];
-            acc = acc + cur[i].w * x[k0 + 4 * i + 3];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) cur[i] = nxt[i];
+        asm volatile("" : "+v"(acc));
     }
-    if (ev) {
+    return acc;
+}
+
+// This thread's share of chunk c: W float4 q of rows r0 + RPP*i (row
+// stride wstride float4) and x float4 q of token row r0.
+__device__ __forceinline__ void rb_load(rb_f4 (&wr)[RB_WPT], rb_f4 &xr, const rb_f4 *wsrc, long long wstride,
+                                        const rb_f4 *xsrc, int c) {
+#pragma unroll
+    for (int i = 0; i < RB_WPT; i++) wr[i] = wsrc[i * wstride + c * RB_Q];
+    xr = xsrc[c * RB_Q];
+}
+
+__device__ __forceinline__ void rb_store(const rb_f4 (&wr)[RB_WPT], const rb_f4 &xr, RbShared &sh, int b, int q,
+                                         int r0) {
+    constexpr int RPP = RB_THREADS / RB_Q;
+#pragma unroll
+    for (int i = 0; i < RB_WPT; i++) sh.wb[b][q][(r0 + RPP * i) ^ (q & 7)] = wr[i];
+    sh.xb[b][r0][q] = xr;
+}
+
+__global__ __launch_bounds__(RB_THREADS) void k_router_batch(const float *__restrict__ xn, const float *__restrict__ Wr,
+                                                             const float *__restrict__ bias, int T, int H, int E,
+                                                             float *__restrict__ logits) {
+    extern __shared__ rb_f4 rb_lds[];
+    RbShared &sh = *reinterpret_cast<RbShared *>(rb_lds);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e0 = blockIdx.y * 64, t0 = blockIdx.x * RB_TOK;
+    // thread tid loads float4 q = tid % RB_Q of W rows e0 + tid / RB_Q + RPP*i
+    // (E is a multiple of 64, so all exist) and of x row t0 + tid / RB_Q
+    // (tokens >= T read the last token instead; their results are never
+    // stored), so every load is unconditional and addresses are one base plus
+    // uniform strides
+    constexpr int RPP = RB_THREADS / RB_Q;   // rows per pass (= RB_TOK)
+    const int q = tid % RB_Q, r0 = tid / RB_Q;
+    const rb_f4 *wsrc = reinterpret_cast<const rb_f4 *>(Wr + (long long)(e0 + r0) * H) + q;
+    const long long wstride = (long long)RPP * H / 4;   // float4 between this thread's rows
+    const rb_f4 *xsrc = reinterpret_cast<const rb_f4 *>(xn + (long long)(t0 + r0 < T ? t0 + r0 : T - 1) * H) + q;
+    rb_f4 wr[RB_WPT], xr;
+    const int NC = H / RB_KC;
+    rb_load(wr, xr, wsrc, wstride, xsrc, 0);
+    rb_store(wr, xr, sh, 0, q, r0);
+    __syncthreads();
+    float acc = 0.f;
+    for (int c = 0; c < NC; c++) {
+        const int b = c & 1;
+        if (c + 1 < NC) rb_load(wr, xr, wsrc, wstride, xsrc, c + 1);
+        acc = rb_chunk(sh, b, lane, wave, acc);
+        if (c + 1 < NC) rb_store(wr, xr, sh, b ^ 1, q, r0);
+        __syncthreads();
+    }
+    const int t = t0 + wave, e = e0 + lane;
+    if (t < T && e < E) {
         if (bias) acc = acc + bias[e];
         logits[(long long)t * E + e] = acc;
     }
@@ -608,8 +671,9 @@ hipError_t launch_router(const float *xn, const float *router, const float *bias
         if (H == 512) return launch_router_dpp<8>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
     }
     const size_t lds = (size_t)H * 4 + 2 * RT_TILE_FLOATS * 4;
-    if (T >= 32 && H % 16 == 0) {
-        hipLaunchKernelGGL(k_router_lane, dim3(T, (E + 63) / 64), dim3(64), 0, st, xn, router, bias, H, E, logits);
+    if (T >= 32 && H % RB_KC == 0 && E % 64 == 0) {
+        hipLaunchKernelGGL(k_router_batch, dim3((T + RB_TOK - 1) / RB_TOK, (E + 63) / 64), dim3(RB_THREADS),
+                           sizeof(RbShared), st, xn, router, bias, T, H, E, logits);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
         return launch_topk(logits, T, E, top_k, sel_idx, sel_w, st);
