@@ -59,11 +59,14 @@ int tbq_matvec(const void *W, int qtype, int M, int K, const float *x, float *y,
 
 /* Kernel choice for tbq_matvec (no counterpart in the reference: it has one
  * CUDA kernel per format).  AUTO picks the fastest kernel for the shape;
- * FMA is the byte->fp32 fma kernel every format has; INTDOT is the
- * v_dot4-based kernel (Q4_K) and fails for shapes it does not cover. */
+ * FMA is the byte->fp32 fma kernel every format has; INTDOT is the Q4_K
+ * v_dot4 kernel specialised for K <= 16384; KQ is the v_dot4 kernel shared
+ * by Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 and Q8_K (K a multiple of 64,
+ * at most 16384).  INTDOT and KQ fail for shapes they do not cover. */
 #define TBQ_MV_AUTO 0
 #define TBQ_MV_FMA 1
 #define TBQ_MV_INTDOT 2
+#define TBQ_MV_KQ 3
 int tbq_matvec_variant(const void *W, int qtype, int M, int K, const float *x, float *y, int variant,
                        void *stream);
 

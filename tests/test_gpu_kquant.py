@@ -130,8 +130,64 @@ def test_matvec_q4k_activation_range(oracle, scale):
     assert np.all(gpu_matvec(W, fm.Q4_K, M, K, x0, tb.TBQ_MV_INTDOT) == 0.0)
 
 
+KQ_FORMATS = [fm.Q2_K, fm.Q3_K, fm.Q4_K, fm.Q5_K, fm.Q6_K, fm.Q8_0, fm.Q4_0, fm.Q8_K]
+
+
+@pytest.mark.parametrize("qt", KQ_FORMATS)
+@pytest.mark.parametrize("M,K", [(1, 256), (5, 512), (200, 768), (1000, 2048), (4096, 4096), (333, 8192),
+                                 (700, 12288), (65, 16384)])
+def test_matvec_kq_kernel(oracle, qt, M, K):
+    """The shared integer-dot kernel for every block format: row slices of
+    4..64 units, rows split over 2..4 waves (K > 4096), ragged M."""
+    rng = np.random.default_rng(M * 13 + K + 7 * qt)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, qt, M, K, x, tb.TBQ_MV_KQ), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+
+
+@pytest.mark.parametrize("qt", [fm.Q8_0, fm.Q4_0])
+@pytest.mark.parametrize("K", [64, 128, 192])
+def test_matvec_kq_short_rows(oracle, qt, K):
+    """32-weight block formats at K below one 256-weight super-block."""
+    M = 300
+    rng = np.random.default_rng(K + qt)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, qt, M, K, x, tb.TBQ_MV_KQ), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+
+
+@pytest.mark.parametrize("qt", KQ_FORMATS)
+@pytest.mark.parametrize("scale", [1e-30, 1e-3, 1e3, 1e30])
+def test_matvec_kq_activation_range(oracle, qt, scale):
+    """One power-of-two exponent per 64 elements keeps the shared kernel in
+    tolerance for tiny and huge activations and for 1000x outlier channels;
+    x = 0 gives exact zeros."""
+    rng = np.random.default_rng(23 + qt)
+    M, K = 256, 4096
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = (synth.activations(K, rng) * np.float32(scale)).astype(np.float32)
+    x[rng.choice(K, 12, replace=False)] *= np.float32(1000.0)
+    ref = oracle.matvec(W, qt, M, K, x)
+    assert rel_l2(gpu_matvec(W, qt, M, K, x, tb.TBQ_MV_KQ), ref) <= MATVEC_TOL
+    x0 = np.zeros(K, np.float32)
+    assert np.all(gpu_matvec(W, qt, M, K, x0, tb.TBQ_MV_KQ) == 0.0)
+
+
+def test_matvec_kq_rejects_uncovered_shapes():
+    import torch
+    W = empty(4096, torch.uint8)
+    x = empty(4096, torch.float32)
+    y = empty(4, torch.float32)
+    with pytest.raises(tb.TbqError):
+        tb.matvec(W, fm.Q8_0, 4, 96, x, y, variant=tb.TBQ_MV_KQ)     # K not a multiple of 64
+    with pytest.raises(tb.TbqError):
+        tb.matvec(W, fm.F16, 4, 256, x, y, variant=tb.TBQ_MV_KQ)     # no integer form
+
+
 def test_matvec_exact_one_hot():
-    # Q8_0 weights in {0, 1} with d = 1: every output is one x value exactly
+    # Q8_0 weights in {0, 1} with d = 1: every output of the fp32 kernel is
+    # one x value exactly (the integer-dot kernels round x to 2^-23 of a
+    # unit's max |x| and are checked to tolerance elsewhere)
     M, K = 300, 1024
     rng = np.random.default_rng(3)
     W = np.zeros((M, K // 32, 34), np.uint8)
@@ -140,7 +196,7 @@ def test_matvec_exact_one_hot():
     for m, j in enumerate(cols):
         W[m, j // 32, 2 + j % 32] = 1
     x = rng.standard_normal(K).astype(np.float32)
-    assert np.array_equal(gpu_matvec(W.reshape(M, -1), fm.Q8_0, M, K, x), x[cols])
+    assert np.array_equal(gpu_matvec(W.reshape(M, -1), fm.Q8_0, M, K, x, tb.TBQ_MV_FMA), x[cols])
 
 
 def test_matvec_rejects_bad_input():

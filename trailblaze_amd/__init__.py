@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(HERE, "libtbq.so")
 
 TBQ_MOE_FP32 = 0
 TBQ_MOE_BF16 = 1
-TBQ_MV_AUTO, TBQ_MV_FMA, TBQ_MV_INTDOT = 0, 1, 2
+TBQ_MV_AUTO, TBQ_MV_FMA, TBQ_MV_INTDOT, TBQ_MV_KQ = 0, 1, 2, 3
 
 # (name, restype, argtypes) for every symbol declared in include/tbq.h and
 # include/tb_gguf_dequant.h.

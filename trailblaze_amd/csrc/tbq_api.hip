@@ -129,13 +129,21 @@ static int check_matvec(const void *W, int qt, int M, int K, const float *x, con
 int tbq_matvec_variant(const void *W, int qt, int M, int K, const float *x, float *y, int variant, void *s) {
     if (!ensure_init()) return 0;
     if (!check_matvec(W, qt, M, K, x, y)) return 0;
-    if (variant < TBQ_MV_AUTO || variant > TBQ_MV_INTDOT) return fail("tbq_matvec_variant: unknown variant %d", variant);
+    if (variant < TBQ_MV_AUTO || variant > TBQ_MV_KQ) return fail("tbq_matvec_variant: unknown variant %d", variant);
     if (M == 0) return 1;
-    if (variant != TBQ_MV_FMA && qt == QT_Q4_K) {
+    // Q4_K rows of up to 64 units keep x's digits in registers in the
+    // specialised kernel; everything else integer-dot goes to the shared one.
+    const bool q4k_special = qt == QT_Q4_K && (variant == TBQ_MV_INTDOT || (variant == TBQ_MV_AUTO && K <= 4096));
+    if (q4k_special) {
         hipError_t e = launch_matvec_q4k(W, M, K, x, y, S(s), g_cu);
+        if (e != hipErrorNotSupported) return hip_ok(e, "matvec launch (Q4_K int-dot)");
+    }
+    if (variant == TBQ_MV_AUTO || variant == TBQ_MV_KQ) {
+        hipError_t e = launch_matvec_kq(qt, W, M, K, x, y, S(s), g_cu);
         if (e != hipErrorNotSupported) return hip_ok(e, "matvec launch (int-dot)");
     }
-    if (variant == TBQ_MV_INTDOT) return fail("tbq_matvec_variant: no int-dot kernel for qtype %d K=%d", qt, K);
+    if (variant == TBQ_MV_INTDOT || variant == TBQ_MV_KQ)
+        return fail("tbq_matvec_variant: no int-dot kernel for qtype %d K=%d", qt, K);
     if ((size_t)K * 4 + (size_t)(K / 16) * 4 > 64 * 1024)
         return fail("K=%d exceeds the LDS-resident x limit of the fma kernel", K);
     return hip_ok(launch_matvec_generic(qt, W, M, K, x, y, S(s), g_cu), "matvec launch");

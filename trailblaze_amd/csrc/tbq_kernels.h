@@ -23,6 +23,7 @@ hipError_t launch_dequant(int qt, const void *W, long long nweights, float *out,
 hipError_t launch_matvec_generic(int qt, const void *W, int M, int K, const float *x, float *y,
                                  hipStream_t s, int n_cu);
 hipError_t launch_matvec_q4k(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu);
+hipError_t launch_matvec_kq(int qt, const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu);
 hipError_t launch_expf(const float *in, float *out, long long n, hipStream_t s);
 hipError_t launch_route(const float *xn, const float *router, const float *bias, int T, int H, int E,
                         int top_k, int *sel_idx, float *sel_w, hipStream_t st);

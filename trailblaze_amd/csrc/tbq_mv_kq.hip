@@ -1,0 +1,720 @@
+// tbq_mv_kq.hip -- decode matvec y = W x on integer dot products for the
+// block formats Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 and Q8_K
+// (tb_gguf_dequant_matvec, layer4/tb_gguf.c:376-419; block layouts
+// layer4/tb_gguf.c:110-288).
+//
+// x representation.  x is cut into units of 64 elements.  Each unit gets one
+// power-of-two scale 2^s (max |x| of the unit maps just below 2^22) and
+// X_i = rint(x_i * 2^s) is written in balanced base 256,
+//     X = 65536*h + 256*m + l,   h, m, l signed bytes,
+// so sum_i q_i x_i over any run of a unit is 2^-s * (65536*sum q h +
+// 256*sum q m + sum q l), where every inner sum is an exact v_dot4_i32_i8
+// chain over weight bytes.  x is represented to 2^-23 of the unit's max |x|,
+// which keeps the matvec within ~1e-7 relative of the reference's fp32 sum
+// (the parity bound is 1e-5).
+//
+// Weights.  A lane unpacks its unit's quants into bytes (4 per dword) in one
+// of two element orders, and the digits of x are staged in the same order:
+//   PAIR     dword 2k holds elements 8k+{0,2,4,6}, dword 2k+1 holds 8k+{1,3,5,7}
+//            (nibble-packed and 2-bit-packed formats: low/high nibbles, and
+//            v_perm of a dword with itself shifted by 4 for 2-bit fields);
+//   NATURAL  dword t holds elements 4t..4t+3 (int8 formats).
+// Dwords 4g..4g+3 always hold the unit's 16-element group g.  Per-group
+// integer scales multiply the digit sums in integer arithmetic
+// (v_mad_i32_i24), so each unit converts to fp32 once; offsets and mins are
+// applied with the fp32 group sums of x.
+//
+// Work split.  Lane = one unit of a row, LPR lanes per row (a row slice of
+// <= 64 units); rows longer than 64 units are split over S waves of the
+// workgroup whose partial sums meet in LDS.  A lane keeps its unit's digits
+// in VGPRs for every row it visits; rows are grid-strided, and the weights
+// of the next pass are loaded before the current pass is reduced.
+#include "tbq_kernels.h"
+#include "tbq_kquant.hpp"
+
+
+namespace tbq {
+
+constexpr int KQ_UNIT = 52;   // LDS dwords per unit: 3 digit planes x 16 + 2^-s + pad
+
+// Launch shape: KQ_NW waves per workgroup (split into slices for K > 4096;
+// KQ_G3 row groups of 3 slices for K <= 12288), at most KQ_WG_PER_CU
+// workgroups per CU, KQ_R rows per wave and pass, KQ_D passes prefetched.
+#ifndef KQ_NW
+#define KQ_NW 16
+#endif
+#ifndef KQ_R
+#define KQ_R 1
+#endif
+#ifndef KQ_D
+#define KQ_D 1
+#endif
+#ifndef KQ_G3
+#define KQ_G3 4
+#endif
+#ifndef KQ_WG_PER_CU
+#define KQ_WG_PER_CU 1
+#endif
+
+// The unit's digits in registers.
+struct KqX {
+    uint32_t h[16], m[16], l[16];
+    float isc;       // 2^-s
+    float gs[4];     // fp32 sums of x over the unit's 16-element groups
+};
+
+__device__ __forceinline__ uint32_t bfe(uint32_t v, int off, int w) { return __builtin_amdgcn_ubfe(v, off, w); }
+__device__ __forceinline__ int sbfe(uint32_t v, int off, int w) { return __builtin_amdgcn_sbfe((int)v, off, w); }
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+__device__ __forceinline__ uint32_t mulu24(uint32_t a, uint32_t b) { return (uint32_t)__umul24(a, b); }
+
+// N little-endian dwords starting at a 2-byte-aligned address p, read with
+// 4-byte-aligned loads and realigned in registers (v_alignbyte_b32 with a
+// per-lane shift of 0 or 2 bytes): a load that is not 4-byte aligned costs
+// about 1.5x the HBM time of an aligned one on this part, whatever its
+// width.  The reads cover [p - 2, p + 4N + 2) when p is 2 mod 4 and exactly
+// [p, p + 4N) otherwise, so a run that ends where its block ends (always
+// 4-byte aligned in the layouts below when p is) never reads past it.
+template <int N>
+__device__ __forceinline__ void ld_dw(const uint8_t *p, uint32_t *out) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t sh = (uint32_t)(a & 3u);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(a - sh);
+    uint32_t w[N + 1];
+    int i = 0;
+    for (; i + 4 <= N; i += 4) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(q + i);
+        w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+    }
+    for (; i + 2 <= N; i += 2) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(q + i);
+        w[i] = v.x; w[i + 1] = v.y;
+    }
+    for (; i < N; i++) w[i] = q[i];
+    w[N] = *reinterpret_cast<const uint32_t *>((a + 4 * N - 1) & ~(uintptr_t)3);
+#pragma unroll
+    for (int j = 0; j < N; j++) out[j] = __builtin_amdgcn_alignbyte(w[j + 1], w[j], sh);
+}
+
+// ---------------------------------------------------------------------------
+// Staging: NT threads write the digits of all U units into LDS, in two
+// phases so that x's loads can be issued before a kernel's weight loads
+// (the memory counter is in order: data loaded first can be waited for
+// alone).  Task (unit u, dword t) handles the 4 elements of dword t; the 16
+// tasks of a unit are 16 consecutive lanes (max |x| over the unit by DPP),
+// the 4 tasks of a group are a DPP quad (group sum).  Each thread handles at
+// most MAXT tasks (MAXT * NT >= 16 * U).
+// ---------------------------------------------------------------------------
+template <int NT, bool PAIR, int MAXT>
+struct KqStager {
+    float e[MAXT][4];
+
+    // PAIR dword t = 2k + par holds elements 8k + par + {0, 2, 4, 6}: four
+    // loads at a per-lane base, no selection after the data arrives.
+    // Loads are unconditional (tasks past the end re-read the last one and
+    // are never stored), so no branch hides them from the wait counter.
+    __device__ __forceinline__ void load(const float *__restrict__ x, int U) {
+#pragma unroll
+        for (int i = 0; i < MAXT; i++) {
+            const int task = min(i * NT + (int)threadIdx.x, U * 16 - 1);
+            const int u = task >> 4, t = task & 15;
+            if constexpr (PAIR) {
+                const float *p = x + 64 * u + 8 * (t >> 1) + (t & 1);
+#pragma unroll
+                for (int j = 0; j < 4; j++) e[i][j] = p[2 * j];
+            } else {
+                const float4 a = *reinterpret_cast<const float4 *>(x + 64 * u + 4 * t);
+                e[i][0] = a.x; e[i][1] = a.y; e[i][2] = a.z; e[i][3] = a.w;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(int U, uint32_t *xd, float *gs) const {
+#pragma unroll
+        for (int i = 0; i < MAXT; i++) {
+            const int task = i * NT + (int)threadIdx.x;
+            const bool ok = task < U * 16;        // uniform over each 16-lane row
+            const int u = task >> 4, t = task & 15;
+            const float *e = this->e[i];
+            float mx = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
+            float sm = (e[0] + e[1]) + (e[2] + e[3]);
+            mx = fmaxf(mx, dpp_f32<DPP_QXOR1>(mx));
+            mx = fmaxf(mx, dpp_f32<DPP_QXOR2>(mx));
+            mx = fmaxf(mx, dpp_f32<DPP_HALF_MIRROR>(mx));
+            mx = fmaxf(mx, dpp_f32<DPP_MIRROR>(mx));
+            sm += dpp_f32<DPP_QXOR1>(sm);
+            sm += dpp_f32<DPP_QXOR2>(sm);
+            int ex = 0;
+            frexpf(mx, &ex);
+            int s = mx > 0.f ? 22 - ex : 0;
+            s = s > 126 ? 126 : (s < -126 ? -126 : s);
+            const float sc = ldexpf(1.f, s);
+            uint32_t dh = 0, dm = 0, dl = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int X = (int)rintf(e[b] * sc);
+                const int l = (int)(int8_t)(X & 0xFF);
+                const int X1 = (X - l) >> 8;
+                const int m = (int)(int8_t)(X1 & 0xFF);
+                const int h = (X1 - m) >> 8;
+                dh |= (uint32_t)(h & 0xFF) << (8 * b);
+                dm |= (uint32_t)(m & 0xFF) << (8 * b);
+                dl |= (uint32_t)(l & 0xFF) << (8 * b);
+            }
+            if (ok) {
+                uint32_t *unit = xd + u * KQ_UNIT;
+                unit[t] = dh;
+                unit[16 + t] = dm;
+                unit[32 + t] = dl;
+                if (t == 0) unit[48] = __builtin_bit_cast(uint32_t, ldexpf(1.f, -s));
+                if ((t & 3) == 0) gs[4 * u + (t >> 2)] = sm;
+            }
+        }
+    }
+};
+
+__device__ __forceinline__ void kq_xload(const uint32_t *xd, const float *gs, int u, KqX &x) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(xd + u * KQ_UNIT);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 a = p[i], b = p[4 + i], c = p[8 + i];
+        x.h[4 * i] = a.x; x.h[4 * i + 1] = a.y; x.h[4 * i + 2] = a.z; x.h[4 * i + 3] = a.w;
+        x.m[4 * i] = b.x; x.m[4 * i + 1] = b.y; x.m[4 * i + 2] = b.z; x.m[4 * i + 3] = b.w;
+        x.l[4 * i] = c.x; x.l[4 * i + 1] = c.y; x.l[4 * i + 2] = c.z; x.l[4 * i + 3] = c.w;
+    }
+    x.isc = __builtin_bit_cast(float, xd[u * KQ_UNIT + 48]);
+    const float4 g = *reinterpret_cast<const float4 *>(gs + 4 * u);
+    x.gs[0] = g.x; x.gs[1] = g.y; x.gs[2] = g.z; x.gs[3] = g.w;
+}
+
+// Digit sums of weight dwords q[0..N) against digit dwords T0..T0+N.
+template <int N>
+__device__ __forceinline__ void kq_dots(const uint32_t *q, const KqX &x, int T0, int &ah, int &am, int &al) {
+#pragma unroll
+    for (int j = 0; j < N; j++) {
+        ah = __builtin_amdgcn_sdot4((int)q[j], (int)x.h[T0 + j], ah, false);
+        am = __builtin_amdgcn_sdot4((int)q[j], (int)x.m[T0 + j], am, false);
+        al = __builtin_amdgcn_sdot4((int)q[j], (int)x.l[T0 + j], al, false);
+    }
+}
+
+// Integer-scaled digit accumulators -> fp32: 65536*H + 256*Mm + L.
+__device__ __forceinline__ float kq_combine(int H, int Mm, int L) {
+    return fmaf((float)H, 65536.f, fmaf((float)Mm, 256.f, (float)L));
+}
+
+// 2-bit fields of one dword (16 elements, 4 per byte at bits 0-1, 2-3, 4-5,
+// 6-7) as PAIR-ordered bytes: q[0] = [e0,e2,e4,e6], q[1] = [e1,e3,e5,e7],
+// q[2] = [e8,e10,e12,e14], q[3] = [e9,e11,e13,e15].  v_perm of Q with Q>>4
+// puts the fields of elements 4j and 4j+2 (4j+1 and 4j+3) at bits 0-1
+// (2-3) of consecutive bytes.
+__device__ __forceinline__ void unpack2(uint32_t Q, uint32_t *q) {
+    const uint32_t S = Q >> 4;
+    const uint32_t R0 = __builtin_amdgcn_perm(S, Q, 0x05010400u);
+    const uint32_t R1 = __builtin_amdgcn_perm(S, Q, 0x07030602u);
+    q[0] = R0 & 0x03030303u;
+    q[1] = (R0 >> 2) & 0x03030303u;
+    q[2] = R1 & 0x03030303u;
+    q[3] = (R1 >> 2) & 0x03030303u;
+}
+
+// Bits 0,2,4,6 (even) or 1,3,5,7 (odd) of byte b moved to bit SH of bytes
+// 0..3.  One multiply spreads the four bits; its cross terms only collide at
+// positions whose carries land on bits the mask clears.
+template <int SH>
+__device__ __forceinline__ uint32_t spread_even(uint32_t b) {
+    return mulu24(b & 0x55u, (1u << SH) | (1u << (SH + 6)) | (1u << (SH + 12)) | (1u << (SH + 18)));
+}
+template <int SH>
+__device__ __forceinline__ uint32_t spread_odd(uint32_t b) {
+    return mulu24(b & 0xAAu, (1u << (SH - 1)) | (1u << (SH + 5)) | (1u << (SH + 11)) | (1u << (SH + 17)));
+}
+
+// ---------------------------------------------------------------------------
+// Per-format unit loads and dots.  Unit u of a row: super-block u/4, weights
+// 64*(u%4)..+63 (256-weight formats); blocks 2u, 2u+1 (32-weight formats).
+// ---------------------------------------------------------------------------
+template <int QT> struct KqFmt;
+
+// Q2_K (layer4/tb_gguf.c:210-225): sc[16]@0 (scale lo nibble, min hi
+// nibble per 16 weights), qs[64]@16 (weight i at bits 2(i&3) of qs[i>>2]),
+// d@80, dmin@82.  w = fl(fl(d*sc)*q) - fl(dmin*m).
+template <> struct KqFmt<QT_Q2_K> {
+    static constexpr bool PAIR = true;
+    struct Unit { uint4 qs; uint32_t sc, dd; };
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 84;
+        const int p = u & 3;
+        w.qs = ld_u128(b + 16 + 16 * p);
+        w.sc = ld_u32(b + 4 * p);
+        w.dd = ld_u32(b + 80);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x) {
+        const uint32_t qv[4] = {w.qs.x, w.qs.y, w.qs.z, w.qs.w};
+        int H = 0, Mm = 0, L = 0;
+        float mn = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            uint32_t q[4];
+            unpack2(qv[g], q);
+            int ah = 0, am = 0, al = 0;
+            kq_dots<4>(q, x, 4 * g, ah, am, al);
+            const int s = (int)bfe(w.sc, 8 * g, 4), m = (int)bfe(w.sc, 8 * g + 4, 4);
+            H = mad24(s, ah, H);
+            Mm = mad24(s, am, Mm);
+            L = mad24(s, al, L);
+            mn = fmaf((float)m, x.gs[g], mn);
+        }
+        const float d = f16_ref(w.dd & 0xFFFFu), dmin = f16_ref(w.dd >> 16);
+        return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
+    }
+};
+
+// Q3_K (layer4/tb_gguf.c:230-257): hmask[32]@0 (weight i: bit i&7 of
+// hmask[i>>3]), qs[64]@32 (2-bit, as Q2_K), sc[12]@96, d@108.  Group j of
+// 16 uses scale slot j&7: lo4 from sc[slot>>1] nibble slot&1, hi2 from
+// sc[8+(slot>>2)] bits 2(slot&3); S = d*((lo4|hi2<<4)-32); w = S*(q3-4).
+template <> struct KqFmt<QT_Q3_K> {
+    static constexpr bool PAIR = true;
+    struct Unit { uint4 qs; uint2 hm; uint32_t lo; uint2 hi; };
+    // 110-byte blocks: every other block starts 2 mod 4, so runs go through
+    // ld_dw; d is a naturally aligned 16-bit load
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 110;
+        const int p = u & 3;
+        uint32_t t[4];
+        ld_dw<4>(b + 32 + 16 * p, t);
+        w.qs = make_uint4(t[0], t[1], t[2], t[3]);
+        ld_dw<2>(b + 8 * p, t);
+        w.hm = make_uint2(t[0], t[1]);
+        ld_dw<1>(b + 96, &w.lo);                 // sc[0..3]
+        ld_dw<1>(b + 104, &w.hi.x);              // sc[8..11]
+        w.hi.y = (uint32_t)ld_u16(b + 108) << 16; // d in the high half
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
+        const int p1 = u & 1;   // groups 4p..4p+3 use slots 4*(p&1)..+3
+        const uint32_t qv[4] = {w.qs.x, w.qs.y, w.qs.z, w.qs.w};
+        const uint32_t hi2b = bfe(w.hi.x, 8 * p1, 8);        // sc[8 + (p&1)]
+        int H = 0, Mm = 0, L = 0;
+        float mn = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            uint32_t q[4];
+            unpack2(qv[g], q);
+            const uint32_t hv = ((g < 2) ? w.hm.x : w.hm.y) >> (16 * (g & 1));   // bytes 2g, 2g+1
+            const uint32_t h1 = hv >> 8;
+            q[0] = (spread_even<2>(hv) & 0x04040404u) | q[0];
+            q[1] = (spread_odd<2>(hv) & 0x04040404u) | q[1];
+            q[2] = (spread_even<2>(h1) & 0x04040404u) | q[2];
+            q[3] = (spread_odd<2>(h1) & 0x04040404u) | q[3];
+            int ah = 0, am = 0, al = 0;
+            kq_dots<4>(q, x, 4 * g, ah, am, al);
+            const int lo4 = (int)bfe(w.lo, 16 * p1 + 4 * g, 4);
+            const int hi2 = (int)bfe(hi2b, 2 * g, 2);
+            const int s = (lo4 | (hi2 << 4)) - 32;
+            H = mad24(s, ah, H);
+            Mm = mad24(s, am, Mm);
+            L = mad24(s, al, L);
+            mn = fmaf((float)s, x.gs[g], mn);
+        }
+        const float d = f16_ref(w.hi.y >> 16);
+        return d * fmaf(x.isc, kq_combine(H, Mm, L), -4.f * mn);
+    }
+};
+
+// Q4_K (layer4/tb_gguf.c:148-180): d@0, dmin@2, sc[12]@4, qs[128]@16.
+// Sub-block j<4: scale sc[j]&63, min sc[j+4]&63; j>=4: scale sc[j+4]&63,
+// min byte 12+j of the block (qs[j-4]).
+template <> struct KqFmt<QT_Q4_K> {
+    static constexpr bool PAIR = true;
+    struct Unit { uint4 hdr, q0, q1; uint32_t mind; };
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 144;
+        const int p = u & 3;
+        w.hdr = ld_u128(b);
+        w.q0 = ld_u128(b + 16 + 32 * p);
+        w.q1 = ld_u128(b + 32 + 32 * p);
+        w.mind = ld_u32(b + 16);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
+        const int p = u & 3;
+        const uint32_t sw = p < 2 ? w.hdr.y : w.hdr.w;
+        const uint32_t mw = p < 2 ? w.hdr.z : w.mind;
+        const int sh = 16 * (p & 1);
+        const uint32_t qv[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        int H = 0, Mm = 0, L = 0;
+        float mn = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            uint32_t q[8];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                q[2 * k] = qv[4 * j + k] & 0x0F0F0F0Fu;
+                q[2 * k + 1] = (qv[4 * j + k] >> 4) & 0x0F0F0F0Fu;
+            }
+            int ah = 0, am = 0, al = 0;
+            kq_dots<8>(q, x, 8 * j, ah, am, al);
+            const int s = (int)bfe(sw, sh + 8 * j, 6), m = (int)bfe(mw, sh + 8 * j, 6);
+            H = mad24(s, ah, H);
+            Mm = mad24(s, am, Mm);
+            L = mad24(s, al, L);
+            mn = fmaf((float)m, x.gs[2 * j] + x.gs[2 * j + 1], mn);
+        }
+        const float d = f16_ref(w.hdr.x & 0xFFFFu), dmin = f16_ref(w.hdr.x >> 16);
+        return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
+    }
+};
+
+// Q5_K (layer4/tb_gguf.c:262-279 with q4_k_unpack_scales :122-145): d@0,
+// dmin@2, sc[12]@4, qh[32]@16 (weight i: bit i&7 of qh[i>>3]), qs[128]@48.
+// j<4: scale sc[j]&63, min sc[j+4]&63; j>=4, k=j-4: scale
+// (sc[k]>>6)|((sc[k+8]&15)<<2), min (sc[k+4]>>6)|((sc[k+12]&15)<<2) where
+// sc[12..15] are qh[0..3].
+template <> struct KqFmt<QT_Q5_K> {
+    static constexpr bool PAIR = true;
+    struct Unit { uint4 hdr, q0, q1; uint32_t qh0; uint2 qh; };
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 176;
+        const int p = u & 3;
+        w.hdr = ld_u128(b);
+        w.qh0 = ld_u32(b + 16);
+        w.qh = *reinterpret_cast<const uint2 *>(b + 16 + 8 * p);
+        w.q0 = ld_u128(b + 48 + 32 * p);
+        w.q1 = ld_u128(b + 64 + 32 * p);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
+        const int p = u & 3;
+        const uint32_t qv[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        int H = 0, Mm = 0, L = 0;
+        float mn = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            uint32_t q[8];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int kk = 4 * j + k;                    // qs dword of the unit, qh byte kk
+                const uint32_t hb = bfe(kk < 4 ? w.qh.x : w.qh.y, 8 * (kk & 3), 8);
+                q[2 * k] = (spread_even<4>(hb) & 0x10101010u) | (qv[kk] & 0x0F0F0F0Fu);
+                q[2 * k + 1] = (spread_odd<4>(hb) & 0x10101010u) | ((qv[kk] >> 4) & 0x0F0F0F0Fu);
+            }
+            int ah = 0, am = 0, al = 0;
+            kq_dots<8>(q, x, 8 * j, ah, am, al);
+            int s, m;
+            const int jj = 2 * p + j;   // sub-block within the super-block
+            if (jj < 4) {
+                s = (int)bfe(w.hdr.y, 8 * jj, 6);
+                m = (int)bfe(w.hdr.z, 8 * jj, 6);
+            } else {
+                const int k = jj - 4;   // 0..3
+                s = (int)(bfe(w.hdr.y, 8 * k + 6, 2) | (bfe(w.hdr.w, 8 * k, 4) << 2));
+                m = (int)(bfe(w.hdr.z, 8 * k + 6, 2) | (bfe(w.qh0, 8 * k, 4) << 2));
+            }
+            H = mad24(s, ah, H);
+            Mm = mad24(s, am, Mm);
+            L = mad24(s, al, L);
+            mn = fmaf((float)m, x.gs[2 * j] + x.gs[2 * j + 1], mn);
+        }
+        const float d = f16_ref(w.hdr.x & 0xFFFFu), dmin = f16_ref(w.hdr.x >> 16);
+        return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
+    }
+};
+
+// Q6_K (layer4/tb_gguf.c:190-204): ql[128]@0 (weight i: nibble i&1 of
+// ql[i>>1]), qh[64]@128 (bits 2(i&3) of qh[i>>2]), int8 sc[16]@192, d@208.
+// w = fl(d*sc[i>>4]) * (q - 32).
+template <> struct KqFmt<QT_Q6_K> {
+    static constexpr bool PAIR = true;
+    struct Unit { uint4 ql0, ql1, qh; uint32_t sc, d; };
+    // 210-byte blocks: every other block starts 2 mod 4 (ld_dw)
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 210;
+        const int p = u & 3;
+        uint32_t t[8];
+        ld_dw<8>(b + 32 * p, t);
+        w.ql0 = make_uint4(t[0], t[1], t[2], t[3]);
+        w.ql1 = make_uint4(t[4], t[5], t[6], t[7]);
+        ld_dw<4>(b + 128 + 16 * p, t);
+        w.qh = make_uint4(t[0], t[1], t[2], t[3]);
+        ld_dw<1>(b + 192 + 4 * p, &w.sc);
+        w.d = ld_u16(b + 208);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
+        const uint32_t qv[8] = {w.ql0.x, w.ql0.y, w.ql0.z, w.ql0.w, w.ql1.x, w.ql1.y, w.ql1.z, w.ql1.w};
+        const uint32_t hv[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+        int H = 0, Mm = 0, L = 0;
+        float mn = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            uint32_t q[4];
+            const uint32_t QH = hv[g], S = QH >> 4;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const int k = 2 * g + c;   // ql dword k: weights 8k..8k+7; qh bytes 2k, 2k+1
+                const uint32_t R = __builtin_amdgcn_perm(S, QH, c ? 0x07030602u : 0x05010400u);
+                q[2 * c] = ((R << 4) & 0x30303030u) | (qv[k] & 0x0F0F0F0Fu);
+                q[2 * c + 1] = ((R << 2) & 0x30303030u) | ((qv[k] >> 4) & 0x0F0F0F0Fu);
+            }
+            int ah = 0, am = 0, al = 0;
+            kq_dots<4>(q, x, 4 * g, ah, am, al);
+            const int s = sbfe(w.sc, 8 * g, 8);
+            H = mad24(s, ah, H);
+            Mm = mad24(s, am, Mm);
+            L = mad24(s, al, L);
+            mn = fmaf((float)s, x.gs[g], mn);
+        }
+        const float d = f16_ref(w.d);
+        return d * fmaf(x.isc, kq_combine(H, Mm, L), -32.f * mn);
+    }
+};
+
+// Q8_0 (layer4/tb_gguf.c:183-187): d@0, int8 qs[32]@2; w = d*q.
+template <> struct KqFmt<QT_Q8_0> {
+    static constexpr bool PAIR = false;
+    struct Unit { uint4 a0, a1, b0, b1; uint32_t d0, d1; };
+    // unit = 68 bytes (4-byte aligned when the row is): block 0's quants
+    // start 2 mod 4 (ld_dw), block 1's are aligned
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)u * 68;
+        uint32_t t[8];
+        w.d0 = ld_u16(b);
+        ld_dw<8>(b + 2, t);
+        w.a0 = make_uint4(t[0], t[1], t[2], t[3]);
+        w.a1 = make_uint4(t[4], t[5], t[6], t[7]);
+        w.d1 = ld_u16(b + 34);
+        ld_dw<8>(b + 36, t);
+        w.b0 = make_uint4(t[0], t[1], t[2], t[3]);
+        w.b1 = make_uint4(t[4], t[5], t[6], t[7]);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
+        const uint32_t q0[8] = {w.a0.x, w.a0.y, w.a0.z, w.a0.w, w.a1.x, w.a1.y, w.a1.z, w.a1.w};
+        const uint32_t q1[8] = {w.b0.x, w.b0.y, w.b0.z, w.b0.w, w.b1.x, w.b1.y, w.b1.z, w.b1.w};
+        int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
+        kq_dots<8>(q0, x, 0, h0, m0, l0);
+        kq_dots<8>(q1, x, 8, h1, m1, l1);
+        const float f0 = f16_ref(w.d0) * kq_combine(h0, m0, l0);
+        return fmaf(f16_ref(w.d1), kq_combine(h1, m1, l1), f0) * x.isc;
+    }
+};
+
+// Q4_0 (layer4/tb_gguf.c:110-118): d@0, qs[16]@2; weight 2i = low nibble of
+// qs[i], 2i+1 = high nibble; w = d*(q-8).
+template <> struct KqFmt<QT_Q4_0> {
+    static constexpr bool PAIR = true;
+    struct Unit { uint4 a, b; uint32_t d0, d1; };
+    // unit = 36 bytes: block 0's quants start 2 mod 4 when the unit is
+    // aligned (ld_dw)
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)u * 36;
+        uint32_t t[4];
+        w.d0 = ld_u16(b);
+        ld_dw<4>(b + 2, t);
+        w.a = make_uint4(t[0], t[1], t[2], t[3]);
+        w.d1 = ld_u16(b + 18);
+        ld_dw<4>(b + 20, t);
+        w.b = make_uint4(t[0], t[1], t[2], t[3]);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
+        float r = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint4 v = j ? w.b : w.a;
+            const uint32_t qv[4] = {v.x, v.y, v.z, v.w};
+            uint32_t q[8];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                q[2 * k] = qv[k] & 0x0F0F0F0Fu;
+                q[2 * k + 1] = (qv[k] >> 4) & 0x0F0F0F0Fu;
+            }
+            int ah = 0, am = 0, al = 0;
+            kq_dots<8>(q, x, 8 * j, ah, am, al);
+            const float sx = x.gs[2 * j] + x.gs[2 * j + 1];
+            r = fmaf(f16_ref(j ? w.d1 : w.d0), fmaf(x.isc, kq_combine(ah, am, al), -8.f * sx), r);
+        }
+        return r;
+    }
+};
+
+// Q8_K (layer4/tb_gguf.c:283-288): f32 d@0, int8 qs[256]@4; w = d*q.
+template <> struct KqFmt<QT_Q8_K> {
+    static constexpr bool PAIR = false;
+    struct Unit { uint4 q[4]; uint32_t d; };
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 292;
+        const int p = u & 3;
+        w.d = ld_u32(b);
+#pragma unroll
+        for (int i = 0; i < 4; i++) w.q[i] = ld_u128(b + 4 + 64 * p + 16 * i);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
+        uint32_t q[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            q[4 * i] = w.q[i].x; q[4 * i + 1] = w.q[i].y; q[4 * i + 2] = w.q[i].z; q[4 * i + 3] = w.q[i].w;
+        }
+        int ah = 0, am = 0, al = 0;
+        kq_dots<16>(q, x, 0, ah, am, al);
+        return __builtin_bit_cast(float, w.d) * x.isc * kq_combine(ah, am, al);
+    }
+};
+
+// Uniform entry for formats whose dot does not need the unit index.
+template <int QT>
+__device__ __forceinline__ float kq_dot(const typename KqFmt<QT>::Unit &w, const KqX &x, int u) {
+    if constexpr (QT == QT_Q2_K) return KqFmt<QT>::dot(w, x);
+    else return KqFmt<QT>::dot(w, x, u);
+}
+
+// ---------------------------------------------------------------------------
+// The kernel.  Wave w of the workgroup: row slice s = w % S (units
+// s*LPR .. s*LPR+LPR-1), row group g = w / S.  Workgroup b owns rows
+// [b*rpw, min((b+1)*rpw, M)); one pass covers RWG = G*R*RPP of them (RPP =
+// 64/LPR rows per wave per step p < R), so a wave has R rows' weights in
+// flight per pass, and the weights of the next D passes are loaded before
+// the current pass is reduced.
+// ---------------------------------------------------------------------------
+template <int QT, int LPR, int S, int G, int R, int D>
+__global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict__ W, int M, int K, long long rb,
+                                                      const float *__restrict__ x, float *__restrict__ y, int rpw) {
+    using F = KqFmt<QT>;
+    constexpr int NT = S * G * 64, RPP = 64 / LPR, RW = R * RPP, RWG = G * RW;
+    constexpr int MAXT = (16 * 64 * S + NT - 1) / NT;   // U <= 64 * S
+    extern __shared__ uint32_t smem[];
+    const int U = K / 64;
+    uint32_t *xd = smem;
+    float *gs = reinterpret_cast<float *>(smem + U * KQ_UNIT);
+    float *red = gs + 4 * U;   // [2][G][S][RW], S > 1 only
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int s = wave % S, g = wave / S;
+    const int lr = lane % LPR, rsub = lane / LPR;
+    const int u = s * LPR + lr;
+    const bool lv = u < U;
+    const int row0 = blockIdx.x * rpw + g * RW + rsub;   // row of pass 0, step 0
+    const int rend = min((blockIdx.x + 1) * rpw, M);
+    const int npass = (rpw + RWG - 1) / RWG;
+
+    // Every load below is unconditional: rows past the workgroup's last
+    // re-read its last row and lanes past the row's last unit re-read unit
+    // 0; their results are discarded.  A load under a branch would make the
+    // compiler wait for all outstanding loads where the branch rejoins,
+    // which serialises the prefetch with this pass's arithmetic.
+    const int ul = lv ? u : 0;
+    typename F::Unit buf[D + 1][R];   // buf[0] = this pass, buf[i] = pass + i
+    auto load = [&](typename F::Unit *dst, int pass) {
+#pragma unroll
+        for (int p = 0; p < R; p++) {
+            const int r = min(row0 + pass * RWG + p * RPP, rend - 1);
+            F::load(W + (long long)r * rb, ul, dst[p]);
+        }
+    };
+    KqStager<NT, F::PAIR, MAXT> xs;
+    xs.load(x, U);
+    __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
+#pragma unroll
+    for (int i = 0; i < D; i++) load(buf[i], i);
+    xs.store(U, xd, gs);
+    __syncthreads();
+    KqX xr;
+    kq_xload(xd, gs, ul, xr);
+
+    for (int pass = 0; pass < npass; ++pass) {
+        load(buf[D], pass + D);
+        float acc[R];
+#pragma unroll
+        for (int p = 0; p < R; p++) {
+            const int r = row0 + pass * RWG + p * RPP;
+            const float v = kq_dot<QT>(buf[0][p], xr, ul);
+            acc[p] = group_sum<LPR>((r < rend && lv) ? v : 0.f);
+        }
+        if constexpr (S == 1) {
+#pragma unroll
+            for (int p = 0; p < R; p++) {
+                const int r = row0 + pass * RWG + p * RPP;
+                if (lr == 0 && r < rend) y[r] = acc[p];
+            }
+        } else {
+            float *rbuf = red + (pass & 1) * (G * S * RW);
+#pragma unroll
+            for (int p = 0; p < R; p++)
+                if (lr == 0) rbuf[(g * S + s) * RW + p * RPP + rsub] = acc[p];
+            __syncthreads();
+            if (s == 0) {
+#pragma unroll
+                for (int p = 0; p < R; p++) {
+                    const int r = row0 + pass * RWG + p * RPP;
+                    if (lr == 0 && r < rend) {
+                        float t = rbuf[(g * S) * RW + p * RPP + rsub];
+#pragma unroll
+                        for (int ss = 1; ss < S; ss++) t += rbuf[(g * S + ss) * RW + p * RPP + rsub];
+                        y[r] = t;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < D; i++)
+#pragma unroll
+            for (int p = 0; p < R; p++) buf[i][p] = buf[i + 1][p];
+    }
+}
+
+template <int QT, int LPR, int S, int G, int R, int D>
+static hipError_t launch_kq(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int grid,
+                            int rpw) {
+    constexpr int RPP = 64 / LPR;
+    const int U = K / 64;
+    const long long rb = (long long)(K / block_weights(QT)) * block_bytes(QT);
+    const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (S > 1 ? (size_t)2 * G * S * R * RPP * 4 : 0);
+    hipLaunchKernelGGL((k_mv_kq<QT, LPR, S, G, R, D>), dim3(grid), dim3(S * G * 64), lds, st,
+                       (const uint8_t *)W, M, K, rb, x, y, rpw);
+    return hipGetLastError();
+}
+
+// Launch shape for one row slice width: G row groups of S waves, at most
+// KQ_WG_PER_CU workgroups per CU (each stages x once), rows split evenly over
+// the workgroups; each wave streams R = KQ_R rows per pass with the next
+// KQ_D passes' weights in flight.
+template <int QT, int LPR, int S, int G>
+static hipError_t launch_kq_shape(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu) {
+    constexpr int RPP = 64 / LPR, R = KQ_R, D = KQ_D;
+    const long long cap = (long long)n_cu * KQ_WG_PER_CU;
+    const long long need = ((long long)M + G * R * RPP - 1) / (G * R * RPP);
+    const int grid = (int)(need < cap ? need : cap);
+    const int rpw = (M + grid - 1) / grid;
+    return launch_kq<QT, LPR, S, G, R, D>(W, M, K, x, y, st, grid, rpw);
+}
+
+template <int QT>
+static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu) {
+    const int U = K / 64;
+    constexpr int NW = KQ_NW;
+    if (U <= 4) return launch_kq_shape<QT, 4, 1, NW>(W, M, K, x, y, st, n_cu);
+    if (U <= 8) return launch_kq_shape<QT, 8, 1, NW>(W, M, K, x, y, st, n_cu);
+    if (U <= 16) return launch_kq_shape<QT, 16, 1, NW>(W, M, K, x, y, st, n_cu);
+    if (U <= 32) return launch_kq_shape<QT, 32, 1, NW>(W, M, K, x, y, st, n_cu);
+    if (U <= 64) return launch_kq_shape<QT, 64, 1, NW>(W, M, K, x, y, st, n_cu);
+    if (U <= 128) return launch_kq_shape<QT, 64, 2, NW / 2>(W, M, K, x, y, st, n_cu);
+    if (U <= 192) return launch_kq_shape<QT, 64, 3, KQ_G3>(W, M, K, x, y, st, n_cu);
+    if (U <= 256) return launch_kq_shape<QT, 64, 4, NW / 4>(W, M, K, x, y, st, n_cu);
+    return hipErrorNotSupported;
+}
+
+// Returns hipErrorNotSupported for formats or shapes this kernel does not
+// cover (K must be a multiple of 64 and at most 16384).
+hipError_t launch_matvec_kq(int qt, const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu) {
+    if (K % 64 || K > 16384 || K <= 0) return hipErrorNotSupported;
+    const bool sb256 = block_weights(qt) == 256;
+    if (sb256 && K % 256) return hipErrorNotSupported;
+    switch (qt) {
+    case QT_Q2_K: return launch_kq_q<QT_Q2_K>(W, M, K, x, y, st, n_cu);
+    case QT_Q3_K: return launch_kq_q<QT_Q3_K>(W, M, K, x, y, st, n_cu);
+    case QT_Q4_K: return launch_kq_q<QT_Q4_K>(W, M, K, x, y, st, n_cu);
+    case QT_Q5_K: return launch_kq_q<QT_Q5_K>(W, M, K, x, y, st, n_cu);
+    case QT_Q6_K: return launch_kq_q<QT_Q6_K>(W, M, K, x, y, st, n_cu);
+    case QT_Q8_0: return launch_kq_q<QT_Q8_0>(W, M, K, x, y, st, n_cu);
+    case QT_Q4_0: return launch_kq_q<QT_Q4_0>(W, M, K, x, y, st, n_cu);
+    case QT_Q8_K: return launch_kq_q<QT_Q8_K>(W, M, K, x, y, st, n_cu);
+    default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace tbq

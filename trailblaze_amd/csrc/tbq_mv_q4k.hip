@@ -91,25 +91,29 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int lr = lane % LPR, rsub = lane / LPR;
     const bool lv = lr < U;
+    const int ul = lv ? lr : 0;
     XStager<NT, (4 * 128 + NT - 1) / NT> xs;   // K <= 4096
     xs.load(x, K);
+    __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
     const int base = (blockIdx.x * NW + wave) * R * RPP + rsub;
+    // Unconditional loads (rows past M re-read row M-1, idle lanes unit 0;
+    // their results are discarded): under a branch, the compiler would wait
+    // for the weights before staging x.
     Q4KUnit w[R];
 #pragma unroll
     for (int p = 0; p < R; p++) {
-        const int r = base + p * RPP;
-        if (r < M && lv) q4k_load(W + (long long)r * rb, lr, w[p]);
+        const int r = min(base + p * RPP, M - 1);
+        q4k_load(W + (long long)r * rb, ul, w[p]);
     }
     xs.store(xd, K);
     __syncthreads();
     XUnit xu;
-    if (lv) xunit_load(xd, lr, xu);
+    xunit_load(xd, ul, xu);
 #pragma unroll
     for (int p = 0; p < R; p++) {
         const int r = base + p * RPP;
-        float acc = 0.f;
-        if (r < M && lv) acc = q4k_unit_dot(w[p], lr, xu, 0.f);
-        acc = group_sum<LPR>(acc);
+        const float v = q4k_unit_dot(w[p], ul, xu, 0.f);
+        const float acc = group_sum<LPR>((r < M && lv) ? v : 0.f);
         if (lr == 0 && r < M) y[r] = acc;
     }
 }

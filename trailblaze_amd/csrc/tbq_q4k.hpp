@@ -43,16 +43,17 @@ template <int NT, int MAXT>
 struct XStager {
     float4 v[MAXT][2];
 
+    // Unconditional loads (tasks past the end re-read the last task and are
+    // never stored), so no branch makes the compiler wait for every load
+    // in flight where it rejoins.
     __device__ __forceinline__ void load(const float *__restrict__ x, int K, int nvec = 1) {
         const int ntask = 4 * (K / 32) * nvec;
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
-            const int t = threadIdx.x + i * NT;
-            if (t < ntask) {
-                const float4 *xp = reinterpret_cast<const float4 *>(x + 8 * t);
-                v[i][0] = xp[0];
-                v[i][1] = xp[1];
-            }
+            const int t = min((int)threadIdx.x + i * NT, ntask - 1);
+            const float4 *xp = reinterpret_cast<const float4 *>(x + 8 * t);
+            v[i][0] = xp[0];
+            v[i][1] = xp[1];
         }
     }
 
@@ -60,8 +61,9 @@ struct XStager {
         const int ntask = 4 * (K / 32) * nvec;
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
+            // every round runs on every lane (no early exit: that would let the
+            // compiler sink x's loads below the weights'); only tasks < ntask store
             const int t = threadIdx.x + i * NT;
-            if (t - (int)(threadIdx.x & 3) >= ntask) break;   // uniform over the task's 4 lanes
             const int g = t >> 2, o = t & 3;
             const float4 a = v[i][0], b = v[i][1];
             const float e8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
