@@ -2,8 +2,8 @@
 order bit-exact against tb_route_experts semantics, MoE outputs within
 rel-L2 1e-5 of the oracle on the output and on the MoE delta (out - resid),
 at the reference's golden layer, at the Qwen3-30B-A3B shapes of
-BASELINE.json (batch 1 and 16), with a Zipf-skewed router bias, and
-through the C11 host block."""
+BASELINE.json (batch 1 and 16), with a Zipf-skewed router bias, on tied, nearly tied and
+underflowing logits, and through the C11 host block."""
 import ctypes as C
 
 import numpy as np
@@ -67,6 +67,37 @@ def test_route_golden_logit_vectors(oracle):
         assert bits_equal(w[0, :kk], ref_w)
         off_l += E
         off_s += kk
+
+
+@pytest.mark.parametrize("case", ["tie4", "tie_boundary", "near_tie", "underflow"])
+def test_route_ties_and_underflow(oracle, case):
+    """The slot scan's tie rule (first slot holding the minimum; strictly
+    larger enters) and probabilities that underflow to zero."""
+    rng = np.random.default_rng(7)
+    E, k = 64, 8
+    lg = rng.standard_normal(E).astype(np.float32)
+    if case == "tie4":
+        lg[:8] = 1.0          # the fill leaves equal minima; the next entry picks among them
+        lg[20] = 3.0
+    elif case == "tie_boundary":
+        lg[:] = np.float32(-2.0)
+        lg[::5] = np.float32(1.5)  # 13 equal leaders for 8 slots
+    elif case == "near_tie":
+        top = np.argsort(-lg)
+        lg[top[8]] = np.nextafter(lg[top[7]], np.float32(-np.inf))   # 8th and 9th one ulp apart
+    else:
+        lg[:] = np.float32(-200.0)  # probabilities of the tail underflow to zero
+        lg[3] = 0.0
+        lg[40] = np.float32(-199.0)
+    H = 512
+    xn = np.zeros((1, H), np.float32)
+    xn[0, :E] = lg
+    router = np.zeros((E, H), np.float32)
+    router[np.arange(E), np.arange(E)] = 1.0
+    idx, w = gpu_route(xn, router, None, k)
+    ri, rw = oracle.route(lg, k)
+    assert np.array_equal(idx[0], ri)
+    assert bits_equal(w[0], rw)
 
 
 @pytest.mark.parametrize("T", [1, 16, 512])

@@ -131,9 +131,11 @@ int tbq_matvec_variant(const void *W, int qt, int M, int K, const float *x, floa
     if (!check_matvec(W, qt, M, K, x, y)) return 0;
     if (variant < TBQ_MV_AUTO || variant > TBQ_MV_KQ) return fail("tbq_matvec_variant: unknown variant %d", variant);
     if (M == 0) return 1;
-    // Q4_K rows of up to 64 units keep x's digits in registers in the
-    // specialised kernel; everything else integer-dot goes to the shared one.
-    const bool q4k_special = qt == QT_Q4_K && (variant == TBQ_MV_INTDOT || (variant == TBQ_MV_AUTO && K <= 4096));
+    // The specialised Q4_K kernel takes one row per wave in a single pass
+    // (rows of up to 64 units keep x's digits in registers); taller
+    // matrices stream better through the shared kernel's row passes.
+    const bool q4k_special =
+        qt == QT_Q4_K && (variant == TBQ_MV_INTDOT || (variant == TBQ_MV_AUTO && K <= 4096 && M <= 8192));
     if (q4k_special) {
         hipError_t e = launch_matvec_q4k(W, M, K, x, y, S(s), g_cu);
         if (e != hipErrorNotSupported) return hip_ok(e, "matvec launch (Q4_K int-dot)");

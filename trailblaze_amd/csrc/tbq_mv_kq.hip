@@ -96,6 +96,16 @@ __device__ __forceinline__ void ld_dw(const uint8_t *p, uint32_t *out) {
     for (int j = 0; j < N; j++) out[j] = __builtin_amdgcn_alignbyte(w[j + 1], w[j], sh);
 }
 
+// Loads of the per-format unit loaders: wide loads at 4-byte-aligned
+// addresses, ld_dw for runs that are only 2-byte aligned.
+struct GMem {
+    static __device__ __forceinline__ uint4 ld128(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+    static __device__ __forceinline__ uint2 ld64(const uint8_t *p) { return *reinterpret_cast<const uint2 *>(p); }
+    static __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+    static __device__ __forceinline__ uint32_t ld16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
+    template <int N>
+    static __device__ __forceinline__ void ldw(const uint8_t *p, uint32_t *out) { ld_dw<N>(p, out); }
+};
 // ---------------------------------------------------------------------------
 // Staging: NT threads write the digits of all U units into LDS, in two
 // phases so that x's loads can be issued before a kernel's weight loads
@@ -245,9 +255,9 @@ template <> struct KqFmt<QT_Q2_K> {
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
         const uint8_t *b = row + (size_t)(u >> 2) * 84;
         const int p = u & 3;
-        w.qs = ld_u128(b + 16 + 16 * p);
-        w.sc = ld_u32(b + 4 * p);
-        w.dd = ld_u32(b + 80);
+        w.qs = GMem::ld128(b + 16 + 16 * p);
+        w.sc = GMem::ld32(b + 4 * p);
+        w.dd = GMem::ld32(b + 80);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x) {
         const uint32_t qv[4] = {w.qs.x, w.qs.y, w.qs.z, w.qs.w};
@@ -283,13 +293,13 @@ template <> struct KqFmt<QT_Q3_K> {
         const uint8_t *b = row + (size_t)(u >> 2) * 110;
         const int p = u & 3;
         uint32_t t[4];
-        ld_dw<4>(b + 32 + 16 * p, t);
+        GMem::template ldw<4>(b + 32 + 16 * p, t);
         w.qs = make_uint4(t[0], t[1], t[2], t[3]);
-        ld_dw<2>(b + 8 * p, t);
+        GMem::template ldw<2>(b + 8 * p, t);
         w.hm = make_uint2(t[0], t[1]);
-        ld_dw<1>(b + 96, &w.lo);                 // sc[0..3]
-        ld_dw<1>(b + 104, &w.hi.x);              // sc[8..11]
-        w.hi.y = (uint32_t)ld_u16(b + 108) << 16; // d in the high half
+        GMem::template ldw<1>(b + 96, &w.lo);                 // sc[0..3]
+        GMem::template ldw<1>(b + 104, &w.hi.x);              // sc[8..11]
+        w.hi.y = (uint32_t)GMem::ld16(b + 108) << 16; // d in the high half
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
         const int p1 = u & 1;   // groups 4p..4p+3 use slots 4*(p&1)..+3
@@ -331,10 +341,10 @@ template <> struct KqFmt<QT_Q4_K> {
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
         const uint8_t *b = row + (size_t)(u >> 2) * 144;
         const int p = u & 3;
-        w.hdr = ld_u128(b);
-        w.q0 = ld_u128(b + 16 + 32 * p);
-        w.q1 = ld_u128(b + 32 + 32 * p);
-        w.mind = ld_u32(b + 16);
+        w.hdr = GMem::ld128(b);
+        w.q0 = GMem::ld128(b + 16 + 32 * p);
+        w.q1 = GMem::ld128(b + 32 + 32 * p);
+        w.mind = GMem::ld32(b + 16);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
         const int p = u & 3;
@@ -376,11 +386,11 @@ template <> struct KqFmt<QT_Q5_K> {
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
         const uint8_t *b = row + (size_t)(u >> 2) * 176;
         const int p = u & 3;
-        w.hdr = ld_u128(b);
-        w.qh0 = ld_u32(b + 16);
-        w.qh = *reinterpret_cast<const uint2 *>(b + 16 + 8 * p);
-        w.q0 = ld_u128(b + 48 + 32 * p);
-        w.q1 = ld_u128(b + 64 + 32 * p);
+        w.hdr = GMem::ld128(b);
+        w.qh0 = GMem::ld32(b + 16);
+        w.qh = GMem::ld64(b + 16 + 8 * p);
+        w.q0 = GMem::ld128(b + 48 + 32 * p);
+        w.q1 = GMem::ld128(b + 64 + 32 * p);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
         const int p = u & 3;
@@ -430,13 +440,13 @@ template <> struct KqFmt<QT_Q6_K> {
         const uint8_t *b = row + (size_t)(u >> 2) * 210;
         const int p = u & 3;
         uint32_t t[8];
-        ld_dw<8>(b + 32 * p, t);
+        GMem::template ldw<8>(b + 32 * p, t);
         w.ql0 = make_uint4(t[0], t[1], t[2], t[3]);
         w.ql1 = make_uint4(t[4], t[5], t[6], t[7]);
-        ld_dw<4>(b + 128 + 16 * p, t);
+        GMem::template ldw<4>(b + 128 + 16 * p, t);
         w.qh = make_uint4(t[0], t[1], t[2], t[3]);
-        ld_dw<1>(b + 192 + 4 * p, &w.sc);
-        w.d = ld_u16(b + 208);
+        GMem::template ldw<1>(b + 192 + 4 * p, &w.sc);
+        w.d = GMem::ld16(b + 208);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
         const uint32_t qv[8] = {w.ql0.x, w.ql0.y, w.ql0.z, w.ql0.w, w.ql1.x, w.ql1.y, w.ql1.z, w.ql1.w};
@@ -476,12 +486,12 @@ template <> struct KqFmt<QT_Q8_0> {
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
         const uint8_t *b = row + (size_t)u * 68;
         uint32_t t[8];
-        w.d0 = ld_u16(b);
-        ld_dw<8>(b + 2, t);
+        w.d0 = GMem::ld16(b);
+        GMem::template ldw<8>(b + 2, t);
         w.a0 = make_uint4(t[0], t[1], t[2], t[3]);
         w.a1 = make_uint4(t[4], t[5], t[6], t[7]);
-        w.d1 = ld_u16(b + 34);
-        ld_dw<8>(b + 36, t);
+        w.d1 = GMem::ld16(b + 34);
+        GMem::template ldw<8>(b + 36, t);
         w.b0 = make_uint4(t[0], t[1], t[2], t[3]);
         w.b1 = make_uint4(t[4], t[5], t[6], t[7]);
     }
@@ -506,11 +516,11 @@ template <> struct KqFmt<QT_Q4_0> {
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
         const uint8_t *b = row + (size_t)u * 36;
         uint32_t t[4];
-        w.d0 = ld_u16(b);
-        ld_dw<4>(b + 2, t);
+        w.d0 = GMem::ld16(b);
+        GMem::template ldw<4>(b + 2, t);
         w.a = make_uint4(t[0], t[1], t[2], t[3]);
-        w.d1 = ld_u16(b + 18);
-        ld_dw<4>(b + 20, t);
+        w.d1 = GMem::ld16(b + 18);
+        GMem::template ldw<4>(b + 20, t);
         w.b = make_uint4(t[0], t[1], t[2], t[3]);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
@@ -541,9 +551,9 @@ template <> struct KqFmt<QT_Q8_K> {
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
         const uint8_t *b = row + (size_t)(u >> 2) * 292;
         const int p = u & 3;
-        w.d = ld_u32(b);
+        w.d = GMem::ld32(b);
 #pragma unroll
-        for (int i = 0; i < 4; i++) w.q[i] = ld_u128(b + 4 + 64 * p + 16 * i);
+        for (int i = 0; i < 4; i++) w.q[i] = GMem::ld128(b + 4 + 64 * p + 16 * i);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
         uint32_t q[16];
@@ -686,14 +696,14 @@ static hipError_t launch_kq_shape(const void *W, int M, int K, const float *x, f
 template <int QT>
 static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu) {
     const int U = K / 64;
-    constexpr int NW = KQ_NW;
+    constexpr int NW = KQ_NW, G3 = KQ_G3;
     if (U <= 4) return launch_kq_shape<QT, 4, 1, NW>(W, M, K, x, y, st, n_cu);
     if (U <= 8) return launch_kq_shape<QT, 8, 1, NW>(W, M, K, x, y, st, n_cu);
     if (U <= 16) return launch_kq_shape<QT, 16, 1, NW>(W, M, K, x, y, st, n_cu);
     if (U <= 32) return launch_kq_shape<QT, 32, 1, NW>(W, M, K, x, y, st, n_cu);
     if (U <= 64) return launch_kq_shape<QT, 64, 1, NW>(W, M, K, x, y, st, n_cu);
     if (U <= 128) return launch_kq_shape<QT, 64, 2, NW / 2>(W, M, K, x, y, st, n_cu);
-    if (U <= 192) return launch_kq_shape<QT, 64, 3, KQ_G3>(W, M, K, x, y, st, n_cu);
+    if (U <= 192) return launch_kq_shape<QT, 64, 3, G3>(W, M, K, x, y, st, n_cu);
     if (U <= 256) return launch_kq_shape<QT, 64, 4, NW / 4>(W, M, K, x, y, st, n_cu);
     return hipErrorNotSupported;
 }
