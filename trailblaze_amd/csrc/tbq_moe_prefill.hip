@@ -12,25 +12,30 @@
 //                     (exact, undone in the GEMM epilogues): x for gate/up,
 //                     the SwiGLU activations for down.
 //   k_moe_f16<0,NS>   act[p] = swiglu(x_t . W_gate[e], x_t . W_up[e]) for a
-//                     128-pair x 64-column tile (128 weight rows: 64 gate and
-//                     64 up rows), K = H, fp32 out.
-//   k_moe_f16<1,NS>   y[p] = act[p] . W_down[e] for 128 pairs x 128 rows, K = F.
+//                     tile of <= 128 pairs x 128 columns (256 weight rows:
+//                     128 gate and 128 up rows), K = H, fp32 out.
+//   k_moe_f16<1,NS>   y[p] = act[p] . W_down[e] for <= 128 pairs x 256 rows,
+//                     K = F.
 //   (k_combine)       out = resid + sum over slots in slot order (tbq_moe.hip).
+//
+// Weights never pass through LDS.  Each lane dequantises its own MFMA A
+// operands in registers: in v_mfma_f32_32x32x16_f16, lane l supplies row
+// l % 32 and eight consecutive k of the 16 per step, the half h = l / 32
+// choosing which eight.  Within a 128-column chunk the k order is permuted
+// (the products are summed over k, so any order shared by both operands
+// gives the same sum): step ks, half h covers chunk columns 64h + 8ks .. +8,
+// so a lane's 64 weights per chunk are two whole Q4_K sub-blocks -- 32
+// contiguous quant bytes and one scale/min pair each.  Only the activation
+// tile is shared by the workgroup's 8 waves: it is staged in LDS, double
+// buffered, one barrier per chunk.  Weight loads run two chunks ahead,
+// activation loads one.
 //
 // Dequantisation to fp16.  A nibble q becomes the fp16 number 1 + q/16 by
 // placing q in the mantissa (0x3C00 | q << 6), for two weights per dword:
 // one 24-bit multiply spreads a quant byte's two nibbles into the two
-// halves, one AND-OR masks them and sets the exponent; v_pk_add_f16 with
-// -1 (exact) gives q/16, and v_pk_fma_f16 with (16 S, -M) gives S q - M with
-// only the fp16 roundings of 16 S, M and the result.  About 2 VALU
-// operations per weight, where byte->fp32 conversion + fma + bf16 packing
-// takes 4.5.
-//
-// Per 128-column chunk of K each thread dequantises two Q4_K sub-blocks into
-// LDS (each weight once per tile) and copies its share of the tile's fp16
-// activation rows; v_mfma_f32_32x32x16_f16 accumulates in fp32, each wave
-// owning 32 weight rows x up to four 32-pair sub-tiles (sub-tiles past the
-// tile's pairs are skipped).  Global loads run one chunk ahead.
+// halves, one AND and one OR mask them and set the exponent; v_pk_add_f16
+// with -1 (exact) gives q/16, and v_pk_fma_f16 with (16 S, -M) gives S q - M
+// with only the fp16 roundings of 16 S, M and the result.
 //
 // Accuracy: fp16 weights and activations (11-bit mantissa), fp32
 // accumulation; outputs land within 1e-2 relative L2 of the fp32 reference.
@@ -48,54 +53,93 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int PF_MT = 128;         // pairs per tile (four 32-pair MFMA sub-tiles)
-constexpr int PF_KC = 128;         // K columns staged per chunk (half a Q4_K super-block)
+constexpr int PF_KC = 128;         // K columns per chunk (half a Q4_K super-block)
 constexpr int PF_LD = PF_KC + 8;   // LDS row stride in halves (padding breaks bank aliasing)
-constexpr int PF_THREADS = 256;
-constexpr int PF_ROWS = 128;       // weight rows per workgroup
-constexpr size_t PF_LDS_BYTES = (size_t)(PF_ROWS + PF_MT) * PF_LD * 2;   // W and X tiles, single-buffered
+#ifndef PF_WAVES
+#define PF_WAVES 8
+#endif
+constexpr int PF_THREADS = 64 * PF_WAVES;   // 32 weight rows per wave
+constexpr int PF_ROWS = 32 * PF_WAVES;      // weight rows per workgroup
+constexpr int PF_COLS = PF_ROWS / 2;        // gate/up columns per workgroup
+constexpr size_t PF_LDS_BYTES = (size_t)2 * PF_MT * PF_LD * 2 + PF_MT * 8;   // two activation tiles, pair ids, scales
 
 struct PfTile {
-    int e, start, n;
+    int e, n;
 };
 
 // ---------------------------------------------------------------------------
-// Dispatch: one workgroup of 1024 threads.  pairs p = t*k + s.
+// Dispatch: one workgroup of 1024 threads.  pairs p = t*k + s.  Tiles are
+// listed heaviest first (by 32-pair sub-tile count), so the
+// longest workgroups start first and the grid's tail is short; tile T's
+// pairs are tpair[128T .. 128T + n) (-1 after), its activation rows ttok
+// (= pair / k, the token).
 // ---------------------------------------------------------------------------
+constexpr int PF_MAX_TILES = 65536 * 8 / PF_MT + 256;
+
 __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_idx, int T, int k, int E,
                                                    int *__restrict__ perm, PfTile *__restrict__ tiles,
-                                                   int *__restrict__ ntiles) {
-    __shared__ int hist[256], off[257], toff[257], cur[256];
+                                                   int *__restrict__ ntiles, int *__restrict__ tpair,
+                                                   int *__restrict__ ttok) {
+    constexpr int NQ = PF_MT / 32;   // sub-tile count classes 1..NQ
+    __shared__ int hist[256], off[257], cur[256], scan[256];
+    __shared__ int qcnt[NQ + 1], qbase[NQ + 2];
+    __shared__ int t_e[PF_MAX_TILES], t_start[PF_MAX_TILES];
     const int tid = threadIdx.x, P = T * k;
-    for (int e = tid; e < 256; e += 1024) { hist[e] = 0; cur[e] = 0; }
+    if (tid < 256) { hist[tid] = 0; cur[tid] = 0; }
+    if (tid <= NQ) qcnt[tid] = 0;
     __syncthreads();
     for (int p = tid; p < P; p += 1024) atomicAdd(&hist[sel_idx[(p / k) * 8 + p % k]], 1);
     __syncthreads();
-    if (tid == 0) {
-        int o = 0, to = 0;
-        for (int e = 0; e < E; e++) {
-            off[e] = o;
-            toff[e] = to;
-            o += hist[e];
-            to += (hist[e] + PF_MT - 1) / PF_MT;
-        }
-        off[E] = o;
-        toff[E] = to;
-        *ntiles = to;
+    // exclusive prefix sum of hist over 256 experts (Hillis-Steele in LDS);
+    // tiles counted per sub-tile class
+    if (tid < 256) scan[tid] = tid < E ? hist[tid] : 0;
+    if (tid < E) {
+        const int n = hist[tid];
+        for (int s0 = 0; s0 < n; s0 += PF_MT) atomicAdd(&qcnt[(min(PF_MT, n - s0) + 31) / 32], 1);
     }
     __syncthreads();
+    for (int d = 1; d < 256; d <<= 1) {
+        const int v = tid < 256 && tid >= d ? scan[tid - d] : 0;
+        __syncthreads();
+        if (tid < 256) scan[tid] += v;
+        __syncthreads();
+    }
+    if (tid < 256) off[tid + 1] = scan[tid];
+    if (tid == 0) {
+        off[0] = 0;
+        // classes NQ (heaviest) first
+        int b = 0;
+        for (int q = NQ; q >= 1; q--) {
+            qbase[q] = b;
+            b += qcnt[q];
+            qcnt[q] = 0;
+        }
+        *ntiles = b;
+        qbase[0] = b;
+    }
+    __syncthreads();
+    if (tid < E) {
+        const int n = hist[tid];
+        for (int s0 = 0; s0 < n; s0 += PF_MT) {
+            const int q = (min(PF_MT, n - s0) + 31) / 32;
+            const int t = qbase[q] + atomicAdd(&qcnt[q], 1);
+            t_e[t] = tid;
+            t_start[t] = off[tid] + s0;
+        }
+    }
     for (int p = tid; p < P; p += 1024) {
         const int e = sel_idx[(p / k) * 8 + p % k];
         perm[off[e] + atomicAdd(&cur[e], 1)] = p;
     }
-    for (int e = tid; e < E; e += 1024) {
-        const int n = hist[e];
-        for (int i = 0; i * PF_MT < n; i++) {
-            PfTile tl;
-            tl.e = e;
-            tl.start = off[e] + i * PF_MT;
-            tl.n = n - i * PF_MT < PF_MT ? n - i * PF_MT : PF_MT;
-            tiles[toff[e] + i] = tl;
-        }
+    __syncthreads();
+    const int nt = qbase[0];
+    for (int i = tid; i < nt * PF_MT; i += 1024) {
+        const int t = i / PF_MT, j = i % PF_MT, e = t_e[t];
+        const int n = min(PF_MT, off[e + 1] - t_start[t]);
+        if (j == 0) tiles[t] = PfTile{e, n};
+        const int p = j < n ? perm[t_start[t] + j] : -1;
+        tpair[i] = p;
+        ttok[i] = p >= 0 ? p / k : -1;
     }
 }
 
@@ -134,187 +178,223 @@ __global__ __launch_bounds__(256) void k_rows_f16(const float *__restrict__ in, 
 }
 
 // ---------------------------------------------------------------------------
-// Staging helpers.
+// Weight staging.
 // ---------------------------------------------------------------------------
-// Raw bytes of one 32-weight Q4_K sub-block j of a super-block: scale/min
-// inputs and the 16 quant bytes.
-struct Q4Sub {
-    u32x4 hdr, q;
-    unsigned mind;
+// One lane's weights for a 128-column chunk: the 64 weights of sub-blocks
+// j0 and j0 + 1 of a row's Q4_K super-block (j0 even) and the three header
+// dwords they need: d/dmin, and the scale and min dwords of their half of the
+// super-block (bytes 4..11 for j0 < 4; bytes 12..19 for j0 >= 4, where the
+// mins are quant bytes 0..3, layer4/tb_gguf.c:163-168).
+struct Q4Pair {
+    unsigned dd, sw, mw;
+    u32x4 q0, q1;
 };
 
-__device__ __forceinline__ void q4sub_load(const uint8_t *sb, int j, Q4Sub &r) {
-    r.hdr = *reinterpret_cast<const u32x4 *>(sb);
-    r.q = *reinterpret_cast<const u32x4 *>(sb + 16 + 16 * j);
-    r.mind = *reinterpret_cast<const unsigned *>(sb + 16);
+__device__ __forceinline__ void q4pair_load(const uint8_t *sb, int j0, Q4Pair &r) {
+    r.dd = *reinterpret_cast<const unsigned *>(sb);
+    const uint2 sm = *reinterpret_cast<const uint2 *>(sb + (j0 < 4 ? 4 : 12));
+    r.sw = sm.x;
+    r.mw = sm.y;
+    r.q0 = *reinterpret_cast<const u32x4 *>(sb + 16 + 16 * j0);
+    r.q1 = *reinterpret_cast<const u32x4 *>(sb + 32 + 16 * j0);
 }
 
-// Dequantise (reference scale/min selection, layer4/tb_gguf.c:163-168) and
-// write 32 fp16 weights to dst (16-byte aligned).
-__device__ __forceinline__ void q4sub_store_f16(const Q4Sub &r, int j, _Float16 *dst) {
-    const float d = f16_ref(r.hdr.x & 0xFFFFu), dmin = f16_ref(r.hdr.x >> 16);
-    const unsigned sw = j < 4 ? r.hdr.y : r.hdr.w;
-    const unsigned mw = j < 4 ? r.hdr.z : r.mind;
-    const int sh = 8 * (j & 3);
-    const float S = d * (float)((sw >> sh) & 63), Mn = dmin * (float)((mw >> sh) & 63);
-    const _Float16 s16 = (_Float16)(16.f * S), nm = (_Float16)(-Mn);
-    const f16x2 S16 = {s16, s16}, NM = {nm, nm}, ONE = {(_Float16)1.f, (_Float16)1.f};
-    const unsigned qv[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-    unsigned o[16];
+__device__ __forceinline__ float h2f(unsigned bits) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(bits & 0xFFFFu));
+}
+
+// Four quant bytes -> eight fp16 weights S q - Mn (low nibble first, the
+// reference's order), as one MFMA operand.
+__device__ __forceinline__ f16x8 q4dword_f16(unsigned q, f16x2 S16, f16x2 NM) {
+    const f16x2 ONE = {(_Float16)1.f, (_Float16)1.f};
+    unsigned o[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            // quant byte (hi << 4 | lo) -> halves (1 + lo/16, 1 + hi/16)
-            const unsigned y = (qv[i] >> (8 * b)) & 0xFFu;
-            const unsigned t = (__umul24(y, 0x40040u) & 0x03C003C0u) | 0x3C003C00u;
-            const f16x2 v = __builtin_bit_cast(f16x2, t) - ONE;
-            o[4 * i + b] = __builtin_bit_cast(unsigned, __builtin_elementwise_fma(v, S16, NM));
-        }
+    for (int b = 0; b < 4; b++) {
+        // quant byte (hi << 4 | lo) -> halves (1 + lo/16, 1 + hi/16)
+        const unsigned y = (q >> (8 * b)) & 0xFFu;
+        const unsigned t = (__umul24(y, 0x40040u) & 0x03C003C0u) | 0x3C003C00u;
+        const f16x2 v = __builtin_bit_cast(f16x2, t) - ONE;
+        o[b] = __builtin_bit_cast(unsigned, __builtin_elementwise_fma(v, S16, NM));
     }
-    u32x4 *d4 = reinterpret_cast<u32x4 *>(dst);
-#pragma unroll
-    for (int i = 0; i < 4; i++) d4[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+    return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
+}
+
+// The lane's four A operands of sub-block j0 + u (steps 4u .. 4u + 3 of the
+// chunk use its quant dwords 0..3).
+__device__ __forceinline__ void q4pair_frags(const Q4Pair &r, int j0, int u, f16x8 *a) {
+    const int sh = 8 * ((j0 + u) & 3);
+    const float S = h2f(r.dd) * (float)((r.sw >> sh) & 63), Mn = h2f(r.dd >> 16) * (float)((r.mw >> sh) & 63);
+    const _Float16 s16 = (_Float16)(16.f * S), nm = (_Float16)(-Mn);
+    const f16x2 S16 = {s16, s16}, NM = {nm, nm};
+    const u32x4 q = u ? r.q1 : r.q0;
+    a[0] = q4dword_f16(q.x, S16, NM);
+    a[1] = q4dword_f16(q.y, S16, NM);
+    a[2] = q4dword_f16(q.z, S16, NM);
+    a[3] = q4dword_f16(q.w, S16, NM);
 }
 
 // ---------------------------------------------------------------------------
-// Expert tile GEMM.  grid = (max tiles, F/64) for MODE 0, (max tiles, H/128)
-// for MODE 1; K = NS * 128.
-//   MODE 0: local weight row r = 32w + j is gate row 16w + j (j < 16) or up
-//   row 16w + j - 16 of the workgroup's 64 columns, so a lane's accumulator
-//   registers i and i + 8 hold gate and up of the same (column, pair) and
-//   SwiGLU needs no data exchange; X rows are tokens (pair / k) of x.
-//   MODE 1: local row r is down row 128*blockIdx.y + r; X rows are pairs of
-//   act.  xinv[X row] undoes the row's fp16 scaling.
-// Thread staging per chunk: W items tid + 256i (i < 2) = (row it/4, sub-block
-// it%4 of the chunk); X segments tid + 256i (i < 8) = (pair it/16, 8 halves
-// at 8*(it%16)).
+// Expert tile GEMM.  1-D grid of max tiles x ncb row blocks (ncb = F/PF_COLS
+// for MODE 0, H/PF_ROWS for MODE 1); K = NS * 128.
+//   MODE 0: wave w, lane row i = l % 32 is gate (i < 16) or up (i >= 16)
+//   column PF_COLS*cb + 16w + i % 16, so a lane's accumulator registers r
+//   and r + 8 hold gate and up of the same (column, pair) and SwiGLU needs
+//   no data exchange; X rows are tokens (ttok) of x.
+//   MODE 1: lane row i is down row PF_ROWS*cb + 32w + i; X rows are pairs
+//   (tpair) of act.  xinv[X row] undoes the row's fp16 scaling.
+// Activation staging per chunk: segments tid + 512m (m < 4) = (pair it/16,
+// 8 halves at 8*(it%16)).  Every global load is unconditional (indices
+// clamped, results selected), so the compiler's wait counts stay exact.
 // ---------------------------------------------------------------------------
 template <int MODE, int NS>
-__global__ __launch_bounds__(PF_THREADS, 2) void k_moe_f16(const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1,
-                                                           const _Float16 *__restrict__ X, int x_rows,
-                                                           const float *__restrict__ xinv, const int *__restrict__ perm,
-                                                           const PfTile *__restrict__ tiles, const int *__restrict__ ntiles,
-                                                           int H, int F, int k, float *__restrict__ out) {
+__global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1,
+                                                        const _Float16 *__restrict__ X, int x_rows,
+                                                        const float *__restrict__ xinv, const int *__restrict__ tpair,
+                                                        const int *__restrict__ ttok, const PfTile *__restrict__ tiles,
+                                                        const int *__restrict__ ntiles, int ncb, int H, int F,
+                                                        float *__restrict__ out) {
     constexpr int K = NS * PF_KC;
-    constexpr int XPT = PF_MT * PF_KC / 8 / PF_THREADS;   // 16-byte X segments per thread per chunk
-    extern __shared__ __attribute__((aligned(16))) _Float16 pf_lds[];
-    _Float16 *Ws = pf_lds;                     // [PF_ROWS][PF_LD]
-    _Float16 *Xs = pf_lds + PF_ROWS * PF_LD;   // [PF_MT][PF_LD]
-    if ((int)blockIdx.x >= *ntiles) return;
-    const PfTile tl = tiles[blockIdx.x];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    constexpr int XPT = PF_MT * PF_KC / 8 / PF_THREADS;   // 16-byte activation segments per thread per chunk
+    extern __shared__ __attribute__((aligned(16))) _Float16 pf_lds[];   // [2][PF_MT][PF_LD]
+    // workgroup -> (tile, row block), tile-major so the heavy tiles, listed
+    // first, start first.  The tile record and its row lists are loaded
+    // together (the row lists of a tile past the end are never used).
+    const int tix = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, lh = lane >> 5;
+    const int *xrows = (MODE == 0 ? ttok : tpair) + tix * PF_MT;
+    int px[XPT];
+#pragma unroll
+    for (int m = 0; m < XPT; m++) px[m] = xrows[(tid + PF_THREADS * m) >> 4];
+    const int po = tid < PF_MT ? tpair[tix * PF_MT + tid] : -1;
+    const int pxo = tid < PF_MT ? xrows[tid] : -1;
+    if (tix >= *ntiles) return;
+    const PfTile tl = tiles[tix];
     const long long rb = (long long)(K / 256) * 144;
 
-    const uint8_t *wrow[2];
-    int wr_local[2], wj[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int it = tid + PF_THREADS * i, r = it >> 2;
-        wr_local[i] = r;
-        wj[i] = it & 3;
-        if (MODE == 0) {
-            const int jj = r & 31, col = blockIdx.y * 64 + 16 * (r >> 5) + (jj & 15);
-            wrow[i] = (jj < 16 ? W0 : W1) + ((long long)tl.e * F + col) * rb;
-        } else {
-            wrow[i] = W0 + ((long long)tl.e * H + blockIdx.y * PF_ROWS + r) * rb;
-        }
+    const uint8_t *wrow;
+    if (MODE == 0) {
+        const int col = cb * PF_COLS + 16 * wave + (li & 15);
+        wrow = (li < 16 ? W0 : W1) + ((long long)tl.e * F + col) * rb;
+    } else {
+        wrow = W0 + ((long long)tl.e * H + cb * PF_ROWS + 32 * wave + li) * rb;
     }
-    // X rows through a range-checked buffer descriptor: rows past the tile's
-    // pair count get an offset beyond the buffer, which loads zeros without a
-    // memory access, so every load is unconditional (static wait counts)
+    auto wload = [&](Q4Pair &w, int s) { q4pair_load(wrow + (long long)(s >> 1) * 144, 4 * (s & 1) + 2 * lh, w); };
+    Q4Pair w0, w1, w2;
+    wload(w0, 0);
+    wload(w1, min(1, NS - 1));
+
+    // the tile's pair ids and activation-row scales, for the epilogue, in
+    // LDS behind the two activation buffers
+    int *po_s = reinterpret_cast<int *>(pf_lds + 2 * PF_MT * PF_LD);
+    float *sc_s = reinterpret_cast<float *>(po_s + PF_MT);
+    if (tid < PF_MT) {
+        po_s[tid] = po;
+        sc_s[tid] = pxo >= 0 ? xinv[pxo] : 0.f;
+    }
+
+    // activation rows through a range-checked buffer descriptor: rows past
+    // the tile's pair count (id -1) get an offset beyond the buffer, which
+    // loads zeros without a memory access
     const int xbytes = x_rows * K * 2;
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *)X, (short)0, xbytes, 0x00020000);
     int xoff[XPT];
 #pragma unroll
-    for (int i = 0; i < XPT; i++) {
-        const int it = tid + PF_THREADS * i, pr = it >> 4;
-        if (pr < tl.n) {
-            const int p = perm[tl.start + pr];
-            xoff[i] = ((MODE == 0 ? p / k : p) * K + 8 * (it & 15)) * 2;
-        } else {
-            xoff[i] = xbytes;
-        }
+    for (int m = 0; m < XPT; m++) {
+        const int it = tid + PF_THREADS * m;
+        xoff[m] = px[m] >= 0 ? (px[m] * K + 8 * (it & 15)) * 2 : xbytes;
     }
-
-    struct Slot {
-        Q4Sub w[2];
-        u32x4 x[XPT];
+    u32x4 xr[XPT];
+    auto xload = [&](int s) {
+#pragma unroll
+        for (int m = 0; m < XPT; m++)
+            xr[m] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[m] < xbytes ? xoff[m] + s * PF_KC * 2 : xbytes, 0, 0);
     };
-    auto load = [&](Slot &sl, int s) {
-        const int kc = s * PF_KC;
+    auto xstore = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) q4sub_load(wrow[i] + (long long)(kc / 256) * 144, 4 * (s & 1) + wj[i], sl.w[i]);
-#pragma unroll
-        for (int i = 0; i < XPT; i++)
-            sl.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[i] < xbytes ? xoff[i] + kc * 2 : xbytes, 0, 0);
-    };
-    auto store = [&](const Slot &sl, int s) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) q4sub_store_f16(sl.w[i], 4 * (s & 1) + wj[i], Ws + wr_local[i] * PF_LD + 32 * wj[i]);
-#pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const int it = tid + PF_THREADS * i;
-            *reinterpret_cast<u32x4 *>(Xs + (it >> 4) * PF_LD + 8 * (it & 15)) = sl.x[i];
+        for (int m = 0; m < XPT; m++) {
+            const int it = tid + PF_THREADS * m;
+            *reinterpret_cast<u32x4 *>(pf_lds + (buf * PF_MT + (it >> 4)) * PF_LD + 8 * (it & 15)) = xr[m];
         }
     };
+    xload(0);
+    xstore(0);
+    xload(min(1, NS - 1));
+    __syncthreads();
 
     const int nsub = (tl.n + 31) / 32;   // 1..4, uniform over the workgroup
     f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
-    Slot sa, sb;
-    load(sa, 0);
-    const _Float16 *wb = Ws + (32 * wave + (lane & 31)) * PF_LD + 8 * (lane >> 5);
-    const _Float16 *xb = Xs + (lane & 31) * PF_LD + 8 * (lane >> 5);
-    // one chunk: prefetch the next into `nxt`, stage `cur`, multiply; the
-    // slots are named, not indexed, so the chunk loop need not be unrolled
-    // to keep them in registers (NS is even)
-    auto chunk = [&](int s, const Slot &cur, Slot &nxt) {
-        if (s + 1 < NS) load(nxt, s + 1);
-        if (s > 0) __syncthreads();   // the previous chunk's MFMA reads are done
-        store(cur, s);
-        __syncthreads();
+    const _Float16 *xfrag = pf_lds + li * PF_LD + 64 * lh;
+    // steps 4u .. 4u + 3 of a chunk for the sub-tiles that hold pairs: one
+    // uniform branch per sub-tile, so every accumulator keeps its registers
+    // (a switch over the sub-tile count gives each arm its own allocation
+    // and costs a copy of the accumulators per chunk)
+    auto mma = [&](const f16x8 *a, const _Float16 *xb, int u) {
 #pragma unroll
-        for (int ks = 0; ks < PF_KC; ks += 16) {
-            const f16x8 av = *reinterpret_cast<const f16x8 *>(wb + ks);
+        for (int t = 0; t < 4; t++) {
+            if (t < nsub) {
+                f16x8 bv[4];
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                if (t < nsub) {
-                    const f16x8 bv = *reinterpret_cast<const f16x8 *>(xb + 32 * t * PF_LD + ks);
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[t], 0, 0, 0);
-                }
+                for (int ks = 0; ks < 4; ks++)
+                    bv[ks] = *reinterpret_cast<const f16x8 *>(xb + 32 * t * PF_LD + 8 * (4 * u + ks));
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks], bv[ks], acc[t], 0, 0, 0);
             }
         }
     };
-#pragma unroll 2
-    for (int s = 0; s < NS; s += 2) {
-        chunk(s, sa, sb);
-        chunk(s + 1, sb, sa);
+    // chunk s: weights of chunk s + 2 into wn (ring of three named slots, so
+    // the loop need not be unrolled to keep them in registers), activations
+    // of chunk s + 2 into registers after staging chunk s + 1's into LDS.
+    // Chunks past the end reload the last one and skip the work.
+    // Every path through a chunk issues the same global loads (the compiler
+    // merges wait counts over paths, and a path with fewer loads would make
+    // it wait for the prefetches too).
+    auto chunk = [&](int s, const Q4Pair &wc, Q4Pair &wn) {
+        wload(wn, min(s + 2, NS - 1));
+        if (s < NS) {
+            const int j0 = 4 * (s & 1) + 2 * lh;
+            const _Float16 *xb = xfrag + (s & 1) * PF_MT * PF_LD;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                f16x8 a[4];
+                q4pair_frags(wc, j0, u, a);
+                mma(a, xb, u);
+            }
+            // buffer last read in chunk s - 1, before the previous barrier
+            if (s + 1 < NS) xstore((s + 1) & 1);
+        }
+        xload(min(s + 2, NS - 1));
+        if (s < NS) __syncthreads();
+    };
+    for (int s = 0; s < NS; s += 3) {
+        chunk(s, w0, w2);
+        chunk(s + 1, w1, w0);
+        chunk(s + 2, w2, w1);
     }
-    // accumulator register i of lane l: row 8(i/4) + 4(l/32) + i%4 of the
+    // accumulator register r of lane l: row 8(r/4) + 4(l/32) + r%4 of the
     // wave's 32, pair 32t + l%32 of the tile
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        const int pr = 32 * t + (lane & 31);
+        const int pr = 32 * t + li;
         if (t < nsub && pr < tl.n) {
-            const int p = perm[tl.start + pr];
-            const float sc = xinv[MODE == 0 ? p / k : p];
+            const int p = po_s[pr];
+            const float sc = sc_s[pr];
             if (MODE == 0) {
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
                     float a[4];
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
-                        const int i = 4 * h + c;
-                        const float g = acc[t][i] * sc, u = acc[t][i + 8] * sc;
-                        a[c] = g / (1.0f + expf_glibc(-g)) * u;
+                        const int r = 4 * h + c;
+                        const float g = acc[t][r] * sc, u = acc[t][r + 8] * sc;
+                        a[c] = g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
                     }
-                    const int col = blockIdx.y * 64 + 16 * wave + 8 * h + 4 * (lane >> 5);
+                    const int col = cb * PF_COLS + 16 * wave + 8 * h + 4 * lh;
                     *reinterpret_cast<float4 *>(out + (long long)p * F + col) = make_float4(a[0], a[1], a[2], a[3]);
                 }
             } else {
 #pragma unroll
                 for (int h = 0; h < 4; h++) {
-                    const int row = blockIdx.y * PF_ROWS + 32 * wave + 8 * h + 4 * (lane >> 5);
+                    const int row = cb * PF_ROWS + 32 * wave + 8 * h + 4 * lh;
                     *reinterpret_cast<float4 *>(out + (long long)p * H + row) =
                         make_float4(acc[t][4 * h] * sc, acc[t][4 * h + 1] * sc, acc[t][4 * h + 2] * sc,
                                     acc[t][4 * h + 3] * sc);
@@ -328,24 +408,24 @@ size_t prefill_workspace_bytes(int T, int k, int E, int H, int F) {
     const size_t P = (size_t)T * k;
     const size_t max_tiles = (P + PF_MT - 1) / PF_MT + E;
     auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
-    return up(P * 4) + up(max_tiles * sizeof(PfTile)) + 256 + up(P * F * 2) + up((size_t)T * H * 2) + up(P * 4) +
-           up((size_t)T * 4);
+    return up(P * 4) + up(max_tiles * sizeof(PfTile)) + 256 + 2 * up(max_tiles * PF_MT * 4) + up(P * F * 2) +
+           up((size_t)T * H * 2) + up(P * 4) + up((size_t)T * 4);
 }
 
 template <int MODE>
-static hipError_t launch_moe_f16(int ns, dim3 grid, hipStream_t st, const uint8_t *W0, const uint8_t *W1,
-                                 const _Float16 *X, int x_rows, const float *xinv, const int *perm, const PfTile *tiles,
-                                 const int *ntiles, int H, int F, int k, float *out) {
+static hipError_t launch_moe_f16(int ns, unsigned nwg, hipStream_t st, const uint8_t *W0, const uint8_t *W1,
+                                 const _Float16 *X, int x_rows, const float *xinv, const int *tpair, const int *ttok,
+                                 const PfTile *tiles, const int *ntiles, int ncb, int H, int F, float *out) {
     // more than 64 KiB of dynamic LDS is opted into once per kernel
-#define TBQ_NS(N)                                                                                                   \
-    case N: {                                                                                                       \
-        static const hipError_t attr = hipFuncSetAttribute((const void *)k_moe_f16<MODE, N>,                        \
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize,              \
-                                                           (int)PF_LDS_BYTES);                                      \
-        if (attr != hipSuccess) return attr;                                                                        \
-        hipLaunchKernelGGL((k_moe_f16<MODE, N>), grid, dim3(PF_THREADS), PF_LDS_BYTES, st, W0, W1, X, x_rows, xinv, \
-                           perm, tiles, ntiles, H, F, k, out);                                                      \
-        break;                                                                                                      \
+#define TBQ_NS(N)                                                                                                  \
+    case N: {                                                                                                      \
+        static const hipError_t attr = hipFuncSetAttribute((const void *)k_moe_f16<MODE, N>,                       \
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,             \
+                                                           (int)PF_LDS_BYTES);                                     \
+        if (attr != hipSuccess) return attr;                                                                       \
+        hipLaunchKernelGGL((k_moe_f16<MODE, N>), dim3(nwg), dim3(PF_THREADS), PF_LDS_BYTES, st, W0, W1, X, x_rows, \
+                           xinv, tpair, ttok, tiles, ntiles, ncb, H, F, out);                                      \
+        break;                                                                                                     \
     }
     switch (ns) {
         TBQ_NS(2) TBQ_NS(4) TBQ_NS(6) TBQ_NS(8) TBQ_NS(12) TBQ_NS(16) TBQ_NS(24) TBQ_NS(32)
@@ -358,14 +438,16 @@ static hipError_t launch_moe_f16(int ns, dim3 grid, hipStream_t st, const uint8_
 
 // Experts on MFMA for Q4_K weights; routing already in a.sel_idx/a.sel_w.
 // Uses a.act (pairs x F fp32), a.y (pairs x H fp32) and `scratch`
-// (prefill_workspace_bytes).  K = H (gate/up) and F (down) must be 256,
-// 512, 768, 1024, 1536, 2048, 3072 or 4096.
+// (prefill_workspace_bytes).  H and F must be 256, 512, 768, 1024, 1536,
+// 2048, 3072 or 4096, H a multiple of PF_ROWS and F of PF_COLS; T <= 65536.
 hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t st) {
     auto ok_k = [](int K) {
         const int n = K / PF_KC;
         return K % 256 == 0 && (n == 2 || n == 4 || n == 6 || n == 8 || n == 12 || n == 16 || n == 24 || n == 32);
     };
-    if (a.qtype != QT_Q4_K || !ok_k(a.H) || !ok_k(a.F) || a.F % 64 || a.H % PF_ROWS) return hipErrorNotSupported;
+    if (a.qtype != QT_Q4_K || !ok_k(a.H) || !ok_k(a.F) || a.H % PF_ROWS || a.F % PF_COLS || a.T > 65536 ||
+        a.E > 256)
+        return hipErrorNotSupported;
     const size_t P = (size_t)a.T * a.k;
     const int max_tiles = (int)((P + PF_MT - 1) / PF_MT + a.E);
     auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
@@ -373,22 +455,26 @@ hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t s
     int *perm = (int *)w; w += up(P * 4);
     PfTile *tiles = (PfTile *)w; w += up((size_t)max_tiles * sizeof(PfTile));
     int *ntiles = (int *)w; w += 256;
+    int *tpair = (int *)w; w += up((size_t)max_tiles * PF_MT * 4);
+    int *ttok = (int *)w; w += up((size_t)max_tiles * PF_MT * 4);
     _Float16 *act16 = (_Float16 *)w; w += up(P * a.F * 2);
     _Float16 *x16 = (_Float16 *)w; w += up((size_t)a.T * a.H * 2);
     float *ainv = (float *)w; w += up(P * 4);
     float *xinv = (float *)w;
     hipLaunchKernelGGL(k_rows_f16, dim3(a.T), dim3(256), 0, st, a.xn, a.H, x16, xinv);
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, st, a.sel_idx, a.T, a.k, a.E, perm, tiles, ntiles);
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, st, a.sel_idx, a.T, a.k, a.E, perm, tiles, ntiles, tpair,
+                       ttok);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    err = launch_moe_f16<0>(a.H / PF_KC, dim3(max_tiles, a.F / 64), st, (const uint8_t *)a.gate, (const uint8_t *)a.up,
-                            x16, a.T, xinv, perm, tiles, ntiles, a.H, a.F, a.k, a.act);
+    const int ncb0 = a.F / PF_COLS, ncb1 = a.H / PF_ROWS;
+    err = launch_moe_f16<0>(a.H / PF_KC, (unsigned)(max_tiles * ncb0), st, (const uint8_t *)a.gate,
+                            (const uint8_t *)a.up, x16, a.T, xinv, tpair, ttok, tiles, ntiles, ncb0, a.H, a.F, a.act);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_rows_f16, dim3((unsigned)P), dim3(256), 0, st, a.act, a.F, act16, ainv);
     err = hipGetLastError();
     if (err != hipSuccess) return err;
-    return launch_moe_f16<1>(a.F / PF_KC, dim3(max_tiles, a.H / PF_ROWS), st, (const uint8_t *)a.down, nullptr, act16,
-                             (int)P, ainv, perm, tiles, ntiles, a.H, a.F, a.k, a.y);
+    return launch_moe_f16<1>(a.F / PF_KC, (unsigned)(max_tiles * ncb1), st, (const uint8_t *)a.down, nullptr, act16,
+                             (int)P, ainv, tpair, ttok, tiles, ntiles, ncb1, a.H, a.F, a.y);
 }
 
 }  // namespace tbq
