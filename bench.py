@@ -228,7 +228,7 @@ def moe_leg(tb, fm, synth, torch, rng, stream):
         us = s / (reps * ntok) * 1e6
         moe[f"decode_b{T}"] = dict(us_per_layer=us, us_per_token=us / T)
         log(f"MoE decode b={T}: {us:.1f} us/layer  {us / T:.2f} us/token")
-    # prefill, Zipf-skewed routing, grouped bf16 MFMA experts
+    # prefill, Zipf-skewed routing, grouped fp16 MFMA experts
     T = 512
     bias = synth.zipf_router_bias(E, 1.1, 1.0, rng)
     Lb = tb.moe_layer(H, F, E, k, fm.Q4_K, L._keep[0], L._keep[1], L._keep[2], L._keep[3], bias=d(bias))
@@ -239,7 +239,7 @@ def moe_leg(tb, fm, synth, torch, rng, stream):
     s = time_region(lambda: tb.moe_forward(Lb, T, xs, rs, out, workspace=ws_t, mode=tb.TBQ_MOE_BF16), 20, 3, stream)
     us = s / 20 * 1e6
     moe["prefill_512_bf16_mfma"] = dict(us_per_layer=us, us_per_token=us / T)
-    log(f"MoE prefill T=512 (bf16 MFMA): {us:.1f} us/layer  {us / T:.3f} us/token")
+    log(f"MoE prefill T=512 (fp16 MFMA): {us:.1f} us/layer  {us / T:.3f} us/token")
     return moe
 
 

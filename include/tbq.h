@@ -92,7 +92,9 @@ typedef struct {
 } tbq_moe_layer;
 
 #define TBQ_MOE_FP32 0      /* fp32 decode kernels; outputs within 1e-5 rel-L2 */
-#define TBQ_MOE_BF16 1      /* prefill: grouped bf16 MFMA; within 1e-2 rel-L2 */
+#define TBQ_MOE_BF16 1      /* prefill: grouped 16-bit MFMA (fp16 operands with
+                               power-of-two row scaling, fp32 accumulate);
+                               within 1e-2 rel-L2 */
 
 /* Workspace bytes tbq_moe_forward needs for T tokens in `mode` (T <= 65536). */
 size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode);

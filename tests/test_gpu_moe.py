@@ -69,12 +69,11 @@ def test_route_golden_logit_vectors(oracle):
         off_s += kk
 
 
-@pytest.mark.parametrize("case", ["tie4", "tie_boundary", "near_tie", "underflow"])
-def test_route_ties_and_underflow(oracle, case):
-    """The slot scan's tie rule (first slot holding the minimum; strictly
-    larger enters) and probabilities that underflow to zero."""
+def tie_case_logits(case):
+    """64 logits that exercise the slot scan's tie rule (first slot holding
+    the minimum; strictly larger enters) or underflowing probabilities."""
     rng = np.random.default_rng(7)
-    E, k = 64, 8
+    E = 64
     lg = rng.standard_normal(E).astype(np.float32)
     if case == "tie4":
         lg[:8] = 1.0          # the fill leaves equal minima; the next entry picks among them
@@ -89,6 +88,14 @@ def test_route_ties_and_underflow(oracle, case):
         lg[:] = np.float32(-200.0)  # probabilities of the tail underflow to zero
         lg[3] = 0.0
         lg[40] = np.float32(-199.0)
+    return lg
+
+
+@pytest.mark.parametrize("case", ["tie4", "tie_boundary", "near_tie", "underflow"])
+def test_route_ties_and_underflow(oracle, case):
+    """The slot scan's tie rule and probabilities that underflow to zero."""
+    lg = tie_case_logits(case)
+    E, k = lg.size, 8
     H = 512
     xn = np.zeros((1, H), np.float32)
     xn[0, :E] = lg
@@ -148,6 +155,50 @@ def test_moe_decode_config(oracle, qwen_layer, T):
     assert rel_l2(out - resid, ref - resid) <= TOL
 
 
+def test_moe_decode_router_many_tokens(oracle):
+    """Routing inside tbq_moe_forward over 512 decode tokens (32 batches of
+    16): every index, slot and weight equal to the reference's."""
+    H, F, E, k = 2048, 256, 128, 8
+    router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=41)
+    import torch
+    L = tb.moe_layer(H, F, E, k, fm.Q4_K, dev(router), dev(gate), dev(up), dev(down))
+    rng = np.random.default_rng(41)
+    T = 16
+    ws = torch.zeros(tb.moe_workspace_size(L, T), dtype=torch.uint8, device="cuda")
+    out = empty(T * H, torch.float32)
+    for b in range(32):
+        xn = synth.activations((T, H), rng)
+        resid = np.zeros((T, H), np.float32)
+        idx = empty(T * 8, torch.int32)
+        w = empty(T * 8, torch.float32)
+        tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws)
+        idx, w = host(idx).reshape(T, 8), host(w).reshape(T, 8)
+        lg = oracle.router_logits(xn, router, None)
+        for t in range(T):
+            ri, rw = oracle.route(lg[t], k)
+            assert np.array_equal(idx[t], ri), (b, t)
+            assert bits_equal(w[t], rw), (b, t)
+
+
+@pytest.mark.parametrize("case", ["tie4", "tie_boundary", "near_tie", "underflow"])
+def test_moe_decode_router_ties(oracle, case):
+    """Tied, nearly tied and underflowing logits through tbq_moe_forward:
+    the reference's indices, slot order and weights bit for bit."""
+    lg = tie_case_logits(case)
+    E, k, H, F = lg.size, 8, 512, 256
+    router = np.zeros((E, H), np.float32)
+    router[np.arange(E), np.arange(E)] = 1.0
+    _, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=13)
+    xn = np.zeros((1, H), np.float32)
+    xn[0, :E] = lg
+    resid = synth.activations((1, H), np.random.default_rng(13))
+    out, idx, w = gpu_moe(xn, resid, router, gate, up, down, F, k, fm.Q4_K)
+    ref, ridx, rw = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
+    assert np.array_equal(idx, ridx)
+    assert bits_equal(w, rw)
+    assert rel_l2(out - resid, ref - resid) <= TOL
+
+
 @pytest.mark.parametrize("qt", [fm.Q2_K, fm.Q3_K, fm.Q5_K, fm.Q6_K, fm.Q8_0])
 def test_moe_other_formats(oracle, qt):
     H, F, E, k, T = 512, 256, 16, 4, 3
@@ -181,7 +232,7 @@ def test_moe_host_block(oracle):
 
 
 # ---------------------------------------------------------------------------
-# Prefill: grouped bf16 MFMA experts (tolerance 1e-2 rel-L2, routing exact)
+# Prefill: grouped fp16 MFMA experts (tolerance 1e-2 rel-L2, routing exact)
 # ---------------------------------------------------------------------------
 PREFILL_TOL = 1e-2
 

@@ -224,7 +224,7 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     if (!check_moe(L, T)) return 0;
     if (mode != TBQ_MOE_FP32 && mode != TBQ_MOE_BF16) return fail("tbq_moe_forward: unknown mode %d", mode);
     if (mode == TBQ_MOE_BF16 && (L->qtype != QT_Q4_K || L->F % 128 || L->H % 128))
-        return fail("tbq_moe_forward: the bf16 MFMA path takes Q4_K experts with H, F multiples of 256");
+        return fail("tbq_moe_forward: the prefill MFMA path takes Q4_K experts with H, F multiples of 256");
     if (!xn || !resid || !out || !aligned16(xn) || !aligned16(resid) || !aligned16(out))
         return fail("tbq_moe_forward: null or misaligned activation pointer");
     if (T == 0) return 1;
@@ -260,7 +260,7 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     a.y = (float *)(ws + off); off += align256((size_t)T * a.k * a.H * 4);
     a.sel_idx = sel_idx ? sel_idx : ws_idx;
     a.sel_w = sel_w ? sel_w : ws_w;
-    if (mode == TBQ_MOE_BF16) return hip_ok(launch_moe_bf16(a, ws + off, S(s)), "moe launch (bf16 MFMA)");
+    if (mode == TBQ_MOE_BF16) return hip_ok(launch_moe_bf16(a, ws + off, S(s)), "moe launch (prefill MFMA)");
     return hip_ok(launch_moe_fp32(a, S(s)), "moe launch");
 }
 

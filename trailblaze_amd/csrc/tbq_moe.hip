@@ -285,7 +285,7 @@ hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Prefill: exact routing, then grouped bf16-MFMA experts and the
+// Prefill: exact routing, then grouped fp16-MFMA experts and the
 // slot-ordered combine.
 hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st) {
     hipError_t err = launch_router(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.logits,

@@ -19,6 +19,23 @@ __device__ __forceinline__ float rdlane(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
+// Ordered integer key of a float: key(a) < key(b) iff a < b for non-NaN a, b
+// (with -0 just below +0, which never matters here: probabilities are +0 or
+// positive); NaN maps to the lowest key.  topk_unkey inverts it.
+__device__ __forceinline__ int topk_key(float f) {
+    const int b = __builtin_bit_cast(int, f);
+    return f != f ? (int)0x80000000 : b ^ ((b >> 31) & 0x7FFFFFFF);
+}
+__device__ __forceinline__ float topk_unkey(int k) { return __builtin_bit_cast(float, k ^ ((k >> 31) & 0x7FFFFFFF)); }
+// min of two wave-uniform ints as one scalar instruction (left to itself the
+// compiler moves such mins to the vector unit and back, a round trip of
+// latency on every step of the slot scan)
+__device__ __forceinline__ int topk_smin(int a, int b) {
+    int r;
+    asm("s_min_i32 %0, %1, %2" : "=s"(r) : "s"(a), "s"(b) : "scc");
+    return r;
+}
+
 template <int NJ>
 __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int t, float *P,
                                           int *__restrict__ sel_idx, float *__restrict__ sel_w) {
@@ -72,43 +89,88 @@ __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int
     float pr[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) pr[j] = lane + 64 * j < E ? ex[j] / ssum : 0.f;
-    // Slot scan: lane i < k holds slot i (value ws, expert wi); lanes k..7
-    // hold +inf so they never count as the minimum.  wl is the current
-    // minimum over the k slots, which never decreases, and ms the first slot
-    // holding it.  Expert e enters iff pr[e] > wl at its turn (a float
-    // compare, so a NaN never enters): candidates are taken in expert order
-    // from a ballot that is re-filtered against the new minimum after every
-    // entry, so only entries cost a sequential step.
+    // Slot scan.  Values compare as ordered integer keys (key() below: a
+    // float's order for all non-NaN values; a NaN gets the lowest key, so it
+    // never enters, as the reference's float compare never lets it), so the
+    // eight slots live in scalar registers and an entry costs scalar
+    // instructions only.  wl is the current minimum over the k slots (slots
+    // k..7 hold the largest key and never count), which never decreases, and
+    // ms the first slot holding it.  Expert e enters iff key(pr[e]) > wl at
+    // its turn: candidates are taken in expert order from a ballot that is
+    // re-filtered against the new minimum after every entry, so only entries
+    // cost a sequential step.
     const int k = top_k > 8 ? 8 : top_k;
-    float ws = lane < k ? -1e30f : __builtin_huge_valf();
-    int wi = 0;
-    float wl = -1e30f;
-    int ms = 0;
+    constexpr int KMIN = (int)0x80000000;
+    int kx[NJ];   // lanes past E get the lowest key: never a candidate
+#pragma unroll
+    for (int j = 0; j < NJ; j++) kx[j] = lane + 64 * j < E ? topk_key(pr[j]) : KMIN;
+    int sk[8], si[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        sk[s] = s < k ? topk_key(-1e30f) : 0x7FFFFFFF;
+        si[s] = 0;
+    }
+    int wl = topk_key(-1e30f), ms = 0;
+    // min over the slots and the first slot holding it, in scalar registers
+    auto slot_min = [&]() {
+        int m = sk[0];
+#pragma unroll
+        for (int s = 1; s < 8; s++) m = topk_smin(m, sk[s]);
+        wl = m;
+        int f = 7;
+#pragma unroll
+        for (int s = 6; s >= 0; s--) f = sk[s] == m ? s : f;
+        ms = f;
+    };
+    // While slots are empty every probability (>= +0) beats the -1e30 they
+    // hold, so experts 0..k-1 fill slots 0..k-1 unless one of them is NaN
+    // (which never enters); then the scan starts at expert k.
+    unsigned long long skip = 0;
+    if (E >= k && !__ballot(lane < k && kx[0] == KMIN)) {
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            if (s < k) {
+                sk[s] = __builtin_amdgcn_readlane(kx[0], s);
+                si[s] = s;
+            }
+        }
+        slot_min();
+        skip = (1ull << k) - 1;
+    }
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const bool valid = lane + 64 * j < E;
-        unsigned long long cand = __ballot(valid && pr[j] > wl);
+        unsigned long long cand = __ballot(kx[j] > wl) & ~(j == 0 ? skip : 0ull);
         while (cand) {
             const int l = __builtin_ctzll(cand);
-            const float val = rdlane(pr[j], l);
-            if (lane == ms) {
-                ws = val;
-                wi = 64 * j + l;
+            const int val = __builtin_amdgcn_readlane(kx[j], l);
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                sk[s] = s == ms ? val : sk[s];
+                si[s] = s == ms ? 64 * j + l : si[s];
             }
-            wl = rdlane(group8_min(ws), 0);
-            ms = __builtin_ctzll(__ballot(lane < 8 && ws == wl));
+            slot_min();
             cand &= cand - 1;
-            cand &= __ballot(valid && pr[j] > wl);
+            cand &= __ballot(kx[j] > wl);
         }
     }
+    // renormalise over the k slots in slot order (sequential fp32 sum)
     float wsum = 0.f;
-    for (int i = 0; i < k; i++) wsum = wsum + rdlane(ws, i);
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+        if (s < k) wsum = wsum + topk_unkey(sk[s]);
     if (lane < 8) {
+        int io = -1, ks = 0;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            io = lane == s ? si[s] : io;
+            ks = lane == s ? sk[s] : ks;
+        }
         float wo = 0.f;
-        int io = -1;
         if (lane < k) {
+            const float ws = topk_unkey(ks);
             wo = wsum > 0.f ? ws / wsum : ws;
-            io = wi;
+        } else {
+            io = -1;
         }
         sel_idx[t * 8 + lane] = io;
         sel_w[t * 8 + lane] = wo;
