@@ -53,6 +53,8 @@ def parse():
     p.add_argument("--quick", action="store_true", help="skip the sweep/MoE/CPU legs")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--moe-only", action="store_true", help="only the MoE leg (profiling)")
+    p.add_argument("--dense-only", action="store_true", help="only the dense decode leg (profiling)")
+    p.add_argument("--no-dense", action="store_true", help="skip the dense decode leg")
     p.add_argument("--pmc-calib", action="store_true",
                    help="counter-collection run: the headline matvec as direct launches, then a plain "
                         "copy of PMC_COPY_BYTES (the HBM-byte calibration of FETCH_SIZE / WRITE_SIZE)")
@@ -172,6 +174,9 @@ def gpu_leg(args):
     res["abi_matvec_us"] = (time.perf_counter() - t0) / n_abi * 1e6
     log(f"tb_cuda_matvec_device (host x/y, synchronous): {res['abi_matvec_us']:.1f} us/call")
 
+    if args.dense_only:
+        res["dense"] = dense_leg(torch, stream)
+        return res
     if args.moe_only:
         res["moe"] = moe_leg(tb, fm, synth, torch, rng, stream)
         return res
@@ -201,7 +206,52 @@ def gpu_leg(args):
     res["sweep"] = sweep
 
     res["moe"] = moe_leg(tb, fm, synth, torch, rng, stream)
+    if not args.no_dense and not args.quick:
+        res["dense"] = dense_leg(torch, stream)
     return res
+
+
+def dense_leg(torch, stream):
+    """Dense Qwen3-4B-shaped decode: one token at KV context 4096
+    (the cache filled N(0,1), decoding position 4095), random-init Q4_K
+    layers and Q6_K tied embedding/lm_head; one step = one token through 36
+    layers and the lm_head, replayed from a HIP graph.  The matvecs alone
+    (same shapes and weights, one graph) are timed beside it."""
+    from trailblaze_amd import formats as fm
+    from trailblaze_amd.dense import QWEN3_4B, SyntheticDense
+    c = QWEN3_4B
+    m = SyntheticDense(c, seed=4)
+    m.k_cache.normal_()
+    m.v_cache.normal_()
+    logits = torch.empty(c.vocab, dtype=torch.float32, device="cuda")
+    pos = c.max_ctx - 1
+    reps = 20
+    s = time_region(lambda: m.decode(1234, pos, logits), reps, 3, stream)
+    us = s / reps * 1e6
+    shapes = m.matvec_shapes()
+    xs = torch.randn(max(K for _, _, K, _ in shapes), device="cuda")
+    ys = torch.empty(max(M for _, M, _, _ in shapes), device="cuda")
+
+    def mvs():
+        for qt, M, K, W in shapes:
+            tb_matvec(W, qt, M, K, xs, ys)
+    smv = time_region(mvs, reps, 3, stream)
+    mv_us = smv / reps * 1e6
+    wbytes = sum(fm.weight_bytes(qt, M, K) for qt, M, K, _ in shapes)
+    kv_bytes = 2 * c.n_layers * c.n_kv_heads * c.max_ctx * c.head_dim * 4
+    bound_us = (wbytes + kv_bytes) / (HBM_PEAK_GBS * 1e3)
+    log(f"dense Qwen3-4B decode @ctx {c.max_ctx}: {us:.0f} us/token = {1e6 / us:.0f} tok/s; "
+        f"matvecs {mv_us:.0f} us ({wbytes / mv_us / 1e3:.0f} GB/s); HBM bound {bound_us:.0f} us")
+    del m
+    torch.cuda.empty_cache()
+    return dict(us_per_token=us, tokens_per_s=1e6 / us, matvec_us=mv_us, matvec_gbs=wbytes / mv_us / 1e3,
+                other_us=us - mv_us, weight_bytes=wbytes, kv_bytes=kv_bytes, hbm_bound_us=bound_us,
+                frac_of_bound=bound_us / us)
+
+
+def tb_matvec(W, qt, M, K, x, y):
+    import trailblaze_amd as tb
+    tb.matvec(W, qt, M, K, x, y)
 
 
 def moe_leg(tb, fm, synth, torch, rng, stream):
@@ -331,7 +381,7 @@ def main():
         "extra": {"device": res["device"], "warm_mall_gbs": round(h["warm_gbs"], 1),
                   "warm_us_per_launch": round(h["warm_us_per_launch"], 3),
                   "abi_matvec_us": None if res.get("abi_matvec_us") is None else round(res["abi_matvec_us"], 2),
-                  "sweep": res.get("sweep"), "moe": res.get("moe"),
+                  "sweep": res.get("sweep"), "moe": res.get("moe"), "dense": res.get("dense"),
                   "cpu_detail": None if cpu is None else cpu["detail"]},
     }
     print(json.dumps(line), flush=True)

@@ -115,6 +115,47 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
 int tbq_moe_block_host(const tbq_moe_layer *L, int T, const float *xn_host, const float *resid_host,
                        float *out_host, int *sel_idx_host, float *sel_w_host, int mode);
 
+/* ---- dense decode (Qwen3-style transformer, one token) ------------------ */
+/* No counterpart in the reference as an entry point: the reference's forward
+ * is the static tb_layer_forward (layer4/tb_infer.c:553-883), whose
+ * attention path differs from the model's (head_dim, RoPE pairing, QK-norm
+ * order).  This is the model's forward on libtbq's matvecs, for decode
+ * benchmarks and serving; all pointers in the structs are device pointers.
+ * Weights use the reference's row-major block layout; the fused tensors are
+ * the separate GGUF tensors' rows concatenated in the order given. */
+typedef struct {
+    const float *attn_norm;   /* [hidden] */
+    const float *q_norm;      /* [head_dim] */
+    const float *k_norm;      /* [head_dim] */
+    const float *ffn_norm;    /* [hidden] */
+    const void *wqkv;         /* [(n_heads + 2 n_kv_heads) head_dim][hidden]: q | k | v rows */
+    const void *wo;           /* [hidden][n_heads head_dim] */
+    const void *wgu;          /* [2 ffn][hidden]: gate | up rows */
+    const void *wdown;        /* [hidden][ffn] */
+} tbq_dense_layer;
+
+typedef struct {
+    int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx;
+    float norm_eps, rope_theta;
+    int qtype_layers;         /* qtype of wqkv/wo/wgu/wdown (any tbq_matvec qtype) */
+    int qtype_embd;           /* qtype of tok_embd and lm_head */
+    const void *tok_embd;     /* [vocab][hidden] (may alias lm_head: tied embeddings) */
+    const void *lm_head;      /* [vocab][hidden] */
+    const float *output_norm; /* [hidden] */
+    const tbq_dense_layer *layers;   /* host array of n_layers */
+    float *k_cache;           /* [n_layers][n_kv_heads][max_ctx][head_dim] fp32 */
+    float *v_cache;           /* same */
+} tbq_dense_model;
+
+/* Workspace bytes tbq_dense_decode needs (no zero-fill required). */
+size_t tbq_dense_workspace_size(const tbq_dense_model *m);
+/* logits[vocab] for `token` at position `pos` (0 <= pos < max_ctx); appends
+ * the token's K and V at `pos` of every layer's cache and attends over
+ * positions 0..pos.  head_dim 64 or 128; n_heads / n_kv_heads in {1, 2, 4,
+ * 8}; hidden, ffn and n_heads*head_dim multiples of 256. */
+int tbq_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
 /* ---- test hooks -------------------------------------------------------- */
 /* out[i] = expf(in[i]) evaluated by the device code the router uses. */
 int tbq_expf_device(const float *in, float *out, size_t n, void *stream);

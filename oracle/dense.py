@@ -1,0 +1,104 @@
+"""Float64 restatement of one dense (Qwen3-style) decode step, the checker for
+tbq_dense_decode.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/ (and nothing in the product).
+
+The layer is the model's forward, not the reference's: the reference's
+tb_layer_forward (layer4/tb_infer.c:553-883) takes head_dim = hidden /
+n_heads when the file gives none, applies RoPE with interleaved pairs
+(tb_rope_apply, :142-153) to each K head n_heads / n_kv_heads times, and
+applies QK-norm after RoPE.  Here QK-norm comes first, RoPE rotates the
+pairs (i, i + D/2) once per head, and head_dim is the model's.  The pieces
+that agree with the reference are its rmsnorm (layer1/tb_tensor.c:194-199:
+x * (1 / sqrt(mean(x^2) + eps)) * w), its online-softmax GQA attention
+(layer1/tb_tensor.c:300-405: kv head = h / (n_heads / n_kv_heads), scale
+1/sqrt(D)), SwiGLU (layer4/tb_infer.c:130-135) and the dequantised matvecs
+(pinned bit-exact elsewhere).  No reference test covers this forward:
+parity unpinned against the reference; the functions below are pinned by
+the closed-form checks in tests/test_oracle.py (RoPE: rotation, norm and
+relative-position invariance; attention: brute-force softmax; rmsnorm).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def rmsnorm(x, w, eps):
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt(np.mean(x * x) + eps) * np.asarray(w, np.float64)
+
+
+def rope(x, pos, theta):
+    """Rotate-half RoPE of one head vector x (length D) at position pos."""
+    x = np.asarray(x, np.float64)
+    D = x.size
+    j = np.arange(D // 2)
+    ang = pos * theta ** (-2.0 * j / D)
+    c, s = np.cos(ang), np.sin(ang)
+    a, b = x[:D // 2], x[D // 2:]
+    return np.concatenate([a * c - b * s, a * s + b * c])
+
+
+def attention(q, kc, vc, n_pos):
+    """q [NQ][D]; kc, vc [NKV][>=n_pos][D]; softmax(q k / sqrt(D)) v over
+    positions 0..n_pos-1, query head h on kv head h // (NQ / NKV)."""
+    NQ, D = q.shape
+    G = NQ // kc.shape[0]
+    out = np.empty((NQ, D))
+    for h in range(NQ):
+        k = kc[h // G, :n_pos].astype(np.float64)
+        v = vc[h // G, :n_pos].astype(np.float64)
+        s = k @ q[h] / np.sqrt(D)
+        p = np.exp(s - s.max())
+        out[h] = p @ v / p.sum()
+    return out
+
+
+def silu_mul(g, u):
+    return g / (1.0 + np.exp(-g)) * u
+
+
+class DenseOracle:
+    """Dequantises the model's weights once (oracle.dequant_rows, bit-exact to
+    the reference's decoders) and runs decode steps in float64 with its own
+    fp64 KV cache."""
+
+    def __init__(self, oracle, cfg, host):
+        c = self.cfg = cfg
+        deq = lambda W, qt, M, K: oracle.dequant_rows(W, qt, M, K).astype(np.float64)
+        QR = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
+        self.layers = []
+        for t in host["layers"]:
+            self.layers.append({
+                "attn_norm": t["attn_norm"], "q_norm": t["q_norm"], "k_norm": t["k_norm"],
+                "ffn_norm": t["ffn_norm"],
+                "wqkv": deq(t["wqkv"], c.qtype_layers, QR, c.hidden),
+                "wo": deq(t["wo"], c.qtype_layers, c.hidden, c.n_heads * c.head_dim),
+                "wgu": deq(t["wgu"], c.qtype_layers, 2 * c.ffn, c.hidden),
+                "wdown": deq(t["wdown"], c.qtype_layers, c.hidden, c.ffn)})
+        self.lm = deq(host["lm_head"], c.qtype_embd, c.vocab, c.hidden)
+        self.output_norm = host["output_norm"]
+        shape = (c.n_layers, c.n_kv_heads, c.max_ctx, c.head_dim)
+        self.kc = np.zeros(shape)
+        self.vc = np.zeros(shape)
+
+    def decode(self, token, pos):
+        c = self.cfg
+        D, NQ, NKV = c.head_dim, c.n_heads, c.n_kv_heads
+        x = self.lm[token].copy()           # tied embeddings: tok_embd is lm_head
+        for l, L in enumerate(self.layers):
+            h = rmsnorm(x, L["attn_norm"], c.norm_eps)
+            qkv = L["wqkv"] @ h
+            q = qkv[:NQ * D].reshape(NQ, D)
+            k = qkv[NQ * D:(NQ + NKV) * D].reshape(NKV, D)
+            v = qkv[(NQ + NKV) * D:].reshape(NKV, D)
+            q = np.stack([rope(rmsnorm(q[i], L["q_norm"], c.norm_eps), pos, c.rope_theta) for i in range(NQ)])
+            k = np.stack([rope(rmsnorm(k[i], L["k_norm"], c.norm_eps), pos, c.rope_theta) for i in range(NKV)])
+            self.kc[l, :, pos] = k
+            self.vc[l, :, pos] = v
+            att = attention(q, self.kc[l], self.vc[l], pos + 1)
+            x = x + L["wo"] @ att.reshape(-1)
+            h = rmsnorm(x, L["ffn_norm"], c.norm_eps)
+            gu = L["wgu"] @ h
+            x = x + L["wdown"] @ silu_mul(gu[:c.ffn], gu[c.ffn:])
+        return self.lm @ rmsnorm(x, self.output_norm, c.norm_eps)

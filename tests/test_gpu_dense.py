@@ -1,0 +1,92 @@
+"""GPU parity of tbq_dense_decode (one-token decode of a dense Qwen3-style
+model, BASELINE configs[2]'s forward) against the float64 oracle in
+oracle/dense.py, through the C-ABI: logits within rel-L2 DENSE_TOL of the
+oracle at every step, and the K/V appended to the cache.  Cases: GQA group
+sizes 2 and 4, head_dim 64 and 128, a context that spans several attention
+chunks, and a second layer format."""
+import numpy as np
+import pytest
+
+import trailblaze_amd as tb
+from conftest import rel_l2
+from gpu_util import host
+from trailblaze_amd import formats as fm
+
+pytestmark = pytest.mark.gpu
+# fp32 kernels (int-dot matvecs, fp32 norms and attention) against float64
+DENSE_TOL = 1e-4
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    print("device:", tb.init(), flush=True)
+
+
+def _model(cfg, seed):
+    from trailblaze_amd.dense import SyntheticDense
+    return SyntheticDense(cfg, seed, keep_host=True)
+
+
+def test_dense_decode_steps(oracle):
+    """Five consecutive tokens from an empty cache (GQA 2, head_dim 64)."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=512,
+                      max_ctx=256)
+    m = _model(cfg, 1)
+    ref = DenseOracle(oracle, cfg, m.host)
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    for pos, tok in enumerate([3, 200, 17, 511, 0]):
+        print("dense step", pos, flush=True)
+        m.decode(tok, pos, logits)
+        want = ref.decode(tok, pos)
+        err = rel_l2(host(logits), want)
+        assert err <= DENSE_TOL, (pos, err)
+    kc = host(m.k_cache).reshape(ref.kc.shape)
+    vc = host(m.v_cache).reshape(ref.vc.shape)
+    assert rel_l2(kc[:, :, :5], ref.kc[:, :, :5]) <= DENSE_TOL
+    assert rel_l2(vc[:, :, :5], ref.vc[:, :, :5]) <= DENSE_TOL
+    assert not np.any(kc[:, :, 5:])   # nothing written past pos
+
+
+@pytest.mark.parametrize("qt", [fm.Q4_K, fm.Q8_0])
+def test_dense_decode_long_context(oracle, qt):
+    """GQA 4, head_dim 128, a cache pre-filled to position 299 (three
+    attention chunks), decode at 300 and 301."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=1, hidden=512, n_heads=8, n_kv_heads=2, head_dim=128, ffn=768, vocab=256,
+                      max_ctx=512, qtype_layers=qt)
+    m = _model(cfg, 2)
+    ref = DenseOracle(oracle, cfg, m.host)
+    rng = np.random.default_rng(5)
+    P = 300
+    kc = np.zeros(ref.kc.shape, np.float32)
+    vc = np.zeros(ref.vc.shape, np.float32)
+    kc[:, :, :P] = rng.standard_normal(kc[:, :, :P].shape)
+    vc[:, :, :P] = rng.standard_normal(vc[:, :, :P].shape)
+    m.k_cache.copy_(torch.from_numpy(kc))
+    m.v_cache.copy_(torch.from_numpy(vc))
+    ref.kc[:] = kc
+    ref.vc[:] = vc
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    for pos, tok in ((P, 7), (P + 1, 255)):
+        print("dense long-context step", pos, flush=True)
+        m.decode(tok, pos, logits)
+        err = rel_l2(host(logits), ref.decode(tok, pos))
+        assert err <= DENSE_TOL, (pos, err)
+
+
+def test_dense_decode_rejects_bad_position():
+    import torch
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=1, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=256, vocab=256,
+                      max_ctx=16)
+    m = _model(cfg, 3)
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    with pytest.raises(tb.TbqError, match="pos"):
+        m.decode(0, 16, logits)
+    with pytest.raises(tb.TbqError, match="token"):
+        m.decode(256, 0, logits)

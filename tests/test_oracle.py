@@ -294,3 +294,47 @@ def test_route_vs_compiled_reference(oracle, reference):
         i1, w1 = oracle.route(lg, k)
         i2, w2 = reference.route(lg, k)
         assert np.array_equal(i1, i2) and bits_equal(w1, w2)
+
+
+# --------------------------------------------------------------------------
+# Dense decode oracle (oracle/dense.py): closed forms that a wrong index,
+# sign or pairing breaks.
+# --------------------------------------------------------------------------
+def test_dense_rope_closed_forms():
+    from oracle.dense import rope
+    rng = np.random.default_rng(3)
+    D, theta = 64, 1e6
+    q, k = rng.standard_normal(D), rng.standard_normal(D)
+    assert np.allclose(rope(q, 0, theta), q)                               # identity at 0
+    assert np.isclose(np.linalg.norm(rope(q, 37, theta)), np.linalg.norm(q))   # a rotation
+    # pair (0, D/2) turns by exactly pos radians (frequency theta^0 = 1)
+    e = np.zeros(D)
+    e[0] = 1.0
+    r = rope(e, 5, theta)
+    assert np.isclose(r[0], np.cos(5)) and np.isclose(r[D // 2], np.sin(5))
+    assert np.allclose(np.delete(r, [0, D // 2]), 0)
+    # scores depend on the position difference only
+    for m, n, t in ((3, 1, 10), (100, 7, 1000), (4095, 0, 1)):
+        a = rope(q, m, theta) @ rope(k, n, theta)
+        b = rope(q, m + t, theta) @ rope(k, n + t, theta)
+        assert np.isclose(a, b, rtol=1e-9, atol=1e-9)
+
+
+def test_dense_attention_and_rmsnorm_closed_forms():
+    from oracle.dense import attention, rmsnorm
+    rng = np.random.default_rng(4)
+    NQ, NKV, D, n = 8, 2, 16, 11
+    q = rng.standard_normal((NQ, D))
+    kc = rng.standard_normal((NKV, 20, D))
+    vc = rng.standard_normal((NKV, 20, D))
+    out = attention(q, kc, vc, n)
+    for h in range(NQ):          # brute force: explicit softmax weights
+        g = h // (NQ // NKV)
+        w = np.array([np.exp(q[h] @ kc[g, p] / np.sqrt(D)) for p in range(n)])
+        assert np.allclose(out[h], sum(w[p] * vc[g, p] for p in range(n)) / w.sum())
+    assert np.allclose(attention(q, kc, vc, 1), np.repeat(vc[:, :1], NQ // NKV, axis=0).reshape(NQ, D))
+    assert np.allclose(attention(np.zeros((NQ, D)), kc, vc, n),
+                       np.repeat(vc[:, :n].mean(1), NQ // NKV, axis=0))
+    x = np.full(32, 3.0)
+    assert np.allclose(rmsnorm(x, np.full(32, 2.0), 0.0), 2.0)
+    assert np.allclose(rmsnorm(-x, np.ones(32), 0.0), -1.0)

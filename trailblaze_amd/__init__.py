@@ -47,6 +47,8 @@ SYMBOLS = {
     "tbq_moe_workspace_size": (_sz, [_vp, _i, _i]),
     "tbq_moe_forward": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _vp]),
     "tbq_moe_block_host": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _i]),
+    "tbq_dense_workspace_size": (_sz, [_vp]),
+    "tbq_dense_decode": (_i, [_vp, _i, _i, _vp, _vp, _sz, _vp]),
     "tbq_expf_device": (_i, [_vp, _vp, _sz, _vp]),
     "tbq_expf_host": (_f, [_f]),
     # include/tb_gguf_dequant.h (the reference ABI)

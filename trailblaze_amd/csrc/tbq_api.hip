@@ -264,6 +264,47 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     return hip_ok(launch_moe_fp32(a, S(s)), "moe launch");
 }
 
+static int check_dense(const tbq_dense_model *m) {
+    if (!m || !m->layers) return fail("tbq_dense: null model");
+    if (m->n_layers <= 0 || m->hidden <= 0 || m->n_heads <= 0 || m->n_kv_heads <= 0 || m->ffn <= 0 || m->vocab <= 0 ||
+        m->max_ctx <= 0)
+        return fail("tbq_dense: non-positive size");
+    if (m->head_dim != 64 && m->head_dim != 128) return fail("tbq_dense: head_dim must be 64 or 128");
+    const int G = m->n_heads / m->n_kv_heads;
+    if (m->n_heads % m->n_kv_heads || (G != 1 && G != 2 && G != 4 && G != 8))
+        return fail("tbq_dense: n_heads / n_kv_heads must be 1, 2, 4 or 8");
+    if (m->hidden % 256 || m->ffn % 256 || (m->n_heads * m->head_dim) % 256)
+        return fail("tbq_dense: hidden, ffn and n_heads*head_dim must be multiples of 256");
+    if (!tbq_qtype_supported(m->qtype_layers) || !tbq_qtype_supported(m->qtype_embd))
+        return fail("tbq_dense: unsupported qtype");
+    if (!m->tok_embd || !m->lm_head || !m->output_norm || !m->k_cache || !m->v_cache)
+        return fail("tbq_dense: null tensor");
+    for (int l = 0; l < m->n_layers; l++) {
+        const tbq_dense_layer &L = m->layers[l];
+        if (!L.attn_norm || !L.q_norm || !L.k_norm || !L.ffn_norm || !L.wqkv || !L.wo || !L.wgu || !L.wdown)
+            return fail("tbq_dense: null tensor in layer %d", l);
+        if (!aligned16(L.wqkv) || !aligned16(L.wo) || !aligned16(L.wgu) || !aligned16(L.wdown))
+            return fail("tbq_dense: layer %d weights must be 16-byte aligned", l);
+    }
+    return 1;
+}
+
+size_t tbq_dense_workspace_size(const tbq_dense_model *m) {
+    if (!check_dense(m)) return 0;
+    return dense_workspace_bytes(m);
+}
+
+int tbq_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *workspace,
+                     size_t ws_bytes, void *s) {
+    if (!ensure_init()) return 0;
+    if (!check_dense(m)) return 0;
+    if (token < 0 || token >= m->vocab) return fail("tbq_dense_decode: token %d out of range", token);
+    if (pos < 0 || pos >= m->max_ctx) return fail("tbq_dense_decode: pos %d out of range", pos);
+    if (!logits || !workspace) return fail("tbq_dense_decode: null logits or workspace");
+    if (ws_bytes < dense_workspace_bytes(m)) return fail("tbq_dense_decode: workspace too small");
+    return hip_ok(launch_dense_decode(m, token, pos, logits, workspace, S(s)), "dense decode launch");
+}
+
 int tbq_expf_device(const float *in, float *out, size_t n, void *s) {
     if (!ensure_init()) return 0;
     if (!in || !out) return fail("tbq_expf_device: null pointer");

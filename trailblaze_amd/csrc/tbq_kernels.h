@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "../../include/tbq.h"
+
 namespace tbq {
 
 struct MoeArgs {
@@ -34,5 +36,8 @@ hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st);
 size_t prefill_workspace_bytes(int T, int k, int E, int H, int F);
 hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t st);
 hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st);
+size_t dense_workspace_bytes(const tbq_dense_model *m);
+hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,
+                               hipStream_t st);
 
 }  // namespace tbq
