@@ -116,11 +116,13 @@ int tbq_moe_block_host(const tbq_moe_layer *L, int T, const float *xn_host, cons
                        float *out_host, int *sel_idx_host, float *sel_w_host, int mode);
 
 /* ---- dense decode (Qwen3-style transformer, one token) ------------------ */
-/* No counterpart in the reference as an entry point: the reference's forward
- * is the static tb_layer_forward (layer4/tb_infer.c:553-883), whose
- * attention path differs from the model's (head_dim, RoPE pairing, QK-norm
- * order).  This is the model's forward on libtbq's matvecs, for decode
- * benchmarks and serving; all pointers in the structs are device pointers.
+/* The step of tb_infer_decode (layer4/tb_infer.c:889-1050: embedding row,
+ * layers, output_norm, lm_head falling back to token_embd) for a dense
+ * model.  The reference's layer is the static tb_layer_forward
+ * (layer4/tb_infer.c:553-883), whose attention path differs from the
+ * model's (head_dim, RoPE pairing, QK-norm order).  This is the model's
+ * forward on libtbq's matvecs, for decode benchmarks and serving; all
+ * pointers in the structs are device pointers.
  * Weights use the reference's row-major block layout; the fused tensors are
  * the separate GGUF tensors' rows concatenated in the order given. */
 typedef struct {
