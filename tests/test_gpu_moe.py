@@ -17,6 +17,7 @@ from trailblaze_amd import synth
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
+COUNTER_BYTES = 256 * 1024   # counter area at the start of the MoE workspace
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -45,7 +46,15 @@ def gpu_moe(xn, resid, router, gate, up, down, F, k, qt, bias=None, mode=tb.TBQ_
     w = empty(T * 8, torch.float32)
     ws = torch.zeros(tb.moe_workspace_size(L, T, mode), dtype=torch.uint8, device="cuda")
     tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws, mode=mode)
+    assert_counters_zero(ws)
     return host(out).reshape(T, H), host(idx).reshape(T, 8), host(w).reshape(T, 8)
+
+
+def assert_counters_zero(ws):
+    """The workspace's counter words (the router's per-token arrival
+    counters) are zero after every call."""
+    c = host(ws[:COUNTER_BYTES])
+    assert not c.any(), np.flatnonzero(c.view(np.uint32))[:8]
 
 
 def test_route_golden_logit_vectors(oracle):
@@ -178,6 +187,30 @@ def test_moe_decode_router_many_tokens(oracle):
             ri, rw = oracle.route(lg[t], k)
             assert np.array_equal(idx[t], ri), (b, t)
             assert bits_equal(w[t], rw), (b, t)
+
+
+def test_moe_decode_repeated_calls(oracle):
+    """One workspace across calls of different batch sizes (1, 16, 3, 1):
+    outputs in tolerance every time and the counter words back at zero
+    after each call."""
+    import torch
+    H, F, E, k = 2048, 256, 128, 8
+    router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=52)
+    L = tb.moe_layer(H, F, E, k, fm.Q4_K, dev(router), dev(gate), dev(up), dev(down))
+    ws = torch.zeros(tb.moe_workspace_size(L, 16), dtype=torch.uint8, device="cuda")
+    rng = np.random.default_rng(52)
+    for T in (1, 16, 3, 1):
+        print("moe repeated call T=", T, flush=True)
+        xn = synth.activations((T, H), rng)
+        resid = synth.activations((T, H), rng)
+        out = empty(T * H, torch.float32)
+        idx = empty(T * 8, torch.int32)
+        w = empty(T * 8, torch.float32)
+        tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws)
+        ref, ridx, _ = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
+        assert np.array_equal(host(idx).reshape(T, 8), ridx), T
+        assert rel_l2(host(out).reshape(T, H) - resid, ref - resid) <= TOL, T
+        assert_counters_zero(ws)
 
 
 @pytest.mark.parametrize("case", ["tie4", "tie_boundary", "near_tie", "underflow"])

@@ -277,15 +277,20 @@ __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn,
     router_dpp_chunks<0, NC>(w4, x4, j, wb, xb, acc);
     if (j == 15 && ev) {
         if (bias) acc = acc + bias[e];
-        logits[(long long)t * E + e] = acc;
+        __hip_atomic_store(logits + (long long)t * E + e, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // last arriving workgroup of this token does the top-k
-    __threadfence();
+    // The last arriving workgroup of this token does the top-k.  The logits
+    // cross workgroups as device-scope atomic stores and loads (coherent
+    // across the XCDs' L2s without a cache write-back or invalidate, which a
+    // device-scope fence would cost in every workgroup): each workgroup
+    // waits until its stores have completed before it takes its ticket, and
+    // the last one reads the logits with device-scope atomic loads.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     unsigned ticket = 0;
-    if (lane == 0) ticket = atomicAdd(counters + t, 1u);
+    if (lane == 0) ticket = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     ticket = (unsigned)__builtin_amdgcn_readfirstlane((int)ticket);
     if (ticket != gridDim.y - 1) return;
-    __threadfence();
+    asm volatile("" ::: "memory");
     topk_wave<NJ>(logits + (long long)t * E, E, top_k, t, P, sel_idx, sel_w);
     if (lane == 0) counters[t] = 0u;
 }
@@ -296,8 +301,14 @@ __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn,
 // [32, 64) the up row (LPR = 32 lanes hold one 64-weight unit each when
 // H = 2048; larger H loops units).
 // ---------------------------------------------------------------------------
-constexpr int GU_THREADS = 512;
-constexpr int GU_ROWS = 2;   // output rows per wave
+#ifndef TBQ_GU_WAVES
+#define TBQ_GU_WAVES 8
+#endif
+#ifndef TBQ_GU_ROWS
+#define TBQ_GU_ROWS 2
+#endif
+constexpr int GU_THREADS = 64 * TBQ_GU_WAVES;
+constexpr int GU_ROWS = TBQ_GU_ROWS;   // output rows per wave
 
 template <int UPL>
 __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
@@ -314,7 +325,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
     const uint8_t *Wb = (half ? up : gate) + (long long)e * F * rb;
     const int r0 = (blockIdx.x * (GU_THREADS / 64) + wave) * GU_ROWS;
 
-    XStager<GU_THREADS, 2> xs;   // H <= 8192
+    XStager<GU_THREADS, (1024 + GU_THREADS - 1) / GU_THREADS> xs;   // H <= 8192
     xs.load(xn + (long long)t * H, H);
     Q4KUnit raw[GU_ROWS][UPL];
 #pragma unroll

@@ -27,15 +27,6 @@ __device__ __forceinline__ int topk_key(float f) {
     return f != f ? (int)0x80000000 : b ^ ((b >> 31) & 0x7FFFFFFF);
 }
 __device__ __forceinline__ float topk_unkey(int k) { return __builtin_bit_cast(float, k ^ ((k >> 31) & 0x7FFFFFFF)); }
-// min of two wave-uniform ints as one scalar instruction (left to itself the
-// compiler moves such mins to the vector unit and back, a round trip of
-// latency on every step of the slot scan)
-__device__ __forceinline__ int topk_smin(int a, int b) {
-    int r;
-    asm("s_min_i32 %0, %1, %2" : "=s"(r) : "s"(a), "s"(b) : "scc");
-    return r;
-}
-
 template <int NJ>
 __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int t, float *P,
                                           int *__restrict__ sel_idx, float *__restrict__ sel_w) {
@@ -45,7 +36,7 @@ __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? __builtin_nontemporal_load(lg + e) : NEG;
+        v[j] = e < E ? __hip_atomic_load(lg + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : NEG;
     }
     float m = v[0];
 #pragma unroll
@@ -89,51 +80,39 @@ __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int
     float pr[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) pr[j] = lane + 64 * j < E ? ex[j] / ssum : 0.f;
-    // Slot scan.  Values compare as ordered integer keys (key() below: a
+    // Slot scan.  Values compare as ordered integer keys (topk_key: a
     // float's order for all non-NaN values; a NaN gets the lowest key, so it
-    // never enters, as the reference's float compare never lets it), so the
-    // eight slots live in scalar registers and an entry costs scalar
-    // instructions only.  wl is the current minimum over the k slots (slots
-    // k..7 hold the largest key and never count), which never decreases, and
-    // ms the first slot holding it.  Expert e enters iff key(pr[e]) > wl at
-    // its turn: candidates are taken in expert order from a ballot that is
-    // re-filtered against the new minimum after every entry, so only entries
-    // cost a sequential step.
+    // never enters, as the reference's float compare never lets it).  The
+    // eight slots live in lanes 0..7 of vk (key) and vi (expert); slots k..7
+    // and lanes past 7 hold the largest key and never count.  wl is the
+    // current minimum over the slots (a DPP min over the 8 lanes), which never
+    // decreases, and ms the first slot holding it (lowest set bit of a
+    // ballot).  Expert e enters iff key(pr[e]) > wl at its turn: candidates
+    // are taken in expert order from a ballot that is re-filtered against the
+    // new minimum after every entry, so only entries cost a sequential step,
+    // and an entry is a handful of instructions.
     const int k = top_k > 8 ? 8 : top_k;
-    constexpr int KMIN = (int)0x80000000;
+    constexpr int KMIN = (int)0x80000000, KMAX = 0x7FFFFFFF;
     int kx[NJ];   // lanes past E get the lowest key: never a candidate
 #pragma unroll
     for (int j = 0; j < NJ; j++) kx[j] = lane + 64 * j < E ? topk_key(pr[j]) : KMIN;
-    int sk[8], si[8];
-#pragma unroll
-    for (int s = 0; s < 8; s++) {
-        sk[s] = s < k ? topk_key(-1e30f) : 0x7FFFFFFF;
-        si[s] = 0;
-    }
+    int vk = lane < k ? topk_key(-1e30f) : KMAX, vi = 0;
     int wl = topk_key(-1e30f), ms = 0;
-    // min over the slots and the first slot holding it, in scalar registers
     auto slot_min = [&]() {
-        int m = sk[0];
-#pragma unroll
-        for (int s = 1; s < 8; s++) m = topk_smin(m, sk[s]);
-        wl = m;
-        int f = 7;
-#pragma unroll
-        for (int s = 6; s >= 0; s--) f = sk[s] == m ? s : f;
-        ms = f;
+        int m = vk;
+        m = min(m, __builtin_amdgcn_mov_dpp(m, DPP_QXOR1, 0xF, 0xF, false));
+        m = min(m, __builtin_amdgcn_mov_dpp(m, DPP_QXOR2, 0xF, 0xF, false));
+        m = min(m, __builtin_amdgcn_mov_dpp(m, DPP_HALF_MIRROR, 0xF, 0xF, false));
+        wl = __builtin_amdgcn_readfirstlane(m);
+        ms = __builtin_ctzll(__ballot(vk == wl));
     };
     // While slots are empty every probability (>= +0) beats the -1e30 they
     // hold, so experts 0..k-1 fill slots 0..k-1 unless one of them is NaN
     // (which never enters); then the scan starts at expert k.
     unsigned long long skip = 0;
     if (E >= k && !__ballot(lane < k && kx[0] == KMIN)) {
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            if (s < k) {
-                sk[s] = __builtin_amdgcn_readlane(kx[0], s);
-                si[s] = s;
-            }
-        }
+        vk = lane < k ? kx[0] : KMAX;
+        vi = lane;
         slot_min();
         skip = (1ull << k) - 1;
     }
@@ -143,15 +122,18 @@ __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int
         while (cand) {
             const int l = __builtin_ctzll(cand);
             const int val = __builtin_amdgcn_readlane(kx[j], l);
-#pragma unroll
-            for (int s = 0; s < 8; s++) {
-                sk[s] = s == ms ? val : sk[s];
-                si[s] = s == ms ? 64 * j + l : si[s];
-            }
+            vk = lane == ms ? val : vk;
+            vi = lane == ms ? 64 * j + l : vi;
             slot_min();
             cand &= cand - 1;
             cand &= __ballot(kx[j] > wl);
         }
+    }
+    int sk[8], si[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        sk[s] = __builtin_amdgcn_readlane(vk, s);
+        si[s] = __builtin_amdgcn_readlane(vi, s);
     }
     // renormalise over the k slots in slot order (sequential fp32 sum)
     float wsum = 0.f;
