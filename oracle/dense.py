@@ -55,7 +55,8 @@ def attention(q, kc, vc, n_pos):
 
 
 def silu_mul(g, u):
-    return g / (1.0 + np.exp(-g)) * u
+    with np.errstate(over="ignore"):   # exp(-g) = inf for g << 0 gives g / inf = -0, the limit
+        return g / (1.0 + np.exp(-g)) * u
 
 
 class DenseOracle:

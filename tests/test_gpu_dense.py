@@ -79,6 +79,27 @@ def test_dense_decode_long_context(oracle, qt):
         assert err <= DENSE_TOL, (pos, err)
 
 
+def test_dense_decode_qwen3_4b_layer(oracle):
+    """One layer at the Qwen3-4B widths (hidden 2560, 32/8 heads of 128, ffn
+    9728), so every matvec runs the kernel and staging prologue the full
+    model uses: add+RMSNorm into the q|k|v (register-x Q4_K kernel) and
+    gate|up (K-quant kernel, 19456 rows) stagings, SwiGLU into the down
+    staging (K = 9728 over three slices), the final norm into a Q6_K lm_head."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=1, hidden=2560, n_heads=32, n_kv_heads=8, head_dim=128, ffn=9728, vocab=1024,
+                      max_ctx=64)
+    m = _model(cfg, 4)
+    ref = DenseOracle(oracle, cfg, m.host)
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    for pos, tok in enumerate([11, 1000, 5]):
+        print("dense qwen3-4b-width step", pos, flush=True)
+        m.decode(tok, pos, logits)
+        err = rel_l2(host(logits), ref.decode(tok, pos))
+        assert err <= DENSE_TOL, (pos, err)
+
+
 def test_dense_decode_rejects_bad_position():
     import torch
     from trailblaze_amd.dense import DenseConfig

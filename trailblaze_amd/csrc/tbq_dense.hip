@@ -2,16 +2,16 @@
 // on gfx950, built on libtbq's K-quant matvecs.
 //
 // Per layer (x: fp32 residual stream, h: normed activations):
-//   h = rmsnorm(x += y_prev) * attn_norm           k_add_rmsnorm
-//   qkv = Wqkv h   (q | k | v rows, Q4_K)           tbq_matvec
+//   h = rmsnorm(x += y_prev) * attn_norm           } one matvec launch: the
+//   qkv = Wqkv h   (q | k | v rows, Q4_K)           } norm is its x staging
 //   per head: rmsnorm(q_h) * q_norm, rmsnorm(k_h) * k_norm, RoPE (rotate-half
 //   pairs i, i + D/2, angle pos * theta^(-2i/D)); k, v appended to the cache;
 //   attn = softmax(q K^T / sqrt(D)) V over positions 0..pos, GQA
 //                                                    k_attn_partial + k_attn_combine
 //   y = Wo attn                                      tbq_matvec
-//   h = rmsnorm(x += y) * ffn_norm                   k_add_rmsnorm
-//   gu = Wgu h     (gate | up rows)                  tbq_matvec
-//   a = silu(g) * u                                  k_swiglu
+//   h = rmsnorm(x += y) * ffn_norm                   } one matvec launch: the
+//   gu = Wgu h     (gate | up rows)                  } norm is its x staging,
+//   a = silu(g) * u                                  } silu(g) * u its epilogue
 //   y = Wdown a                                      tbq_matvec
 // then h = rmsnorm(x += y) * output_norm and logits = Wlm h.  The token's
 // embedding is row `token` of tok_embd, dequantised exactly.
@@ -21,7 +21,8 @@
 // rotated once.  The reference's forward (layer4/tb_infer.c:553-883)
 // differs in each of these; its rmsnorm (layer1/tb_tensor.c:194-199) and
 // online-softmax attention (layer1/tb_tensor.c:300-405) compute the same
-// functions as k_add_rmsnorm and the attention kernels here.
+// functions as the matvecs' PRO_NORM staging prologue and the attention
+// kernels here.
 //
 // Attention: the cache is [layer][kv head][max_ctx][D] fp32.  A workgroup
 // owns one kv head and a chunk of ATT_CH positions and serves all G query
@@ -50,23 +51,25 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return s;
 }
 
-// x += y (y may be null), h = x * rsqrt(mean(x^2) + eps) * w.  One workgroup.
-__global__ __launch_bounds__(1024) void k_add_rmsnorm(float *__restrict__ x, const float *__restrict__ y,
+// v = x + y (y may be null), h = v * rsqrt(mean(v^2) + eps) * w, and v
+// stored to vo when vo is not null.  One workgroup.  Used where the matvec
+// that follows has no fused staging prologue for the shape.
+__global__ __launch_bounds__(1024) void k_add_rmsnorm(const float *__restrict__ x, const float *__restrict__ y,
                                                       const float *__restrict__ w, int n, float eps,
-                                                      float *__restrict__ h) {
+                                                      float *__restrict__ h, float *__restrict__ vo) {
     __shared__ float red[16];
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = x[i];
-        if (y) {
-            v = v + y[i];
-            x[i] = v;
-        }
+        const float v = y ? x[i] + y[i] : x[i];
         ss += v * v;
     }
     ss = block_sum(ss, red);
     const float r = 1.0f / sqrtf(ss / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) h[i] = x[i] * r * w[i];
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = y ? x[i] + y[i] : x[i];
+        if (vo) vo[i] = v;
+        h[i] = v * r * w[i];
+    }
 }
 
 // RoPE table of one step: rc[j] = cos, rc[D/2 + j] = sin of pos *
@@ -290,17 +293,14 @@ __global__ __launch_bounds__(D) void k_attn_combine(const float *__restrict__ pa
     out[h * D + d] = num / den;
 }
 
-// a = silu(g) * u with gu = [g (n) | u (n)].
+// a = silu(g) * u with gu = [g (n) | u (n)] (unfused fallback).
 __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, int n, float *__restrict__ a) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) {
-        const float g = gu[i], u = gu[n + i];
-        a[i] = g / (1.0f + expf(-g)) * u;
-    }
+    if (i < n) a[i] = pro_swiglu(gu[i], gu[n + i]);
 }
 
 struct DenseWs {
-    float *x, *h, *qkv, *att, *y, *gu, *a, *part, *rope;
+    float *x, *x2, *h, *qkv, *att, *y, *gu, *a, *part, *rope;
 };
 
 static size_t up256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -317,6 +317,7 @@ static DenseWs dense_ws(const tbq_dense_model *m, void *ws, size_t *total) {
     };
     DenseWs w;
     w.x = take(H);
+    w.x2 = take(H);
     w.h = take(H);
     w.qkv = take(QD + 2 * KD);
     w.att = take(QD);
@@ -363,40 +364,68 @@ static hipError_t launch_attn_d(int G, const float *qkv, const float *qn, const 
     }
 }
 
-// Validation happens in the C-ABI wrapper; the matvecs go through the same
-// dispatch as tbq_matvec.
+// out = W prologue(x) for one matvec of the step (mode = PRO_* | MV_GLU):
+// the kernels with the fused staging prologue / GLU epilogue where they
+// cover the shape (the same choice of kernel as tbq_matvec otherwise), else
+// the elementwise steps as launches of their own around tbq_matvec, through
+// tmp_x (K floats) and tmp_y (2M floats, MV_GLU only).
+static hipError_t dense_mv(int qt, const void *W, int M, int K, const float *x, float *out, int mode, const MvPro &pro,
+                           float *tmp_x, float *tmp_y, hipStream_t st) {
+    hipError_t e = hipErrorNotSupported;
+    if (qt == QT_Q4_K && K <= 4096 && M <= 8192) e = launch_matvec_q4k_pro(mode, pro, W, M, K, x, out, st);
+    if (e == hipErrorNotSupported) e = launch_matvec_kq_pro(mode, pro, qt, W, M, K, x, out, st, tbq_cu_count());
+    if (e != hipErrorNotSupported) return e;
+    const float *xin = x;
+    if (mode & PRO_NORM) {
+        hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(1024), 0, st, x, pro.y, pro.w, K, pro.eps, tmp_x, pro.vo);
+        xin = tmp_x;
+    }
+    if (!(mode & MV_GLU)) return tbq_matvec(W, qt, M, K, xin, out, st) ? hipSuccess : hipErrorUnknown;
+    if (!tbq_matvec(W, qt, 2 * M, K, xin, tmp_y, st)) return hipErrorUnknown;
+    hipLaunchKernelGGL(k_swiglu, dim3((M + 255) / 256), dim3(256), 0, st, tmp_y, M, out);
+    return hipGetLastError();
+}
+
+// Validation happens in the C-ABI wrapper.  The residual stream alternates
+// between w.x and w.x2: the add + RMSNorm before a matvec is that matvec's
+// staging prologue, whose workgroup 0 stores x + y into the other buffer
+// (the others are still reading x).
 hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,
                                hipStream_t st) {
-    const int H = m->hidden, D = m->head_dim, NQ = m->n_heads, NKV = m->n_kv_heads, G = NQ / NKV;
-    const int QKVR = (NQ + 2 * NKV) * D;
+    const int H = m->hidden, D = m->head_dim, NQ = m->n_heads, NKV = m->n_kv_heads, G = NQ / NKV, F = m->ffn;
+    const int QKVR = (NQ + 2 * NKV) * D, qt = m->qtype_layers;
     const DenseWs w = dense_ws(m, ws, nullptr);
     const size_t erb = tbq_row_bytes(m->qtype_embd, H);
-    hipError_t err = launch_dequant(m->qtype_embd, (const uint8_t *)m->tok_embd + (size_t)token * erb, H, w.x, st);
+    float *xa = w.x, *xb = w.x2;
+    hipError_t err = launch_dequant(m->qtype_embd, (const uint8_t *)m->tok_embd + (size_t)token * erb, H, xa, st);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(64), 0, st, pos, m->rope_theta, D, w.rope);
     const float *yprev = nullptr;
-    auto mv = [&](const void *W, int M, int K, const float *xin, float *yout) -> hipError_t {
-        return tbq_matvec(W, m->qtype_layers, M, K, xin, yout, st) ? hipSuccess : hipErrorUnknown;
-    };
     for (int l = 0; l < m->n_layers; l++) {
         const tbq_dense_layer &L = m->layers[l];
         const size_t kvoff = (size_t)l * NKV * m->max_ctx * D;
-        hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(1024), 0, st, w.x, yprev, L.attn_norm, H, m->norm_eps, w.h);
-        if ((err = mv(L.wqkv, QKVR, H, w.h, w.qkv)) != hipSuccess) return err;
+        // qkv = Wqkv rmsnorm(xa + yprev); xb = xa + yprev
+        const MvPro pa{yprev, L.attn_norm, xb, m->norm_eps};
+        if ((err = dense_mv(qt, L.wqkv, QKVR, H, xa, w.qkv, PRO_NORM, pa, w.h, nullptr, st)) != hipSuccess) return err;
         err = D == 128 ? launch_attn_d<128>(G, w.qkv, L.q_norm, L.k_norm, NQ, NKV, pos, w.rope, m->norm_eps,
                                             m->k_cache + kvoff, m->v_cache + kvoff, m->max_ctx, w.part, w.att, st)
                        : launch_attn_d<64>(G, w.qkv, L.q_norm, L.k_norm, NQ, NKV, pos, w.rope, m->norm_eps,
                                            m->k_cache + kvoff, m->v_cache + kvoff, m->max_ctx, w.part, w.att, st);
         if (err != hipSuccess) return err;
-        if ((err = mv(L.wo, H, NQ * D, w.att, w.y)) != hipSuccess) return err;
-        hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(1024), 0, st, w.x, w.y, L.ffn_norm, H, m->norm_eps, w.h);
-        if ((err = mv(L.wgu, 2 * m->ffn, H, w.h, w.gu)) != hipSuccess) return err;
-        hipLaunchKernelGGL(k_swiglu, dim3((m->ffn + 255) / 256), dim3(256), 0, st, w.gu, m->ffn, w.a);
-        if ((err = mv(L.wdown, H, m->ffn, w.a, w.y)) != hipSuccess) return err;
+        if ((err = dense_mv(qt, L.wo, H, NQ * D, w.att, w.y, PRO_NONE, MvPro{}, nullptr, nullptr, st)) != hipSuccess)
+            return err;
+        // a = silu(Wg h) * (Wu h) with h = rmsnorm(xb + y); xa = xb + y
+        const MvPro pf{w.y, L.ffn_norm, xa, m->norm_eps};
+        if ((err = dense_mv(qt, L.wgu, F, H, xb, w.a, PRO_NORM | MV_GLU, pf, w.h, w.gu, st)) != hipSuccess) return err;
+        // y = Wdown a
+        if ((err = dense_mv(qt, L.wdown, H, F, w.a, w.y, PRO_NONE, MvPro{}, nullptr, nullptr, st)) != hipSuccess)
+            return err;
         yprev = w.y;
     }
-    hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(1024), 0, st, w.x, yprev, m->output_norm, H, m->norm_eps, w.h);
-    if (!tbq_matvec(m->lm_head, m->qtype_embd, m->vocab, H, w.h, logits, st)) return hipErrorUnknown;
+    const MvPro po{yprev, m->output_norm, nullptr, m->norm_eps};
+    if ((err = dense_mv(m->qtype_embd, m->lm_head, m->vocab, H, xa, logits, PRO_NORM, po, w.h, nullptr, st)) !=
+        hipSuccess)
+        return err;
     return hipGetLastError();
 }
 

@@ -177,6 +177,32 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Sum of one float per thread over the workgroup (blockDim.x a multiple of
+// 64, at most 2048), in a fixed order; every thread gets it.
+__device__ __forceinline__ float pro_block_sum(float v) {
+    __shared__ float red[32];
+    v = group_sum<64>(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += red[i];
+    return s;
+}
+
+// An empty asm statement that takes v and gives it back and clobbers
+// memory: code that uses v stays after it, loads issued before it stay
+// before it.
+__device__ __forceinline__ void pro_pin(float &v) { asm volatile("" : "+v"(v) : : "memory"); }
+__device__ __forceinline__ void pro_pin(float4 &v) {
+    pro_pin(v.x);
+    pro_pin(v.y);
+    pro_pin(v.z);
+    pro_pin(v.w);
+}
+
+// silu(g) * u, as the unfused k_swiglu computes it.
+__device__ __forceinline__ float pro_swiglu(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) {
     return *reinterpret_cast<const uint32_t *>(p);
 }

@@ -8,6 +8,24 @@
 
 namespace tbq {
 
+// Fusions of the dense decode's elementwise steps into a matvec, so they
+// need no launch of their own.  Staging prologue (how x is formed):
+//   PRO_NONE    x
+//   PRO_NORM    v = x[i] + y[i] (y may be null),
+//               x'[i] = v * (1 / sqrt(mean(v^2) + eps)) * w[i] over the K
+//               elements; workgroup 0 also stores v to vo (if not null)
+// Every workgroup forms the whole normalised vector itself (one block-wide
+// sum of squares), so no workgroup waits for another.  Epilogue flag MV_GLU
+// (K-quant kernel): W holds 2M rows, gate rows then up rows, and
+// y[r] = silu(W[r] x') * (W[M + r] x'); one wave computes both rows.
+enum : int { PRO_NONE = 0, PRO_NORM = 2, MV_GLU = 4 };
+struct MvPro {
+    const float *y;   // PRO_NORM: added to x (null: nothing added)
+    const float *w;   // PRO_NORM: weights [K]
+    float *vo;        // PRO_NORM: x + y for the caller (null: not stored)
+    float eps;
+};
+
 struct MoeArgs {
     int T, H, F, E, top_k, k, qtype;
     const float *xn, *resid, *router, *bias;
@@ -26,6 +44,13 @@ hipError_t launch_matvec_generic(int qt, const void *W, int M, int K, const floa
                                  hipStream_t s, int n_cu);
 hipError_t launch_matvec_q4k(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu);
 hipError_t launch_matvec_kq(int qt, const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu);
+// The same kernels with a staging prologue (mode = PRO_* | MV_GLU);
+// hipErrorNotSupported where they do not cover the shape or mode (the q4k
+// one: K <= 4096, no MV_GLU).
+hipError_t launch_matvec_q4k_pro(int mode, const MvPro &pro, const void *W, int M, int K, const float *x, float *y,
+                                 hipStream_t s);
+hipError_t launch_matvec_kq_pro(int mode, const MvPro &pro, int qt, const void *W, int M, int K, const float *x,
+                                float *y, hipStream_t s, int n_cu);
 hipError_t launch_expf(const float *in, float *out, long long n, hipStream_t s);
 hipError_t launch_route(const float *xn, const float *router, const float *bias, int T, int H, int E,
                         int top_k, int *sel_idx, float *sel_w, hipStream_t st);

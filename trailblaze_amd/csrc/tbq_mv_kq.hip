@@ -115,27 +115,84 @@ struct GMem {
 // the 4 tasks of a group are a DPP quad (group sum).  Each thread handles at
 // most MAXT tasks (MAXT * NT >= 16 * U).
 // ---------------------------------------------------------------------------
-template <int NT, bool PAIR, int MAXT>
+template <int NT, bool PAIR, int MAXT, int PRO = PRO_NONE>
 struct KqStager {
     float e[MAXT][4];
+    float p1[MAXT][4], p2[MAXT][4];   // PRO_NORM inputs: y, w
 
     // PAIR dword t = 2k + par holds elements 8k + par + {0, 2, 4, 6}: four
     // loads at a per-lane base, no selection after the data arrives.
     // Loads are unconditional (tasks past the end re-read the last one and
     // are never stored), so no branch hides them from the wait counter.
-    __device__ __forceinline__ void load(const float *__restrict__ x, int U) {
+    template <typename F4>
+    __device__ __forceinline__ void ld4(const float *__restrict__ src, int task, F4 &o) const {
+        const int u = task >> 4, t = task & 15;
+        if constexpr (PAIR) {
+            const float *p = src + 64 * u + 8 * (t >> 1) + (t & 1);
+#pragma unroll
+            for (int j = 0; j < 4; j++) o[j] = p[2 * j];
+        } else {
+            const float4 a = *reinterpret_cast<const float4 *>(src + 64 * u + 4 * t);
+            o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+        }
+    }
+
+    __device__ __forceinline__ void load(const float *__restrict__ x, int U, const MvPro &pro = MvPro{}) {
+        const float *yp = (PRO == PRO_NORM && pro.y) ? pro.y : x;   // no y: loads x, adds 0
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
             const int task = min(i * NT + (int)threadIdx.x, U * 16 - 1);
-            const int u = task >> 4, t = task & 15;
-            if constexpr (PAIR) {
-                const float *p = x + 64 * u + 8 * (t >> 1) + (t & 1);
-#pragma unroll
-                for (int j = 0; j < 4; j++) e[i][j] = p[2 * j];
-            } else {
-                const float4 a = *reinterpret_cast<const float4 *>(x + 64 * u + 4 * t);
-                e[i][0] = a.x; e[i][1] = a.y; e[i][2] = a.z; e[i][3] = a.w;
+            ld4(x, task, e[i]);
+            if constexpr (PRO == PRO_NORM) {
+                ld4(yp, task, p1[i]);
+                ld4(pro.w, task, p2[i]);
             }
+        }
+    }
+
+    // The prologue, in registers, between load() and store(), called after
+    // the kernel has issued its weight loads.  Every thread of the workgroup
+    // calls it.  Its inputs pass through pro_pin first, so the compiler
+    // cannot start it (and wait for x) ahead of the weight loads.
+    __device__ __forceinline__ void apply(int U, const MvPro &pro = MvPro{}) {
+        if constexpr (PRO != PRO_NONE) {
+#pragma unroll
+            for (int i = 0; i < MAXT; i++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    pro_pin(e[i][c]);
+                    pro_pin(p1[i][c]);
+                    pro_pin(p2[i][c]);
+                }
+        }
+        if constexpr (PRO == PRO_NORM) {
+            const bool hy = pro.y != nullptr;
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < MAXT; i++) {
+                const int task = i * NT + (int)threadIdx.x;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    e[i][c] = e[i][c] + (hy ? p1[i][c] : 0.f);
+                    if (task < U * 16) ss += e[i][c] * e[i][c];
+                }
+                if (blockIdx.x == 0 && pro.vo && task < U * 16) {
+                    const int u = task >> 4, t = task & 15;
+                    if constexpr (PAIR) {
+                        float *p = pro.vo + 64 * u + 8 * (t >> 1) + (t & 1);
+#pragma unroll
+                        for (int j = 0; j < 4; j++) p[2 * j] = e[i][j];
+                    } else {
+                        *reinterpret_cast<float4 *>(pro.vo + 64 * u + 4 * t) =
+                            make_float4(e[i][0], e[i][1], e[i][2], e[i][3]);
+                    }
+                }
+            }
+            const float r = 1.0f / sqrtf(pro_block_sum(ss) / (float)(64 * U) + pro.eps);
+#pragma unroll
+            for (int i = 0; i < MAXT; i++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) e[i][c] = e[i][c] * r * p2[i][c];
         }
     }
 
@@ -582,17 +639,24 @@ __device__ __forceinline__ float kq_dot(const typename KqFmt<QT>::Unit &w, const
 // flight per pass, and the weights of the next D passes are loaded before
 // the current pass is reduced.
 // ---------------------------------------------------------------------------
-template <int QT, int LPR, int S, int G, int R, int D>
+//
+// GLU: M counts output rows; output row r is a pair of weight rows, r (gate)
+// and M + r (up), taken by the same lanes in one pass (RP = 2 rows in
+// flight), and y[r] = silu(gate) * up.
+template <int QT, int LPR, int S, int G, int R, int D, int PRO, bool GLU>
 __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict__ W, int M, int K, long long rb,
-                                                      const float *__restrict__ x, float *__restrict__ y, int rpw) {
+                                                      const float *__restrict__ x, float *__restrict__ y, int rpw,
+                                                      MvPro pro) {
     using F = KqFmt<QT>;
-    constexpr int NT = S * G * 64, RPP = 64 / LPR, RW = R * RPP, RWG = G * RW;
+    constexpr int RL = GLU ? 1 : R;   // output rows per lane group and pass
+    constexpr int RP = GLU ? 2 : R;   // weight rows per lane group and pass
+    constexpr int NT = S * G * 64, RPP = 64 / LPR, RW = RL * RPP, RWG = G * RW, RWP = RP * RPP;
     constexpr int MAXT = (16 * 64 * S + NT - 1) / NT;   // U <= 64 * S
     extern __shared__ uint32_t smem[];
     const int U = K / 64;
     uint32_t *xd = smem;
     float *gs = reinterpret_cast<float *>(smem + U * KQ_UNIT);
-    float *red = gs + 4 * U;   // [2][G][S][RW], S > 1 only
+    float *red = gs + 4 * U;   // [2][G][S][RWP], S > 1 only
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int s = wave % S, g = wave / S;
     const int lr = lane % LPR, rsub = lane / LPR;
@@ -608,19 +672,22 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
     // compiler wait for all outstanding loads where the branch rejoins,
     // which serialises the prefetch with this pass's arithmetic.
     const int ul = lv ? u : 0;
-    typename F::Unit buf[D + 1][R];   // buf[0] = this pass, buf[i] = pass + i
+    typename F::Unit buf[D + 1][RP];   // buf[0] = this pass, buf[i] = pass + i
+    // output row of step p of a pass, and the weight row it reads
+    auto orow = [&](int pass, int p) { return row0 + pass * RWG + (GLU ? 0 : p * RPP); };
     auto load = [&](typename F::Unit *dst, int pass) {
 #pragma unroll
-        for (int p = 0; p < R; p++) {
-            const int r = min(row0 + pass * RWG + p * RPP, rend - 1);
+        for (int p = 0; p < RP; p++) {
+            const int r = min(orow(pass, p), rend - 1) + (GLU ? p * M : 0);
             F::load(W + (long long)r * rb, ul, dst[p]);
         }
     };
-    KqStager<NT, F::PAIR, MAXT> xs;
-    xs.load(x, U);
+    KqStager<NT, F::PAIR, MAXT, PRO> xs;
+    xs.load(x, U, pro);
     __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
 #pragma unroll
     for (int i = 0; i < D; i++) load(buf[i], i);
+    xs.apply(U, pro);
     xs.store(U, xd, gs);
     __syncthreads();
     KqX xr;
@@ -628,54 +695,58 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
 
     for (int pass = 0; pass < npass; ++pass) {
         load(buf[D], pass + D);
-        float acc[R];
+        float acc[RP];
 #pragma unroll
-        for (int p = 0; p < R; p++) {
-            const int r = row0 + pass * RWG + p * RPP;
+        for (int p = 0; p < RP; p++) {
+            const int r = orow(pass, p);
             const float v = kq_dot<QT>(buf[0][p], xr, ul);
             acc[p] = group_sum<LPR>((r < rend && lv) ? v : 0.f);
         }
-        if constexpr (S == 1) {
+        if constexpr (S > 1) {
+            // the slices' partial sums meet in LDS; every slice adds them in
+            // slice order (slice 0 stores)
+            float *rbuf = red + (pass & 1) * (G * S * RWP);
 #pragma unroll
-            for (int p = 0; p < R; p++) {
-                const int r = row0 + pass * RWG + p * RPP;
-                if (lr == 0 && r < rend) y[r] = acc[p];
-            }
-        } else {
-            float *rbuf = red + (pass & 1) * (G * S * RW);
-#pragma unroll
-            for (int p = 0; p < R; p++)
-                if (lr == 0) rbuf[(g * S + s) * RW + p * RPP + rsub] = acc[p];
+            for (int p = 0; p < RP; p++)
+                if (lr == 0) rbuf[(g * S + s) * RWP + p * RPP + rsub] = acc[p];
             __syncthreads();
-            if (s == 0) {
 #pragma unroll
-                for (int p = 0; p < R; p++) {
-                    const int r = row0 + pass * RWG + p * RPP;
-                    if (lr == 0 && r < rend) {
-                        float t = rbuf[(g * S) * RW + p * RPP + rsub];
+            for (int p = 0; p < RP; p++) {
+                float t = rbuf[(g * S) * RWP + p * RPP + rsub];
 #pragma unroll
-                        for (int ss = 1; ss < S; ss++) t += rbuf[(g * S + ss) * RW + p * RPP + rsub];
-                        y[r] = t;
-                    }
+                for (int ss = 1; ss < S; ss++) t += rbuf[(g * S + ss) * RWP + p * RPP + rsub];
+                acc[p] = t;
+            }
+        }
+        if (s == 0) {
+            if constexpr (GLU) {
+                const int r = orow(pass, 0);
+                if (lr == 0 && r < rend) y[r] = pro_swiglu(acc[0], acc[1]);
+            } else {
+#pragma unroll
+                for (int p = 0; p < RP; p++) {
+                    const int r = orow(pass, p);
+                    if (lr == 0 && r < rend) y[r] = acc[p];
                 }
             }
         }
 #pragma unroll
         for (int i = 0; i < D; i++)
 #pragma unroll
-            for (int p = 0; p < R; p++) buf[i][p] = buf[i + 1][p];
+            for (int p = 0; p < RP; p++) buf[i][p] = buf[i + 1][p];
     }
 }
 
-template <int QT, int LPR, int S, int G, int R, int D>
+template <int QT, int LPR, int S, int G, int R, int D, int PRO, bool GLU>
 static hipError_t launch_kq(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int grid,
-                            int rpw) {
+                            int rpw, const MvPro &pro) {
     constexpr int RPP = 64 / LPR;
     const int U = K / 64;
     const long long rb = (long long)(K / block_weights(QT)) * block_bytes(QT);
-    const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (S > 1 ? (size_t)2 * G * S * R * RPP * 4 : 0);
-    hipLaunchKernelGGL((k_mv_kq<QT, LPR, S, G, R, D>), dim3(grid), dim3(S * G * 64), lds, st,
-                       (const uint8_t *)W, M, K, rb, x, y, rpw);
+    constexpr int RP = GLU ? 2 : R;
+    const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (S > 1 ? (size_t)2 * G * S * RP * RPP * 4 : 0);
+    hipLaunchKernelGGL((k_mv_kq<QT, LPR, S, G, R, D, PRO, GLU>), dim3(grid), dim3(S * G * 64), lds, st,
+                       (const uint8_t *)W, M, K, rb, x, y, rpw, pro);
     return hipGetLastError();
 }
 
@@ -683,46 +754,66 @@ static hipError_t launch_kq(const void *W, int M, int K, const float *x, float *
 // KQ_WG_PER_CU workgroups per CU (each stages x once), rows split evenly over
 // the workgroups; each wave streams R = KQ_R rows per pass with the next
 // KQ_D passes' weights in flight.
-template <int QT, int LPR, int S, int G>
-static hipError_t launch_kq_shape(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu) {
-    constexpr int RPP = 64 / LPR, R = KQ_R, D = KQ_D;
+template <int QT, int LPR, int S, int G, int PRO, bool GLU>
+static hipError_t launch_kq_shape(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu,
+                                  const MvPro &pro) {
+    constexpr int RPP = 64 / LPR, R = KQ_R, D = KQ_D, RL = GLU ? 1 : R;
     const long long cap = (long long)n_cu * KQ_WG_PER_CU;
-    const long long need = ((long long)M + G * R * RPP - 1) / (G * R * RPP);
+    const long long need = ((long long)M + G * RL * RPP - 1) / (G * RL * RPP);
     const int grid = (int)(need < cap ? need : cap);
     const int rpw = (M + grid - 1) / grid;
-    return launch_kq<QT, LPR, S, G, R, D>(W, M, K, x, y, st, grid, rpw);
+    return launch_kq<QT, LPR, S, G, R, D, PRO, GLU>(W, M, K, x, y, st, grid, rpw, pro);
 }
 
-template <int QT>
-static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu) {
+template <int QT, int PRO, bool GLU>
+static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu,
+                              const MvPro &pro) {
     const int U = K / 64;
     constexpr int NW = KQ_NW, G3 = KQ_G3;
-    if (U <= 4) return launch_kq_shape<QT, 4, 1, NW>(W, M, K, x, y, st, n_cu);
-    if (U <= 8) return launch_kq_shape<QT, 8, 1, NW>(W, M, K, x, y, st, n_cu);
-    if (U <= 16) return launch_kq_shape<QT, 16, 1, NW>(W, M, K, x, y, st, n_cu);
-    if (U <= 32) return launch_kq_shape<QT, 32, 1, NW>(W, M, K, x, y, st, n_cu);
-    if (U <= 64) return launch_kq_shape<QT, 64, 1, NW>(W, M, K, x, y, st, n_cu);
-    if (U <= 128) return launch_kq_shape<QT, 64, 2, NW / 2>(W, M, K, x, y, st, n_cu);
-    if (U <= 192) return launch_kq_shape<QT, 64, 3, G3>(W, M, K, x, y, st, n_cu);
-    if (U <= 256) return launch_kq_shape<QT, 64, 4, NW / 4>(W, M, K, x, y, st, n_cu);
+    if (U <= 4) return launch_kq_shape<QT, 4, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    if (U <= 8) return launch_kq_shape<QT, 8, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    if (U <= 16) return launch_kq_shape<QT, 16, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    if (U <= 32) return launch_kq_shape<QT, 32, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    if (U <= 64) return launch_kq_shape<QT, 64, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    if (U <= 128) return launch_kq_shape<QT, 64, 2, NW / 2, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    if (U <= 192) return launch_kq_shape<QT, 64, 3, G3, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    if (U <= 256) return launch_kq_shape<QT, 64, 4, NW / 4, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     return hipErrorNotSupported;
 }
 
 // Returns hipErrorNotSupported for formats or shapes this kernel does not
 // cover (K must be a multiple of 64 and at most 16384).
-hipError_t launch_matvec_kq(int qt, const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu) {
+template <int PRO, bool GLU>
+static hipError_t launch_matvec_kq_p(int qt, const void *W, int M, int K, const float *x, float *y, hipStream_t st,
+                                     int n_cu, const MvPro &pro) {
     if (K % 64 || K > 16384 || K <= 0) return hipErrorNotSupported;
     const bool sb256 = block_weights(qt) == 256;
     if (sb256 && K % 256) return hipErrorNotSupported;
     switch (qt) {
-    case QT_Q2_K: return launch_kq_q<QT_Q2_K>(W, M, K, x, y, st, n_cu);
-    case QT_Q3_K: return launch_kq_q<QT_Q3_K>(W, M, K, x, y, st, n_cu);
-    case QT_Q4_K: return launch_kq_q<QT_Q4_K>(W, M, K, x, y, st, n_cu);
-    case QT_Q5_K: return launch_kq_q<QT_Q5_K>(W, M, K, x, y, st, n_cu);
-    case QT_Q6_K: return launch_kq_q<QT_Q6_K>(W, M, K, x, y, st, n_cu);
-    case QT_Q8_0: return launch_kq_q<QT_Q8_0>(W, M, K, x, y, st, n_cu);
-    case QT_Q4_0: return launch_kq_q<QT_Q4_0>(W, M, K, x, y, st, n_cu);
-    case QT_Q8_K: return launch_kq_q<QT_Q8_K>(W, M, K, x, y, st, n_cu);
+    case QT_Q2_K: return launch_kq_q<QT_Q2_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_Q3_K: return launch_kq_q<QT_Q3_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_Q4_K: return launch_kq_q<QT_Q4_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_Q5_K: return launch_kq_q<QT_Q5_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_Q6_K: return launch_kq_q<QT_Q6_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_Q8_0: return launch_kq_q<QT_Q8_0, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_Q4_0: return launch_kq_q<QT_Q4_0, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_Q8_K: return launch_kq_q<QT_Q8_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    default: return hipErrorNotSupported;
+    }
+}
+
+hipError_t launch_matvec_kq(int qt, const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu) {
+    return launch_matvec_kq_p<PRO_NONE, false>(qt, W, M, K, x, y, st, n_cu, MvPro{});
+}
+
+// With a staging prologue and epilogue (mode = PRO_* | MV_GLU; with MV_GLU,
+// W holds 2M rows).
+hipError_t launch_matvec_kq_pro(int mode, const MvPro &pro, int qt, const void *W, int M, int K, const float *x,
+                                float *y, hipStream_t st, int n_cu) {
+    switch (mode) {
+    case PRO_NONE: return launch_matvec_kq_p<PRO_NONE, false>(qt, W, M, K, x, y, st, n_cu, pro);
+    case PRO_NORM: return launch_matvec_kq_p<PRO_NORM, false>(qt, W, M, K, x, y, st, n_cu, pro);
+    case PRO_NORM | MV_GLU: return launch_matvec_kq_p<PRO_NORM, true>(qt, W, M, K, x, y, st, n_cu, pro);
     default: return hipErrorNotSupported;
     }
 }

@@ -82,9 +82,9 @@ __global__ __launch_bounds__(WG) void k_mv_q4k(const uint8_t *__restrict__ W, in
 // RPP = 64/LPR rows (rows wave_base + p*RPP + rsub); all R passes' weight
 // loads are in flight before x is staged.  No grid-stride loop: the grid
 // covers M exactly.
-template <int LPR, int R, int NW>
+template <int LPR, int R, int NW, int PRO>
 __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict__ W, int M, int K, long long rb,
-                                                      const float *__restrict__ x, float *__restrict__ y) {
+                                                      const float *__restrict__ x, float *__restrict__ y, MvPro pro) {
     extern __shared__ uint32_t xd[];
     constexpr int NT = NW * 64, RPP = 64 / LPR;
     const int U = K / 64;
@@ -92,8 +92,8 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
     const int lr = lane % LPR, rsub = lane / LPR;
     const bool lv = lr < U;
     const int ul = lv ? lr : 0;
-    XStager<NT, (4 * 128 + NT - 1) / NT> xs;   // K <= 4096
-    xs.load(x, K);
+    XStager<NT, (4 * 128 + NT - 1) / NT, PRO> xs;   // K <= 4096
+    xs.load(x, K, 1, pro);
     __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
     const int base = (blockIdx.x * NW + wave) * R * RPP + rsub;
     // Unconditional loads (rows past M re-read row M-1, idle lanes unit 0;
@@ -105,6 +105,7 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
         const int r = min(base + p * RPP, M - 1);
         q4k_load(W + (long long)r * rb, ul, w[p]);
     }
+    xs.apply(K, pro);
     xs.store(xd, K);
     __syncthreads();
     XUnit xu;
@@ -118,14 +119,27 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
     }
 }
 
-template <int LPR, int R, int NW>
-static hipError_t launch_q4k_xr(const void *W, int M, int K, const float *x, float *y, hipStream_t s) {
+template <int LPR, int R, int NW, int PRO>
+static hipError_t launch_q4k_xr(const void *W, int M, int K, const float *x, float *y, hipStream_t s,
+                                const MvPro &pro) {
     constexpr int ROWS_PER_WG = NW * R * (64 / LPR);
     const int grid = (M + ROWS_PER_WG - 1) / ROWS_PER_WG;
     const long long rb = (long long)(K / 256) * 144;
     const size_t lds = (size_t)(K / 32) * XD_PER_SB * 4;
-    hipLaunchKernelGGL((k_mv_q4k_xr<LPR, R, NW>), dim3(grid), dim3(NW * 64), lds, s, (const uint8_t *)W, M, K, rb, x, y);
+    hipLaunchKernelGGL((k_mv_q4k_xr<LPR, R, NW, PRO>), dim3(grid), dim3(NW * 64), lds, s, (const uint8_t *)W, M, K,
+                       rb, x, y, pro);
     return hipGetLastError();
+}
+
+template <int PRO>
+static hipError_t launch_q4k_xr_k(const void *W, int M, int K, const float *x, float *y, hipStream_t s,
+                                  const MvPro &pro) {
+    const int U = K / 64;
+    if (U <= 4) return launch_q4k_xr<4, Q4K_XR_R, Q4K_XR_NW, PRO>(W, M, K, x, y, s, pro);
+    if (U <= 8) return launch_q4k_xr<8, Q4K_XR_R, Q4K_XR_NW, PRO>(W, M, K, x, y, s, pro);
+    if (U <= 16) return launch_q4k_xr<16, Q4K_XR_R, Q4K_XR_NW, PRO>(W, M, K, x, y, s, pro);
+    if (U <= 32) return launch_q4k_xr<32, Q4K_XR_R, Q4K_XR_NW, PRO>(W, M, K, x, y, s, pro);
+    return launch_q4k_xr<64, Q4K_XR_R, Q4K_XR_NW, PRO>(W, M, K, x, y, s, pro);
 }
 
 template <int LPR, int UPL>
@@ -144,15 +158,24 @@ static hipError_t launch_q4k_t(const void *W, int M, int K, const float *x, floa
 hipError_t launch_matvec_q4k(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu) {
     const int U = K / 64;
     if (K % 256 || U < 4) return hipErrorNotSupported;
-    if (U <= 4) return launch_q4k_xr<4, Q4K_XR_R, Q4K_XR_NW>(W, M, K, x, y, s);
-    if (U <= 8) return launch_q4k_xr<8, Q4K_XR_R, Q4K_XR_NW>(W, M, K, x, y, s);
-    if (U <= 16) return launch_q4k_xr<16, Q4K_XR_R, Q4K_XR_NW>(W, M, K, x, y, s);
-    if (U <= 32) return launch_q4k_xr<32, Q4K_XR_R, Q4K_XR_NW>(W, M, K, x, y, s);
-    if (U <= 64) return launch_q4k_xr<64, Q4K_XR_R, Q4K_XR_NW>(W, M, K, x, y, s);
+    if (U <= 64) return launch_q4k_xr_k<PRO_NONE>(W, M, K, x, y, s, MvPro{});
     if (U <= 128) return launch_q4k_t<64, 2>(W, M, K, x, y, s, n_cu);
     if (U <= 192) return launch_q4k_t<64, 3>(W, M, K, x, y, s, n_cu);
     if (U <= 256) return launch_q4k_t<64, 4>(W, M, K, x, y, s, n_cu);
     return hipErrorNotSupported;
+}
+
+// With a staging prologue: the register-x kernel only (K <= 4096);
+// hipErrorNotSupported otherwise.
+hipError_t launch_matvec_q4k_pro(int mode, const MvPro &pro, const void *W, int M, int K, const float *x, float *y,
+                                 hipStream_t s) {
+    const int U = K / 64;
+    if (K % 256 || U < 4 || U > 64) return hipErrorNotSupported;
+    switch (mode) {
+    case PRO_NONE: return launch_q4k_xr_k<PRO_NONE>(W, M, K, x, y, s, pro);
+    case PRO_NORM: return launch_q4k_xr_k<PRO_NORM>(W, M, K, x, y, s, pro);
+    default: return hipErrorNotSupported;
+    }
 }
 
 }  // namespace tbq

@@ -14,6 +14,7 @@
 // significant bits per sub-block), far inside the 1e-5 parity bound.
 #pragma once
 
+#include "tbq_kernels.h"
 #include "tbq_kquant.hpp"
 
 namespace tbq {
@@ -39,21 +40,85 @@ constexpr int XD_PER_SB = XD_UNIT / 2;   // LDS dwords per sub-block on average
 // bits and its little-endian bytes are the digits: l = byte0 and m = byte1
 // unsigned, h = byte2 signed, X = 65536*h + 256*m + l.  Six dwords are
 // stored: {h, m, l} x {even elements (low nibbles), odd (high nibbles)}.
-template <int NT, int MAXT>
+template <int NT, int MAXT, int PRO = PRO_NONE>
 struct XStager {
     float4 v[MAXT][2];
+    float4 p1[MAXT][2], p2[MAXT][2];   // PRO_NORM inputs: y, w
 
     // Unconditional loads (tasks past the end re-read the last task and are
     // never stored), so no branch makes the compiler wait for every load
     // in flight where it rejoins.
-    __device__ __forceinline__ void load(const float *__restrict__ x, int K, int nvec = 1) {
+    __device__ __forceinline__ void load(const float *__restrict__ x, int K, int nvec = 1,
+                                         const MvPro &pro = MvPro{}) {
         const int ntask = 4 * (K / 32) * nvec;
+        const float *yp = (PRO == PRO_NORM && pro.y) ? pro.y : x;   // no y: loads x, adds 0
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
             const int t = min((int)threadIdx.x + i * NT, ntask - 1);
             const float4 *xp = reinterpret_cast<const float4 *>(x + 8 * t);
             v[i][0] = xp[0];
             v[i][1] = xp[1];
+            if constexpr (PRO == PRO_NORM) {
+                const float4 *q = reinterpret_cast<const float4 *>(yp + 8 * t);
+                const float4 *w = reinterpret_cast<const float4 *>(pro.w + 8 * t);
+                p1[i][0] = q[0];
+                p1[i][1] = q[1];
+                p2[i][0] = w[0];
+                p2[i][1] = w[1];
+            }
+        }
+    }
+
+    // The prologue, in registers, between load() and store() (one vector,
+    // nvec = 1), called after the kernel has issued its weight loads.  Every
+    // thread of the workgroup calls it.  The prologue's inputs first pass
+    // through empty asm statements that clobber memory: otherwise the
+    // compiler computes the prologue as soon as x arrives, ahead of the
+    // weight loads, and their latency then adds to x's.
+    __device__ __forceinline__ void apply(int K, const MvPro &pro = MvPro{}) {
+        if constexpr (PRO != PRO_NONE) {
+#pragma unroll
+            for (int i = 0; i < MAXT; i++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    pro_pin(v[i][h]);
+                    pro_pin(p1[i][h]);
+                    pro_pin(p2[i][h]);
+                }
+        }
+        if constexpr (PRO == PRO_NORM) {
+            const int ntask = 4 * (K / 32);
+            const bool hy = pro.y != nullptr;
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < MAXT; i++) {
+                const int t = (int)threadIdx.x + i * NT;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    float *a = reinterpret_cast<float *>(&v[i][h]);
+                    const float *y = reinterpret_cast<const float *>(&p1[i][h]);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        a[c] = a[c] + (hy ? y[c] : 0.f);
+                        if (t < ntask) ss += a[c] * a[c];
+                    }
+                }
+                if (blockIdx.x == 0 && pro.vo && t < ntask) {
+                    float4 *o = reinterpret_cast<float4 *>(pro.vo + 8 * t);
+                    o[0] = v[i][0];
+                    o[1] = v[i][1];
+                }
+            }
+            const float r = 1.0f / sqrtf(pro_block_sum(ss) / (float)K + pro.eps);
+#pragma unroll
+            for (int i = 0; i < MAXT; i++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    float *a = reinterpret_cast<float *>(&v[i][h]);
+                    const float *w = reinterpret_cast<const float *>(&p2[i][h]);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) a[c] = a[c] * r * w[c];
+                }
         }
     }
 
