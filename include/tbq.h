@@ -154,7 +154,8 @@ size_t tbq_dense_workspace_size(const tbq_dense_model *m);
 /* logits[vocab] for `token` at position `pos` (0 <= pos < max_ctx); appends
  * the token's K and V at `pos` of every layer's cache and attends over
  * positions 0..pos.  head_dim 64 or 128; n_heads / n_kv_heads in {1, 2, 4,
- * 8}; hidden, ffn and n_heads*head_dim multiples of 256. */
+ * 8}; hidden, ffn and n_heads*head_dim multiples of 256; max_ctx <= 131072.
+ * Calls that share a workspace must not overlap. */
 int tbq_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *workspace,
                      size_t workspace_bytes, void *stream);
 

@@ -273,6 +273,7 @@ static int check_dense(const tbq_dense_model *m) {
     const int G = m->n_heads / m->n_kv_heads;
     if (m->n_heads % m->n_kv_heads || (G != 1 && G != 2 && G != 4 && G != 8))
         return fail("tbq_dense: n_heads / n_kv_heads must be 1, 2, 4 or 8");
+    if (m->max_ctx > 131072) return fail("tbq_dense: max_ctx above 131072");
     if (m->hidden % 256 || m->ffn % 256 || (m->n_heads * m->head_dim) % 256)
         return fail("tbq_dense: hidden, ffn and n_heads*head_dim must be multiples of 256");
     if (!tbq_qtype_supported(m->qtype_layers) || !tbq_qtype_supported(m->qtype_embd))

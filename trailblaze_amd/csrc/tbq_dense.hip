@@ -35,8 +35,15 @@
 
 namespace tbq {
 
-constexpr int ATT_CH = 128;        // positions per attention workgroup
-constexpr int ATT_THREADS = 256;
+#ifndef TBQ_ATT_CH
+#define TBQ_ATT_CH 128
+#endif
+constexpr int ATT_CH = TBQ_ATT_CH;   // positions per attention workgroup
+#ifndef TBQ_ATT_THREADS
+#define TBQ_ATT_THREADS 512
+#endif
+constexpr int ATT_THREADS = TBQ_ATT_THREADS;
+constexpr int ATT_PARTS = ATT_THREADS / ATT_CH;   // threads per position in the score phase
 
 // Block-wide sum of one float per thread (blockDim.x a multiple of 64,
 // <= 1024); every thread gets the result.
@@ -133,7 +140,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_partial(const float *__res
     float *Vs = Ks + ATT_CH * KLD;           // [ATT_CH][D]
     float *qs = Vs + ATT_CH * D;             // [G][D]
     float *sc = qs + G * D;                  // [G][ATT_CH]
-    float *pd = sc + G * ATT_CH;             // [2][G][ATT_CH]
+    float *pd = sc + G * ATT_CH;             // [ATT_PARTS][G][ATT_CH]
     const int kvh = blockIdx.x, ch = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int n_pos = pos + 1, p0 = ch * ATT_CH;
     const long long hbase = (long long)kvh * max_ctx * D;
@@ -182,17 +189,18 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_partial(const float *__res
         }
     }
     __syncthreads();
-    // scores: thread = (position p, half of the dims), K row from LDS
+    // scores: thread = (position p, part of the dims), K row from LDS
     {
+        constexpr int DP = D / ATT_PARTS;
         const int p = tid % ATT_CH, half = tid / ATT_CH;
-        const float *krow = Ks + p * KLD + half * (D / 2);
+        const float *krow = Ks + p * KLD + half * DP;
         float acc[G];
 #pragma unroll
         for (int g = 0; g < G; g++) acc[g] = 0.f;
 #pragma unroll
-        for (int c = 0; c < D / 8; c++) {
+        for (int c = 0; c < DP / 4; c++) {
             const float4 k4 = *reinterpret_cast<const float4 *>(krow + 4 * c);
-            const int d = half * (D / 2) + 4 * c;
+            const int d = half * DP + 4 * c;
 #pragma unroll
             for (int g = 0; g < G; g++)
                 acc[g] += qs[g * D + d] * k4.x + qs[g * D + d + 1] * k4.y + qs[g * D + d + 2] * k4.z +
@@ -204,7 +212,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_partial(const float *__res
     __syncthreads();
     for (int i = tid; i < G * ATT_CH; i += ATT_THREADS) {
         const int g = i / ATT_CH, p = i % ATT_CH;
-        sc[i] = p0 + p < n_pos ? pd[g * ATT_CH + p] + pd[(G + g) * ATT_CH + p] : -__builtin_huge_valf();
+        float t = pd[g * ATT_CH + p];
+#pragma unroll
+        for (int q = 1; q < ATT_PARTS; q++) t += pd[(q * G + g) * ATT_CH + p];
+        sc[i] = p0 + p < n_pos ? t : -__builtin_huge_valf();
     }
     __syncthreads();
     // per-head max and exp; wave w takes heads w, w + 4, ...
@@ -262,7 +273,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_partial(const float *__res
 
 template <int D, int G>
 constexpr size_t attn_lds_bytes() {
-    return (size_t)4 * (ATT_CH * (D + 4) + ATT_CH * D + G * D + G * ATT_CH + 2 * G * ATT_CH);
+    return (size_t)4 * (ATT_CH * (D + 4) + ATT_CH * D + G * D + G * ATT_CH + ATT_PARTS * G * ATT_CH);
 }
 
 // out[h][d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c.  grid = NQ,
