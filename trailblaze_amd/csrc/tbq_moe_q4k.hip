@@ -438,9 +438,8 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
 // fl(w*x)) over k ascending.  Each 64-k chunk of the 64 experts' W (16 KB)
 // and of the 4 tokens' x is loaded once per workgroup with coalesced 16-byte
 // loads and stored to LDS transposed ([k/4][expert] float4), so lane e's
-// ds_read_b128 is conflict-free and x is a broadcast read.  Global loads run
-// three chunks ahead through a 4-slot register ring (the loop is unrolled by
-// 4 so every slot index is static).  Requires H % 256 == 0.
+// ds_read_b128 is conflict-free and x is a broadcast read.  A chunk's global
+// loads are issued while the previous chunk is summed.  Requires H % 256 == 0.
 // grid = (ceil(T/4), ceil(E/64)), 256 threads.
 // ---------------------------------------------------------------------------
 constexpr int RB_TOK = 4, RB_KC = 256, RB_THREADS = 64 * RB_TOK;
@@ -460,21 +459,46 @@ struct RbShared {
     rb_f4 xb[2][RB_TOK][RB_Q];    // [buffer][token][k/4]
 };
 
-// Sum one chunk from LDS, 16 k at a time; the empty asm statements (tied to
-// acc) keep the compiler from hoisting the whole chunk's LDS reads ahead of
-// the arithmetic, which would push the in-flight global loads to scratch.
+// Sum one chunk from LDS, 16 k (4 float4) at a time, with the next group's
+// LDS reads issued before the current group's arithmetic (two register
+// slots, static indices); the empty asm statements (tied to acc) keep the
+// compiler from hoisting more of the chunk's reads, which would push the
+// in-flight global loads to scratch.
 __device__ __forceinline__ float rb_chunk(const RbShared &sh, int b, int lane, int wave, float acc) {
+    constexpr int NG = RB_Q / 4;
+    rb_f4 w[2][4], xv[2][4];
 #pragma unroll
-    for (int q0 = 0; q0 < RB_Q; q0 += 4) {
+    for (int q = 0; q < 4; q++) {
+        w[0][q] = sh.wb[b][q][lane ^ (q & 7)];
+        xv[0][q] = sh.xb[b][wave][q];
+    }
 #pragma unroll
-        for (int q = q0; q < q0 + 4; q++) {
-            const rb_f4 w = sh.wb[b][q][lane ^ (q & 7)];
-            const rb_f4 xv = sh.xb[b][wave][q];
-            acc = acc + w.x * xv.x;
-            acc = acc + w.y * xv.y;
-            acc = acc + w.z * xv.z;
-            acc = acc + w.w * xv.w;
+    for (int g = 0; g < NG; g++) {
+        if (g + 1 < NG) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int qq = 4 * (g + 1) + q;
+                w[(g + 1) & 1][q] = sh.wb[b][qq][lane ^ (qq & 7)];
+                xv[(g + 1) & 1][q] = sh.xb[b][wave][qq];
+            }
         }
+        // the 16 products first (independent), then the dependent adds back
+        // to back: interleaved, every add would wait for the multiply just
+        // issued as well as for the previous add
+        float p[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const rb_f4 ww = w[g & 1][q], xx = xv[g & 1][q];
+            p[4 * q] = ww.x * xx.x;
+            p[4 * q + 1] = ww.y * xx.y;
+            p[4 * q + 2] = ww.z * xx.z;
+            p[4 * q + 3] = ww.w * xx.w;
+        }
+        asm volatile("" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]), "+v"(p[4]), "+v"(p[5]), "+v"(p[6]),
+                     "+v"(p[7]), "+v"(p[8]), "+v"(p[9]), "+v"(p[10]), "+v"(p[11]), "+v"(p[12]), "+v"(p[13]),
+                     "+v"(p[14]), "+v"(p[15]));
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc = acc + p[i];
         asm volatile("" : "+v"(acc));
     }
     return acc;
