@@ -1,0 +1,124 @@
+"""GPU tests of the GGUF loader (include/tbq_gguf.h): every tensor of every
+format libtbq knows (F32/F16/BF16 norms and routers included) uploaded bit
+for bit; a dense model assembled from a file decodes to the same logits, bit
+for bit, as the same weights handed to tbq_dense_decode directly, and within
+the dense tolerance of the float64 oracle; a MoE layer from a file routes and
+combines as the oracle does."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import trailblaze_amd as tb
+from conftest import bits_equal, rel_l2
+from gguf_write import dense_gguf_tensors, write_gguf
+from gpu_util import dev, empty, host
+from test_gguf import KV, sample_tensors
+from trailblaze_amd import formats as fm
+from trailblaze_amd import synth
+from trailblaze_amd.gguf import GgufFile, dense_decode
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    print("device:", tb.init(), flush=True)
+
+
+def test_gguf_upload_all_bit_exact(tmp_path):
+    ts = sample_tensors(np.random.default_rng(9))
+    path = tmp_path / "all.gguf"
+    write_gguf(path, KV, ts, alignment=64)
+    with GgufFile(path) as g:
+        n = g.upload_all()
+        assert n == len(ts) - 1   # all but the unknown qtype
+        for name, qt, dims, data in ts:
+            p = g.device_ptr(name)
+            if name == "unknown":
+                assert p == 0
+                continue
+            raw = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+            back = np.empty_like(raw)
+            assert tb.lib().tbq_memcpy_d2h(back.ctypes.data_as(C.c_void_p), C.c_void_p(p), raw.size, None)
+            assert tb.lib().tbq_stream_sync(None)
+            assert np.array_equal(back, raw), name
+        assert g.upload_all() == n   # idempotent
+
+
+def test_gguf_dense_model_decode(tmp_path, oracle):
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import DenseConfig, SyntheticDense
+    cfg = DenseConfig(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=512, max_ctx=64)
+    syn = SyntheticDense(cfg, 11, keep_host=True)
+    kv, ts = dense_gguf_tensors(cfg, syn.host)
+    path = tmp_path / "dense.gguf"
+    write_gguf(path, kv, ts)
+    ref = DenseOracle(oracle, cfg, syn.host)
+    with GgufFile(path) as g:
+        m, ws = g.dense_model(cfg.max_ctx)
+        assert (m.n_layers, m.hidden, m.n_heads, m.n_kv_heads, m.head_dim, m.ffn, m.vocab) == \
+               (2, 256, 4, 2, 64, 512, 512)
+        assert m.qtype_layers == cfg.qtype_layers and m.qtype_embd == cfg.qtype_embd
+        assert m.lm_head == m.tok_embd   # no output.weight: tied
+        a = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+        b = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+        for pos, tok in enumerate([5, 300, 511]):
+            print("gguf dense step", pos, flush=True)
+            dense_decode(m, ws, tok, pos, a)
+            syn.decode(tok, pos, b)
+            la, lb = host(a), host(b)
+            assert bits_equal(la, lb), pos
+            assert rel_l2(la, ref.decode(tok, pos)) <= 1e-4, pos
+
+
+def test_gguf_dense_model_rejects_mixed_qtypes(tmp_path):
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=1, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=256, vocab=256, max_ctx=16)
+    rng = np.random.default_rng(3)
+    host = {"lm_head": synth.kquant_matrix(fm.Q6_K, 256, 256, rng), "output_norm": np.ones(256, np.float32),
+            "layers": [{"attn_norm": np.ones(256), "q_norm": np.ones(64), "k_norm": np.ones(64),
+                        "ffn_norm": np.ones(256), "wqkv": synth.kquant_matrix(fm.Q4_K, 512, 256, rng),
+                        "wo": synth.kquant_matrix(fm.Q4_K, 256, 256, rng),
+                        "wgu": synth.kquant_matrix(fm.Q4_K, 512, 256, rng),
+                        "wdown": synth.kquant_matrix(fm.Q4_K, 256, 256, rng)}]}
+    kv, ts = dense_gguf_tensors(cfg, host)
+    ts = [(n, fm.Q8_0, d, synth.kquant_matrix(fm.Q8_0, d[1], d[0], rng)) if n == "blk.0.attn_v.weight" else (n, q, d, x)
+          for n, q, d, x in ts]
+    path = tmp_path / "mixed.gguf"
+    write_gguf(path, kv, ts)
+    with GgufFile(path) as g:
+        with pytest.raises(tb.TbqError, match="attn_v.*qtype"):
+            g.dense_model(16)
+
+
+def test_gguf_moe_layer(tmp_path, oracle):
+    import torch
+    H, F, E, k = 512, 256, 16, 4
+    router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=21)
+    kv = [("general.architecture", "str", "qwen3moe"), ("qwen3moe.embedding_length", "u32", H),
+          ("qwen3moe.expert_count", "u32", E), ("qwen3moe.expert_used_count", "u32", k),
+          ("qwen3moe.expert_feed_forward_length", "u32", F)]
+    ts = [("blk.0.ffn_gate_inp.weight", fm.F32, (H, E), router),
+          ("blk.0.ffn_gate_exps.weight", fm.Q4_K, (H, F, E), gate),
+          ("blk.0.ffn_up_exps.weight", fm.Q4_K, (H, F, E), up),
+          ("blk.0.ffn_down_exps.weight", fm.Q4_K, (F, H, E), down)]
+    path = tmp_path / "moe.gguf"
+    write_gguf(path, kv, ts)
+    rng = np.random.default_rng(21)
+    T = 3
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    with GgufFile(path) as g:
+        L = g.moe_layer(0)
+        assert (L.H, L.F, L.E, L.top_k, L.qtype) == (H, F, E, k, fm.Q4_K)
+        out = empty(T * H, torch.float32)
+        idx = empty(T * 8, torch.int32)
+        w = empty(T * 8, torch.float32)
+        ws = torch.zeros(tb.moe_workspace_size(L, T), dtype=torch.uint8, device="cuda")
+        tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws)
+        ref, ridx, rw = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
+        assert np.array_equal(host(idx).reshape(T, 8), ridx)
+        assert bits_equal(host(w).reshape(T, 8), rw)
+        assert rel_l2(host(out).reshape(T, H) - resid, ref - resid) <= 1e-5

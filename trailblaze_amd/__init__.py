@@ -23,8 +23,8 @@ TBQ_MOE_FP32 = 0
 TBQ_MOE_BF16 = 1
 TBQ_MV_AUTO, TBQ_MV_FMA, TBQ_MV_INTDOT, TBQ_MV_KQ = 0, 1, 2, 3
 
-# (name, restype, argtypes) for every symbol declared in include/tbq.h and
-# include/tb_gguf_dequant.h.
+# (name, restype, argtypes) for every symbol declared in include/tbq.h,
+# include/tbq_gguf.h and include/tb_gguf_dequant.h.
 _vp, _i, _sz, _f = C.c_void_p, C.c_int, C.c_size_t, C.c_float
 SYMBOLS = {
     # include/tbq.h
@@ -51,6 +51,21 @@ SYMBOLS = {
     "tbq_dense_decode": (_i, [_vp, _i, _i, _vp, _vp, _sz, _vp]),
     "tbq_expf_device": (_i, [_vp, _vp, _sz, _vp]),
     "tbq_expf_host": (_f, [_f]),
+    # include/tbq_gguf.h
+    "tbq_gguf_open": (_vp, [C.c_char_p]),
+    "tbq_gguf_close": (None, [_vp]),
+    "tbq_gguf_n_tensors": (_i, [_vp]),
+    "tbq_gguf_find": (_i, [_vp, C.c_char_p]),
+    "tbq_gguf_tensor_name": (C.c_char_p, [_vp, _i]),
+    "tbq_gguf_tensor_info": (_i, [_vp, _i, _vp, _vp, _vp, _vp]),
+    "tbq_gguf_tensor_host": (_vp, [_vp, _i]),
+    "tbq_gguf_get_int": (_i, [_vp, C.c_char_p, _vp]),
+    "tbq_gguf_get_float": (_i, [_vp, C.c_char_p, _vp]),
+    "tbq_gguf_get_str": (_i, [_vp, C.c_char_p, _vp, _sz]),
+    "tbq_gguf_upload_all": (_i, [_vp]),
+    "tbq_gguf_tensor_device": (_vp, [_vp, _i]),
+    "tbq_gguf_dense_model": (_i, [_vp, _i, _vp, _vp, _i]),
+    "tbq_gguf_moe_layer": (_i, [_vp, _i, _vp]),
     # include/tb_gguf_dequant.h (the reference ABI)
     "tb_cuda_init": (_i, []),
     "tb_cuda_upload_tensor": (_vp, [_vp, _sz]),

@@ -77,6 +77,9 @@ extern "C" {
 
 int tbq_init(void) { return ensure_init(); }
 const char *tbq_last_error(void) { return g_err; }
+
+// Error setter for libtbq's C11 host files (hidden: not part of the ABI).
+__attribute__((visibility("hidden"))) int tbq_host_fail(const char *msg) { return fail("%s", msg); }
 const char *tbq_device_name(void) { return g_name; }
 int tbq_cu_count(void) { return g_cu; }
 
