@@ -130,16 +130,22 @@ typedef struct {
     const float *q_norm;      /* [head_dim] */
     const float *k_norm;      /* [head_dim] */
     const float *ffn_norm;    /* [hidden] */
-    const void *wqkv;         /* [(n_heads + 2 n_kv_heads) head_dim][hidden]: q | k | v rows */
+    const void *wqkv;         /* [(n_heads + 2 n_kv_heads) head_dim][hidden]: q | k | v rows,
+                                 or NULL: wq, wk, wv below */
     const void *wo;           /* [hidden][n_heads head_dim] */
-    const void *wgu;          /* [2 ffn][hidden]: gate | up rows */
+    const void *wgu;          /* [2 ffn][hidden]: gate | up rows, or NULL: wgate, wup below */
     const void *wdown;        /* [hidden][ffn] */
+    /* separate matrices of a layer whose q, k, v (gate, up) differ in qtype */
+    const void *wq, *wk, *wv; /* [n_heads head_dim], [n_kv_heads head_dim] x2 rows of [hidden] */
+    const void *wgate, *wup;  /* [ffn][hidden] each */
+    /* qtype of each matrix; 0 = the model's qtype_layers */
+    int qt_qkv, qt_o, qt_gu, qt_down, qt_q, qt_k, qt_v, qt_gate, qt_up;
 } tbq_dense_layer;
 
 typedef struct {
     int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx;
     float norm_eps, rope_theta;
-    int qtype_layers;         /* qtype of wqkv/wo/wgu/wdown (any tbq_matvec qtype) */
+    int qtype_layers;         /* qtype of the layer matrices whose qt_* field is 0 (any tbq_matvec qtype) */
     int qtype_embd;           /* qtype of tok_embd and lm_head */
     const void *tok_embd;     /* [vocab][hidden] (may alias lm_head: tied embeddings) */
     const void *lm_head;      /* [vocab][hidden] */

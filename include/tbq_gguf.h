@@ -70,10 +70,11 @@ const void *tbq_gguf_tensor_device(const tbq_gguf *g, int i);
  * attn_k_norm, attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down},
  * token_embd, output_norm and output (tied to token_embd when absent).
  * Uploads what is not resident yet, fuses each layer's q|k|v and gate|up
- * rows into one device matrix and allocates fp32 KV caches of max_ctx
- * positions, all owned by g.  `layers` is a caller array of n_layers
- * entries (tbq_gguf_get_int(g, "<arch>.block_count", ...)).  The layers'
- * seven matrices must share one qtype (0 and a message otherwise). */
+ * rows into one device matrix where they share a qtype (mixed-quant files,
+ * e.g. a Q6_K attn_v among Q4_K matrices, keep them separate, each with its
+ * own qtype) and allocates fp32 KV caches of max_ctx positions, all owned
+ * by g.  `layers` is a caller array of n_layers entries
+ * (tbq_gguf_get_int(g, "<arch>.block_count", ...)). */
 int tbq_gguf_dense_model(tbq_gguf *g, int max_ctx, tbq_dense_model *m, tbq_dense_layer *layers, int n_layers);
 
 /* MoE layer `layer` of the file (tensors blk.N.ffn_gate_inp (router, F32),

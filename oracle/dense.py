@@ -65,18 +65,33 @@ class DenseOracle:
     fp64 KV cache."""
 
     def __init__(self, oracle, cfg, host):
+        """host["layers"][l] holds wqkv (or wq, wk, wv), wo, wgu (or wgate,
+        wup), wdown and the norms; an optional qt_<name> gives that matrix's
+        qtype (default cfg.qtype_layers)."""
         c = self.cfg = cfg
+        D, NQ, NKV = c.head_dim, c.n_heads, c.n_kv_heads
         deq = lambda W, qt, M, K: oracle.dequant_rows(W, qt, M, K).astype(np.float64)
-        QR = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
+        QR = (NQ + 2 * NKV) * D
         self.layers = []
         for t in host["layers"]:
+            qt = lambda name: t.get("qt_" + name, c.qtype_layers)
+            if "wqkv" in t:
+                wqkv = deq(t["wqkv"], qt("wqkv"), QR, c.hidden)
+            else:
+                wqkv = np.concatenate([deq(t["wq"], qt("wq"), NQ * D, c.hidden),
+                                       deq(t["wk"], qt("wk"), NKV * D, c.hidden),
+                                       deq(t["wv"], qt("wv"), NKV * D, c.hidden)])
+            if "wgu" in t:
+                wgu = deq(t["wgu"], qt("wgu"), 2 * c.ffn, c.hidden)
+            else:
+                wgu = np.concatenate([deq(t["wgate"], qt("wgate"), c.ffn, c.hidden),
+                                      deq(t["wup"], qt("wup"), c.ffn, c.hidden)])
             self.layers.append({
                 "attn_norm": t["attn_norm"], "q_norm": t["q_norm"], "k_norm": t["k_norm"],
-                "ffn_norm": t["ffn_norm"],
-                "wqkv": deq(t["wqkv"], c.qtype_layers, QR, c.hidden),
-                "wo": deq(t["wo"], c.qtype_layers, c.hidden, c.n_heads * c.head_dim),
-                "wgu": deq(t["wgu"], c.qtype_layers, 2 * c.ffn, c.hidden),
-                "wdown": deq(t["wdown"], c.qtype_layers, c.hidden, c.ffn)})
+                "ffn_norm": t["ffn_norm"], "wqkv": wqkv,
+                "wo": deq(t["wo"], qt("wo"), c.hidden, NQ * D),
+                "wgu": wgu,
+                "wdown": deq(t["wdown"], qt("wdown"), c.hidden, c.ffn)})
         self.lm = deq(host["lm_head"], c.qtype_embd, c.vocab, c.hidden)
         self.output_norm = host["output_norm"]
         shape = (c.n_layers, c.n_kv_heads, c.max_ctx, c.head_dim)

@@ -79,17 +79,27 @@ def dense_gguf_tensors(cfg, host, arch="qwen3"):
     ts = [("token_embd.weight", c.qtype_embd, (c.hidden, c.vocab), host["lm_head"]),
           ("output_norm.weight", fm.F32, (c.hidden,), f32(host["output_norm"]))]
     for l, t in enumerate(host["layers"]):
-        qkv, gu = t["wqkv"], t["wgu"]
+        qt = lambda name: t.get("qt_" + name, c.qtype_layers)
+        if "wqkv" in t:
+            qkv = t["wqkv"]
+            q, k, v = qkv[:NQ * D], qkv[NQ * D:(NQ + NKV) * D], qkv[(NQ + NKV) * D:]
+            qq = qk = qv = qt("wqkv")
+        else:
+            q, k, v, qq, qk, qv = t["wq"], t["wk"], t["wv"], qt("wq"), qt("wk"), qt("wv")
+        if "wgu" in t:
+            gate, up, qg, qu = t["wgu"][:c.ffn], t["wgu"][c.ffn:], qt("wgu"), qt("wgu")
+        else:
+            gate, up, qg, qu = t["wgate"], t["wup"], qt("wgate"), qt("wup")
         p = f"blk.{l}."
         ts += [(p + "attn_norm.weight", fm.F32, (c.hidden,), f32(t["attn_norm"])),
-               (p + "attn_q.weight", c.qtype_layers, (c.hidden, NQ * D), qkv[:NQ * D]),
-               (p + "attn_k.weight", c.qtype_layers, (c.hidden, NKV * D), qkv[NQ * D:(NQ + NKV) * D]),
-               (p + "attn_v.weight", c.qtype_layers, (c.hidden, NKV * D), qkv[(NQ + NKV) * D:]),
+               (p + "attn_q.weight", qq, (c.hidden, NQ * D), q),
+               (p + "attn_k.weight", qk, (c.hidden, NKV * D), k),
+               (p + "attn_v.weight", qv, (c.hidden, NKV * D), v),
                (p + "attn_q_norm.weight", fm.F32, (D,), f32(t["q_norm"])),
                (p + "attn_k_norm.weight", fm.F32, (D,), f32(t["k_norm"])),
-               (p + "attn_output.weight", c.qtype_layers, (NQ * D, c.hidden), t["wo"]),
+               (p + "attn_output.weight", qt("wo"), (NQ * D, c.hidden), t["wo"]),
                (p + "ffn_norm.weight", fm.F32, (c.hidden,), f32(t["ffn_norm"])),
-               (p + "ffn_gate.weight", c.qtype_layers, (c.hidden, c.ffn), gu[:c.ffn]),
-               (p + "ffn_up.weight", c.qtype_layers, (c.hidden, c.ffn), gu[c.ffn:]),
-               (p + "ffn_down.weight", c.qtype_layers, (c.ffn, c.hidden), t["wdown"])]
+               (p + "ffn_gate.weight", qg, (c.hidden, c.ffn), gate),
+               (p + "ffn_up.weight", qu, (c.hidden, c.ffn), up),
+               (p + "ffn_down.weight", qt("wdown"), (c.ffn, c.hidden), t["wdown"])]
     return kv, ts

@@ -73,24 +73,43 @@ def test_gguf_dense_model_decode(tmp_path, oracle):
             assert rel_l2(la, ref.decode(tok, pos)) <= 1e-4, pos
 
 
-def test_gguf_dense_model_rejects_mixed_qtypes(tmp_path):
+def test_gguf_dense_model_mixed_qtypes(tmp_path, oracle):
+    """A mixed-quant file (as llama.cpp's Q4_K_M recipes write them): layer 0
+    has a Q6_K attn_v and gate / up of different formats, layer 1 a Q6_K
+    ffn_down and a Q5_K attn_output; q|k|v and gate|up then stay separate
+    matrices, each with its own qtype."""
+    import torch
+    from oracle.dense import DenseOracle
     from trailblaze_amd.dense import DenseConfig
-    cfg = DenseConfig(n_layers=1, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=256, vocab=256, max_ctx=16)
-    rng = np.random.default_rng(3)
-    host = {"lm_head": synth.kquant_matrix(fm.Q6_K, 256, 256, rng), "output_norm": np.ones(256, np.float32),
-            "layers": [{"attn_norm": np.ones(256), "q_norm": np.ones(64), "k_norm": np.ones(64),
-                        "ffn_norm": np.ones(256), "wqkv": synth.kquant_matrix(fm.Q4_K, 512, 256, rng),
-                        "wo": synth.kquant_matrix(fm.Q4_K, 256, 256, rng),
-                        "wgu": synth.kquant_matrix(fm.Q4_K, 512, 256, rng),
-                        "wdown": synth.kquant_matrix(fm.Q4_K, 256, 256, rng)}]}
-    kv, ts = dense_gguf_tensors(cfg, host)
-    ts = [(n, fm.Q8_0, d, synth.kquant_matrix(fm.Q8_0, d[1], d[0], rng)) if n == "blk.0.attn_v.weight" else (n, q, d, x)
-          for n, q, d, x in ts]
+    cfg = DenseConfig(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=256, max_ctx=32)
+    c, rng = cfg, np.random.default_rng(31)
+    D, NQ, NKV = c.head_dim, c.n_heads, c.n_kv_heads
+    norm = lambda n: (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    mat = lambda qt, M, K: synth.kquant_matrix(qt, M, K, rng)
+    l0 = {"attn_norm": norm(256), "q_norm": norm(64), "k_norm": norm(64), "ffn_norm": norm(256),
+          "wq": mat(fm.Q4_K, NQ * D, 256), "wk": mat(fm.Q4_K, NKV * D, 256), "wv": mat(fm.Q6_K, NKV * D, 256),
+          "qt_wq": fm.Q4_K, "qt_wk": fm.Q4_K, "qt_wv": fm.Q6_K,
+          "wo": mat(fm.Q4_K, 256, NQ * D), "wgate": mat(fm.Q4_K, 512, 256), "wup": mat(fm.Q5_K, 512, 256),
+          "qt_wgate": fm.Q4_K, "qt_wup": fm.Q5_K, "wdown": mat(fm.Q4_K, 256, 512)}
+    l1 = {"attn_norm": norm(256), "q_norm": norm(64), "k_norm": norm(64), "ffn_norm": norm(256),
+          "wqkv": mat(fm.Q4_K, (NQ + 2 * NKV) * D, 256), "wo": mat(fm.Q5_K, 256, NQ * D), "qt_wo": fm.Q5_K,
+          "wgu": mat(fm.Q4_K, 1024, 256), "wdown": mat(fm.Q6_K, 256, 512), "qt_wdown": fm.Q6_K}
+    hostd = {"layers": [l0, l1], "lm_head": mat(fm.Q6_K, 256, 256), "output_norm": norm(256)}
+    kv, ts = dense_gguf_tensors(cfg, hostd)
     path = tmp_path / "mixed.gguf"
     write_gguf(path, kv, ts)
+    ref = DenseOracle(oracle, cfg, hostd)
     with GgufFile(path) as g:
-        with pytest.raises(tb.TbqError, match="attn_v.*qtype"):
-            g.dense_model(16)
+        m, ws = g.dense_model(cfg.max_ctx)
+        L0, L1 = m.layers[0], m.layers[1]
+        assert not L0.wqkv and L0.wq and (L0.qt_q, L0.qt_k, L0.qt_v) == (fm.Q4_K, fm.Q4_K, fm.Q6_K)
+        assert not L0.wgu and (L0.qt_gate, L0.qt_up) == (fm.Q4_K, fm.Q5_K)
+        assert L1.wqkv and L1.wgu and (L1.qt_o, L1.qt_down) == (fm.Q5_K, fm.Q6_K)
+        logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+        for pos, tok in enumerate([1, 77, 255, 3]):
+            print("gguf mixed-quant step", pos, flush=True)
+            dense_decode(m, ws, tok, pos, logits)
+            assert rel_l2(host(logits), ref.decode(tok, pos)) <= 1e-4, pos
 
 
 def test_gguf_moe_layer(tmp_path, oracle):

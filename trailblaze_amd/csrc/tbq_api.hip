@@ -283,12 +283,18 @@ static int check_dense(const tbq_dense_model *m) {
         return fail("tbq_dense: unsupported qtype");
     if (!m->tok_embd || !m->lm_head || !m->output_norm || !m->k_cache || !m->v_cache)
         return fail("tbq_dense: null tensor");
+    auto qt_ok = [m](int q) { return tbq_qtype_supported(q ? q : m->qtype_layers); };
+    auto w_ok = [](const void *p) { return p && aligned16(p); };
     for (int l = 0; l < m->n_layers; l++) {
         const tbq_dense_layer &L = m->layers[l];
-        if (!L.attn_norm || !L.q_norm || !L.k_norm || !L.ffn_norm || !L.wqkv || !L.wo || !L.wgu || !L.wdown)
-            return fail("tbq_dense: null tensor in layer %d", l);
-        if (!aligned16(L.wqkv) || !aligned16(L.wo) || !aligned16(L.wgu) || !aligned16(L.wdown))
-            return fail("tbq_dense: layer %d weights must be 16-byte aligned", l);
+        if (!L.attn_norm || !L.q_norm || !L.k_norm || !L.ffn_norm)
+            return fail("tbq_dense: null norm weights in layer %d", l);
+        const bool qkv = L.wqkv ? w_ok(L.wqkv) && qt_ok(L.qt_qkv)
+                                : w_ok(L.wq) && w_ok(L.wk) && w_ok(L.wv) && qt_ok(L.qt_q) && qt_ok(L.qt_k) && qt_ok(L.qt_v);
+        const bool gu = L.wgu ? w_ok(L.wgu) && qt_ok(L.qt_gu)
+                              : w_ok(L.wgate) && w_ok(L.wup) && qt_ok(L.qt_gate) && qt_ok(L.qt_up);
+        if (!qkv || !gu || !w_ok(L.wo) || !w_ok(L.wdown) || !qt_ok(L.qt_o) || !qt_ok(L.qt_down))
+            return fail("tbq_dense: layer %d: a weight matrix is null, not 16-byte aligned or of an unsupported qtype", l);
     }
     return 1;
 }

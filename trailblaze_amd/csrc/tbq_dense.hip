@@ -404,7 +404,8 @@ static hipError_t dense_mv(int qt, const void *W, int M, int K, const float *x, 
 hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,
                                hipStream_t st) {
     const int H = m->hidden, D = m->head_dim, NQ = m->n_heads, NKV = m->n_kv_heads, G = NQ / NKV, F = m->ffn;
-    const int QKVR = (NQ + 2 * NKV) * D, qt = m->qtype_layers;
+    const int QKVR = (NQ + 2 * NKV) * D;
+    auto qt_of = [m](int q) { return q ? q : m->qtype_layers; };
     const DenseWs w = dense_ws(m, ws, nullptr);
     const size_t erb = tbq_row_bytes(m->qtype_embd, H);
     float *xa = w.x, *xb = w.x2;
@@ -415,21 +416,45 @@ hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, flo
     for (int l = 0; l < m->n_layers; l++) {
         const tbq_dense_layer &L = m->layers[l];
         const size_t kvoff = (size_t)l * NKV * m->max_ctx * D;
-        // qkv = Wqkv rmsnorm(xa + yprev); xb = xa + yprev
-        const MvPro pa{yprev, L.attn_norm, xb, m->norm_eps};
-        if ((err = dense_mv(qt, L.wqkv, QKVR, H, xa, w.qkv, PRO_NORM, pa, w.h, nullptr, st)) != hipSuccess) return err;
+        // qkv = Wqkv rmsnorm(xa + yprev); xb = xa + yprev (stored by the first
+        // launch only when q, k and v are separate matrices)
+        const MvPro pa{yprev, L.attn_norm, xb, m->norm_eps}, pa2{yprev, L.attn_norm, nullptr, m->norm_eps};
+        if (L.wqkv) {
+            err = dense_mv(qt_of(L.qt_qkv), L.wqkv, QKVR, H, xa, w.qkv, PRO_NORM, pa, w.h, nullptr, st);
+        } else {
+            err = dense_mv(qt_of(L.qt_q), L.wq, NQ * D, H, xa, w.qkv, PRO_NORM, pa, w.h, nullptr, st);
+            if (err == hipSuccess)
+                err = dense_mv(qt_of(L.qt_k), L.wk, NKV * D, H, xa, w.qkv + NQ * D, PRO_NORM, pa2, w.h, nullptr, st);
+            if (err == hipSuccess)
+                err = dense_mv(qt_of(L.qt_v), L.wv, NKV * D, H, xa, w.qkv + (NQ + NKV) * D, PRO_NORM, pa2, w.h,
+                               nullptr, st);
+        }
+        if (err != hipSuccess) return err;
         err = D == 128 ? launch_attn_d<128>(G, w.qkv, L.q_norm, L.k_norm, NQ, NKV, pos, w.rope, m->norm_eps,
                                             m->k_cache + kvoff, m->v_cache + kvoff, m->max_ctx, w.part, w.att, st)
                        : launch_attn_d<64>(G, w.qkv, L.q_norm, L.k_norm, NQ, NKV, pos, w.rope, m->norm_eps,
                                            m->k_cache + kvoff, m->v_cache + kvoff, m->max_ctx, w.part, w.att, st);
         if (err != hipSuccess) return err;
-        if ((err = dense_mv(qt, L.wo, H, NQ * D, w.att, w.y, PRO_NONE, MvPro{}, nullptr, nullptr, st)) != hipSuccess)
+        if ((err = dense_mv(qt_of(L.qt_o), L.wo, H, NQ * D, w.att, w.y, PRO_NONE, MvPro{}, nullptr, nullptr, st)) !=
+            hipSuccess)
             return err;
         // a = silu(Wg h) * (Wu h) with h = rmsnorm(xb + y); xa = xb + y
-        const MvPro pf{w.y, L.ffn_norm, xa, m->norm_eps};
-        if ((err = dense_mv(qt, L.wgu, F, H, xb, w.a, PRO_NORM | MV_GLU, pf, w.h, w.gu, st)) != hipSuccess) return err;
+        const MvPro pf{w.y, L.ffn_norm, xa, m->norm_eps}, pf2{w.y, L.ffn_norm, nullptr, m->norm_eps};
+        if (L.wgu) {
+            err = dense_mv(qt_of(L.qt_gu), L.wgu, F, H, xb, w.a, PRO_NORM | MV_GLU, pf, w.h, w.gu, st);
+        } else {
+            err = dense_mv(qt_of(L.qt_gate), L.wgate, F, H, xb, w.gu, PRO_NORM, pf, w.h, nullptr, st);
+            if (err == hipSuccess)
+                err = dense_mv(qt_of(L.qt_up), L.wup, F, H, xb, w.gu + F, PRO_NORM, pf2, w.h, nullptr, st);
+            if (err == hipSuccess) {
+                hipLaunchKernelGGL(k_swiglu, dim3((F + 255) / 256), dim3(256), 0, st, w.gu, F, w.a);
+                err = hipGetLastError();
+            }
+        }
+        if (err != hipSuccess) return err;
         // y = Wdown a
-        if ((err = dense_mv(qt, L.wdown, H, F, w.a, w.y, PRO_NONE, MvPro{}, nullptr, nullptr, st)) != hipSuccess)
+        if ((err = dense_mv(qt_of(L.qt_down), L.wdown, H, F, w.a, w.y, PRO_NONE, MvPro{}, nullptr, nullptr, st)) !=
+            hipSuccess)
             return err;
         yprev = w.y;
     }

@@ -19,7 +19,10 @@ _vp, _i, _f = C.c_void_p, C.c_int, C.c_float
 
 class DenseLayer(C.Structure):
     _fields_ = [("attn_norm", _vp), ("q_norm", _vp), ("k_norm", _vp), ("ffn_norm", _vp),
-                ("wqkv", _vp), ("wo", _vp), ("wgu", _vp), ("wdown", _vp)]
+                ("wqkv", _vp), ("wo", _vp), ("wgu", _vp), ("wdown", _vp),
+                ("wq", _vp), ("wk", _vp), ("wv", _vp), ("wgate", _vp), ("wup", _vp),
+                ("qt_qkv", _i), ("qt_o", _i), ("qt_gu", _i), ("qt_down", _i), ("qt_q", _i), ("qt_k", _i),
+                ("qt_v", _i), ("qt_gate", _i), ("qt_up", _i)]
 
 
 class DenseModel(C.Structure):

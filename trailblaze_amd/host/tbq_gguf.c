@@ -469,33 +469,62 @@ int tbq_gguf_dense_model(tbq_gguf *g, int max_ctx, tbq_dense_model *m, tbq_dense
         return failf("tbq_gguf_dense_model: token_embd / output shapes or qtypes disagree");
     int on = need(g, 1, 0, H, -1, "output_norm.weight");
     if (on < 0 || !upload(g, te) || !upload(g, head)) return 0;
-    int qt = -1;
+    int qt = -1;   /* the model's qtype_layers: layer 0's attn_q */
     for (int l = 0; l < n_layers; l++) {
-        const int iq = need(g, 0, qt, H, NQ * D, "blk.%d.attn_q.weight", l);
-        if (iq < 0) return 0;
-        if (qt < 0) qt = g->t[iq].qtype;
-        const int ik = need(g, 0, qt, H, NKV * D, "blk.%d.attn_k.weight", l);
-        const int iv = need(g, 0, qt, H, NKV * D, "blk.%d.attn_v.weight", l);
-        const int io = need(g, 1, qt, NQ * D, H, "blk.%d.attn_output.weight", l);
-        const int ig = need(g, 0, qt, H, F, "blk.%d.ffn_gate.weight", l);
-        const int iu = need(g, 0, qt, H, F, "blk.%d.ffn_up.weight", l);
-        const int id = need(g, 1, qt, F, H, "blk.%d.ffn_down.weight", l);
+        const int iq = need(g, 0, -1, H, NQ * D, "blk.%d.attn_q.weight", l);
+        const int ik = need(g, 0, -1, H, NKV * D, "blk.%d.attn_k.weight", l);
+        const int iv = need(g, 0, -1, H, NKV * D, "blk.%d.attn_v.weight", l);
+        const int io = need(g, 1, -1, NQ * D, H, "blk.%d.attn_output.weight", l);
+        const int ig = need(g, 0, -1, H, F, "blk.%d.ffn_gate.weight", l);
+        const int iu = need(g, 0, -1, H, F, "blk.%d.ffn_up.weight", l);
+        const int id = need(g, 1, -1, F, H, "blk.%d.ffn_down.weight", l);
         const int ian = need(g, 1, 0, H, -1, "blk.%d.attn_norm.weight", l);
         const int iqn = need(g, 1, 0, D, -1, "blk.%d.attn_q_norm.weight", l);
         const int ikn = need(g, 1, 0, D, -1, "blk.%d.attn_k_norm.weight", l);
         const int ifn = need(g, 1, 0, H, -1, "blk.%d.ffn_norm.weight", l);
-        if (ik < 0 || iv < 0 || io < 0 || ig < 0 || iu < 0 || id < 0 || ian < 0 || iqn < 0 || ikn < 0 || ifn < 0)
+        if (iq < 0 || ik < 0 || iv < 0 || io < 0 || ig < 0 || iu < 0 || id < 0 || ian < 0 || iqn < 0 || ikn < 0 ||
+            ifn < 0)
             return 0;
+        if (qt < 0) qt = g->t[iq].qtype;
+        /* a qt_* field of 0 means qtype_layers, so an F32 matrix needs qtype_layers F32 */
+        const int mats[7] = {iq, ik, iv, io, ig, iu, id};
+        for (int k = 0; k < 7; k++)
+            if (g->t[mats[k]].qtype == 0 && qt != 0)
+                return failf("tbq_gguf_dense_model: %s is F32 among quantised layer matrices", g->t[mats[k]].name);
         tbq_dense_layer *ly = &layers[l];
+        memset(ly, 0, sizeof *ly);
         ly->attn_norm = (const float *)g->t[ian].dev;
         ly->q_norm = (const float *)g->t[iqn].dev;
         ly->k_norm = (const float *)g->t[ikn].dev;
         ly->ffn_norm = (const float *)g->t[ifn].dev;
-        ly->wqkv = fuse(g, iq, ik, iv);
-        ly->wgu = fuse(g, ig, iu, -1);
         ly->wo = g->t[io].dev;
+        ly->qt_o = g->t[io].qtype;
         ly->wdown = g->t[id].dev;
-        if (!ly->wqkv || !ly->wgu) return 0;
+        ly->qt_down = g->t[id].qtype;
+        /* one fused device matrix where the rows share a qtype, else the
+         * separate matrices (one launch each) */
+        if (g->t[iq].qtype == g->t[ik].qtype && g->t[iq].qtype == g->t[iv].qtype) {
+            if (!(ly->wqkv = fuse(g, iq, ik, iv))) return 0;
+            ly->qt_qkv = g->t[iq].qtype;
+        } else {
+            if (!upload(g, iq) || !upload(g, ik) || !upload(g, iv)) return 0;
+            ly->wq = g->t[iq].dev;
+            ly->wk = g->t[ik].dev;
+            ly->wv = g->t[iv].dev;
+            ly->qt_q = g->t[iq].qtype;
+            ly->qt_k = g->t[ik].qtype;
+            ly->qt_v = g->t[iv].qtype;
+        }
+        if (g->t[ig].qtype == g->t[iu].qtype) {
+            if (!(ly->wgu = fuse(g, ig, iu, -1))) return 0;
+            ly->qt_gu = g->t[ig].qtype;
+        } else {
+            if (!upload(g, ig) || !upload(g, iu)) return 0;
+            ly->wgate = g->t[ig].dev;
+            ly->wup = g->t[iu].dev;
+            ly->qt_gate = g->t[ig].qtype;
+            ly->qt_up = g->t[iu].qtype;
+        }
     }
     const size_t kv_bytes = (size_t)L * (size_t)NKV * (size_t)max_ctx * (size_t)D * 4;
     float *kc = (float *)own(g, kv_bytes), *vc = (float *)own(g, kv_bytes);
