@@ -79,6 +79,34 @@ def test_dense_decode_long_context(oracle, qt):
         assert err <= DENSE_TOL, (pos, err)
 
 
+@pytest.mark.parametrize("nq,nkv,D", [(4, 4, 64), (8, 1, 64), (8, 1, 128), (4, 2, 128)])
+def test_dense_decode_gqa_groups(oracle, nq, nkv, D):
+    """Every query-heads-per-kv-head group the attention kernel is built for
+    (1 = multi-head, 2, 4, 8) at both head dims, over two chunks of cache."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import DenseConfig
+    H = max(256, nq * D)
+    cfg = DenseConfig(n_layers=1, hidden=H, n_heads=nq, n_kv_heads=nkv, head_dim=D, ffn=256, vocab=256,
+                      max_ctx=320)
+    m = _model(cfg, 7)
+    ref = DenseOracle(oracle, cfg, m.host)
+    rng = np.random.default_rng(11)
+    P = 140   # positions 0..139 cached: the step attends over two 128-position chunks
+    kc = np.zeros(ref.kc.shape, np.float32)
+    vc = np.zeros(ref.vc.shape, np.float32)
+    kc[:, :, :P] = rng.standard_normal(kc[:, :, :P].shape)
+    vc[:, :, :P] = rng.standard_normal(vc[:, :, :P].shape)
+    m.k_cache.copy_(torch.from_numpy(kc))
+    m.v_cache.copy_(torch.from_numpy(vc))
+    ref.kc[:] = kc
+    ref.vc[:] = vc
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    print("dense gqa", nq, nkv, D, flush=True)
+    m.decode(9, P, logits)
+    assert rel_l2(host(logits), ref.decode(9, P)) <= DENSE_TOL
+
+
 def test_dense_decode_qwen3_4b_layer(oracle):
     """One layer at the Qwen3-4B widths (hidden 2560, 32/8 heads of 128, ffn
     9728), so every matvec runs the kernel and staging prologue the full
