@@ -128,6 +128,25 @@ def test_dense_decode_qwen3_4b_layer(oracle):
         assert err <= DENSE_TOL, (pos, err)
 
 
+@pytest.mark.parametrize("qt", [fm.Q4_K, fm.Q8_0])
+def test_dense_decode_wide_hidden(oracle, qt):
+    """hidden 4608 (72 units per row): the q|k|v, gate|up and lm_head
+    matvecs run the K-quant kernel with rows split over two waves, with the
+    add+RMSNorm prologue and the SwiGLU epilogue on that split."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=1, hidden=4608, n_heads=32, n_kv_heads=4, head_dim=128, ffn=512, vocab=256,
+                      max_ctx=64, qtype_layers=qt)
+    m = _model(cfg, 8)
+    ref = DenseOracle(oracle, cfg, m.host)
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    for pos, tok in enumerate([4, 200]):
+        print("dense wide-hidden step", pos, flush=True)
+        m.decode(tok, pos, logits)
+        assert rel_l2(host(logits), ref.decode(tok, pos)) <= DENSE_TOL, pos
+
+
 def test_dense_decode_rejects_bad_position():
     import torch
     from trailblaze_amd.dense import DenseConfig
