@@ -382,8 +382,12 @@ static hipError_t launch_attn_d(int G, const float *qkv, const float *qn, const 
 // tmp_x (K floats) and tmp_y (2M floats, MV_GLU only).
 static hipError_t dense_mv(int qt, const void *W, int M, int K, const float *x, float *out, int mode, const MvPro &pro,
                            float *tmp_x, float *tmp_y, hipStream_t st) {
+    // the register-x Q4_K kernel for plain matvecs; with the norm prologue
+    // the K-quant kernel, measured 1.3 us per layer faster at the Qwen3-4B
+    // shapes
     hipError_t e = hipErrorNotSupported;
-    if (qt == QT_Q4_K && K <= 4096 && M <= 8192) e = launch_matvec_q4k_pro(mode, pro, W, M, K, x, out, st);
+    if (qt == QT_Q4_K && K <= 4096 && M <= 8192 && mode == PRO_NONE)
+        e = launch_matvec_q4k_pro(mode, pro, W, M, K, x, out, st);
     if (e == hipErrorNotSupported) e = launch_matvec_kq_pro(mode, pro, qt, W, M, K, x, out, st, tbq_cu_count());
     if (e != hipErrorNotSupported) return e;
     const float *xin = x;
