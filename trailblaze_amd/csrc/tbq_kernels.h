@@ -56,10 +56,14 @@ hipError_t launch_route(const float *xn, const float *router, const float *bias,
                         int top_k, int *sel_idx, float *sel_w, hipStream_t st);
 hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st);
 hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
-                         float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st);
+                         float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st,
+                         _Float16 *x16 = nullptr, float *xinv = nullptr, bool *x16_done = nullptr);
 hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st);
 size_t prefill_workspace_bytes(int T, int k, int E, int H, int F);
-hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t st);
+hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t st, bool x16_done = false);
+// Where the prefill scratch keeps the tokens' fp16 rows and their inverse
+// scales (so the router can write them).
+void prefill_x16(const MoeArgs &a, void *scratch, _Float16 **x16, float **xinv);
 hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st);
 size_t dense_workspace_bytes(const tbq_dense_model *m);
 hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,

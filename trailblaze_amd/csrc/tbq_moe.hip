@@ -288,12 +288,17 @@ hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
 // Prefill: exact routing, then grouped fp16-MFMA experts and the
 // slot-ordered combine.
 hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st) {
+    // the batch router also writes the tokens' fp16 rows for the expert GEMMs
+    _Float16 *x16 = nullptr;
+    float *xinv = nullptr;
+    bool x16_done = false;
+    if (a.qtype == QT_Q4_K) prefill_x16(a, scratch, &x16, &xinv);
     hipError_t err = launch_router(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.logits,
-                                   a.T >= 32 ? nullptr : a.counters, a.sel_idx, a.sel_w, st);
+                                   a.T >= 32 ? nullptr : a.counters, a.sel_idx, a.sel_w, st, x16, xinv, &x16_done);
     if (err == hipErrorNotSupported)
         err = launch_route(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.sel_idx, a.sel_w, st);
     if (err != hipSuccess) return err;
-    err = launch_moe_prefill_q4k(a, scratch, st);
+    err = launch_moe_prefill_q4k(a, scratch, st, x16_done);
     if (err != hipSuccess) return err;
     long long n = (long long)a.T * a.H;
     int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);

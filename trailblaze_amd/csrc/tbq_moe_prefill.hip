@@ -440,7 +440,18 @@ static hipError_t launch_moe_f16(int ns, unsigned nwg, hipStream_t st, const uin
 // Uses a.act (pairs x F fp32), a.y (pairs x H fp32) and `scratch`
 // (prefill_workspace_bytes).  H and F must be 256, 512, 768, 1024, 1536,
 // 2048, 3072 or 4096, H a multiple of PF_ROWS and F of PF_COLS; T <= 65536.
-hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t st) {
+void prefill_x16(const MoeArgs &a, void *scratch, _Float16 **x16, float **xinv) {
+    const size_t P = (size_t)a.T * a.k;
+    const size_t max_tiles = (P + PF_MT - 1) / PF_MT + a.E;
+    auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    char *w = (char *)scratch;
+    w += up(P * 4) + up(max_tiles * sizeof(PfTile)) + 256 + 2 * up(max_tiles * PF_MT * 4) + up(P * a.F * 2);
+    *x16 = (_Float16 *)w;
+    w += up((size_t)a.T * a.H * 2) + up(P * 4);
+    *xinv = (float *)w;
+}
+
+hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t st, bool x16_done) {
     auto ok_k = [](int K) {
         const int n = K / PF_KC;
         return K % 256 == 0 && (n == 2 || n == 4 || n == 6 || n == 8 || n == 12 || n == 16 || n == 24 || n == 32);
@@ -461,7 +472,7 @@ hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t s
     _Float16 *x16 = (_Float16 *)w; w += up((size_t)a.T * a.H * 2);
     float *ainv = (float *)w; w += up(P * 4);
     float *xinv = (float *)w;
-    hipLaunchKernelGGL(k_rows_f16, dim3(a.T), dim3(256), 0, st, a.xn, a.H, x16, xinv);
+    if (!x16_done) hipLaunchKernelGGL(k_rows_f16, dim3(a.T), dim3(256), 0, st, a.xn, a.H, x16, xinv);
     hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, st, a.sel_idx, a.T, a.k, a.E, perm, tiles, ntiles, tpair,
                        ttok);
     hipError_t err = hipGetLastError();

@@ -521,9 +521,53 @@ __device__ __forceinline__ void rb_store(const rb_f4 (&wr)[RB_WPT], const rb_f4 
     sh.xb[b][r0][q] = xr;
 }
 
+// One row of x to fp16 by one wave, scaled by the power of two that puts
+// its max |value| in [2^14, 2^15); xinv = the inverse scale.  The same
+// arithmetic as the prefill's k_rows_f16.  H a multiple of 256, <= 8192.
+__device__ __forceinline__ void rb_row_f16(const float *__restrict__ x, int H, _Float16 *__restrict__ o,
+                                           float *__restrict__ inv) {
+    const int lane = threadIdx.x & 63;
+    const rb_f4 *r = reinterpret_cast<const rb_f4 *>(x);
+    rb_f4 v[32];   // H / 256 float4 per lane
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        if (256 * i < H) {   // uniform
+            v[i] = r[lane + 64 * i];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        }
+    }
+    mx = wave_max(mx);
+    int e = 0;
+    frexpf(mx, &e);
+    int sh = mx > 0.f ? 15 - e : 0;
+    sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
+    const float sc = ldexpf(1.f, sh);
+    uint2 *out = reinterpret_cast<uint2 *>(o);
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        if (256 * i < H) {
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            const h2 a = {(_Float16)(v[i].x * sc), (_Float16)(v[i].y * sc)};
+            const h2 b = {(_Float16)(v[i].z * sc), (_Float16)(v[i].w * sc)};
+            out[lane + 64 * i] = make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+        }
+    }
+    if (lane == 0) *inv = ldexpf(1.f, -sh);
+}
+
+// With x16 set, the grid has one more row of workgroups (blockIdx.y ==
+// gridDim.y - 1) that write the tokens' fp16 rows for the prefill GEMMs
+// (one wave per token) instead of logits.
 __global__ __launch_bounds__(RB_THREADS) void k_router_batch(const float *__restrict__ xn, const float *__restrict__ Wr,
                                                              const float *__restrict__ bias, int T, int H, int E,
-                                                             float *__restrict__ logits) {
+                                                             float *__restrict__ logits, _Float16 *__restrict__ x16,
+                                                             float *__restrict__ xinv) {
+    if (x16 && blockIdx.y == gridDim.y - 1) {   // uniform
+        const int t = blockIdx.x * RB_TOK + (int)(threadIdx.x >> 6);
+        if (t < T) rb_row_f16(xn + (long long)t * H, H, x16 + (long long)t * H, xinv + t);
+        return;
+    }
     extern __shared__ rb_f4 rb_lds[];
     RbShared &sh = *reinterpret_cast<RbShared *>(rb_lds);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -592,7 +636,9 @@ static hipError_t launch_router_dpp(const float *xn, const float *router, const 
 // kernel does both in one launch; otherwise an LDS-tiled logits kernel and
 // a top-k kernel.  hipErrorNotSupported when H does not fit either tiling.
 hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
-                         float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st) {
+                         float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st,
+                         _Float16 *x16, float *xinv, bool *x16_done) {
+    if (x16_done) *x16_done = false;
     if (counters && T < 32) {
         if (H == 2048) return launch_router_dpp<32>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
         if (H == 1024) return launch_router_dpp<16>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
@@ -600,10 +646,13 @@ hipError_t launch_router(const float *xn, const float *router, const float *bias
     }
     const size_t lds = (size_t)H * 4 + 2 * RT_TILE_FLOATS * 4;
     if (T >= 32 && H % RB_KC == 0 && E % 64 == 0) {
-        hipLaunchKernelGGL(k_router_batch, dim3((T + RB_TOK - 1) / RB_TOK, (E + 63) / 64), dim3(RB_THREADS),
-                           sizeof(RbShared), st, xn, router, bias, T, H, E, logits);
+        const bool rows = x16 && xinv && H <= 8192;
+        hipLaunchKernelGGL(k_router_batch, dim3((T + RB_TOK - 1) / RB_TOK, (E + 63) / 64 + (rows ? 1 : 0)),
+                           dim3(RB_THREADS), sizeof(RbShared), st, xn, router, bias, T, H, E, logits,
+                           rows ? x16 : nullptr, xinv);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
+        if (x16_done) *x16_done = rows;
         return launch_topk(logits, T, E, top_k, sel_idx, sel_w, st);
     }
     if (H > 8192) return hipErrorNotSupported;
