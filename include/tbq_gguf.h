@@ -17,6 +17,9 @@
  * tbq_last_error().
  *
  * Calls that return int: 1 = done, 0 = failure (tbq_last_error() says why).
+ * A handle may be read from several threads; the calls that upload or
+ * assemble (tbq_gguf_upload_all, tbq_gguf_dense_model, tbq_gguf_moe_layer)
+ * must not run concurrently on one handle.
  */
 #ifndef TBQ_GGUF_H
 #define TBQ_GGUF_H
