@@ -11,11 +11,23 @@
  * layer4/tb_gguf.c:376-419).  qtype ids are ggml's (layer4/tb_gguf.h:24):
  * 0 F32, 1 F16, 2 Q4_0, 8 Q8_0, 10 Q2_K, 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K,
  * 15 Q8_K, 30 BF16.
+ *
+ * TBQ_GGML | id selects ggml's own on-disk layout of the same format (what
+ * llama.cpp writes; ggml-quants.c dequantize_row_*), which the reference's
+ * decoders do not read (their comment at layer4/tb_gguf.c:63-85 cites ggml,
+ * their code differs): the block fields sit at the same byte offsets, but
+ * ggml assigns quant bits to weights in 32-byte runs, unpacks the 6-bit
+ * K-quant scales differently and decodes fp16 subnormals as IEEE.  Every
+ * call that takes a qtype accepts these ids (for F32, BF16 and Q8_K the two
+ * layouts are one); the prefill MFMA mode of tbq_moe_forward takes only
+ * the reference's Q4_K.
  */
 #ifndef TBQ_H
 #define TBQ_H
 
 #include <stddef.h>
+
+#define TBQ_GGML 0x100
 
 #ifdef __cplusplus
 extern "C" {
@@ -46,8 +58,9 @@ int tbq_qtype_supported(int qtype);
 
 /* ---- dequantise (bit-exact hook) --------------------------------------- */
 /* out[nrows*K] = the reference's dequantised weights, bit for bit
- * (tb_gguf_dequant_row, layer4/tb_gguf.h:90).  K must be a multiple of the
- * block size (and of 8). */
+ * (tb_gguf_dequant_row, layer4/tb_gguf.h:90); for a TBQ_GGML id, ggml's
+ * dequantize_row_* values.  K must be a multiple of the block size (and of
+ * 8). */
 int tbq_dequant(const void *W, int qtype, int nrows, int K, float *out, void *stream);
 
 /* ---- decode matvec ----------------------------------------------------- */

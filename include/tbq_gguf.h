@@ -65,6 +65,15 @@ int tbq_gguf_upload_all(tbq_gguf *g);
 /* Device copy of tensor i (NULL before upload or for an unknown qtype). */
 const void *tbq_gguf_tensor_device(const tbq_gguf *g, int i);
 
+/* Block layout the assembled models and layers below read the file's
+ * quantised tensors in: 0 (the default) = the reference's layouts, as its
+ * decoders read every file (layer4/tb_gguf.c:110-288); TBQ_GGML = ggml's,
+ * as llama.cpp writes them.  The qtype fields of tbq_gguf_dense_model and
+ * tbq_gguf_moe_layer then carry TBQ_GGML.  Tensor bytes are uploaded
+ * unchanged either way; tbq_gguf_tensor_info keeps reporting the file's
+ * ids.  No counterpart in the reference, which has no layout choice. */
+int tbq_gguf_set_layout(tbq_gguf *g, int layout);
+
 /* A dense (llama / qwen3-style) model from the file: architecture from
  * general.architecture, sizes from its metadata (block_count,
  * embedding_length, attention.head_count[_kv], attention.key_length,

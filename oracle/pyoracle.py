@@ -51,6 +51,8 @@ class Oracle:
         L.tbo_f16_to_f32.argtypes = [C.c_uint16]
         L.tbo_bf16_to_f32.restype = C.c_float
         L.tbo_bf16_to_f32.argtypes = [C.c_uint16]
+        L.tbo_f16_ieee.restype = C.c_float
+        L.tbo_f16_ieee.argtypes = [C.c_uint16]
         L.tbo_row_bytes.restype = C.c_size_t
         L.tbo_row_bytes.argtypes = [C.c_int, C.c_int]
         L.tbo_dequant_row.argtypes = [_u8p, C.c_int, C.c_int, _f32p]
@@ -71,6 +73,10 @@ class Oracle:
 
     def f16(self, h: int) -> float:
         return self.lib.tbo_f16_to_f32(h)
+
+    def f16_ieee(self, h: int) -> float:
+        """ggml's fp16 decode (IEEE binary16, subnormals included)."""
+        return self.lib.tbo_f16_ieee(h)
 
     def row_bytes(self, qtype: int, K: int) -> int:
         return int(self.lib.tbo_row_bytes(qtype, K))

@@ -64,6 +64,10 @@ float tbo_bf16_to_f32(uint16_t b) {
 /* Block geometry as tabulated in layer4/tb_gguf.c:380-394. */
 int tbo_block_geometry(int qtype, int *bw, int *bb) {
     int w, b;
+    if (qtype & 0x100) {   /* ggml's layout of a format: the same geometry */
+        if (qtype == (0x100 | 21)) return 0;
+        qtype &= 0xFF;
+    }
     switch (qtype) {
     case 0: w = 1; b = 4; break;
     case 1: w = 1; b = 2; break;
@@ -229,6 +233,10 @@ static void blk_q8_k(const uint8_t *b, float *out) {
  * n_weights outputs exist; callers pass multiples of the block size.
  * Unknown qtype (including 21, which only the matvec table knows) zeroes. */
 void tbo_dequant_row(const void *data, int qtype, int n, float *out) {
+    if (qtype & 0x100) {   /* ggml's layouts: ggml_layout.c */
+        tbo_ggml_dequant_row(data, qtype, n, out);
+        return;
+    }
     const uint8_t *p = (const uint8_t *)data;
     int done = 0;
     void (*blk)(const uint8_t *, float *) = 0;

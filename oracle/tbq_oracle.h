@@ -28,6 +28,11 @@
  *                          Q8_K activation quantiser): parity unpinned;
  *                          closed-form round-trip bound only
  *   tbo_dot_q4k_avx512s    timing baseline only (never a parity target)
+ *   tbo_f16_ieee,          ggml's layouts (qtype | 0x100, ggml_layout.c):
+ *   tbo_ggml_dequant_row   f16 against numpy on all 65536 inputs; decoders
+ *                          against an independent block packer and closed
+ *                          forms.  ggml is absent here: parity unpinned
+ *                          against ggml's own output.
  */
 #ifndef TBQ_ORACLE_H
 #define TBQ_ORACLE_H
@@ -47,7 +52,13 @@ float tbo_bf16_to_f32(uint16_t b);
 int tbo_block_geometry(int qtype, int *block_weights, int *block_bytes);
 size_t tbo_row_bytes(int qtype, int K);
 
+/* qtype | 0x100 selects ggml's layout of the format (ggml_layout.c). */
 void tbo_dequant_row(const void *data, int qtype, int n_weights, float *out);
+/* ggml's dequantize_row_* for qtype | 0x100 (or the plain id); 0 = unknown
+ * format (out zeroed). */
+int tbo_ggml_dequant_row(const void *data, int qtype, int n_weights, float *out);
+/* IEEE binary16 -> binary32 (ggml's GGML_FP16_TO_FP32). */
+float tbo_f16_ieee(uint16_t h);
 void tbo_dequant_matvec(const void *W, int qtype, int M, int K,
                         const float *x, float *out);
 /* Dequantise M rows of K weights into out[M*K] (row stride tbo_row_bytes). */

@@ -76,10 +76,11 @@ def dense_gguf_tensors(cfg, host, arch="qwen3"):
           (f"{arch}.rope.freq_base", "f32", c.rope_theta),
           ("tokenizer.ggml.tokens", "arr", ("str", [f"t{i}" for i in range(8)]))]
     f32 = lambda a: np.asarray(a, np.float32)
-    ts = [("token_embd.weight", c.qtype_embd, (c.hidden, c.vocab), host["lm_head"]),
+    c_embd = c.qtype_embd & 0xFF   # a file holds plain ggml ids, whatever layout reads it
+    ts = [("token_embd.weight", c_embd, (c.hidden, c.vocab), host["lm_head"]),
           ("output_norm.weight", fm.F32, (c.hidden,), f32(host["output_norm"]))]
     for l, t in enumerate(host["layers"]):
-        qt = lambda name: t.get("qt_" + name, c.qtype_layers)
+        qt = lambda name: t.get("qt_" + name, c.qtype_layers) & 0xFF
         if "wqkv" in t:
             qkv = t["wqkv"]
             q, k, v = qkv[:NQ * D], qkv[NQ * D:(NQ + NKV) * D], qkv[(NQ + NKV) * D:]

@@ -66,6 +66,7 @@ SYMBOLS = {
     "tbq_gguf_tensor_device": (_vp, [_vp, _i]),
     "tbq_gguf_dense_model": (_i, [_vp, _i, _vp, _vp, _i]),
     "tbq_gguf_moe_layer": (_i, [_vp, _i, _vp]),
+    "tbq_gguf_set_layout": (_i, [_vp, _i]),
     # include/tb_gguf_dequant.h (the reference ABI)
     "tb_cuda_init": (_i, []),
     "tb_cuda_upload_tensor": (_vp, [_vp, _sz]),

@@ -44,10 +44,14 @@ int hip_ok(hipError_t e, const char *what) {
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Plain ids are the reference's layouts; QT_GGML | id is ggml's layout of
+// the same format (TBQ_GGML in tbq.h).
 bool known_qtype(int qt) {
-    switch (qt) {
+    switch (canon_qt(qt)) {
     case QT_F32: case QT_F16: case QT_BF16: case QT_Q4_0: case QT_Q8_0: case QT_Q2_K:
     case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_Q8_K:
+    case QT_GF16: case QT_GQ4_0: case QT_GQ8_0: case QT_GQ2_K: case QT_GQ3_K:
+    case QT_GQ4_K: case QT_GQ5_K: case QT_GQ6_K:
         return true;
     default:
         return false;
@@ -109,6 +113,7 @@ int tbq_qtype_supported(int qt) { return known_qtype(qt) ? 1 : 0; }
 
 int tbq_dequant(const void *W, int qt, int nrows, int K, float *out, void *s) {
     if (!ensure_init()) return 0;
+    qt = canon_qt(qt);
     if (!known_qtype(qt)) return fail("tbq_dequant: unsupported qtype %d", qt);
     if (nrows < 0 || K <= 0 || K % block_weights(qt) || K % 8) return fail("tbq_dequant: K=%d not a multiple of the block size", K);
     if (!W || !out || !aligned16(out)) return fail("tbq_dequant: null or misaligned pointer");
@@ -123,7 +128,7 @@ static int check_matvec(const void *W, int qt, int M, int K, const float *x, con
     if (K > 16384) return fail("K=%d exceeds the LDS-resident x limit (16384)", K);
     if (!W || !x || !y) return fail("null pointer");
     if (!aligned16(x)) return fail("x must be 16-byte aligned");
-    if ((qt == QT_Q4_K || qt == QT_Q5_K || qt == QT_F32) && !aligned16(W))
+    if (((qt & 0xFF) == QT_Q4_K || (qt & 0xFF) == QT_Q5_K || qt == QT_F32) && !aligned16(W))
         return fail("W must be 16-byte aligned for qtype %d", qt);
     if (((uintptr_t)W & 1u)) return fail("W must be 2-byte aligned");
     return 1;
@@ -131,6 +136,7 @@ static int check_matvec(const void *W, int qt, int M, int K, const float *x, con
 
 int tbq_matvec_variant(const void *W, int qt, int M, int K, const float *x, float *y, int variant, void *s) {
     if (!ensure_init()) return 0;
+    qt = canon_qt(qt);
     if (!check_matvec(W, qt, M, K, x, y)) return 0;
     if (variant < TBQ_MV_AUTO || variant > TBQ_MV_KQ) return fail("tbq_matvec_variant: unknown variant %d", variant);
     if (M == 0) return 1;
@@ -211,7 +217,8 @@ static int check_moe(const tbq_moe_layer *L, int T) {
     if (T < 0 || T > MAX_TOKENS || L->E <= 0 || L->E > 256 || L->top_k <= 0) return fail("tbq_moe_forward: bad T/E/top_k");
     if (L->H <= 0 || L->F <= 0 || L->H % 256 || L->F % 256) return fail("tbq_moe_forward: H and F must be multiples of 256");
     switch (L->qtype) {
-    case QT_Q2_K: case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_Q8_0: break;
+    case QT_Q2_K: case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_Q8_0:
+    case QT_GQ2_K: case QT_GQ3_K: case QT_GQ4_K: case QT_GQ5_K: case QT_GQ6_K: case QT_GQ8_0: break;
     default: return fail("tbq_moe_forward: expert qtype %d not supported", L->qtype);
     }
     if (!L->router || !L->gate || !L->up || !L->down) return fail("tbq_moe_forward: null weight");
@@ -227,7 +234,8 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     if (!check_moe(L, T)) return 0;
     if (mode != TBQ_MOE_FP32 && mode != TBQ_MOE_BF16) return fail("tbq_moe_forward: unknown mode %d", mode);
     if (mode == TBQ_MOE_BF16 && (L->qtype != QT_Q4_K || L->F % 128 || L->H % 128))
-        return fail("tbq_moe_forward: the prefill MFMA path takes Q4_K experts with H, F multiples of 256");
+        return fail("tbq_moe_forward: the prefill MFMA path takes Q4_K experts (reference layout) with H, F "
+                    "multiples of 256");
     if (!xn || !resid || !out || !aligned16(xn) || !aligned16(resid) || !aligned16(out))
         return fail("tbq_moe_forward: null or misaligned activation pointer");
     if (T == 0) return 1;

@@ -409,11 +409,11 @@ hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, flo
                                hipStream_t st) {
     const int H = m->hidden, D = m->head_dim, NQ = m->n_heads, NKV = m->n_kv_heads, G = NQ / NKV, F = m->ffn;
     const int QKVR = (NQ + 2 * NKV) * D;
-    auto qt_of = [m](int q) { return q ? q : m->qtype_layers; };
+    auto qt_of = [m](int q) { return canon_qt(q ? q : m->qtype_layers); };
     const DenseWs w = dense_ws(m, ws, nullptr);
     const size_t erb = tbq_row_bytes(m->qtype_embd, H);
     float *xa = w.x, *xb = w.x2;
-    hipError_t err = launch_dequant(m->qtype_embd, (const uint8_t *)m->tok_embd + (size_t)token * erb, H, xa, st);
+    hipError_t err = launch_dequant(canon_qt(m->qtype_embd), (const uint8_t *)m->tok_embd + (size_t)token * erb, H, xa, st);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(64), 0, st, pos, m->rope_theta, D, w.rope);
     const float *yprev = nullptr;
@@ -463,7 +463,7 @@ hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, flo
         yprev = w.y;
     }
     const MvPro po{yprev, m->output_norm, nullptr, m->norm_eps};
-    if ((err = dense_mv(m->qtype_embd, m->lm_head, m->vocab, H, xa, logits, PRO_NORM, po, w.h, nullptr, st)) !=
+    if ((err = dense_mv(canon_qt(m->qtype_embd), m->lm_head, m->vocab, H, xa, logits, PRO_NORM, po, w.h, nullptr, st)) !=
         hipSuccess)
         return err;
     return hipGetLastError();

@@ -15,18 +15,35 @@ namespace tbq {
 // ggml type ids used by the reference (layer4/tb_gguf.h:24).
 enum QType : int {
     QT_F32 = 0, QT_F16 = 1, QT_Q4_0 = 2, QT_Q8_0 = 8, QT_Q2_K = 10, QT_Q3_K = 11,
-    QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_Q8_K = 15, QT_BF16 = 30
+    QT_Q4_K = 12, QT_Q5_K = 13, QT_Q6_K = 14, QT_Q8_K = 15, QT_BF16 = 30,
+    // ggml's own on-disk layouts (QT_GGML | ggml id): the block fields sit at
+    // the same byte offsets as in the reference's layouts, but quants, scales
+    // and fp16 fields are read as ggml reads them.  F32, BF16 and Q8_K read
+    // the same in both and are canonicalised to their plain ids by the host.
+    QT_GGML = 0x100,
+    QT_GF16 = QT_GGML | QT_F16, QT_GQ4_0 = QT_GGML | QT_Q4_0, QT_GQ8_0 = QT_GGML | QT_Q8_0,
+    QT_GQ2_K = QT_GGML | QT_Q2_K, QT_GQ3_K = QT_GGML | QT_Q3_K, QT_GQ4_K = QT_GGML | QT_Q4_K,
+    QT_GQ5_K = QT_GGML | QT_Q5_K, QT_GQ6_K = QT_GGML | QT_Q6_K
 };
 
-// weights / bytes per block, layer4/tb_gguf.c:380-394.
+// weights / bytes per block, layer4/tb_gguf.c:380-394 (the same for both
+// layouts of a format).
 __host__ __device__ constexpr int block_weights(int qt) {
-    return (qt == QT_F32 || qt == QT_F16 || qt == QT_BF16) ? 1
-         : (qt == QT_Q4_0 || qt == QT_Q8_0) ? 32 : 256;
+    return ((qt & 0xFF) == QT_F32 || (qt & 0xFF) == QT_F16 || (qt & 0xFF) == QT_BF16) ? 1
+         : ((qt & 0xFF) == QT_Q4_0 || (qt & 0xFF) == QT_Q8_0) ? 32 : 256;
 }
 __host__ __device__ constexpr int block_bytes(int qt) {
-    return qt == QT_F32 ? 4 : (qt == QT_F16 || qt == QT_BF16) ? 2 : qt == QT_Q4_0 ? 18
-         : qt == QT_Q8_0 ? 34 : qt == QT_Q2_K ? 84 : qt == QT_Q3_K ? 110 : qt == QT_Q4_K ? 144
-         : qt == QT_Q5_K ? 176 : qt == QT_Q6_K ? 210 : qt == QT_Q8_K ? 292 : 0;
+    return (qt & 0xFF) == QT_F32 ? 4 : ((qt & 0xFF) == QT_F16 || (qt & 0xFF) == QT_BF16) ? 2
+         : (qt & 0xFF) == QT_Q4_0 ? 18 : (qt & 0xFF) == QT_Q8_0 ? 34 : (qt & 0xFF) == QT_Q2_K ? 84
+         : (qt & 0xFF) == QT_Q3_K ? 110 : (qt & 0xFF) == QT_Q4_K ? 144 : (qt & 0xFF) == QT_Q5_K ? 176
+         : (qt & 0xFF) == QT_Q6_K ? 210 : (qt & 0xFF) == QT_Q8_K ? 292 : 0;
+}
+
+// A ggml-layout id of a format whose reading is the same in both layouts
+// (F32, BF16, Q8_K) becomes the plain id; every other id is returned as is.
+__host__ __device__ constexpr int canon_qt(int qt) {
+    return ((qt & QT_GGML) && ((qt & 0xFF) == QT_F32 || (qt & 0xFF) == QT_BF16 || (qt & 0xFF) == QT_Q8_K))
+               ? (qt & 0xFF) : qt;
 }
 
 // fp16 -> fp32 exactly as layer4/tb_gguf.c:92-101 decodes it.  A zero
@@ -42,6 +59,25 @@ __host__ __device__ __forceinline__ float f16_ref(uint32_t h) {
                   : e == 31 ? (s | 0x7F800000u | (m << 13))
                   : (s | ((e + 112u) << 23) | (m << 13));
     return __builtin_bit_cast(float, bits);
+}
+
+// fp16 -> fp32 as IEEE 754 defines it (ggml's layouts): subnormal halves
+// are m*2^-24 (exact in fp32: m < 2^10), the rest as f16_ref.  Integer and
+// exact fp32 work only, independent of the FP16 denormal mode.
+__host__ __device__ __forceinline__ float f16_ieee(uint32_t h) {
+    const uint32_t e = (h >> 10) & 0x1Fu;
+    if (e == 0) {
+        const float v = (float)(h & 0x3FFu) * 0x1p-24f;
+        return (h & 0x8000u) ? -v : v;
+    }
+    return f16_ref(h);
+}
+
+// The fp16 decoder of a format: IEEE for the ggml layouts.
+template <int QT>
+__host__ __device__ __forceinline__ float f16_of(uint32_t h) {
+    if constexpr ((QT & QT_GGML) != 0) return f16_ieee(h);
+    else return f16_ref(h);
 }
 
 __host__ __device__ __forceinline__ float bf16_ref(uint32_t b) {

@@ -1,5 +1,6 @@
 // tbq_kquant.hpp -- per-format block decoders for the reference's K-quant
-// layouts (layer4/tb_gguf.c:110-288), in two flavours:
+// layouts (layer4/tb_gguf.c:110-288) and ggml's (QT_GGML ids, below), in two
+// flavours:
 //
 //   decode8<QT>(blk, o, out)   eight consecutive weights o..o+7 of one block,
 //                              rounded exactly as the reference rounds them
@@ -164,6 +165,127 @@ __device__ __forceinline__ void decode8<QT_Q8_K>(const uint8_t *b, int o, float 
     float d = __builtin_bit_cast(float, ldu32(b));
 #pragma unroll
     for (int i = 0; i < 8; i++) w[i] = d * (float)(int8_t)ldb(b + 4 + o + i);
+}
+
+// ===========================================================================
+// ggml's on-disk layouts (QT_GGML | id; ggml-quants.c, dequantize_row_*).
+// The fields sit at the reference's byte offsets; what differs is which
+// quant bits, scale and fp16 decoding belong to weight e of a block:
+//   Q4_K/Q5_K  chunk c = e/64, l = e%32: nibble (e/32)&1 of qs[32c+l]; Q5_K
+//              adds bit e/32 of qh[l] as 16.  Sub-block e/32 takes its
+//              6-bit scale and min from get_scale_min_k4 (gq4k_scale_min).
+//   Q6_K       half n = e/128, r = e%128, k = r/32, l = r%32: nibble k>>1 of
+//              ql[64n + 32(k&1) + l], bits 2k of qh[32n + l]; int8 sc[e/16];
+//              q - 32.
+//   Q3_K       n, k, l as Q6_K: bits 2k of qs[32n+l]; bit 4n+k of hmask[l]
+//              (clear: q - 4); scale e/16 of the ggml 6-bit unpack, - 32.
+//   Q2_K       quants as Q3_K's 2-bit part; scale/min byte sc[e/16].
+//   Q4_0       weight l < 16: low nibble of qs[l]; 16 + l: high nibble.
+// fp16 fields decode as IEEE (f16_ieee).  Roundings: w = fl(fl(d*s)*q) -
+// fl(dmin*m) (K formats with mins), fl(fl(d*s)*q) otherwise, fl(q*d) for
+// Q4_0/Q8_0, one rounding per operation.
+// ===========================================================================
+__device__ __forceinline__ void gq4k_scale_min(const uint8_t *b, int j, int &s, int &m) {
+    const uint8_t *q = b + 4;
+    if (j < 4) {
+        s = ldb(q + j) & 63;
+        m = ldb(q + j + 4) & 63;
+    } else {
+        s = (ldb(q + j + 4) & 15) | ((ldb(q + j - 4) >> 6) << 4);
+        m = (ldb(q + j + 4) >> 4) | ((ldb(q + j) >> 6) << 4);
+    }
+}
+__device__ __forceinline__ int gq3k_scale(const uint8_t *b, int i) {
+    const uint8_t *sc = b + 96;
+    const int lo4 = (ldb(sc + (i & 7)) >> (4 * (i >> 3))) & 15;
+    const int hi2 = (ldb(sc + 8 + (i & 3)) >> (2 * (i >> 2))) & 3;
+    return (lo4 | (hi2 << 4)) - 32;
+}
+
+template <>
+__device__ __forceinline__ void decode8<QT_GQ4_K>(const uint8_t *b, int o, float *w) {
+    const float d = f16_ieee(ldu16(b)), dmin = f16_ieee(ldu16(b + 2));
+    int si, mi;
+    gq4k_scale_min(b, o >> 5, si, mi);
+    const float S = d * (float)si, Mn = dmin * (float)mi;
+    const uint8_t *q = b + 16 + 32 * (o >> 6) + (o & 31);
+    const int sh = 4 * ((o >> 5) & 1);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float t = S * (float)((ldb(q + i) >> sh) & 15);
+        w[i] = t - Mn;
+    }
+}
+template <>
+__device__ __forceinline__ void decode8<QT_GQ5_K>(const uint8_t *b, int o, float *w) {
+    const float d = f16_ieee(ldu16(b)), dmin = f16_ieee(ldu16(b + 2));
+    const int j = o >> 5;
+    int si, mi;
+    gq4k_scale_min(b, j, si, mi);
+    const float S = d * (float)si, Mn = dmin * (float)mi;
+    const uint8_t *q = b + 48 + 32 * (o >> 6) + (o & 31);
+    const uint8_t *h = b + 16 + (o & 31);
+    const int sh = 4 * (j & 1);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int v = ((ldb(q + i) >> sh) & 15) | (((ldb(h + i) >> j) & 1) << 4);
+        const float t = S * (float)v;
+        w[i] = t - Mn;
+    }
+}
+template <>
+__device__ __forceinline__ void decode8<QT_GQ6_K>(const uint8_t *b, int o, float *w) {
+    const float d = f16_ieee(ldu16(b + 208));
+    const float ds = d * (float)(int8_t)ldb(b + 192 + (o >> 4));
+    const int n = o >> 7, k = (o >> 5) & 3, l0 = o & 31;
+    const uint8_t *ql = b + 64 * n + 32 * (k & 1) + l0;
+    const uint8_t *qh = b + 128 + 32 * n + l0;
+    const int shl = 4 * (k >> 1), shh = 2 * k;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int v = ((ldb(ql + i) >> shl) & 15) | (((ldb(qh + i) >> shh) & 3) << 4);
+        w[i] = ds * (float)(v - 32);
+    }
+}
+template <>
+__device__ __forceinline__ void decode8<QT_GQ3_K>(const uint8_t *b, int o, float *w) {
+    const float d = f16_ieee(ldu16(b + 108));
+    const float S = d * (float)gq3k_scale(b, o >> 4);
+    const int n = o >> 7, k = (o >> 5) & 3, l0 = o & 31;
+    const uint8_t *q = b + 32 + 32 * n + l0;
+    const uint8_t *hm = b + l0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int v = (int)((ldb(q + i) >> (2 * k)) & 3) - (((ldb(hm + i) >> (4 * n + k)) & 1) ? 0 : 4);
+        w[i] = S * (float)v;
+    }
+}
+template <>
+__device__ __forceinline__ void decode8<QT_GQ2_K>(const uint8_t *b, int o, float *w) {
+    const float d = f16_ieee(ldu16(b + 80)), dmin = f16_ieee(ldu16(b + 82));
+    const uint32_t sm = ldb(b + (o >> 4));
+    const float S = d * (float)(sm & 15), Mn = dmin * (float)(sm >> 4);
+    const int n = o >> 7, k = (o >> 5) & 3, l0 = o & 31;
+    const uint8_t *q = b + 16 + 32 * n + l0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float t = S * (float)((ldb(q + i) >> (2 * k)) & 3);
+        w[i] = t - Mn;
+    }
+}
+template <>
+__device__ __forceinline__ void decode8<QT_GQ8_0>(const uint8_t *b, int o, float *w) {
+    const float d = f16_ieee(ldu16(b));
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i] = d * (float)(int8_t)ldb(b + 2 + o + i);
+}
+template <>
+__device__ __forceinline__ void decode8<QT_GQ4_0>(const uint8_t *b, int o, float *w) {
+    const float d = f16_ieee(ldu16(b));
+    const uint8_t *q = b + 2 + (o & 15);
+    const int sh = 4 * (o >> 4);
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i] = (float)((int)((ldb(q + i) >> sh) & 15) - 8) * d;
 }
 
 // ===========================================================================
@@ -370,6 +492,145 @@ __device__ __forceinline__ float chunk_dot<QT_BF16>(const uint8_t *row, int c, c
         uint32_t v = ldu32(w + 2 * i);
         a = fmaf(bf16_ref(v & 0xFFFF), xl[i], a);
         a = fmaf(bf16_ref(v >> 16), xl[i + 1], a);
+    }
+    return a;
+}
+
+// ---- ggml layouts (the chunk is sub-block c%8 / block c, weights in order).
+// Sum over 32 consecutive bytes q[0..31] of ((q[i] >> sh) & mask) * x[i].
+__device__ __forceinline__ float bits_run_dot32(const uint8_t *q, int sh, uint32_t mask, const float *xl) {
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t v = ldu32(q + 4 * k) >> sh;
+        a0 = fmaf((float)(v & mask), xl[4 * k], a0);
+        a1 = fmaf((float)((v >> 8) & mask), xl[4 * k + 1], a1);
+        a0 = fmaf((float)((v >> 16) & mask), xl[4 * k + 2], a0);
+        a1 = fmaf((float)((v >> 24) & mask), xl[4 * k + 3], a1);
+    }
+    return a0 + a1;
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot<QT_GQ4_K>(const uint8_t *row, int c, const float *xl, const float *xs16) {
+    const uint8_t *b = row + (size_t)(c >> 3) * 144;
+    const int j = c & 7;
+    int si, mi;
+    gq4k_scale_min(b, j, si, mi);
+    const float d = f16_ieee(ldu16(b)), dmin = f16_ieee(ldu16(b + 2));
+    const float sq = bits_run_dot32(b + 16 + 32 * (j >> 1), 4 * (j & 1), 15u, xl);
+    return fmaf(d * (float)si, sq, -(dmin * (float)mi) * (xs16[0] + xs16[1]));
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot<QT_GQ5_K>(const uint8_t *row, int c, const float *xl, const float *xs16) {
+    const uint8_t *b = row + (size_t)(c >> 3) * 176;
+    const int j = c & 7;
+    int si, mi;
+    gq4k_scale_min(b, j, si, mi);
+    const float d = f16_ieee(ldu16(b)), dmin = f16_ieee(ldu16(b + 2));
+    float sq = bits_run_dot32(b + 48 + 32 * (j >> 1), 4 * (j & 1), 15u, xl);
+    sq = fmaf(16.f, bits_run_dot32(b + 16, j, 1u, xl), sq);
+    return fmaf(d * (float)si, sq, -(dmin * (float)mi) * (xs16[0] + xs16[1]));
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot<QT_GQ6_K>(const uint8_t *row, int c, const float *xl, const float *xs16) {
+    const uint8_t *b = row + (size_t)(c >> 3) * 210;
+    const int j = c & 7, n = j >> 2, k = j & 3;
+    const float d = f16_ieee(ldu16(b + 208));
+    const float s0 = d * (float)(int8_t)ldb(b + 192 + 2 * j), s1 = d * (float)(int8_t)ldb(b + 193 + 2 * j);
+    const uint8_t *ql = b + 64 * n + 32 * (k & 1), *qh = b + 128 + 32 * n;
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const int v = ((ldb(ql + i) >> (4 * (k >> 1))) & 15) | (((ldb(qh + i) >> (2 * k)) & 3) << 4);
+        acc[i >> 4] = fmaf((float)v, xl[i], acc[i >> 4]);
+    }
+    const float g0 = fmaf(-32.f, xs16[0], acc[0]);
+    const float g1 = fmaf(-32.f, xs16[1], acc[1]);
+    return fmaf(s0, g0, s1 * g1);
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot<QT_GQ3_K>(const uint8_t *row, int c, const float *xl, const float *xs16) {
+    const uint8_t *b = row + (size_t)(c >> 3) * 110;
+    const int j = c & 7, n = j >> 2, k = j & 3;
+    const float d = f16_ieee(ldu16(b + 108));
+    const float s0 = d * (float)gq3k_scale(b, 2 * j), s1 = d * (float)gq3k_scale(b, 2 * j + 1);
+    const uint8_t *q = b + 32 + 32 * n;
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const int v = ((ldb(q + i) >> (2 * k)) & 3) | (((ldb(b + i) >> (4 * n + k)) & 1) << 2);
+        acc[i >> 4] = fmaf((float)v, xl[i], acc[i >> 4]);
+    }
+    const float g0 = fmaf(-4.f, xs16[0], acc[0]);
+    const float g1 = fmaf(-4.f, xs16[1], acc[1]);
+    return fmaf(s0, g0, s1 * g1);
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot<QT_GQ2_K>(const uint8_t *row, int c, const float *xl, const float *xs16) {
+    const uint8_t *b = row + (size_t)(c >> 3) * 84;
+    const int j = c & 7, n = j >> 2, k = j & 3;
+    const float d = f16_ieee(ldu16(b + 80)), dmin = f16_ieee(ldu16(b + 82));
+    const uint32_t sm = ldu16(b + 2 * j);
+    const uint8_t *q = b + 16 + 32 * n;
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 32; i++) acc[i >> 4] = fmaf((float)((ldb(q + i) >> (2 * k)) & 3), xl[i], acc[i >> 4]);
+    float r = 0.f;
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+        const uint32_t v = (sm >> (8 * g)) & 0xFF;
+        const float S = d * (float)(v & 15), Mn = dmin * (float)(v >> 4);
+        r = fmaf(S, acc[g], r);
+        r = fmaf(-Mn, xs16[g], r);
+    }
+    return r;
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot<QT_GQ8_0>(const uint8_t *row, int c, const float *xl, const float *) {
+    const uint8_t *b = row + (size_t)c * 34;
+    const float d = f16_ieee(ldu16(b));
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t v = ldu32(b + 2 + 4 * k);
+#pragma unroll
+        for (int t = 0; t < 4; t++) a = fmaf((float)(int8_t)(v >> (8 * t)), xl[4 * k + t], a);
+    }
+    return d * a;
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot<QT_GQ4_0>(const uint8_t *row, int c, const float *xl, const float *xs16) {
+    const uint8_t *b = row + (size_t)c * 18;
+    const float d = f16_ieee(ldu16(b));
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t v = ldu32(b + 2 + 4 * k);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            a0 = fmaf((float)((v >> (8 * t)) & 15), xl[4 * k + t], a0);
+            a1 = fmaf((float)((v >> (8 * t + 4)) & 15), xl[16 + 4 * k + t], a1);
+        }
+    }
+    return d * fmaf(-8.f, xs16[0] + xs16[1], a0 + a1);
+}
+
+template <>
+__device__ __forceinline__ float chunk_dot<QT_GF16>(const uint8_t *row, int c, const float *xl, const float *) {
+    const uint8_t *w = row + 64 * c;
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+        const uint32_t v = ldu32(w + 2 * i);
+        a = fmaf(f16_ieee(v & 0xFFFF), xl[i], a);
+        a = fmaf(f16_ieee(v >> 16), xl[i + 1], a);
     }
     return a;
 }

@@ -1,6 +1,7 @@
 // tbq_matvec.hip -- gfx950 kernels for the bit-exact dequant hook and the
 // decode dequant-matvec y = W x (fp32 x, fp32 accumulate) for every block
-// format of the reference's dequant table (layer4/tb_gguf.c:293-419).
+// format of the reference's dequant table (layer4/tb_gguf.c:293-419), in the
+// reference's layouts and in ggml's.
 #include "tbq_kquant.hpp"
 #include "tbq_kernels.h"
 
@@ -22,7 +23,8 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ W, 
             for (int i = 0; i < 8; i++) {
                 const uint8_t *p = W + (e + i) * BB;
                 w[i] = QT == QT_F32 ? __builtin_bit_cast(float, ldu32(p))
-                     : QT == QT_F16 ? f16_ref(ldu16(p)) : bf16_ref(ldu16(p));
+                     : QT == QT_F16 ? f16_ref(ldu16(p)) : QT == QT_GF16 ? f16_ieee(ldu16(p))
+                     : bf16_ref(ldu16(p));
             }
         } else {
             long long blk = e / BW;
@@ -119,6 +121,14 @@ hipError_t launch_dequant(int qt, const void *W, long long nweights, float *out,
     case QT_Q5_K: return launch_dequant_t<QT_Q5_K>(W, nweights, out, s);
     case QT_Q6_K: return launch_dequant_t<QT_Q6_K>(W, nweights, out, s);
     case QT_Q8_K: return launch_dequant_t<QT_Q8_K>(W, nweights, out, s);
+    case QT_GF16: return launch_dequant_t<QT_GF16>(W, nweights, out, s);
+    case QT_GQ4_0: return launch_dequant_t<QT_GQ4_0>(W, nweights, out, s);
+    case QT_GQ8_0: return launch_dequant_t<QT_GQ8_0>(W, nweights, out, s);
+    case QT_GQ2_K: return launch_dequant_t<QT_GQ2_K>(W, nweights, out, s);
+    case QT_GQ3_K: return launch_dequant_t<QT_GQ3_K>(W, nweights, out, s);
+    case QT_GQ4_K: return launch_dequant_t<QT_GQ4_K>(W, nweights, out, s);
+    case QT_GQ5_K: return launch_dequant_t<QT_GQ5_K>(W, nweights, out, s);
+    case QT_GQ6_K: return launch_dequant_t<QT_GQ6_K>(W, nweights, out, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -137,6 +147,14 @@ hipError_t launch_matvec_generic(int qt, const void *W, int M, int K, const floa
     case QT_Q5_K: return launch_mv_q<QT_Q5_K>(W, M, K, x, y, s, n_cu);
     case QT_Q6_K: return launch_mv_q<QT_Q6_K>(W, M, K, x, y, s, n_cu);
     case QT_Q8_K: return launch_mv_q<QT_Q8_K>(W, M, K, x, y, s, n_cu);
+    case QT_GF16: return launch_mv_q<QT_GF16>(W, M, K, x, y, s, n_cu);
+    case QT_GQ4_0: return launch_mv_q<QT_GQ4_0>(W, M, K, x, y, s, n_cu);
+    case QT_GQ8_0: return launch_mv_q<QT_GQ8_0>(W, M, K, x, y, s, n_cu);
+    case QT_GQ2_K: return launch_mv_q<QT_GQ2_K>(W, M, K, x, y, s, n_cu);
+    case QT_GQ3_K: return launch_mv_q<QT_GQ3_K>(W, M, K, x, y, s, n_cu);
+    case QT_GQ4_K: return launch_mv_q<QT_GQ4_K>(W, M, K, x, y, s, n_cu);
+    case QT_GQ5_K: return launch_mv_q<QT_GQ5_K>(W, M, K, x, y, s, n_cu);
+    case QT_GQ6_K: return launch_mv_q<QT_GQ6_K>(W, M, K, x, y, s, n_cu);
     default: return hipErrorInvalidValue;
     }
 }

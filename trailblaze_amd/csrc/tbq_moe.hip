@@ -276,6 +276,12 @@ hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
     case QT_Q5_K: err = launch_moe_q<QT_Q5_K>(a, st); break;
     case QT_Q6_K: err = launch_moe_q<QT_Q6_K>(a, st); break;
     case QT_Q8_0: err = launch_moe_q<QT_Q8_0>(a, st); break;
+    case QT_GQ2_K: err = launch_moe_q<QT_GQ2_K>(a, st); break;
+    case QT_GQ3_K: err = launch_moe_q<QT_GQ3_K>(a, st); break;
+    case QT_GQ4_K: err = launch_moe_q<QT_GQ4_K>(a, st); break;
+    case QT_GQ5_K: err = launch_moe_q<QT_GQ5_K>(a, st); break;
+    case QT_GQ6_K: err = launch_moe_q<QT_GQ6_K>(a, st); break;
+    case QT_GQ8_0: err = launch_moe_q<QT_GQ8_0>(a, st); break;
     default: return hipErrorInvalidValue;
     }
     if (err != hipSuccess) return err;

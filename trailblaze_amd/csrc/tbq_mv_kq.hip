@@ -1,7 +1,7 @@
 // tbq_mv_kq.hip -- decode matvec y = W x on integer dot products for the
 // block formats Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 and Q8_K
 // (tb_gguf_dequant_matvec, layer4/tb_gguf.c:376-419; block layouts
-// layer4/tb_gguf.c:110-288).
+// layer4/tb_gguf.c:110-288), and for ggml's layouts of the same formats.
 //
 // x representation.  x is cut into units of 64 elements.  Each unit gets one
 // power-of-two scale 2^s (max |x| of the unit maps just below 2^22) and
@@ -534,8 +534,9 @@ template <> struct KqFmt<QT_Q6_K> {
     }
 };
 
-// Q8_0 (layer4/tb_gguf.c:183-187): d@0, int8 qs[32]@2; w = d*q.
-template <> struct KqFmt<QT_Q8_0> {
+// Q8_0 (layer4/tb_gguf.c:183-187): d@0, int8 qs[32]@2; w = d*q.  The ggml
+// layout is the same but for its IEEE fp16 d.
+template <int QT> struct KqQ80 {
     static constexpr bool PAIR = false;
     struct Unit { uint4 a0, a1, b0, b1; uint32_t d0, d1; };
     // unit = 68 bytes (4-byte aligned when the row is): block 0's quants
@@ -558,10 +559,13 @@ template <> struct KqFmt<QT_Q8_0> {
         int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
         kq_dots<8>(q0, x, 0, h0, m0, l0);
         kq_dots<8>(q1, x, 8, h1, m1, l1);
-        const float f0 = f16_ref(w.d0) * kq_combine(h0, m0, l0);
-        return fmaf(f16_ref(w.d1), kq_combine(h1, m1, l1), f0) * x.isc;
+        const float f0 = f16_of<QT>(w.d0) * kq_combine(h0, m0, l0);
+        return fmaf(f16_of<QT>(w.d1), kq_combine(h1, m1, l1), f0) * x.isc;
     }
 };
+
+template <> struct KqFmt<QT_Q8_0> : KqQ80<QT_Q8_0> {};
+template <> struct KqFmt<QT_GQ8_0> : KqQ80<QT_GQ8_0> {};
 
 // Q4_0 (layer4/tb_gguf.c:110-118): d@0, qs[16]@2; weight 2i = low nibble of
 // qs[i], 2i+1 = high nibble; w = d*(q-8).
@@ -621,6 +625,260 @@ template <> struct KqFmt<QT_Q8_K> {
         int ah = 0, am = 0, al = 0;
         kq_dots<16>(q, x, 0, ah, am, al);
         return __builtin_bit_cast(float, w.d) * x.isc * kq_combine(ah, am, al);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// ggml's layouts (QT_GGML ids; ggml-quants.c dequantize_row_*), NATURAL
+// element order: in every K format a unit (64 consecutive weights) reads 32
+// quant bytes whose byte l holds elements l and 32 + l, so dword t of the
+// unit's quants is elements 4t..4t+3 after one shift and mask.  fp16 fields
+// decode as IEEE.
+// ---------------------------------------------------------------------------
+
+// Q4_K: d@0, dmin@2, sc[12]@4, qs[128]@16; unit p: nibble j of qs[32p+l] is
+// element 32j + l of sub-block 2p + j; its 6-bit scale and min as ggml's
+// get_scale_min_k4: j' < 4 sc[j'] & 63, sc[j'+4] & 63; else
+// (sc[j'+4] & 15) | (sc[j'-4] >> 6) << 4, (sc[j'+4] >> 4) | (sc[j'] >> 6) << 4.
+__device__ __forceinline__ void gq4k_sm(const uint4 &hdr, int p, int j, int &s, int &m) {
+    const int k = (2 * p + j) & 3;
+    const bool hi = p >= 2;
+    s = hi ? (int)(bfe(hdr.w, 8 * k, 4) | (bfe(hdr.y, 8 * k + 6, 2) << 4)) : (int)bfe(hdr.y, 8 * k, 6);
+    m = hi ? (int)(bfe(hdr.w, 8 * k + 4, 4) | (bfe(hdr.z, 8 * k + 6, 2) << 4)) : (int)bfe(hdr.z, 8 * k, 6);
+}
+
+template <> struct KqFmt<QT_GQ4_K> {
+    static constexpr bool PAIR = false;
+    struct Unit { uint4 hdr, q0, q1; };
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 144;
+        const int p = u & 3;
+        w.hdr = GMem::ld128(b);
+        w.q0 = GMem::ld128(b + 16 + 32 * p);
+        w.q1 = GMem::ld128(b + 32 + 32 * p);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
+        const int p = u & 3;
+        const uint32_t qv[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        int H = 0, Mm = 0, L = 0;
+        float mn = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            uint32_t q[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) q[k] = (qv[k] >> (4 * j)) & 0x0F0F0F0Fu;
+            int ah = 0, am = 0, al = 0;
+            kq_dots<8>(q, x, 8 * j, ah, am, al);
+            int s, m;
+            gq4k_sm(w.hdr, p, j, s, m);
+            H = mad24(s, ah, H);
+            Mm = mad24(s, am, Mm);
+            L = mad24(s, al, L);
+            mn = fmaf((float)m, x.gs[2 * j] + x.gs[2 * j + 1], mn);
+        }
+        const float d = f16_ieee(w.hdr.x & 0xFFFFu), dmin = f16_ieee(w.hdr.x >> 16);
+        return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
+    }
+};
+
+// Q5_K: d@0, dmin@2, sc[12]@4, qh[32]@16, qs[128]@48; Q4_K's reading plus
+// bit 2p + j of qh[l] as 16.
+template <> struct KqFmt<QT_GQ5_K> {
+    static constexpr bool PAIR = false;
+    struct Unit { uint4 hdr, h0, h1, q0, q1; };
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 176;
+        const int p = u & 3;
+        w.hdr = GMem::ld128(b);
+        w.h0 = GMem::ld128(b + 16);
+        w.h1 = GMem::ld128(b + 32);
+        w.q0 = GMem::ld128(b + 48 + 32 * p);
+        w.q1 = GMem::ld128(b + 64 + 32 * p);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
+        const int p = u & 3;
+        const uint32_t qv[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        const uint32_t hv[8] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w};
+        int H = 0, Mm = 0, L = 0;
+        float mn = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int bit = 2 * p + j;
+            uint32_t q[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                q[k] = ((qv[k] >> (4 * j)) & 0x0F0F0F0Fu) | (((hv[k] >> bit) & 0x01010101u) << 4);
+            int ah = 0, am = 0, al = 0;
+            kq_dots<8>(q, x, 8 * j, ah, am, al);
+            int s, m;
+            gq4k_sm(w.hdr, p, j, s, m);
+            H = mad24(s, ah, H);
+            Mm = mad24(s, am, Mm);
+            L = mad24(s, al, L);
+            mn = fmaf((float)m, x.gs[2 * j] + x.gs[2 * j + 1], mn);
+        }
+        const float d = f16_ieee(w.hdr.x & 0xFFFFu), dmin = f16_ieee(w.hdr.x >> 16);
+        return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
+    }
+};
+
+// Q6_K: ql[128]@0, qh[64]@128, int8 sc[16]@192, d@208; unit p (half
+// n = p/2): element e of the unit is nibble p&1 of ql[64n + e] with bits
+// 4(p&1) + 2(e/32) of qh[32n + e%32] above it; scale sc[4p + e/16]; q - 32.
+template <> struct KqFmt<QT_GQ6_K> {
+    static constexpr bool PAIR = false;
+    struct Unit { uint32_t ql[16], qh[8], sc, d; };
+    // 210-byte blocks: every other block starts 2 mod 4 (ld_dw)
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 210;
+        const int p = u & 3, n = p >> 1;
+        GMem::template ldw<16>(b + 64 * n, w.ql);
+        GMem::template ldw<8>(b + 128 + 32 * n, w.qh);
+        GMem::template ldw<1>(b + 192 + 4 * p, &w.sc);
+        w.d = GMem::ld16(b + 208);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
+        const int hs = 4 * (u & 1);
+        int H = 0, Mm = 0, L = 0;
+        float mn = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            uint32_t q[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int t = 4 * g + c;
+                const uint32_t hb = (w.qh[t & 7] >> (hs + 2 * (t >> 3))) & 0x03030303u;
+                q[c] = ((w.ql[t] >> hs) & 0x0F0F0F0Fu) | (hb << 4);
+            }
+            int ah = 0, am = 0, al = 0;
+            kq_dots<4>(q, x, 4 * g, ah, am, al);
+            const int s = sbfe(w.sc, 8 * g, 8);
+            H = mad24(s, ah, H);
+            Mm = mad24(s, am, Mm);
+            L = mad24(s, al, L);
+            mn = fmaf((float)s, x.gs[g], mn);
+        }
+        return f16_ieee(w.d) * fmaf(x.isc, kq_combine(H, Mm, L), -32.f * mn);
+    }
+};
+
+// Q3_K: hmask[32]@0, qs[64]@32, sc[12]@96, d@108; unit p (n = p/2,
+// k0 = 2(p&1)): element e has bits 2(k0 + e/32) of qs[32n + e%32] and bit
+// 4n + k0 + e/32 of hmask[e%32] (set: +4); scale 4p + g of ggml's unpack:
+// lo4 = nibble p/2 of sc[4(p&1) + g], hi2 = bits 2p of sc[8 + g]; value
+// (q3 - 4) * ((lo4 | hi2 << 4) - 32).
+template <> struct KqFmt<QT_GQ3_K> {
+    static constexpr bool PAIR = false;
+    struct Unit { uint32_t qs[8], hm[8], lo, hi, d; };
+    // 110-byte blocks: every other block starts 2 mod 4 (ld_dw)
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 110;
+        const int p = u & 3, n = p >> 1;
+        GMem::template ldw<8>(b + 32 + 32 * n, w.qs);
+        GMem::template ldw<8>(b, w.hm);
+        GMem::template ldw<1>(b + 96 + 4 * (p & 1), &w.lo);
+        GMem::template ldw<1>(b + 104, &w.hi);
+        w.d = GMem::ld16(b + 108);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
+        const int p = u & 3, n = p >> 1, k0 = 2 * (p & 1);
+        int H = 0, Mm = 0, L = 0;
+        float mn = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            uint32_t q[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int t = 4 * g + c, h = t >> 3;
+                q[c] = ((w.qs[t & 7] >> (2 * (k0 + h))) & 0x03030303u) |
+                       (((w.hm[t & 7] >> (4 * n + k0 + h)) & 0x01010101u) << 2);
+            }
+            int ah = 0, am = 0, al = 0;
+            kq_dots<4>(q, x, 4 * g, ah, am, al);
+            const int lo4 = (int)bfe(w.lo, 8 * g + 4 * n, 4);
+            const int hi2 = (int)bfe(w.hi, 8 * g + 2 * p, 2);
+            const int s = (lo4 | (hi2 << 4)) - 32;
+            H = mad24(s, ah, H);
+            Mm = mad24(s, am, Mm);
+            L = mad24(s, al, L);
+            mn = fmaf((float)s, x.gs[g], mn);
+        }
+        return f16_ieee(w.d) * fmaf(x.isc, kq_combine(H, Mm, L), -4.f * mn);
+    }
+};
+
+// Q2_K: sc[16]@0, qs[64]@16, d@80, dmin@82; unit p: element e has bits
+// 2(k0 + e/32) of qs[32n + e%32]; scale/min byte sc[4p + g].
+template <> struct KqFmt<QT_GQ2_K> {
+    static constexpr bool PAIR = false;
+    struct Unit { uint4 q0, q1; uint32_t sc, dd; };
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)(u >> 2) * 84;
+        const int p = u & 3, n = p >> 1;
+        w.q0 = GMem::ld128(b + 16 + 32 * n);
+        w.q1 = GMem::ld128(b + 32 + 32 * n);
+        w.sc = GMem::ld32(b + 4 * p);
+        w.dd = GMem::ld32(b + 80);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
+        const int k0 = 2 * (u & 1);
+        const uint32_t qv[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        int H = 0, Mm = 0, L = 0;
+        float mn = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            uint32_t q[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int t = 4 * g + c;
+                q[c] = (qv[t & 7] >> (2 * (k0 + (t >> 3)))) & 0x03030303u;
+            }
+            int ah = 0, am = 0, al = 0;
+            kq_dots<4>(q, x, 4 * g, ah, am, al);
+            const int s = (int)bfe(w.sc, 8 * g, 4), m = (int)bfe(w.sc, 8 * g + 4, 4);
+            H = mad24(s, ah, H);
+            Mm = mad24(s, am, Mm);
+            L = mad24(s, al, L);
+            mn = fmaf((float)m, x.gs[g], mn);
+        }
+        const float d = f16_ieee(w.dd & 0xFFFFu), dmin = f16_ieee(w.dd >> 16);
+        return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
+    }
+};
+
+// Q4_0: d@0, qs[16]@2; element l < 16 is the low nibble of qs[l], 16 + l
+// the high nibble; w = (q - 8) * d.
+template <> struct KqFmt<QT_GQ4_0> {
+    static constexpr bool PAIR = false;
+    struct Unit { uint4 a, b; uint32_t d0, d1; };
+    static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
+        const uint8_t *b = row + (size_t)u * 36;
+        uint32_t t[4];
+        w.d0 = GMem::ld16(b);
+        GMem::template ldw<4>(b + 2, t);
+        w.a = make_uint4(t[0], t[1], t[2], t[3]);
+        w.d1 = GMem::ld16(b + 18);
+        GMem::template ldw<4>(b + 20, t);
+        w.b = make_uint4(t[0], t[1], t[2], t[3]);
+    }
+    static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
+        float r = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint4 v = j ? w.b : w.a;
+            const uint32_t qv[4] = {v.x, v.y, v.z, v.w};
+            uint32_t q[8];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                q[k] = qv[k] & 0x0F0F0F0Fu;
+                q[4 + k] = (qv[k] >> 4) & 0x0F0F0F0Fu;
+            }
+            int ah = 0, am = 0, al = 0;
+            kq_dots<8>(q, x, 8 * j, ah, am, al);
+            const float sx = x.gs[2 * j] + x.gs[2 * j + 1];
+            r = fmaf(f16_ieee(j ? w.d1 : w.d0), fmaf(x.isc, kq_combine(ah, am, al), -8.f * sx), r);
+        }
+        return r;
     }
 };
 
@@ -798,6 +1056,13 @@ static hipError_t launch_matvec_kq_p(int qt, const void *W, int M, int K, const 
     case QT_Q8_0: return launch_kq_q<QT_Q8_0, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     case QT_Q4_0: return launch_kq_q<QT_Q4_0, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     case QT_Q8_K: return launch_kq_q<QT_Q8_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_GQ2_K: return launch_kq_q<QT_GQ2_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_GQ3_K: return launch_kq_q<QT_GQ3_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_GQ4_K: return launch_kq_q<QT_GQ4_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_GQ5_K: return launch_kq_q<QT_GQ5_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_GQ6_K: return launch_kq_q<QT_GQ6_K, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_GQ8_0: return launch_kq_q<QT_GQ8_0, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    case QT_GQ4_0: return launch_kq_q<QT_GQ4_0, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     default: return hipErrorNotSupported;
     }
 }

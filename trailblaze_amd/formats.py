@@ -19,6 +19,23 @@ SCALE_FIELDS = {Q4_0: (0,), Q8_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 
 
 KQUANTS = (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0)
 
+# GGML | id: ggml's own on-disk layout of the format (TBQ_GGML in
+# include/tbq.h).  Same geometry and field offsets; the quant bits, 6-bit
+# scales and fp16 fields are read as ggml reads them.  F32, BF16 and Q8_K
+# read the same in both layouts.
+GGML = 0x100
+for _q in list(GEOMETRY):
+    GEOMETRY[GGML | _q] = GEOMETRY[_q]
+    NAMES[GGML | _q] = "ggml " + NAMES[_q]
+for _q in list(SCALE_FIELDS):
+    SCALE_FIELDS[GGML | _q] = SCALE_FIELDS[_q]
+GGML_FORMATS = tuple(GGML | q for q in (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, F16))
+
+
+def base(qtype: int) -> int:
+    """The ggml type id of a qtype (the layout flag removed)."""
+    return qtype & 0xFF
+
 
 def row_bytes(qtype: int, K: int) -> int:
     bw, bb = GEOMETRY[qtype]

@@ -80,6 +80,11 @@ class GgufFile:
         _check(lib().tbq_gguf_get_str(self.h, key.encode(), buf, len(buf)), "tbq_gguf_get_str")
         return buf.value.decode()
 
+    def set_layout(self, layout: int) -> None:
+        """0 = the reference's block layouts (default), formats.GGML = ggml's:
+        the qtypes of models and layers assembled afterwards carry the flag."""
+        _check(lib().tbq_gguf_set_layout(self.h, layout), "tbq_gguf_set_layout")
+
     # ---- device residency ------------------------------------------------
     def upload_all(self) -> int:
         n = lib().tbq_gguf_upload_all(self.h)

@@ -67,6 +67,7 @@ struct tbq_gguf {
     tensor_t *t;
     void **owned;        /* fused matrices and KV caches */
     int n_owned, cap_owned;
+    int layout;          /* 0: the reference's block layouts; TBQ_GGML: ggml's */
 };
 
 /* ---- bounds-checked cursor over the map ---------------------------------- */
@@ -446,6 +447,18 @@ static double arch_float(const tbq_gguf *g, const char *arch, const char *suffix
     return tbq_gguf_get_float(g, key, &v) ? v : dflt;
 }
 
+int tbq_gguf_set_layout(tbq_gguf *g, int layout) {
+    if (!g || (layout != 0 && layout != TBQ_GGML)) return failf("tbq_gguf_set_layout: layout must be 0 or TBQ_GGML");
+    g->layout = layout;
+    return 1;
+}
+
+/* The qtype id an assembled model or layer carries for file qtype qt: the
+ * file's ggml id, with TBQ_GGML added when the handle reads ggml's layouts
+ * (F32 stays 0, which the dense model's qt_* fields reserve for "the
+ * model's qtype_layers"; it reads the same in both layouts). */
+static int lq(const tbq_gguf *g, int qt) { return qt == 0 ? 0 : (qt | g->layout); }
+
 int tbq_gguf_dense_model(tbq_gguf *g, int max_ctx, tbq_dense_model *m, tbq_dense_layer *layers, int n_layers) {
     if (!g || !m || !layers || max_ctx <= 0) return failf("tbq_gguf_dense_model: bad arguments");
     if (!tbq_init()) return 0;
@@ -498,32 +511,32 @@ int tbq_gguf_dense_model(tbq_gguf *g, int max_ctx, tbq_dense_model *m, tbq_dense
         ly->k_norm = (const float *)g->t[ikn].dev;
         ly->ffn_norm = (const float *)g->t[ifn].dev;
         ly->wo = g->t[io].dev;
-        ly->qt_o = g->t[io].qtype;
+        ly->qt_o = lq(g, g->t[io].qtype);
         ly->wdown = g->t[id].dev;
-        ly->qt_down = g->t[id].qtype;
+        ly->qt_down = lq(g, g->t[id].qtype);
         /* one fused device matrix where the rows share a qtype, else the
          * separate matrices (one launch each) */
         if (g->t[iq].qtype == g->t[ik].qtype && g->t[iq].qtype == g->t[iv].qtype) {
             if (!(ly->wqkv = fuse(g, iq, ik, iv))) return 0;
-            ly->qt_qkv = g->t[iq].qtype;
+            ly->qt_qkv = lq(g, g->t[iq].qtype);
         } else {
             if (!upload(g, iq) || !upload(g, ik) || !upload(g, iv)) return 0;
             ly->wq = g->t[iq].dev;
             ly->wk = g->t[ik].dev;
             ly->wv = g->t[iv].dev;
-            ly->qt_q = g->t[iq].qtype;
-            ly->qt_k = g->t[ik].qtype;
-            ly->qt_v = g->t[iv].qtype;
+            ly->qt_q = lq(g, g->t[iq].qtype);
+            ly->qt_k = lq(g, g->t[ik].qtype);
+            ly->qt_v = lq(g, g->t[iv].qtype);
         }
         if (g->t[ig].qtype == g->t[iu].qtype) {
             if (!(ly->wgu = fuse(g, ig, iu, -1))) return 0;
-            ly->qt_gu = g->t[ig].qtype;
+            ly->qt_gu = lq(g, g->t[ig].qtype);
         } else {
             if (!upload(g, ig) || !upload(g, iu)) return 0;
             ly->wgate = g->t[ig].dev;
             ly->wup = g->t[iu].dev;
-            ly->qt_gate = g->t[ig].qtype;
-            ly->qt_up = g->t[iu].qtype;
+            ly->qt_gate = lq(g, g->t[ig].qtype);
+            ly->qt_up = lq(g, g->t[iu].qtype);
         }
     }
     const size_t kv_bytes = (size_t)L * (size_t)NKV * (size_t)max_ctx * (size_t)D * 4;
@@ -540,8 +553,8 @@ int tbq_gguf_dense_model(tbq_gguf *g, int max_ctx, tbq_dense_model *m, tbq_dense
     m->max_ctx = max_ctx;
     m->norm_eps = (float)arch_float(g, arch, "attention.layer_norm_rms_epsilon", 1e-6);
     m->rope_theta = (float)arch_float(g, arch, "rope.freq_base", 10000.0);
-    m->qtype_layers = qt;
-    m->qtype_embd = qe;
+    m->qtype_layers = lq(g, qt);
+    m->qtype_embd = lq(g, qe);
     m->tok_embd = g->t[te].dev;
     m->lm_head = g->t[head].dev;
     m->output_norm = (const float *)g->t[on].dev;
@@ -575,7 +588,7 @@ int tbq_gguf_moe_layer(tbq_gguf *g, int layer, tbq_moe_layer *Lout) {
     Lout->F = (int)F;
     Lout->E = (int)E;
     Lout->top_k = (int)K;
-    Lout->qtype = qt;
+    Lout->qtype = lq(g, qt);
     Lout->router = (const float *)g->t[ir].dev;
     Lout->bias = NULL;
     Lout->gate = g->t[ig].dev;

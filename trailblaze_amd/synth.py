@@ -14,8 +14,11 @@ from . import formats as fm
 
 
 def kquant_matrix(qtype: int, M: int, K: int, rng: np.random.Generator) -> np.ndarray:
-    """[M, row_bytes] uint8 matrix of random blocks in the reference layout."""
+    """[M, row_bytes] uint8 matrix of random blocks (random quant and scale
+    bytes, fp16 scale fields in [1e-3, 1e-2]); the fields sit at the same
+    offsets in the reference's layouts and ggml's, so it serves both."""
     bw, bb = fm.GEOMETRY[qtype]
+    qtype = fm.base(qtype)
     if qtype in (fm.F32, fm.F16, fm.BF16):
         if qtype == fm.F32:
             return rng.standard_normal((M, K), dtype=np.float32).view(np.uint8).reshape(M, K * 4)
