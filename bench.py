@@ -181,10 +181,28 @@ def gpu_leg(args):
         res["moe"] = moe_leg(tb, fm, synth, torch, rng, stream)
         return res
     # ---- configs[1] sweep ------------------------------------------------
-    sweep = []
-    for qt2, M2, K2 in [(fm.Q2_K, 12288, 4096), (fm.Q2_K, 4096, 12288), (fm.Q3_K, 12288, 4096),
-                        (fm.Q3_K, 4096, 12288), (fm.Q5_K, 12288, 4096), (fm.Q5_K, 4096, 12288),
-                        (fm.Q8_0, 12288, 4096), (fm.Q8_0, 4096, 12288), (fm.Q6_K, 151936, 4096)]:
+    res["sweep"] = sweep_leg(tb, fm, synth, torch, rng, stream, [
+        (fm.Q2_K, 12288, 4096), (fm.Q2_K, 4096, 12288), (fm.Q3_K, 12288, 4096), (fm.Q3_K, 4096, 12288),
+        (fm.Q5_K, 12288, 4096), (fm.Q5_K, 4096, 12288), (fm.Q8_0, 12288, 4096), (fm.Q8_0, 4096, 12288),
+        (fm.Q6_K, 151936, 4096)])
+    # the same formats in ggml's on-disk layouts (TBQ_GGML ids)
+    G = fm.GGML
+    res["ggml_sweep"] = sweep_leg(tb, fm, synth, torch, rng, stream, [
+        (G | fm.Q4_K, 4096, 4096), (G | fm.Q4_K, 12288, 4096), (G | fm.Q4_K, 4096, 12288),
+        (G | fm.Q6_K, 12288, 4096), (G | fm.Q6_K, 4096, 12288), (G | fm.Q5_K, 12288, 4096),
+        (G | fm.Q3_K, 12288, 4096), (G | fm.Q2_K, 12288, 4096), (G | fm.Q8_0, 12288, 4096)])
+
+    res["moe"] = moe_leg(tb, fm, synth, torch, rng, stream)
+    if not args.no_dense and not args.quick:
+        res["dense"] = dense_leg(torch, stream)
+    return res
+
+
+def sweep_leg(tb, fm, synth, torch, rng, stream, shapes):
+    """Per-launch time of tbq_matvec at each (qtype, M, K), cold: enough
+    rotated weight copies that every launch reads HBM."""
+    out = []
+    for qt2, M2, K2 in shapes:
         Wm = torch.from_numpy(synth.kquant_matrix(qt2, M2, K2, rng)).cuda()
         wb = fm.weight_bytes(qt2, M2, K2)
         nc = max(1, int(np.ceil(2 * 256e6 / wb)))
@@ -199,16 +217,11 @@ def gpu_leg(args):
         s = time_region(st, reps, 2, stream)
         pl = s / (reps * nc)
         b = matvec_bytes(qt2, M2, K2)
-        sweep.append(dict(qt=fm.NAMES[qt2], M=M2, K=K2, us=pl * 1e6, gbs=b / pl / 1e9))
+        out.append(dict(qt=fm.NAMES[qt2], M=M2, K=K2, us=pl * 1e6, gbs=b / pl / 1e9))
         log(f"{fm.NAMES[qt2]} {M2}x{K2}: {pl * 1e6:.2f} us  {b / pl / 1e9:.0f} GB/s")
         del cps, Wm
         torch.cuda.empty_cache()
-    res["sweep"] = sweep
-
-    res["moe"] = moe_leg(tb, fm, synth, torch, rng, stream)
-    if not args.no_dense and not args.quick:
-        res["dense"] = dense_leg(torch, stream)
-    return res
+    return out
 
 
 def dense_leg(torch, stream):
@@ -261,23 +274,29 @@ def moe_leg(tb, fm, synth, torch, rng, stream):
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     L = tb.moe_layer(H, F, E, k, fm.Q4_K, d(router), d(gate), d(up), d(down))
     moe = {}
-    for T in (1, 16):
+
+    def decode(Lx, T, name):
         # 64 different token batches per step, so consecutive layers route to
         # different experts (the 340 MB of experts exceed the MALL)
         ntok = 64
         xs = d(synth.activations((ntok, T, H), rng))
         rs = d(synth.activations((ntok, T, H), rng))
         out = torch.empty((T, H), dtype=torch.float32, device="cuda")
-        ws_t = torch.zeros(tb.moe_workspace_size(L, T), dtype=torch.uint8, device="cuda")
+        ws_t = torch.zeros(tb.moe_workspace_size(Lx, T), dtype=torch.uint8, device="cuda")
 
         def mstep():
             for i in range(ntok):
-                tb.moe_forward(L, T, xs[i], rs[i], out, workspace=ws_t)
+                tb.moe_forward(Lx, T, xs[i], rs[i], out, workspace=ws_t)
         reps = 20
         s = time_region(mstep, reps, 2, stream)
         us = s / (reps * ntok) * 1e6
-        moe[f"decode_b{T}"] = dict(us_per_layer=us, us_per_token=us / T)
-        log(f"MoE decode b={T}: {us:.1f} us/layer  {us / T:.2f} us/token")
+        moe[name] = dict(us_per_layer=us, us_per_token=us / T)
+        log(f"MoE {name}: {us:.1f} us/layer  {us / T:.2f} us/token")
+    for T in (1, 16):
+        decode(L, T, f"decode_b{T}")
+    # the same expert bytes read in ggml's Q4_K layout
+    Lg = tb.moe_layer(H, F, E, k, fm.GGML | fm.Q4_K, L._keep[0], L._keep[1], L._keep[2], L._keep[3])
+    decode(Lg, 1, "decode_b1_ggml_q4k")
     # prefill, Zipf-skewed routing, grouped fp16 MFMA experts
     T = 512
     bias = synth.zipf_router_bias(E, 1.1, 1.0, rng)
@@ -381,7 +400,8 @@ def main():
         "extra": {"device": res["device"], "warm_mall_gbs": round(h["warm_gbs"], 1),
                   "warm_us_per_launch": round(h["warm_us_per_launch"], 3),
                   "abi_matvec_us": None if res.get("abi_matvec_us") is None else round(res["abi_matvec_us"], 2),
-                  "sweep": res.get("sweep"), "moe": res.get("moe"), "dense": res.get("dense"),
+                  "sweep": res.get("sweep"), "ggml_sweep": res.get("ggml_sweep"), "moe": res.get("moe"),
+                  "dense": res.get("dense"),
                   "cpu_detail": None if cpu is None else cpu["detail"]},
     }
     print(json.dumps(line), flush=True)

@@ -94,9 +94,22 @@ def test_ggml_matvec_fma(oracle, qt, M, K):
     assert rel_l2(got, oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
 
 
+@pytest.mark.parametrize("M,K", SHAPES[1:])
+def test_ggml_matvec_q4k_intdot(oracle, M, K):
+    """The Q4_K-specialised kernels (register-x for K <= 4096, the
+    LDS-x kernel above) in ggml's layout."""
+    qt = G | fm.Q4_K
+    print("ggml matvec q4k intdot", M, K, flush=True)
+    rng = np.random.default_rng(3 * M + K)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    got = gpu_matvec(W, qt, M, K, x, tb.TBQ_MV_INTDOT)
+    assert rel_l2(got, oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+
+
 def test_ggml_matvec_auto_q4k_headline(oracle):
-    """The default variant at the headline shape takes the int-dot kernel
-    (the reference-layout-only register-x kernel is skipped)."""
+    """The default variant at the headline shape (the register-x Q4_K
+    kernel in ggml's layout)."""
     qt, M, K = G | fm.Q4_K, 4096, 4096
     rng = np.random.default_rng(44)
     W = synth.kquant_matrix(qt, M, K, rng)
@@ -140,6 +153,28 @@ def test_ggml_moe_decode(oracle, qt):
     assert rel_l2(host(out).reshape(T, H) - resid, ref - resid) <= MATVEC_TOL
     with pytest.raises(tb.TbqError, match="prefill"):
         tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws, mode=tb.TBQ_MOE_BF16)
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_ggml_moe_decode_config(oracle, T):
+    """The Q4_K expert kernels in ggml's layout at the Qwen3-30B-A3B layer
+    shape (H 2048, F 768, 128 experts, top-8)."""
+    import torch
+    H, F, E, k = 2048, 768, 128, 8
+    qt = G | fm.Q4_K
+    router, gate, up, down = synth.moe_layer(H, F, E, qt, seed=31)
+    rng = np.random.default_rng(200 + T)
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    print("ggml moe config T=", T, flush=True)
+    L = tb.moe_layer(H, F, E, k, qt, dev(router), dev(gate), dev(up), dev(down), None)
+    out, idx, w = empty(T * H, torch.float32), empty(T * 8, torch.int32), empty(T * 8, torch.float32)
+    ws = torch.zeros(tb.moe_workspace_size(L, T), dtype=torch.uint8, device="cuda")
+    tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws)
+    ref, ridx, rw = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=qt)
+    assert np.array_equal(host(idx).reshape(T, 8), ridx)
+    assert bits_equal(host(w).reshape(T, 8), rw)
+    assert rel_l2(host(out).reshape(T, H) - resid, ref - resid) <= MATVEC_TOL
 
 
 def test_ggml_gguf_dense_file(tmp_path, oracle):

@@ -143,10 +143,10 @@ int tbq_matvec_variant(const void *W, int qt, int M, int K, const float *x, floa
     // The specialised Q4_K kernel takes one row per wave in a single pass
     // (rows of up to 64 units keep x's digits in registers); taller
     // matrices stream better through the shared kernel's row passes.
-    const bool q4k_special =
-        qt == QT_Q4_K && (variant == TBQ_MV_INTDOT || (variant == TBQ_MV_AUTO && K <= 4096 && M <= 8192));
+    const bool q4k_special = (qt == QT_Q4_K || qt == QT_GQ4_K) &&
+                             (variant == TBQ_MV_INTDOT || (variant == TBQ_MV_AUTO && K <= 4096 && M <= 8192));
     if (q4k_special) {
-        hipError_t e = launch_matvec_q4k(W, M, K, x, y, S(s), g_cu);
+        hipError_t e = launch_matvec_q4k(W, M, K, x, y, S(s), g_cu, qt == QT_GQ4_K);
         if (e != hipErrorNotSupported) return hip_ok(e, "matvec launch (Q4_K int-dot)");
     }
     if (variant == TBQ_MV_AUTO || variant == TBQ_MV_KQ) {

@@ -386,8 +386,8 @@ static hipError_t dense_mv(int qt, const void *W, int M, int K, const float *x, 
     // the K-quant kernel, measured 1.3 us per layer faster at the Qwen3-4B
     // shapes
     hipError_t e = hipErrorNotSupported;
-    if (qt == QT_Q4_K && K <= 4096 && M <= 8192 && mode == PRO_NONE)
-        e = launch_matvec_q4k_pro(mode, pro, W, M, K, x, out, st);
+    if ((qt == QT_Q4_K || qt == QT_GQ4_K) && K <= 4096 && M <= 8192 && mode == PRO_NONE)
+        e = launch_matvec_q4k_pro(mode, pro, W, M, K, x, out, st, qt == QT_GQ4_K);
     if (e == hipErrorNotSupported) e = launch_matvec_kq_pro(mode, pro, qt, W, M, K, x, out, st, tbq_cu_count());
     if (e != hipErrorNotSupported) return e;
     const float *xin = x;

@@ -42,13 +42,15 @@ struct MoeArgs {
 hipError_t launch_dequant(int qt, const void *W, long long nweights, float *out, hipStream_t s);
 hipError_t launch_matvec_generic(int qt, const void *W, int M, int K, const float *x, float *y,
                                  hipStream_t s, int n_cu);
-hipError_t launch_matvec_q4k(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu);
+// The Q4_K kernels read the reference's layout, or ggml's (QT_GQ4_K) when ggml.
+hipError_t launch_matvec_q4k(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu,
+                             bool ggml = false);
 hipError_t launch_matvec_kq(int qt, const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu);
 // The same kernels with a staging prologue (mode = PRO_* | MV_GLU);
 // hipErrorNotSupported where they do not cover the shape or mode (the q4k
 // one: K <= 4096, no MV_GLU).
 hipError_t launch_matvec_q4k_pro(int mode, const MvPro &pro, const void *W, int M, int K, const float *x, float *y,
-                                 hipStream_t s);
+                                 hipStream_t s, bool ggml = false);
 hipError_t launch_matvec_kq_pro(int mode, const MvPro &pro, int qt, const void *W, int M, int K, const float *x,
                                 float *y, hipStream_t s, int n_cu);
 hipError_t launch_expf(const float *in, float *out, long long n, hipStream_t s);
@@ -58,6 +60,7 @@ hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st);
 hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
                          float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st,
                          _Float16 *x16 = nullptr, float *xinv = nullptr, bool *x16_done = nullptr);
+// a.qtype QT_Q4_K or QT_GQ4_K
 hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st);
 size_t prefill_workspace_bytes(int T, int k, int E, int H, int F);
 hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t st, bool x16_done = false);

@@ -195,6 +195,17 @@ __device__ __forceinline__ void gq4k_scale_min(const uint8_t *b, int j, int &s, 
         m = (ldb(q + j + 4) >> 4) | ((ldb(q + j) >> 6) << 4);
     }
 }
+// The same for unit p's sub-block 2p + j (j = 0, 1) of a super-block whose
+// first 16 bytes are hdr (hdr.y, .z, .w = scale bytes 0-3, 4-7, 8-11):
+// j' < 4: sc[j'] & 63, sc[j'+4] & 63; else (sc[j'+4] & 15) | (sc[j'-4] >> 6) << 4,
+// (sc[j'+4] >> 4) | (sc[j'] >> 6) << 4.  Selects, no branch on p.
+__device__ __forceinline__ void gq4k_sm(const uint4 &hdr, int p, int j, int &s, int &m) {
+    const int k = (2 * p + j) & 3;
+    const bool hi = p >= 2;
+    const uint32_t y = hdr.y >> (8 * k), z = hdr.z >> (8 * k), w = hdr.w >> (8 * k);
+    s = hi ? (int)((w & 15) | (((y >> 6) & 3) << 4)) : (int)(y & 63);
+    m = hi ? (int)(((w >> 4) & 15) | (((z >> 6) & 3) << 4)) : (int)(z & 63);
+}
 __device__ __forceinline__ int gq3k_scale(const uint8_t *b, int i) {
     const uint8_t *sc = b + 96;
     const int lo4 = (ldb(sc + (i & 7)) >> (4 * (i >> 3))) & 15;

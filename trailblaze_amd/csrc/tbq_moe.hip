@@ -265,7 +265,7 @@ hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
     if (err == hipErrorNotSupported)
         err = launch_route(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.sel_idx, a.sel_w, st);
     if (err != hipSuccess) return err;
-    if (a.qtype == QT_Q4_K) {
+    if (a.qtype == QT_Q4_K || a.qtype == QT_GQ4_K) {
         err = launch_moe_q4k_experts(a, st);
         if (err != hipErrorNotSupported) return err;
     }

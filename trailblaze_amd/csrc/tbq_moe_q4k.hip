@@ -310,7 +310,7 @@ __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn,
 constexpr int GU_THREADS = 64 * TBQ_GU_WAVES;
 constexpr int GU_ROWS = TBQ_GU_ROWS;   // output rows per wave
 
-template <int UPL>
+template <int UPL, bool GG>
 __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
                                                             const float *__restrict__ xn, const int *__restrict__ sel_idx,
                                                             int H, int F, int k, float *__restrict__ act) {
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
 #pragma unroll
         for (int i = 0; i < UPL; i++) {
             const int u = lr + LPR * i;
-            if (r < F && u < U) q4k_load(Wb + (long long)r * rb, u, raw[rr][i]);
+            if (r < F && u < U) q4k_load<GG>(Wb + (long long)r * rb, u, raw[rr][i]);
         }
     }
     xs.store(xd, H);
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
 #pragma unroll
         for (int i = 0; i < UPL; i++) {
             const int u = lr + LPR * i;
-            if (u < U) acc = q4k_unit_dot(raw[rr][i], u, xd, acc);
+            if (u < U) acc = q4k_unit_dot<GG>(raw[rr][i], u, xd, acc);
         }
         acc = group_sum<32>(acc);
         const float u_val = __shfl(acc, 32);
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
 constexpr int DC_THREADS = 512;
 constexpr int DC_ROWS = 8;   // rows per workgroup
 
-template <int UPL>
+template <int UPL, bool GG>
 __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *__restrict__ down, const float *__restrict__ act,
                                                                  const int *__restrict__ sel_idx, const float *__restrict__ sel_w,
                                                                  const float *__restrict__ resid, int H, int F, int k,
@@ -398,7 +398,7 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
 #pragma unroll
             for (int i = 0; i < UPL; i++) {
                 const int u = lr + LPR * i;
-                if (u < U) q4k_load(row, u, raw[p][i]);
+                if (u < U) q4k_load<GG>(row, u, raw[p][i]);
             }
         }
     }
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
 #pragma unroll
             for (int i = 0; i < UPL; i++) {
                 const int u = lr + LPR * i;
-                if (u < U) acc = q4k_unit_dot(raw[p][i], u, xd + sd * G * XD_PER_SB, acc);
+                if (u < U) acc = q4k_unit_dot<GG>(raw[p][i], u, xd + sd * G * XD_PER_SB, acc);
             }
         }
         acc = group_sum<16>(acc);
@@ -681,33 +681,39 @@ hipError_t launch_router(const float *xn, const float *router, const float *bias
     return launch_topk(logits, T, E, top_k, sel_idx, sel_w, st);
 }
 
-template <int UPL_GU, int UPL_DC>
+template <int UPL_GU, int UPL_DC, bool GG>
 static hipError_t launch_experts_q4k(const MoeArgs &a, hipStream_t st) {
     const int pairs = a.T * a.k;
     {
         const int out_per_wg = (GU_THREADS / 64) * GU_ROWS;
         dim3 grid((a.F + out_per_wg - 1) / out_per_wg, pairs);
         size_t lds = (size_t)(a.H / 32) * XD_PER_SB * 4;
-        hipLaunchKernelGGL((k_gate_up_q4k<UPL_GU>), grid, dim3(GU_THREADS), lds, st, (const uint8_t *)a.gate,
+        hipLaunchKernelGGL((k_gate_up_q4k<UPL_GU, GG>), grid, dim3(GU_THREADS), lds, st, (const uint8_t *)a.gate,
                            (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.k, a.act);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
     dim3 grid(a.H / DC_ROWS, a.T);
     size_t lds = (size_t)a.k * (a.F / 32) * XD_PER_SB * 4;
-    hipLaunchKernelGGL((k_down_combine_q4k<UPL_DC>), grid, dim3(DC_THREADS), lds, st, (const uint8_t *)a.down, a.act,
+    hipLaunchKernelGGL((k_down_combine_q4k<UPL_DC, GG>), grid, dim3(DC_THREADS), lds, st, (const uint8_t *)a.down, a.act,
                        a.sel_idx, a.sel_w, a.resid, a.H, a.F, a.k, a.out);
     return hipGetLastError();
 }
 
-// Expert kernels for Q4_K weights (routing already in a.sel_idx / a.sel_w);
-// hipErrorNotSupported outside H <= 4096, F <= 2048.
-hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st) {
+template <bool GG>
+static hipError_t launch_moe_q4k_experts_g(const MoeArgs &a, hipStream_t st) {
     const int ugu = (a.H / 64 + 31) / 32, udc = (a.F / 64 + 15) / 16;
-    if (ugu == 1 && udc == 1) return launch_experts_q4k<1, 1>(a, st);
-    if (ugu <= 2 && udc <= 1) return launch_experts_q4k<2, 1>(a, st);
-    if (ugu <= 2 && udc <= 2) return launch_experts_q4k<2, 2>(a, st);
+    if (ugu == 1 && udc == 1) return launch_experts_q4k<1, 1, GG>(a, st);
+    if (ugu <= 2 && udc <= 1) return launch_experts_q4k<2, 1, GG>(a, st);
+    if (ugu <= 2 && udc <= 2) return launch_experts_q4k<2, 2, GG>(a, st);
     return hipErrorNotSupported;
+}
+
+// Expert kernels for Q4_K weights, in the reference's layout or ggml's
+// (routing already in a.sel_idx / a.sel_w); hipErrorNotSupported outside
+// H <= 4096, F <= 2048.
+hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st) {
+    return a.qtype == QT_GQ4_K ? launch_moe_q4k_experts_g<true>(a, st) : launch_moe_q4k_experts_g<false>(a, st);
 }
 
 }  // namespace tbq

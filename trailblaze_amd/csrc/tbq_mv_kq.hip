@@ -638,15 +638,7 @@ template <> struct KqFmt<QT_Q8_K> {
 
 // Q4_K: d@0, dmin@2, sc[12]@4, qs[128]@16; unit p: nibble j of qs[32p+l] is
 // element 32j + l of sub-block 2p + j; its 6-bit scale and min as ggml's
-// get_scale_min_k4: j' < 4 sc[j'] & 63, sc[j'+4] & 63; else
-// (sc[j'+4] & 15) | (sc[j'-4] >> 6) << 4, (sc[j'+4] >> 4) | (sc[j'] >> 6) << 4.
-__device__ __forceinline__ void gq4k_sm(const uint4 &hdr, int p, int j, int &s, int &m) {
-    const int k = (2 * p + j) & 3;
-    const bool hi = p >= 2;
-    s = hi ? (int)(bfe(hdr.w, 8 * k, 4) | (bfe(hdr.y, 8 * k + 6, 2) << 4)) : (int)bfe(hdr.y, 8 * k, 6);
-    m = hi ? (int)(bfe(hdr.w, 8 * k + 4, 4) | (bfe(hdr.z, 8 * k + 6, 2) << 4)) : (int)bfe(hdr.z, 8 * k, 6);
-}
-
+// get_scale_min_k4 (gq4k_sm).
 template <> struct KqFmt<QT_GQ4_K> {
     static constexpr bool PAIR = false;
     struct Unit { uint4 hdr, q0, q1; };

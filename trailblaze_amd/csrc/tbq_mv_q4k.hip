@@ -27,7 +27,7 @@ constexpr int WG = 1024;        // threads per workgroup (16 waves share one x s
 // One pass of a wave covers RPP = 64/LPR rows; each lane owns UPL units of
 // its row.  Rows are grid-strided over all waves; the next pass's loads are
 // issued before the current pass is reduced.
-template <int LPR, int UPL>
+template <int LPR, int UPL, bool GG>
 __global__ __launch_bounds__(WG) void k_mv_q4k(const uint8_t *__restrict__ W, int M, int K, long long rb,
                                                const float *__restrict__ x, float *__restrict__ y) {
     extern __shared__ uint32_t xd[];
@@ -45,7 +45,7 @@ __global__ __launch_bounds__(WG) void k_mv_q4k(const uint8_t *__restrict__ W, in
 #pragma unroll
         for (int i = 0; i < UPL; i++) {
             const int u = lr + LPR * i;
-            if (r < M && u < U) q4k_load(W + (long long)r * rb, u, dst[i]);
+            if (r < M && u < U) q4k_load<GG>(W + (long long)r * rb, u, dst[i]);
         }
     };
     load(cur, row);
@@ -62,7 +62,7 @@ __global__ __launch_bounds__(WG) void k_mv_q4k(const uint8_t *__restrict__ W, in
 #pragma unroll
         for (int i = 0; i < UPL; i++) {
             const int u = lr + LPR * i;
-            if (row < M && u < U) acc = q4k_unit_dot(cur[i], u, xd, acc);
+            if (row < M && u < U) acc = q4k_unit_dot<GG>(cur[i], u, xd, acc);
         }
         acc = group_sum<LPR>(acc);
         if (lr == 0 && row < M) y[row] = acc;
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(WG) void k_mv_q4k(const uint8_t *__restrict__ W, in
 // RPP = 64/LPR rows (rows wave_base + p*RPP + rsub); all R passes' weight
 // loads are in flight before x is staged.  No grid-stride loop: the grid
 // covers M exactly.
-template <int LPR, int R, int NW, int PRO>
+template <int LPR, int R, int NW, int PRO, bool GG>
 __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict__ W, int M, int K, long long rb,
                                                       const float *__restrict__ x, float *__restrict__ y, MvPro pro) {
     extern __shared__ uint32_t xd[];
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
 #pragma unroll
     for (int p = 0; p < R; p++) {
         const int r = min(base + p * RPP, M - 1);
-        q4k_load(W + (long long)r * rb, ul, w[p]);
+        q4k_load<GG>(W + (long long)r * rb, ul, w[p]);
     }
     xs.apply(K, pro);
     xs.store(xd, K);
@@ -113,36 +113,36 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
 #pragma unroll
     for (int p = 0; p < R; p++) {
         const int r = base + p * RPP;
-        const float v = q4k_unit_dot(w[p], ul, xu, 0.f);
+        const float v = q4k_unit_dot<GG>(w[p], ul, xu, 0.f);
         const float acc = group_sum<LPR>((r < M && lv) ? v : 0.f);
         if (lr == 0 && r < M) y[r] = acc;
     }
 }
 
-template <int LPR, int R, int NW, int PRO>
+template <int LPR, int R, int NW, int PRO, bool GG>
 static hipError_t launch_q4k_xr(const void *W, int M, int K, const float *x, float *y, hipStream_t s,
                                 const MvPro &pro) {
     constexpr int ROWS_PER_WG = NW * R * (64 / LPR);
     const int grid = (M + ROWS_PER_WG - 1) / ROWS_PER_WG;
     const long long rb = (long long)(K / 256) * 144;
     const size_t lds = (size_t)(K / 32) * XD_PER_SB * 4;
-    hipLaunchKernelGGL((k_mv_q4k_xr<LPR, R, NW, PRO>), dim3(grid), dim3(NW * 64), lds, s, (const uint8_t *)W, M, K,
+    hipLaunchKernelGGL((k_mv_q4k_xr<LPR, R, NW, PRO, GG>), dim3(grid), dim3(NW * 64), lds, s, (const uint8_t *)W, M, K,
                        rb, x, y, pro);
     return hipGetLastError();
 }
 
-template <int PRO>
+template <int PRO, bool GG>
 static hipError_t launch_q4k_xr_k(const void *W, int M, int K, const float *x, float *y, hipStream_t s,
                                   const MvPro &pro) {
     const int U = K / 64;
-    if (U <= 4) return launch_q4k_xr<4, Q4K_XR_R, Q4K_XR_NW, PRO>(W, M, K, x, y, s, pro);
-    if (U <= 8) return launch_q4k_xr<8, Q4K_XR_R, Q4K_XR_NW, PRO>(W, M, K, x, y, s, pro);
-    if (U <= 16) return launch_q4k_xr<16, Q4K_XR_R, Q4K_XR_NW, PRO>(W, M, K, x, y, s, pro);
-    if (U <= 32) return launch_q4k_xr<32, Q4K_XR_R, Q4K_XR_NW, PRO>(W, M, K, x, y, s, pro);
-    return launch_q4k_xr<64, Q4K_XR_R, Q4K_XR_NW, PRO>(W, M, K, x, y, s, pro);
+    if (U <= 4) return launch_q4k_xr<4, Q4K_XR_R, Q4K_XR_NW, PRO, GG>(W, M, K, x, y, s, pro);
+    if (U <= 8) return launch_q4k_xr<8, Q4K_XR_R, Q4K_XR_NW, PRO, GG>(W, M, K, x, y, s, pro);
+    if (U <= 16) return launch_q4k_xr<16, Q4K_XR_R, Q4K_XR_NW, PRO, GG>(W, M, K, x, y, s, pro);
+    if (U <= 32) return launch_q4k_xr<32, Q4K_XR_R, Q4K_XR_NW, PRO, GG>(W, M, K, x, y, s, pro);
+    return launch_q4k_xr<64, Q4K_XR_R, Q4K_XR_NW, PRO, GG>(W, M, K, x, y, s, pro);
 }
 
-template <int LPR, int UPL>
+template <int LPR, int UPL, bool GG>
 static hipError_t launch_q4k_t(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu) {
     constexpr int ROWS_PER_WG = (WG / 64) * (64 / LPR);
     long long need = ((long long)M + ROWS_PER_WG - 1) / ROWS_PER_WG;
@@ -150,30 +150,41 @@ static hipError_t launch_q4k_t(const void *W, int M, int K, const float *x, floa
     int grid = (int)(need < cap ? need : cap);
     long long rb = (long long)(K / 256) * 144;
     size_t lds = (size_t)(K / 32) * XD_PER_SB * 4;
-    hipLaunchKernelGGL((k_mv_q4k<LPR, UPL>), dim3(grid), dim3(WG), lds, s, (const uint8_t *)W, M, K, rb, x, y);
+    hipLaunchKernelGGL((k_mv_q4k<LPR, UPL, GG>), dim3(grid), dim3(WG), lds, s, (const uint8_t *)W, M, K, rb, x, y);
     return hipGetLastError();
 }
 
-// Returns hipErrorNotSupported for shapes this kernel does not cover.
-hipError_t launch_matvec_q4k(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu) {
+template <bool GG>
+static hipError_t launch_matvec_q4k_g(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu) {
     const int U = K / 64;
-    if (K % 256 || U < 4) return hipErrorNotSupported;
-    if (U <= 64) return launch_q4k_xr_k<PRO_NONE>(W, M, K, x, y, s, MvPro{});
-    if (U <= 128) return launch_q4k_t<64, 2>(W, M, K, x, y, s, n_cu);
-    if (U <= 192) return launch_q4k_t<64, 3>(W, M, K, x, y, s, n_cu);
-    if (U <= 256) return launch_q4k_t<64, 4>(W, M, K, x, y, s, n_cu);
-    return hipErrorNotSupported;
+    if (U <= 64) return launch_q4k_xr_k<PRO_NONE, GG>(W, M, K, x, y, s, MvPro{});
+    if (U <= 128) return launch_q4k_t<64, 2, GG>(W, M, K, x, y, s, n_cu);
+    if (U <= 192) return launch_q4k_t<64, 3, GG>(W, M, K, x, y, s, n_cu);
+    return launch_q4k_t<64, 4, GG>(W, M, K, x, y, s, n_cu);
+}
+
+// Returns hipErrorNotSupported for shapes this kernel does not cover.
+// ggml: ggml's Q4_K layout (QT_GQ4_K) instead of the reference's.
+hipError_t launch_matvec_q4k(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu,
+                             bool ggml) {
+    const int U = K / 64;
+    if (K % 256 || U < 4 || U > 256) return hipErrorNotSupported;
+    return ggml ? launch_matvec_q4k_g<true>(W, M, K, x, y, s, n_cu) : launch_matvec_q4k_g<false>(W, M, K, x, y, s, n_cu);
 }
 
 // With a staging prologue: the register-x kernel only (K <= 4096);
 // hipErrorNotSupported otherwise.
 hipError_t launch_matvec_q4k_pro(int mode, const MvPro &pro, const void *W, int M, int K, const float *x, float *y,
-                                 hipStream_t s) {
+                                 hipStream_t s, bool ggml) {
     const int U = K / 64;
     if (K % 256 || U < 4 || U > 64) return hipErrorNotSupported;
     switch (mode) {
-    case PRO_NONE: return launch_q4k_xr_k<PRO_NONE>(W, M, K, x, y, s, pro);
-    case PRO_NORM: return launch_q4k_xr_k<PRO_NORM>(W, M, K, x, y, s, pro);
+    case PRO_NONE:
+        return ggml ? launch_q4k_xr_k<PRO_NONE, true>(W, M, K, x, y, s, pro)
+                    : launch_q4k_xr_k<PRO_NONE, false>(W, M, K, x, y, s, pro);
+    case PRO_NORM:
+        return ggml ? launch_q4k_xr_k<PRO_NORM, true>(W, M, K, x, y, s, pro)
+                    : launch_q4k_xr_k<PRO_NORM, false>(W, M, K, x, y, s, pro);
     default: return hipErrorNotSupported;
     }
 }

@@ -223,21 +223,68 @@ struct Q4KUnit {
     uint32_t mind;
 };
 
-// Unit u of a row: super-block u/4, sub-blocks 2*(u%4) and 2*(u%4)+1.
+// Unit u of a row: super-block u/4, sub-blocks 2*(u%4) and 2*(u%4)+1.  In
+// both layouts the unit's quants are bytes 32p..32p+31 of qs; the
+// reference's layout also needs the first quant dword (its min bytes of
+// sub-blocks 4-7).  GG = ggml's layout (QT_GQ4_K).
+template <bool GG = false>
 __device__ __forceinline__ void q4k_load(const uint8_t *row, int u, Q4KUnit &r) {
     const uint8_t *b = row + (size_t)(u >> 2) * 144;
     const int p = u & 3;
     r.hdr = *reinterpret_cast<const uint4 *>(b);
     r.q0 = *reinterpret_cast<const uint4 *>(b + 16 + 32 * p);
     r.q1 = *reinterpret_cast<const uint4 *>(b + 32 + 32 * p);
-    r.mind = *reinterpret_cast<const uint32_t *>(b + 16);
+    if constexpr (!GG) r.mind = *reinterpret_cast<const uint32_t *>(b + 16);
+}
+
+// ggml's layout: quant byte l of the unit holds element l of sub-block 2p
+// (low nibble) and of sub-block 2p+1 (high nibble).  The digits are staged
+// in even / odd element order per 8-element run, so one v_perm per run and
+// parity gathers bytes 8o + {0,2,4,6} (8o + {1,3,5,7}); their low nibbles
+// feed sub-block 2p, their high nibbles sub-block 2p+1.
+__device__ __forceinline__ float gq4_subblock(const uint32_t *ev, const uint32_t *od, int sh, const uint4 *D, float sx,
+                                              float isc, float S, float Mn, float acc) {
+    const uint32_t *D32 = reinterpret_cast<const uint32_t *>(D);
+    int ah = 0;
+    uint32_t am = 0, al = 0;
+#pragma unroll
+    for (int o = 0; o < 4; o++) {
+        const uint32_t lo = (ev[o] >> sh) & 0x0F0F0F0Fu;
+        const uint32_t hi = (od[o] >> sh) & 0x0F0F0F0Fu;
+        ah = __builtin_amdgcn_sdot4((int)lo, (int)D32[o * 6 + 0], ah, false);
+        ah = __builtin_amdgcn_sdot4((int)hi, (int)D32[o * 6 + 1], ah, false);
+        am = __builtin_amdgcn_udot4(lo, D32[o * 6 + 2], am, false);
+        am = __builtin_amdgcn_udot4(hi, D32[o * 6 + 3], am, false);
+        al = __builtin_amdgcn_udot4(lo, D32[o * 6 + 4], al, false);
+        al = __builtin_amdgcn_udot4(hi, D32[o * 6 + 5], al, false);
+    }
+    const float f = fmaf((float)ah, 65536.f, fmaf((float)am, 256.f, (float)al));
+    acc = fmaf(S * isc, f, acc);
+    return fmaf(-Mn, sx, acc);
 }
 
 // Reference scale/min selection (layer4/tb_gguf.c:163-168): sub-block j<4
 // takes scale byte 4+j and min byte 8+j; j>=4 takes scale byte 8+j and min
-// byte 12+j, i.e. the first four quant bytes.
+// byte 12+j, i.e. the first four quant bytes.  GG: ggml's get_scale_min_k4,
+// IEEE fp16 d and dmin, and ggml's quant order.
+template <bool GG = false>
 __device__ __forceinline__ float q4k_unit_dot(const Q4KUnit &r, int u, const XUnit &x, float acc) {
     const int p = u & 3;
+    if constexpr (GG) {
+        const float d = f16_ieee(r.hdr.x & 0xFFFFu), dmin = f16_ieee(r.hdr.x >> 16);
+        int s0, m0, s1, m1;
+        gq4k_sm(r.hdr, p, 0, s0, m0);
+        gq4k_sm(r.hdr, p, 1, s1, m1);
+        const uint32_t g[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        uint32_t ev[4], od[4];
+#pragma unroll
+        for (int o = 0; o < 4; o++) {
+            ev[o] = __builtin_amdgcn_perm(g[2 * o + 1], g[2 * o], 0x06040200u);
+            od[o] = __builtin_amdgcn_perm(g[2 * o + 1], g[2 * o], 0x07050301u);
+        }
+        acc = gq4_subblock(ev, od, 0, x.d, x.meta.x, x.meta.z, d * (float)s0, dmin * (float)m0, acc);
+        return gq4_subblock(ev, od, 4, x.d + 6, x.meta.y, x.meta.w, d * (float)s1, dmin * (float)m1, acc);
+    }
     const float d = f16_ref(r.hdr.x & 0xFFFFu), dmin = f16_ref(r.hdr.x >> 16);
     const uint32_t sw = p < 2 ? r.hdr.y : r.hdr.w;
     const uint32_t mw = p < 2 ? r.hdr.z : r.mind;
@@ -249,10 +296,11 @@ __device__ __forceinline__ float q4k_unit_dot(const Q4KUnit &r, int u, const XUn
 }
 
 // Same, with the unit's digits read from LDS.
+template <bool GG = false>
 __device__ __forceinline__ float q4k_unit_dot(const Q4KUnit &r, int u, const uint32_t *xd, float acc) {
     XUnit x;
     xunit_load(xd, u, x);
-    return q4k_unit_dot(r, u, x, acc);
+    return q4k_unit_dot<GG>(r, u, x, acc);
 }
 
 }  // namespace tbq
