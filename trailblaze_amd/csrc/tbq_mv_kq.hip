@@ -717,20 +717,36 @@ template <> struct KqFmt<QT_GQ5_K> {
 // Q6_K: ql[128]@0, qh[64]@128, int8 sc[16]@192, d@208; unit p (half
 // n = p/2): element e of the unit is nibble p&1 of ql[64n + e] with bits
 // 4(p&1) + 2(e/32) of qh[32n + e%32] above it; scale sc[4p + e/16]; q - 32.
+// Units 2n and 2n+1 read the same 96 bytes, so the two lanes of a pair
+// (adjacent lanes: the unit's parity is the lane's) split them: lane h
+// loads ql[64n + 32h ..+31] and qh[32n ..+31], forms the 6-bit quants of
+// elements 32h..32h+31 of both units, keeps its own unit's and swaps the
+// other unit's with its partner (DPP quad_perm [1,0,3,2]).  Every lane of
+// the wave runs dot(): lanes past the row's units pair among themselves.
 template <> struct KqFmt<QT_GQ6_K> {
     static constexpr bool PAIR = false;
-    struct Unit { uint32_t ql[16], qh[8], sc, d; };
+    struct Unit { uint32_t ql[8], qh[8], sc, d; };
     // 210-byte blocks: every other block starts 2 mod 4 (ld_dw)
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
         const uint8_t *b = row + (size_t)(u >> 2) * 210;
         const int p = u & 3, n = p >> 1;
-        GMem::template ldw<16>(b + 64 * n, w.ql);
+        GMem::template ldw<8>(b + 64 * n + 32 * (p & 1), w.ql);
         GMem::template ldw<8>(b + 128 + 32 * n, w.qh);
         GMem::template ldw<1>(b + 192 + 4 * p, &w.sc);
         w.d = GMem::ld16(b + 208);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
-        const int hs = 4 * (u & 1);
+        const int h = u & 1;
+        // own unit: nibble h, qh bits 2h + 4h; the partner's: nibble 1-h,
+        // qh bits 4(1-h) + 2h
+        const int so = 4 * h, sho = 6 * h, ss = 4 - 4 * h, shs = 4 - 2 * h;
+        uint32_t mine[8], recv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            mine[k] = ((w.ql[k] >> so) & 0x0F0F0F0Fu) | (((w.qh[k] >> sho) & 0x03030303u) << 4);
+            const uint32_t send = ((w.ql[k] >> ss) & 0x0F0F0F0Fu) | (((w.qh[k] >> shs) & 0x03030303u) << 4);
+            recv[k] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send, DPP_QXOR1, 0xF, 0xF, false);
+        }
         int H = 0, Mm = 0, L = 0;
         float mn = 0.f;
 #pragma unroll
@@ -738,9 +754,8 @@ template <> struct KqFmt<QT_GQ6_K> {
             uint32_t q[4];
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                const int t = 4 * g + c;
-                const uint32_t hb = (w.qh[t & 7] >> (hs + 2 * (t >> 3))) & 0x03030303u;
-                q[c] = ((w.ql[t] >> hs) & 0x0F0F0F0Fu) | (hb << 4);
+                const int t = 4 * (g & 1) + c;   // dword within the 32-element half
+                q[c] = ((g >> 1) == h) ? mine[t] : recv[t];
             }
             int ah = 0, am = 0, al = 0;
             kq_dots<4>(q, x, 4 * g, ah, am, al);
