@@ -255,11 +255,24 @@ def dense_leg(torch, stream):
     bound_us = (wbytes + kv_bytes) / (HBM_PEAK_GBS * 1e3)
     log(f"dense Qwen3-4B decode @ctx {c.max_ctx}: {us:.0f} us/token = {1e6 / us:.0f} tok/s; "
         f"matvecs {mv_us:.0f} us ({wbytes / mv_us / 1e3:.0f} GB/s); HBM bound {bound_us:.0f} us")
+    # batched prefill of a 512-token prompt from position 0 (the host token
+    # copy keeps it out of a graph: timed as direct launches)
+    T = 512
+    toks = np.random.default_rng(5).integers(0, c.vocab, T)
+    sp = time_region(lambda: m.prefill(toks, 0, logits), 5, 2, stream, graph=False)
+    pf_ms = sp / 5 * 1e3
+    layer_params = (c.hidden * (c.n_heads + 2 * c.n_kv_heads) * c.head_dim + c.n_heads * c.head_dim * c.hidden
+                    + 3 * c.ffn * c.hidden)
+    gemm_tflops = 2.0 * layer_params * c.n_layers * T / (pf_ms * 1e-3) / 1e12
+    log(f"dense Qwen3-4B prefill T={T}: {pf_ms:.2f} ms = {T / pf_ms * 1e3:.0f} tok/s "
+        f"(layer GEMMs {gemm_tflops:.0f} TFLOP/s over the whole step; token by token it would be "
+        f"{T * us / 1e3:.0f} ms)")
     del m
     torch.cuda.empty_cache()
     return dict(us_per_token=us, tokens_per_s=1e6 / us, matvec_us=mv_us, matvec_gbs=wbytes / mv_us / 1e3,
                 other_us=us - mv_us, weight_bytes=wbytes, kv_bytes=kv_bytes, hbm_bound_us=bound_us,
-                frac_of_bound=bound_us / us)
+                frac_of_bound=bound_us / us,
+                prefill_512=dict(ms=pf_ms, tokens_per_s=T / pf_ms * 1e3, layer_gemm_tflops=gemm_tflops))
 
 
 def tb_matvec(W, qt, M, K, x, y):

@@ -1,0 +1,111 @@
+"""GPU parity of tbq_dense_prefill, the batched prefill of a dense
+Qwen3-style model (T prompt tokens per layer pass; the reference prefills
+token by token, layer4/tb_infer.c:1068-1075), through the C-ABI:
+  * batched path (Q4_K layers): the last token's logits and the K/V cache
+    rows of every prompt position within PREFILL_TOL of the float64 oracle
+    run token by token, and of libtbq's own decode steps; prompts of 1, 7,
+    130 and 300 tokens (one, two and three 128-token GEMM tiles), from an
+    empty cache and after decoded tokens, head_dim 64 and 128, GQA 2, 4, 8;
+  * the per-token path (any other model): bit-identical to T decode calls;
+  * argument checks."""
+import numpy as np
+import pytest
+
+import trailblaze_amd as tb
+from conftest import bits_equal, rel_l2
+from gpu_util import host
+from trailblaze_amd import formats as fm
+
+pytestmark = pytest.mark.gpu
+# fp16-operand MFMA GEMMs (fp32 accumulate) against float64
+PREFILL_TOL = 1e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    print("device:", tb.init(), flush=True)
+
+
+def _cfg(**kw):
+    from trailblaze_amd.dense import DenseConfig
+    base = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=512, max_ctx=512)
+    base.update(kw)
+    return DenseConfig(**base)
+
+
+def _check_prefill(oracle, cfg, seed, tokens, pre=()):
+    """Decode `pre` token by token, then prefill `tokens`; compare with the
+    oracle over pre + tokens and with libtbq's decode steps."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import SyntheticDense
+    m = SyntheticDense(cfg, seed, keep_host=True)
+    seq = SyntheticDense(cfg, seed)
+    assert m.prefill_batched()
+    ref = DenseOracle(oracle, cfg, m.host)
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    for pos, tok in enumerate(pre):
+        m.decode(tok, pos, logits)
+    print("prefill T=", len(tokens), "pos0=", len(pre), flush=True)
+    m.prefill(tokens, len(pre), logits)
+    got = host(logits)
+    want = None
+    for pos, tok in enumerate(list(pre) + list(tokens)):
+        want = ref.decode(tok, pos)
+    for pos, tok in enumerate(list(pre) + list(tokens)):
+        seq.decode(tok, pos, logits)
+    assert rel_l2(got, want) <= PREFILL_TOL
+    assert rel_l2(got, host(logits)) <= PREFILL_TOL
+    n = len(pre) + len(tokens)
+    kc = host(m.k_cache).reshape(ref.kc.shape)
+    vc = host(m.v_cache).reshape(ref.vc.shape)
+    assert rel_l2(kc[:, :, :n], ref.kc[:, :, :n]) <= PREFILL_TOL
+    assert rel_l2(vc[:, :, :n], ref.vc[:, :, :n]) <= PREFILL_TOL
+    assert not np.any(kc[:, :, n:])
+
+
+@pytest.mark.parametrize("T", [1, 7, 130])
+def test_prefill_from_empty_cache(oracle, T):
+    rng = np.random.default_rng(T)
+    _check_prefill(oracle, _cfg(), 41, rng.integers(0, 512, T))
+
+
+def test_prefill_after_decoded_tokens(oracle):
+    rng = np.random.default_rng(9)
+    _check_prefill(oracle, _cfg(), 42, rng.integers(0, 512, 40), pre=[3, 99, 511, 0, 17])
+
+
+@pytest.mark.parametrize("G", [4, 8])
+def test_prefill_head_dim_128(oracle, G):
+    rng = np.random.default_rng(G)
+    cfg = _cfg(n_layers=1, hidden=512, n_heads=8, n_kv_heads=8 // G, head_dim=128, ffn=768, vocab=256)
+    _check_prefill(oracle, cfg, 43, rng.integers(0, 256, 300))
+
+
+def test_prefill_per_token_path_bit_identical():
+    """A Q8_0 model takes the per-token path: the same logits and cache as
+    the decode step run token by token."""
+    import torch
+    from trailblaze_amd.dense import SyntheticDense
+    cfg = _cfg(qtype_layers=fm.Q8_0, qtype_embd=fm.Q8_0, max_ctx=64)
+    a, b = SyntheticDense(cfg, 44), SyntheticDense(cfg, 44)
+    assert not a.prefill_batched()
+    toks = [5, 6, 7, 500, 1]
+    la = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    lb = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    a.prefill(toks, 0, la)
+    for pos, tok in enumerate(toks):
+        b.decode(tok, pos, lb)
+    assert bits_equal(host(la), host(lb))
+    assert bits_equal(host(a.k_cache), host(b.k_cache)) and bits_equal(host(a.v_cache), host(b.v_cache))
+
+
+def test_prefill_rejects_bad_arguments():
+    import torch
+    from trailblaze_amd.dense import SyntheticDense
+    m = SyntheticDense(_cfg(max_ctx=32), 45)
+    logits = torch.empty(512, dtype=torch.float32, device="cuda")
+    for toks, pos0, what in (([], 0, "T="), ([1] * 30, 3, "positions"), ([1, 512], 0, "out of range"),
+                             ([1, -1], 0, "out of range")):
+        with pytest.raises(tb.TbqError, match=what):
+            m.prefill(toks, pos0, logits)

@@ -49,6 +49,9 @@ SYMBOLS = {
     "tbq_moe_block_host": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _i]),
     "tbq_dense_workspace_size": (_sz, [_vp]),
     "tbq_dense_decode": (_i, [_vp, _i, _i, _vp, _vp, _sz, _vp]),
+    "tbq_dense_prefill_workspace_size": (_sz, [_vp, _i]),
+    "tbq_dense_prefill": (_i, [_vp, _vp, _i, _i, _vp, _vp, _sz, _vp]),
+    "tbq_dense_prefill_batched": (_i, [_vp]),
     "tbq_expf_device": (_i, [_vp, _vp, _sz, _vp]),
     "tbq_expf_host": (_f, [_f]),
     # include/tbq_gguf.h

@@ -323,6 +323,27 @@ int tbq_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits
     return hip_ok(launch_dense_decode(m, token, pos, logits, workspace, S(s)), "dense decode launch");
 }
 
+size_t tbq_dense_prefill_workspace_size(const tbq_dense_model *m, int T) {
+    if (!check_dense(m) || T <= 0 || T > 65536) return 0;
+    return dense_prefill_workspace_bytes(m, T);
+}
+
+int tbq_dense_prefill_batched(const tbq_dense_model *m) { return check_dense(m) && dense_prefill_batched(m) ? 1 : 0; }
+
+int tbq_dense_prefill(const tbq_dense_model *m, const int *tokens_host, int T, int pos0, float *logits,
+                      void *workspace, size_t ws_bytes, void *s) {
+    if (!ensure_init()) return 0;
+    if (!check_dense(m)) return 0;
+    if (T <= 0 || T > 65536) return fail("tbq_dense_prefill: T=%d outside 1..65536", T);
+    if (pos0 < 0 || pos0 > m->max_ctx - T) return fail("tbq_dense_prefill: positions %d..%d outside the cache", pos0, pos0 + T - 1);
+    if (!tokens_host || !logits || !workspace) return fail("tbq_dense_prefill: null tokens, logits or workspace");
+    for (int t = 0; t < T; t++)
+        if (tokens_host[t] < 0 || tokens_host[t] >= m->vocab)
+            return fail("tbq_dense_prefill: token %d at %d out of range", tokens_host[t], t);
+    if (ws_bytes < dense_prefill_workspace_bytes(m, T)) return fail("tbq_dense_prefill: workspace too small");
+    return hip_ok(launch_dense_prefill(m, tokens_host, T, pos0, logits, workspace, S(s)), "dense prefill launch");
+}
+
 int tbq_expf_device(const float *in, float *out, size_t n, void *s) {
     if (!ensure_init()) return 0;
     if (!in || !out) return fail("tbq_expf_device: null pointer");

@@ -469,4 +469,16 @@ hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, flo
     return hipGetLastError();
 }
 
+// logits = Wlm rmsnorm(x + y) * output_norm for one residual row x and the
+// last sublayer's output y (the prefill's last token); ws is a decode
+// workspace.
+hipError_t dense_final_logits(const tbq_dense_model *m, const float *x, const float *y, float *logits, void *ws,
+                              hipStream_t st) {
+    const DenseWs w = dense_ws(m, ws, nullptr);
+    const MvPro po{y, m->output_norm, nullptr, m->norm_eps};
+    const hipError_t err =
+        dense_mv(canon_qt(m->qtype_embd), m->lm_head, m->vocab, m->hidden, x, logits, PRO_NORM, po, w.h, nullptr, st);
+    return err != hipSuccess ? err : hipGetLastError();
+}
+
 }  // namespace tbq

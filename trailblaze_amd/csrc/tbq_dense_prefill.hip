@@ -1,0 +1,380 @@
+// tbq_dense_prefill.hip -- batched prefill of a dense Qwen3-style model on
+// gfx950: the T prompt tokens at positions pos0 .. pos0 + T - 1 go through
+// each layer together, where the reference prefills token by token
+// (layer4/tb_infer.c:1068-1075: one tb_infer_decode step per prompt token).
+//
+// Per layer (x: fp32 residual rows [T][H]; h16: fp16 rows with per-row
+// power-of-two scales, the MFMA GEMMs' operand format):
+//   k_pf_norm        x += y (the previous sublayer's output), h16 =
+//                    rmsnorm(x) * attn_norm
+//   GEMM (mode 1)    qkv = h16 Wqkv^T                  Q4_K, fp16 MFMA
+//   k_pf_qk          per (token, head): QK-norm + RoPE of q (to qb) and k;
+//                    k and v rows written to the cache at pos0 + t
+//   k_pf_attn        causal GQA attention over cache positions 0 .. pos,
+//                    online softmax over 16-position chunks staged in LDS
+//   rows to fp16, GEMM (mode 1)   y = att Wo^T
+//   k_pf_norm        x += y, h16 = rmsnorm(x) * ffn_norm
+//   GEMM (mode 0)    act = silu(h16 Wg^T) * (h16 Wu^T)
+//   rows to fp16, GEMM (mode 1)   y = act Wdown^T
+// then the last token's logits = Wlm rmsnorm(x + y) (the decode step's
+// lm_head matvec with its norm prologue).  The GEMMs are the MoE prefill's
+// MFMA kernel with one expert whose tiles are runs of 128 tokens.
+//
+// Accuracy: fp16 GEMM operands (11-bit mantissa) with fp32 accumulation,
+// fp32 norms, RoPE and attention; the logits land within 1e-2 relative L2
+// of the float64 sequential decode.
+#include "tbq_kernels.h"
+#include "tbq_device.hpp"
+#include "../../include/tbq.h"
+
+namespace tbq {
+
+constexpr int PN_THREADS = 256;
+constexpr int PA_THREADS = 256;
+constexpr int PA_KC = 16;     // cache positions per attention chunk
+
+__device__ __forceinline__ float pf_block_sum(float v, float *red) {
+    v = group_sum<64>(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = 0.f;
+#pragma unroll
+    for (int i = 0; i < PN_THREADS / 64; i++) r += red[i];
+    return r;
+}
+
+__device__ __forceinline__ float pf_block_max(float v, float *red) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = 0.f;
+#pragma unroll
+    for (int i = 0; i < PN_THREADS / 64; i++) r = fmaxf(r, red[i]);
+    return r;
+}
+
+// Row t: v = x[t] + y[t] (y may be null; x[t] = v is stored back when y is
+// not), h = v * rsqrt(mean(v^2) + eps) * w, then h16[t] = h * 2^s in fp16
+// with s putting max |h| in [2^14, 2^15) and hinv[t] = 2^-s.  grid = T.
+// Three passes over the row (the later two re-read x from cache).
+__global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, const float *__restrict__ y,
+                                                        const float *__restrict__ w, int H, float eps,
+                                                        _Float16 *__restrict__ h16, float *__restrict__ hinv) {
+    __shared__ float red[PN_THREADS / 64];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    float *xr = x + (long long)t * H;
+    const float *yr = y ? y + (long long)t * H : nullptr;
+    float ss = 0.f;
+    for (int j = tid; j < H; j += PN_THREADS) {
+        const float a = yr ? xr[j] + yr[j] : xr[j];
+        if (yr) xr[j] = a;
+        ss += a * a;
+    }
+    ss = pf_block_sum(ss, red);   // its barriers also order the stores above before the re-reads
+    const float r = 1.0f / sqrtf(ss / (float)H + eps);
+    float mx = 0.f;
+    for (int j = tid; j < H; j += PN_THREADS) mx = fmaxf(mx, fabsf(xr[j] * r * w[j]));
+    mx = pf_block_max(mx, red);
+    int e = 0;
+    frexpf(mx, &e);
+    int sh = mx > 0.f ? 15 - e : 0;
+    sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
+    const float s = ldexpf(1.f, sh);
+    _Float16 *hr = h16 + (long long)t * H;
+    for (int j = tid; j < H; j += PN_THREADS) hr[j] = (_Float16)(xr[j] * r * w[j] * s);
+    if (tid == 0) hinv[t] = ldexpf(1.f, -sh);
+}
+
+// Head vector (one wave; lane l holds elements l and l + 64, or l for
+// D = 64): RMSNorm with the head's weights, then rotate-half RoPE at
+// position pos, the angle formed as the decode step's table forms it.
+template <int D>
+__device__ __forceinline__ void pf_norm_rope(float (&x)[D / 64], const float *__restrict__ w, int pos, float theta,
+                                             float eps) {
+    const int lane = threadIdx.x & 63;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < D / 64; i++) ss += x[i] * x[i];
+    ss = group_sum<64>(ss);
+    const float r = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+    for (int i = 0; i < D / 64; i++) x[i] = x[i] * r * w[lane + 64 * i];
+    const int j = lane % (D / 2);
+    double sd, cd;
+    sincos((double)pos * pow((double)theta, -2.0 * j / D), &sd, &cd);
+    const float cs = (float)cd, sn = (float)sd;
+    if constexpr (D == 128) {
+        const float a = x[0], b = x[1];
+        x[0] = a * cs - b * sn;
+        x[1] = a * sn + b * cs;
+    } else {
+        const float other = __shfl_xor(x[0], 32);
+        x[0] = lane < 32 ? x[0] * cs - other * sn : other * sn + x[0] * cs;
+    }
+}
+
+// grid = (T, NQ + NKV), one wave.  Head hh < NQ: q head hh of token t,
+// normed, rotated and scaled by 1/sqrt(D) into qb[t][hh]; else k head
+// hh - NQ, normed and rotated, and the matching v head, written to the
+// layer's cache rows pos0 + t.
+template <int D>
+__global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, const float *__restrict__ qn,
+                                              const float *__restrict__ kn, int NQ, int NKV, int pos0, float theta,
+                                              float eps, float *__restrict__ kc, float *__restrict__ vc, int max_ctx,
+                                              float *__restrict__ qb) {
+    const int t = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
+    const int QKVR = (NQ + 2 * NKV) * D, pos = pos0 + t;
+    const float *src = qkv + (long long)t * QKVR + hh * D;
+    float x[D / 64];
+#pragma unroll
+    for (int i = 0; i < D / 64; i++) x[i] = src[lane + 64 * i];
+    pf_norm_rope<D>(x, hh < NQ ? qn : kn, pos, theta, eps);
+    if (hh < NQ) {
+        const float scale = 1.0f / sqrtf((float)D);
+#pragma unroll
+        for (int i = 0; i < D / 64; i++) qb[((long long)t * NQ + hh) * D + lane + 64 * i] = x[i] * scale;
+    } else {
+        const int kvh = hh - NQ;
+        const long long row = ((long long)kvh * max_ctx + pos) * D;
+        const float *vsrc = qkv + (long long)t * QKVR + (NQ + NKV + kvh) * D;
+#pragma unroll
+        for (int i = 0; i < D / 64; i++) {
+            kc[row + lane + 64 * i] = x[i];
+            vc[row + lane + 64 * i] = vsrc[lane + 64 * i];
+        }
+    }
+}
+
+// Causal attention.  grid = (NKV, ceil(T / QB)), 256 threads: the
+// workgroup owns QB = 64 / G tokens x the G query heads of kv head kvh = 64
+// query rows, 4 threads per row, each with a quarter of the head dimension
+// (q and the running output in registers).  Cache positions 0 .. the
+// block's last position are staged in LDS PA_KC at a time; per chunk a row
+// forms its scores (quarter dots summed over the thread quad by DPP),
+// masks positions past its own, and updates its running max, denominator
+// and output (online softmax).  Position 0 is in every row's range, so
+// the running max is finite after the first chunk.
+template <int D, int G>
+__global__ __launch_bounds__(PA_THREADS) void k_pf_attn(const float *__restrict__ qb, const float *__restrict__ kc,
+                                                        const float *__restrict__ vc, int T, int pos0, int NQ,
+                                                        int max_ctx, float *__restrict__ out) {
+    constexpr int QB = 64 / G, DQ = D / 4;
+    __shared__ __attribute__((aligned(16))) float Ks[PA_KC][D];
+    __shared__ __attribute__((aligned(16))) float Vs[PA_KC][D];
+    const int kvh = blockIdx.x, tid = threadIdx.x, r = tid >> 2, qq = tid & 3;
+    const int g = r % G, t = blockIdx.y * QB + r / G;
+    const bool valid = t < T;
+    const int tt = valid ? t : T - 1;
+    const int qpos = pos0 + tt;
+    const int tend = min(T, (int)(blockIdx.y + 1) * QB);
+    const int kend = pos0 + tend;   // positions 0 .. kend - 1
+    float q[DQ], o[DQ];
+    const float *qsrc = qb + ((long long)tt * NQ + kvh * G + g) * D + qq * DQ;
+#pragma unroll
+    for (int i = 0; i < DQ; i++) {
+        q[i] = qsrc[i];
+        o[i] = 0.f;
+    }
+    float m = -__builtin_huge_valf(), l = 0.f;
+    const float *kb = kc + (long long)kvh * max_ctx * D;
+    const float *vb = vc + (long long)kvh * max_ctx * D;
+    for (int c0 = 0; c0 < kend; c0 += PA_KC) {
+        __syncthreads();   // the previous chunk is no longer read
+        for (int f = tid; f < PA_KC * D / 4; f += PA_THREADS) {
+            const int row = f / (D / 4), c4 = f % (D / 4);
+            const int p = min(c0 + row, kend - 1);
+            *reinterpret_cast<float4 *>(&Ks[row][4 * c4]) = *reinterpret_cast<const float4 *>(kb + (long long)p * D + 4 * c4);
+            *reinterpret_cast<float4 *>(&Vs[row][4 * c4]) = *reinterpret_cast<const float4 *>(vb + (long long)p * D + 4 * c4);
+        }
+        __syncthreads();
+        float s[PA_KC];
+        float cm = -__builtin_huge_valf();
+#pragma unroll
+        for (int j = 0; j < PA_KC; j++) {
+            const float4 *kr = reinterpret_cast<const float4 *>(&Ks[j][qq * DQ]);
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < DQ / 4; i++) {
+                const float4 k4 = kr[i];
+                a = fmaf(q[4 * i], k4.x, a);
+                a = fmaf(q[4 * i + 1], k4.y, a);
+                a = fmaf(q[4 * i + 2], k4.z, a);
+                a = fmaf(q[4 * i + 3], k4.w, a);
+            }
+            a += dpp_f32<DPP_QXOR1>(a);
+            a += dpp_f32<DPP_QXOR2>(a);
+            s[j] = c0 + j <= qpos ? a : -__builtin_huge_valf();
+            cm = fmaxf(cm, s[j]);
+        }
+        const float mn = fmaxf(m, cm);
+        const float corr = expf(m - mn);   // 0 on the first chunk (m = -inf)
+        l *= corr;
+#pragma unroll
+        for (int i = 0; i < DQ; i++) o[i] *= corr;
+#pragma unroll
+        for (int j = 0; j < PA_KC; j++) {
+            const float p = expf(s[j] - mn);   // 0 where masked
+            l += p;
+            const float4 *vr = reinterpret_cast<const float4 *>(&Vs[j][qq * DQ]);
+#pragma unroll
+            for (int i = 0; i < DQ / 4; i++) {
+                const float4 v4 = vr[i];
+                o[4 * i] = fmaf(p, v4.x, o[4 * i]);
+                o[4 * i + 1] = fmaf(p, v4.y, o[4 * i + 1]);
+                o[4 * i + 2] = fmaf(p, v4.z, o[4 * i + 2]);
+                o[4 * i + 3] = fmaf(p, v4.w, o[4 * i + 3]);
+            }
+        }
+        m = mn;
+    }
+    if (valid) {
+        const float inv = 1.0f / l;
+        float *dst = out + ((long long)t * NQ + kvh * G + g) * D + qq * DQ;
+#pragma unroll
+        for (int i = 0; i < DQ; i++) dst[i] = o[i] * inv;
+    }
+}
+
+template <int D>
+static hipError_t launch_pf_attn(int G, const float *qb, const float *kc, const float *vc, int T, int pos0, int NQ,
+                                 int NKV, int max_ctx, float *out, hipStream_t st) {
+#define TBQ_PFA(GG)                                                                                                   \
+    case GG:                                                                                                          \
+        hipLaunchKernelGGL((k_pf_attn<D, GG>), dim3(NKV, (T + 64 / GG - 1) / (64 / GG)), dim3(PA_THREADS), 0, st, qb, \
+                           kc, vc, T, pos0, NQ, max_ctx, out);                                                        \
+        return hipGetLastError();
+    switch (G) {
+        TBQ_PFA(1) TBQ_PFA(2) TBQ_PFA(4) TBQ_PFA(8)
+    default:
+        return hipErrorNotSupported;
+    }
+#undef TBQ_PFA
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+static size_t pf_up(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// The batched path covers models whose layers have fused q|k|v and gate|up
+// matrices, all in the reference's Q4_K layout, with row lengths the MFMA
+// kernel is built for and H <= 8192.
+bool dense_prefill_batched(const tbq_dense_model *m) {
+    const int H = m->hidden, QD = m->n_heads * m->head_dim, F = m->ffn;
+    const int QKVR = (m->n_heads + 2 * m->n_kv_heads) * m->head_dim;
+    if (H > 8192 || !gemm_k_supported(H) || !gemm_k_supported(QD) || !gemm_k_supported(F) ||
+        QKVR % 256 || H % 256 || F % 128)
+        return false;
+    auto q4k = [m](int q) { return canon_qt(q ? q : m->qtype_layers) == QT_Q4_K; };
+    for (int l = 0; l < m->n_layers; l++) {
+        const tbq_dense_layer &L = m->layers[l];
+        if (!L.wqkv || !L.wgu || !q4k(L.qt_qkv) || !q4k(L.qt_o) || !q4k(L.qt_gu) || !q4k(L.qt_down)) return false;
+    }
+    return true;
+}
+
+struct PfWs {
+    float *x, *y, *qkv, *qb, *att, *act, *hinv;
+    _Float16 *h16;
+    int *tok;
+    void *gemm, *dec;
+};
+
+static PfWs pf_ws(const tbq_dense_model *m, int T, void *ws, size_t *total) {
+    const size_t H = m->hidden, QD = (size_t)m->n_heads * m->head_dim, F = m->ffn;
+    const size_t QKVR = (size_t)(m->n_heads + 2 * m->n_kv_heads) * m->head_dim;
+    size_t wide = H > QD ? H : QD;
+    wide = wide > F ? wide : F;
+    char *p = (char *)ws;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        void *r = p + off;
+        off += pf_up(bytes);
+        return r;
+    };
+    PfWs w;
+    w.dec = take(dense_workspace_bytes(m));
+    w.tok = (int *)take((size_t)T * 4);
+    if (dense_prefill_batched(m)) {
+        w.x = (float *)take((size_t)T * H * 4);
+        w.y = (float *)take((size_t)T * H * 4);
+        w.qkv = (float *)take((size_t)T * QKVR * 4);
+        w.qb = (float *)take((size_t)T * QD * 4);
+        w.att = (float *)take((size_t)T * QD * 4);
+        w.act = (float *)take((size_t)T * F * 4);
+        w.h16 = (_Float16 *)take((size_t)T * wide * 2);
+        w.hinv = (float *)take((size_t)T * 4);
+        w.gemm = take(dense_gemm_scratch_bytes(T));
+    }
+    if (total) *total = off;
+    return w;
+}
+
+size_t dense_prefill_workspace_bytes(const tbq_dense_model *m, int T) {
+    size_t t = 0;
+    pf_ws(m, T, nullptr, &t);
+    return t;
+}
+
+// tokens: T device ints (in range); the batched path only.
+static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int pos0, float *logits,
+                             hipStream_t st) {
+    const int H = m->hidden, D = m->head_dim, NQ = m->n_heads, NKV = m->n_kv_heads, G = NQ / NKV, F = m->ffn;
+    const int QD = NQ * D, QKVR = (NQ + 2 * NKV) * D;
+    const long long rbh = (long long)(H / 256) * 144;   // Q4_K row bytes at K = H
+    DenseGemmPlan plan;
+    hipError_t err = dense_gemm_plan(T, w.gemm, &plan, st);
+    if (err == hipSuccess) err = launch_dequant_rows(canon_qt(m->qtype_embd), m->tok_embd, w.tok, T, H, w.x, st);
+    for (int l = 0; l < m->n_layers && err == hipSuccess; l++) {
+        const tbq_dense_layer &L = m->layers[l];
+        const size_t kvoff = (size_t)l * NKV * m->max_ctx * D;
+        float *kc = m->k_cache + kvoff, *vc = m->v_cache + kvoff;
+        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, l ? w.y : nullptr, L.attn_norm, H,
+                           m->norm_eps, w.h16, w.hinv);
+        if ((err = launch_dense_gemm(1, plan, L.wqkv, nullptr, w.h16, T, w.hinv, QKVR, H, w.qkv, st)) != hipSuccess) break;
+        if (D == 128) {
+            hipLaunchKernelGGL(k_pf_qk<128>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, L.q_norm, L.k_norm, NQ, NKV,
+                               pos0, m->rope_theta, m->norm_eps, kc, vc, m->max_ctx, w.qb);
+            err = launch_pf_attn<128>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.att, st);
+        } else {
+            hipLaunchKernelGGL(k_pf_qk<64>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, L.q_norm, L.k_norm, NQ, NKV,
+                               pos0, m->rope_theta, m->norm_eps, kc, vc, m->max_ctx, w.qb);
+            err = launch_pf_attn<64>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.att, st);
+        }
+        if (err != hipSuccess) break;
+        if ((err = launch_rows_f16(w.att, T, QD, w.h16, w.hinv, st)) != hipSuccess) break;
+        if ((err = launch_dense_gemm(1, plan, L.wo, nullptr, w.h16, T, w.hinv, H, QD, w.y, st)) != hipSuccess) break;
+        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, w.y, L.ffn_norm, H, m->norm_eps, w.h16,
+                           w.hinv);
+        const uint8_t *wg = (const uint8_t *)L.wgu;
+        if ((err = launch_dense_gemm(0, plan, wg, wg + (long long)F * rbh, w.h16, T, w.hinv, F, H, w.act, st)) !=
+            hipSuccess)
+            break;
+        if ((err = launch_rows_f16(w.act, T, F, w.h16, w.hinv, st)) != hipSuccess) break;
+        err = launch_dense_gemm(1, plan, L.wdown, nullptr, w.h16, T, w.hinv, H, F, w.y, st);
+    }
+    if (err != hipSuccess) return err;
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return dense_final_logits(m, w.x + (size_t)(T - 1) * H, w.y + (size_t)(T - 1) * H, logits, w.dec, st);
+}
+
+hipError_t launch_dense_prefill(const tbq_dense_model *m, const int *tokens_host, int T, int pos0, float *logits,
+                                void *ws, hipStream_t st) {
+    const PfWs w = pf_ws(m, T, ws, nullptr);
+    if (!dense_prefill_batched(m)) {
+        // every other model: the decode step once per token, in order
+        for (int t = 0; t < T; t++) {
+            const hipError_t err = launch_dense_decode(m, tokens_host[t], pos0 + t, logits, w.dec, st);
+            if (err != hipSuccess) return err;
+        }
+        return hipSuccess;
+    }
+    const hipError_t err = hipMemcpyAsync(w.tok, tokens_host, (size_t)T * 4, hipMemcpyHostToDevice, st);
+    if (err != hipSuccess) return err;
+    return pf_batched(m, w, T, pos0, logits, st);
+}
+
+}  // namespace tbq

@@ -40,6 +40,7 @@ struct MoeArgs {
 };
 
 hipError_t launch_dequant(int qt, const void *W, long long nweights, float *out, hipStream_t s);
+hipError_t launch_dequant_rows(int qt, const void *W, const int *idx, int nrows, int K, float *out, hipStream_t s);
 hipError_t launch_matvec_generic(int qt, const void *W, int M, int K, const float *x, float *y,
                                  hipStream_t s, int n_cu);
 // The Q4_K kernels read the reference's layout, or ggml's (QT_GQ4_K) when ggml.
@@ -63,6 +64,21 @@ hipError_t launch_router(const float *xn, const float *router, const float *bias
 // a.qtype QT_Q4_K or QT_GQ4_K
 hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st);
 size_t prefill_workspace_bytes(int T, int k, int E, int H, int F);
+// Dense GEMMs on the prefill MFMA kernel (Q4_K weights, fp16 activations
+// with per-row power-of-two scales): a tile plan over T rows, then
+// out[T][M] = X W^T (mode 1) or silu(X Wg^T) * (X Wu^T) (mode 0).
+struct DenseGemmPlan {
+    void *tiles;
+    int *ntiles, *tpair, *ttok;
+    int nt;
+};
+bool gemm_k_supported(int K);
+size_t dense_gemm_scratch_bytes(int T);
+hipError_t dense_gemm_plan(int T, void *scratch, DenseGemmPlan *p, hipStream_t st);
+hipError_t launch_dense_gemm(int mode, const DenseGemmPlan &p, const void *W0, const void *W1, const _Float16 *X,
+                             int T, const float *xinv, int M, int K, float *out, hipStream_t st);
+// rows of n floats to fp16 with per-row power-of-two scales (inv = 1 / scale)
+hipError_t launch_rows_f16(const float *in, int rows, int n, _Float16 *out, float *inv, hipStream_t st);
 hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t st, bool x16_done = false);
 // Where the prefill scratch keeps the tokens' fp16 rows and their inverse
 // scales (so the router can write them).
@@ -71,5 +87,14 @@ hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st);
 size_t dense_workspace_bytes(const tbq_dense_model *m);
 hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,
                                hipStream_t st);
+hipError_t dense_final_logits(const tbq_dense_model *m, const float *x, const float *y, float *logits, void *ws,
+                              hipStream_t st);
+// Batched prefill (tbq_dense_prefill.hip): whether the model takes the
+// batched path, its workspace, and the T-token prefill (the decode step per
+// token where the batched path does not apply).
+bool dense_prefill_batched(const tbq_dense_model *m);
+size_t dense_prefill_workspace_bytes(const tbq_dense_model *m, int T);
+hipError_t launch_dense_prefill(const tbq_dense_model *m, const int *tokens_host, int T, int pos0, float *logits,
+                                void *ws, hipStream_t st);
 
 }  // namespace tbq

@@ -69,6 +69,42 @@ __global__ __launch_bounds__(256) void k_matvec_generic(const uint8_t *__restric
     }
 }
 
+// Rows idx[0..nrows) of a matrix (row stride rb bytes, K weights) to
+// out[nrows][K], bit-exact as k_dequant.  grid = (ceil(K / 2048), nrows).
+template <int QT>
+__global__ __launch_bounds__(256) void k_dequant_rows(const uint8_t *__restrict__ W, long long rb,
+                                                      const int *__restrict__ idx, int K, float *__restrict__ out) {
+    constexpr int BW = block_weights(QT), BB = block_bytes(QT);
+    const uint8_t *row = W + (long long)idx[blockIdx.y] * rb;
+    float *o = out + (long long)blockIdx.y * K;
+    for (int t = blockIdx.x * 256 + threadIdx.x; t < K / 8; t += gridDim.x * 256) {
+        const int e = t * 8;
+        float w[8];
+        if constexpr (BW == 1) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint8_t *p = row + (long long)(e + i) * BB;
+                w[i] = QT == QT_F32 ? __builtin_bit_cast(float, ldu32(p))
+                     : QT == QT_F16 ? f16_ref(ldu16(p)) : QT == QT_GF16 ? f16_ieee(ldu16(p))
+                     : bf16_ref(ldu16(p));
+            }
+        } else {
+            decode8<QT>(row + (long long)(e / BW) * BB, e % BW, w);
+        }
+        float4 *q = reinterpret_cast<float4 *>(o + e);
+        q[0] = make_float4(w[0], w[1], w[2], w[3]);
+        q[1] = make_float4(w[4], w[5], w[6], w[7]);
+    }
+}
+
+template <int QT>
+static hipError_t launch_dequant_rows_t(const void *W, const int *idx, int nrows, int K, float *out, hipStream_t s) {
+    const long long rb = (long long)(K / block_weights(QT)) * block_bytes(QT);
+    hipLaunchKernelGGL((k_dequant_rows<QT>), dim3((K / 8 + 255) / 256, nrows), dim3(256), 0, s, (const uint8_t *)W, rb,
+                       idx, K, out);
+    return hipGetLastError();
+}
+
 template <int QT>
 static hipError_t launch_dequant_t(const void *W, long long nweights, float *out, hipStream_t s) {
     long long n8 = nweights / 8;
@@ -129,6 +165,32 @@ hipError_t launch_dequant(int qt, const void *W, long long nweights, float *out,
     case QT_GQ4_K: return launch_dequant_t<QT_GQ4_K>(W, nweights, out, s);
     case QT_GQ5_K: return launch_dequant_t<QT_GQ5_K>(W, nweights, out, s);
     case QT_GQ6_K: return launch_dequant_t<QT_GQ6_K>(W, nweights, out, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// Rows idx[i] (device ints, in range) of a [*][K] matrix in format qt.
+hipError_t launch_dequant_rows(int qt, const void *W, const int *idx, int nrows, int K, float *out, hipStream_t s) {
+    switch (qt) {
+    case QT_F32: return launch_dequant_rows_t<QT_F32>(W, idx, nrows, K, out, s);
+    case QT_F16: return launch_dequant_rows_t<QT_F16>(W, idx, nrows, K, out, s);
+    case QT_BF16: return launch_dequant_rows_t<QT_BF16>(W, idx, nrows, K, out, s);
+    case QT_Q4_0: return launch_dequant_rows_t<QT_Q4_0>(W, idx, nrows, K, out, s);
+    case QT_Q8_0: return launch_dequant_rows_t<QT_Q8_0>(W, idx, nrows, K, out, s);
+    case QT_Q2_K: return launch_dequant_rows_t<QT_Q2_K>(W, idx, nrows, K, out, s);
+    case QT_Q3_K: return launch_dequant_rows_t<QT_Q3_K>(W, idx, nrows, K, out, s);
+    case QT_Q4_K: return launch_dequant_rows_t<QT_Q4_K>(W, idx, nrows, K, out, s);
+    case QT_Q5_K: return launch_dequant_rows_t<QT_Q5_K>(W, idx, nrows, K, out, s);
+    case QT_Q6_K: return launch_dequant_rows_t<QT_Q6_K>(W, idx, nrows, K, out, s);
+    case QT_Q8_K: return launch_dequant_rows_t<QT_Q8_K>(W, idx, nrows, K, out, s);
+    case QT_GF16: return launch_dequant_rows_t<QT_GF16>(W, idx, nrows, K, out, s);
+    case QT_GQ4_0: return launch_dequant_rows_t<QT_GQ4_0>(W, idx, nrows, K, out, s);
+    case QT_GQ8_0: return launch_dequant_rows_t<QT_GQ8_0>(W, idx, nrows, K, out, s);
+    case QT_GQ2_K: return launch_dequant_rows_t<QT_GQ2_K>(W, idx, nrows, K, out, s);
+    case QT_GQ3_K: return launch_dequant_rows_t<QT_GQ3_K>(W, idx, nrows, K, out, s);
+    case QT_GQ4_K: return launch_dequant_rows_t<QT_GQ4_K>(W, idx, nrows, K, out, s);
+    case QT_GQ5_K: return launch_dequant_rows_t<QT_GQ5_K>(W, idx, nrows, K, out, s);
+    case QT_GQ6_K: return launch_dequant_rows_t<QT_GQ6_K>(W, idx, nrows, K, out, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -106,6 +106,25 @@ class SyntheticDense:
                                       self.workspace.numel(), _stream(stream)), "tbq_dense_decode")
         return logits
 
+    def prefill(self, tokens, pos0: int, logits, stream=None):
+        """tbq_dense_prefill of `tokens` at positions pos0.. : the last
+        token's logits into `logits`, K/V of every position appended."""
+        import torch
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        n = int(lib().tbq_dense_prefill_workspace_size(C.byref(self.model), len(toks)))
+        ws = getattr(self, "_pf_ws", None)
+        if n > 0 and (ws is None or ws.numel() < n):
+            ws = self._pf_ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+        self._pf_tokens = toks   # read by an asynchronous copy on the stream
+        # (n == 0: bad arguments, which the call itself reports)
+        _check(lib().tbq_dense_prefill(C.byref(self.model), toks.ctypes.data, len(toks), pos0, _ptr(logits),
+                                       _ptr(ws), 0 if ws is None else ws.numel(), _stream(stream)),
+               "tbq_dense_prefill")
+        return logits
+
+    def prefill_batched(self) -> bool:
+        return bool(lib().tbq_dense_prefill_batched(C.byref(self.model)))
+
     def matvec_shapes(self):
         """(qtype, M, K, weight tensor) of every matvec one decode step runs."""
         c = self.cfg
