@@ -12,6 +12,7 @@
 //                    k and v rows written to the cache at pos0 + t
 //   k_pf_attn        causal GQA attention over cache positions 0 .. pos,
 //                    online softmax over 16-position chunks staged in LDS
+//                    (the next chunk prefetched into registers)
 //   rows to fp16, GEMM (mode 1)   y = att Wo^T
 //   k_pf_norm        x += y, h16 = rmsnorm(x) * ffn_norm
 //   GEMM (mode 0)    act = silu(h16 Wg^T) * (h16 Wu^T)
@@ -31,7 +32,8 @@ namespace tbq {
 
 constexpr int PN_THREADS = 256;
 constexpr int PA_THREADS = 256;
-constexpr int PA_KC = 16;     // cache positions per attention chunk
+constexpr int PA_KC = 8;      // cache positions per attention step
+constexpr int PA_KF = 32;     // cache positions per LDS fill (PA_KF / PA_KC steps)
 
 __device__ __forceinline__ float pf_block_sum(float v, float *red) {
     v = group_sum<64>(v);
@@ -58,32 +60,65 @@ __device__ __forceinline__ float pf_block_max(float v, float *red) {
 // Row t: v = x[t] + y[t] (y may be null; x[t] = v is stored back when y is
 // not), h = v * rsqrt(mean(v^2) + eps) * w, then h16[t] = h * 2^s in fp16
 // with s putting max |h| in [2^14, 2^15) and hinv[t] = 2^-s.  grid = T.
-// Three passes over the row (the later two re-read x from cache).
+// A thread holds up to PN_V float4 of the row (H <= 8192), all loaded
+// before any is used.
+constexpr int PN_V = 8;
 __global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, const float *__restrict__ y,
                                                         const float *__restrict__ w, int H, float eps,
                                                         _Float16 *__restrict__ h16, float *__restrict__ hinv) {
     __shared__ float red[PN_THREADS / 64];
-    const int t = blockIdx.x, tid = threadIdx.x;
-    float *xr = x + (long long)t * H;
-    const float *yr = y ? y + (long long)t * H : nullptr;
-    float ss = 0.f;
-    for (int j = tid; j < H; j += PN_THREADS) {
-        const float a = yr ? xr[j] + yr[j] : xr[j];
-        if (yr) xr[j] = a;
-        ss += a * a;
+    const int t = blockIdx.x, tid = threadIdx.x, n4 = H / 4;
+    float4 *xr = reinterpret_cast<float4 *>(x + (long long)t * H);
+    const float4 *yr = reinterpret_cast<const float4 *>(y ? y + (long long)t * H : x + (long long)t * H);
+    const float4 *wr = reinterpret_cast<const float4 *>(w);
+    float4 v[PN_V], b[PN_V], g[PN_V];
+#pragma unroll
+    for (int i = 0; i < PN_V; i++) {
+        const int j = min(tid + PN_THREADS * i, n4 - 1);   // clamped: loads stay unconditional
+        v[i] = xr[j];
+        b[i] = yr[j];
+        g[i] = wr[j];
     }
-    ss = pf_block_sum(ss, red);   // its barriers also order the stores above before the re-reads
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < PN_V; i++) {
+        if (y) {
+            v[i].x += b[i].x; v[i].y += b[i].y; v[i].z += b[i].z; v[i].w += b[i].w;
+        }
+        if (tid + PN_THREADS * i < n4) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    }
+    if (y) {
+#pragma unroll
+        for (int i = 0; i < PN_V; i++)
+            if (tid + PN_THREADS * i < n4) xr[tid + PN_THREADS * i] = v[i];
+    }
+    ss = pf_block_sum(ss, red);
     const float r = 1.0f / sqrtf(ss / (float)H + eps);
     float mx = 0.f;
-    for (int j = tid; j < H; j += PN_THREADS) mx = fmaxf(mx, fabsf(xr[j] * r * w[j]));
+#pragma unroll
+    for (int i = 0; i < PN_V; i++) {
+        v[i].x = v[i].x * r * g[i].x; v[i].y = v[i].y * r * g[i].y;
+        v[i].z = v[i].z * r * g[i].z; v[i].w = v[i].w * r * g[i].w;
+        if (tid + PN_THREADS * i < n4)
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
     mx = pf_block_max(mx, red);
     int e = 0;
     frexpf(mx, &e);
     int sh = mx > 0.f ? 15 - e : 0;
     sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
     const float s = ldexpf(1.f, sh);
-    _Float16 *hr = h16 + (long long)t * H;
-    for (int j = tid; j < H; j += PN_THREADS) hr[j] = (_Float16)(xr[j] * r * w[j] * s);
+    uint2 *hr = reinterpret_cast<uint2 *>(h16 + (long long)t * H);
+#pragma unroll
+    for (int i = 0; i < PN_V; i++) {
+        const int j = tid + PN_THREADS * i;
+        if (j < n4) {
+            const _Float16 a0 = (_Float16)(v[i].x * s), a1 = (_Float16)(v[i].y * s);
+            const _Float16 a2 = (_Float16)(v[i].z * s), a3 = (_Float16)(v[i].w * s);
+            hr[j] = make_uint2((uint32_t)__builtin_bit_cast(uint16_t, a0) | ((uint32_t)__builtin_bit_cast(uint16_t, a1) << 16),
+                               (uint32_t)__builtin_bit_cast(uint16_t, a2) | ((uint32_t)__builtin_bit_cast(uint16_t, a3) << 16));
+        }
+    }
     if (tid == 0) hinv[t] = ldexpf(1.f, -sh);
 }
 
@@ -149,91 +184,148 @@ __global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, con
 
 // Causal attention.  grid = (NKV, ceil(T / QB)), 256 threads: the
 // workgroup owns QB = 64 / G tokens x the G query heads of kv head kvh = 64
-// query rows, 4 threads per row, each with a quarter of the head dimension
-// (q and the running output in registers).  Cache positions 0 .. the
-// block's last position are staged in LDS PA_KC at a time; per chunk a row
-// forms its scores (quarter dots summed over the thread quad by DPP),
-// masks positions past its own, and updates its running max, denominator
-// and output (online softmax).  Position 0 is in every row's range, so
-// the running max is finite after the first chunk.
+// query rows.  PA_TPR = 16 lanes share PA_R = 4 rows, each lane holding a
+// sixteenth of the head dimension of all four (dims 4qq + 4 PA_TPR i + c,
+// so a row group's lanes read one contiguous LDS run), so every K and V
+// value read from LDS serves four rows.  Cache positions 0 .. the block's
+// last position pass through LDS PA_KF at a time, the next fill's rows
+// loaded into registers while the current one is used; per PA_KC step each row
+// forms its scores (partial dots summed over the 16 lanes), masks
+// positions past its own, and updates its running max, denominator and
+// output (online softmax).  Position 0 is in every row's range, so the
+// running maxima are finite after the first chunk.
+constexpr int PA_TPR = 16, PA_R = 4;
+constexpr int PA_ROWS = PA_THREADS / PA_TPR * PA_R;
+
 template <int D, int G>
 __global__ __launch_bounds__(PA_THREADS) void k_pf_attn(const float *__restrict__ qb, const float *__restrict__ kc,
                                                         const float *__restrict__ vc, int T, int pos0, int NQ,
                                                         int max_ctx, float *__restrict__ out) {
-    constexpr int QB = 64 / G, DQ = D / 4;
-    __shared__ __attribute__((aligned(16))) float Ks[PA_KC][D];
-    __shared__ __attribute__((aligned(16))) float Vs[PA_KC][D];
-    const int kvh = blockIdx.x, tid = threadIdx.x, r = tid >> 2, qq = tid & 3;
-    const int g = r % G, t = blockIdx.y * QB + r / G;
-    const bool valid = t < T;
-    const int tt = valid ? t : T - 1;
-    const int qpos = pos0 + tt;
+    constexpr int QB = PA_ROWS / G, DQ = D / PA_TPR, NI = DQ / 4;
+    constexpr int NF = PA_KF * D / 4;                  // float4 of K (and of V) per fill
+    constexpr int NL = (NF + PA_THREADS - 1) / PA_THREADS;
+    static_assert(NI >= 1, "shape");
+    __shared__ __attribute__((aligned(16))) float Ks[PA_KF][D];
+    __shared__ __attribute__((aligned(16))) float Vs[PA_KF][D];
+    const int kvh = blockIdx.x, tid = threadIdx.x, rg = tid / PA_TPR, qq = tid % PA_TPR;
     const int tend = min(T, (int)(blockIdx.y + 1) * QB);
     const int kend = pos0 + tend;   // positions 0 .. kend - 1
-    float q[DQ], o[DQ];
-    const float *qsrc = qb + ((long long)tt * NQ + kvh * G + g) * D + qq * DQ;
-#pragma unroll
-    for (int i = 0; i < DQ; i++) {
-        q[i] = qsrc[i];
-        o[i] = 0.f;
-    }
-    float m = -__builtin_huge_valf(), l = 0.f;
     const float *kb = kc + (long long)kvh * max_ctx * D;
     const float *vb = vc + (long long)kvh * max_ctx * D;
-    for (int c0 = 0; c0 < kend; c0 += PA_KC) {
-        __syncthreads();   // the previous chunk is no longer read
-        for (int f = tid; f < PA_KC * D / 4; f += PA_THREADS) {
-            const int row = f / (D / 4), c4 = f % (D / 4);
-            const int p = min(c0 + row, kend - 1);
-            *reinterpret_cast<float4 *>(&Ks[row][4 * c4]) = *reinterpret_cast<const float4 *>(kb + (long long)p * D + 4 * c4);
-            *reinterpret_cast<float4 *>(&Vs[row][4 * c4]) = *reinterpret_cast<const float4 *>(vb + (long long)p * D + 4 * c4);
+    // native vectors: arrays of HIP's float4 struct carried across loop
+    // iterations are kept in scratch memory
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4 kn[NL], vn[NL];
+    auto fetch = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const int f = tid + PA_THREADS * i, row = f / (D / 4), c4 = f % (D / 4);
+            const long long p = min(c0 + row, kend - 1);
+            kn[i] = *reinterpret_cast<const f32x4 *>(kb + p * D + 4 * c4);
+            vn[i] = *reinterpret_cast<const f32x4 *>(vb + p * D + 4 * c4);
+        }
+    };
+    fetch(0);
+    int qpos[PA_R];
+    float q[PA_R][DQ], o[PA_R][DQ], m[PA_R], l[PA_R];
+#pragma unroll
+    for (int k = 0; k < PA_R; k++) {
+        const int rr = rg * PA_R + k, g = rr % G, t = min((int)blockIdx.y * QB + rr / G, T - 1);
+        qpos[k] = pos0 + t;
+        const float *qsrc = qb + ((long long)t * NQ + kvh * G + g) * D + 4 * qq;
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                q[k][4 * i + c] = qsrc[4 * PA_TPR * i + c];
+                o[k][4 * i + c] = 0.f;
+            }
+        m[k] = -__builtin_huge_valf();
+        l[k] = 0.f;
+    }
+    for (int f0 = 0; f0 < kend; f0 += PA_KF) {
+        __syncthreads();   // the previous fill is no longer read
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const int f = tid + PA_THREADS * i, row = f / (D / 4), c4 = f % (D / 4);
+            if (NF % PA_THREADS == 0 || f < NF) {
+                *reinterpret_cast<f32x4 *>(&Ks[row][4 * c4]) = kn[i];
+                *reinterpret_cast<f32x4 *>(&Vs[row][4 * c4]) = vn[i];
+            }
         }
         __syncthreads();
-        float s[PA_KC];
-        float cm = -__builtin_huge_valf();
+        fetch(f0 + PA_KF < kend ? f0 + PA_KF : f0);   // the next fill (the last one again at the end)
 #pragma unroll
-        for (int j = 0; j < PA_KC; j++) {
-            const float4 *kr = reinterpret_cast<const float4 *>(&Ks[j][qq * DQ]);
-            float a = 0.f;
+        for (int sub = 0; sub < PA_KF / PA_KC; sub++) {
+        const int c0 = f0 + sub * PA_KC;
+        if (c0 >= kend) break;   // uniform
+        float s[PA_R][PA_KC];
 #pragma unroll
-            for (int i = 0; i < DQ / 4; i++) {
-                const float4 k4 = kr[i];
-                a = fmaf(q[4 * i], k4.x, a);
-                a = fmaf(q[4 * i + 1], k4.y, a);
-                a = fmaf(q[4 * i + 2], k4.z, a);
-                a = fmaf(q[4 * i + 3], k4.w, a);
-            }
-            a += dpp_f32<DPP_QXOR1>(a);
-            a += dpp_f32<DPP_QXOR2>(a);
-            s[j] = c0 + j <= qpos ? a : -__builtin_huge_valf();
-            cm = fmaxf(cm, s[j]);
-        }
-        const float mn = fmaxf(m, cm);
-        const float corr = expf(m - mn);   // 0 on the first chunk (m = -inf)
-        l *= corr;
+        for (int k = 0; k < PA_R; k++)
 #pragma unroll
-        for (int i = 0; i < DQ; i++) o[i] *= corr;
+            for (int j = 0; j < PA_KC; j++) s[k][j] = 0.f;
 #pragma unroll
-        for (int j = 0; j < PA_KC; j++) {
-            const float p = expf(s[j] - mn);   // 0 where masked
-            l += p;
-            const float4 *vr = reinterpret_cast<const float4 *>(&Vs[j][qq * DQ]);
+        for (int i = 0; i < NI; i++) {
 #pragma unroll
-            for (int i = 0; i < DQ / 4; i++) {
-                const float4 v4 = vr[i];
-                o[4 * i] = fmaf(p, v4.x, o[4 * i]);
-                o[4 * i + 1] = fmaf(p, v4.y, o[4 * i + 1]);
-                o[4 * i + 2] = fmaf(p, v4.z, o[4 * i + 2]);
-                o[4 * i + 3] = fmaf(p, v4.w, o[4 * i + 3]);
+            for (int j = 0; j < PA_KC; j++) {
+                const float4 k4 = *reinterpret_cast<const float4 *>(&Ks[sub * PA_KC + j][4 * qq + 4 * PA_TPR * i]);
+#pragma unroll
+                for (int k = 0; k < PA_R; k++) {
+                    s[k][j] = fmaf(q[k][4 * i], k4.x, s[k][j]);
+                    s[k][j] = fmaf(q[k][4 * i + 1], k4.y, s[k][j]);
+                    s[k][j] = fmaf(q[k][4 * i + 2], k4.z, s[k][j]);
+                    s[k][j] = fmaf(q[k][4 * i + 3], k4.w, s[k][j]);
+                }
             }
         }
-        m = mn;
+#pragma unroll
+        for (int k = 0; k < PA_R; k++) {
+            float cm = -__builtin_huge_valf();
+#pragma unroll
+            for (int j = 0; j < PA_KC; j++) {
+                const float a = group_sum<PA_TPR>(s[k][j]);
+                s[k][j] = c0 + j <= qpos[k] ? a : -__builtin_huge_valf();
+                cm = fmaxf(cm, s[k][j]);
+            }
+            const float mn = fmaxf(m[k], cm);
+            const float corr = __expf(m[k] - mn);   // 0 on the first chunk (m = -inf)
+            l[k] *= corr;
+#pragma unroll
+            for (int i = 0; i < DQ; i++) o[k][i] *= corr;
+#pragma unroll
+            for (int j = 0; j < PA_KC; j++) {
+                s[k][j] = __expf(s[k][j] - mn);   // 0 where masked
+                l[k] += s[k][j];
+            }
+            m[k] = mn;
+        }
+#pragma unroll
+        for (int j = 0; j < PA_KC; j++) {
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const float4 v4 = *reinterpret_cast<const float4 *>(&Vs[sub * PA_KC + j][4 * qq + 4 * PA_TPR * i]);
+#pragma unroll
+                for (int k = 0; k < PA_R; k++) {
+                    o[k][4 * i] = fmaf(s[k][j], v4.x, o[k][4 * i]);
+                    o[k][4 * i + 1] = fmaf(s[k][j], v4.y, o[k][4 * i + 1]);
+                    o[k][4 * i + 2] = fmaf(s[k][j], v4.z, o[k][4 * i + 2]);
+                    o[k][4 * i + 3] = fmaf(s[k][j], v4.w, o[k][4 * i + 3]);
+                }
+            }
+        }
+        }
     }
-    if (valid) {
-        const float inv = 1.0f / l;
-        float *dst = out + ((long long)t * NQ + kvh * G + g) * D + qq * DQ;
 #pragma unroll
-        for (int i = 0; i < DQ; i++) dst[i] = o[i] * inv;
+    for (int k = 0; k < PA_R; k++) {
+        const int rr = rg * PA_R + k, g = rr % G, t = blockIdx.y * QB + rr / G;
+        if (t < T) {
+            const float inv = 1.0f / l[k];
+            float *dst = out + ((long long)t * NQ + kvh * G + g) * D + 4 * qq;
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+                *reinterpret_cast<float4 *>(dst + 4 * PA_TPR * i) =
+                    make_float4(o[k][4 * i] * inv, o[k][4 * i + 1] * inv, o[k][4 * i + 2] * inv, o[k][4 * i + 3] * inv);
+        }
     }
 }
 
@@ -242,7 +334,7 @@ static hipError_t launch_pf_attn(int G, const float *qb, const float *kc, const 
                                  int NKV, int max_ctx, float *out, hipStream_t st) {
 #define TBQ_PFA(GG)                                                                                                   \
     case GG:                                                                                                          \
-        hipLaunchKernelGGL((k_pf_attn<D, GG>), dim3(NKV, (T + 64 / GG - 1) / (64 / GG)), dim3(PA_THREADS), 0, st, qb, \
+        hipLaunchKernelGGL((k_pf_attn<D, GG>), dim3(NKV, (T + PA_ROWS / GG - 1) / (PA_ROWS / GG)), dim3(PA_THREADS), 0, st, qb, \
                            kc, vc, T, pos0, NQ, max_ctx, out);                                                        \
         return hipGetLastError();
     switch (G) {
