@@ -82,6 +82,38 @@ def test_prefill_head_dim_128(oracle, G):
     _check_prefill(oracle, cfg, 43, rng.integers(0, 256, 300))
 
 
+@pytest.mark.parametrize("G", [1, 2])
+def test_prefill_long_context_many_splits(oracle, G):
+    """A 100-token prompt after 1100 cached positions (N(0,1) K/V in the
+    cache and in the oracle): the attention runs over 8 position splits of
+    more than 128 positions each, then merges them."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import SyntheticDense
+    cfg = _cfg(n_layers=1, n_heads=4, n_kv_heads=4 // G, max_ctx=1536, vocab=256)
+    m = SyntheticDense(cfg, 46, keep_host=True)
+    ref = DenseOracle(oracle, cfg, m.host)
+    rng = np.random.default_rng(12)
+    P = 1100
+    kc = np.zeros(ref.kc.shape, np.float32)
+    vc = np.zeros(ref.vc.shape, np.float32)
+    kc[:, :, :P] = rng.standard_normal(kc[:, :, :P].shape)
+    vc[:, :, :P] = rng.standard_normal(vc[:, :, :P].shape)
+    m.k_cache.copy_(torch.from_numpy(kc))
+    m.v_cache.copy_(torch.from_numpy(vc))
+    ref.kc[:] = kc
+    ref.vc[:] = vc
+    toks = rng.integers(0, 256, 100)
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    print("prefill long context G=", G, flush=True)
+    m.prefill(toks, P, logits)
+    for i, tok in enumerate(toks):
+        want = ref.decode(tok, P + i)
+    assert rel_l2(host(logits), want) <= PREFILL_TOL
+    kcg = host(m.k_cache).reshape(ref.kc.shape)
+    assert rel_l2(kcg[:, :, P:P + 100], ref.kc[:, :, P:P + 100]) <= PREFILL_TOL
+
+
 def test_prefill_per_token_path_bit_identical():
     """A Q8_0 model takes the per-token path: the same logits and cache as
     the decode step run token by token."""

@@ -197,10 +197,18 @@ __global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, con
 constexpr int PA_TPR = 16, PA_R = 4;
 constexpr int PA_ROWS = PA_THREADS / PA_TPR * PA_R;
 
+//
+// Key splits: grid.z = nsplit workgroups per block, split z taking cache
+// positions [z ks, (z + 1) ks) (ks a multiple of PA_KF), so the heavy
+// blocks of a causal prompt (whose rows see every earlier position) are
+// spread over several workgroups.  With nsplit > 1 each writes its rows'
+// unnormalised output, running max and denominator to part[(row * nsplit
+// + z) * (D + 2)], and k_pf_attn_combine merges the splits a row reaches.
 template <int D, int G>
 __global__ __launch_bounds__(PA_THREADS) void k_pf_attn(const float *__restrict__ qb, const float *__restrict__ kc,
                                                         const float *__restrict__ vc, int T, int pos0, int NQ,
-                                                        int max_ctx, float *__restrict__ out) {
+                                                        int max_ctx, int ks, int nsplit, float *__restrict__ part,
+                                                        float *__restrict__ out) {
     constexpr int QB = PA_ROWS / G, DQ = D / PA_TPR, NI = DQ / 4;
     constexpr int NF = PA_KF * D / 4;                  // float4 of K (and of V) per fill
     constexpr int NL = (NF + PA_THREADS - 1) / PA_THREADS;
@@ -209,7 +217,9 @@ __global__ __launch_bounds__(PA_THREADS) void k_pf_attn(const float *__restrict_
     __shared__ __attribute__((aligned(16))) float Vs[PA_KF][D];
     const int kvh = blockIdx.x, tid = threadIdx.x, rg = tid / PA_TPR, qq = tid % PA_TPR;
     const int tend = min(T, (int)(blockIdx.y + 1) * QB);
-    const int kend = pos0 + tend;   // positions 0 .. kend - 1
+    const int k0 = blockIdx.z * ks;                  // this split's positions k0 .. kend - 1
+    const int kend = min(pos0 + tend, k0 + ks);
+    if (k0 >= kend) return;   // no position of the split is seen by the block (uniform)
     const float *kb = kc + (long long)kvh * max_ctx * D;
     const float *vb = vc + (long long)kvh * max_ctx * D;
     // native vectors: arrays of HIP's float4 struct carried across loop
@@ -225,7 +235,7 @@ __global__ __launch_bounds__(PA_THREADS) void k_pf_attn(const float *__restrict_
             vn[i] = *reinterpret_cast<const f32x4 *>(vb + p * D + 4 * c4);
         }
     };
-    fetch(0);
+    fetch(k0);
     int qpos[PA_R];
     float q[PA_R][DQ], o[PA_R][DQ], m[PA_R], l[PA_R];
 #pragma unroll
@@ -243,7 +253,7 @@ __global__ __launch_bounds__(PA_THREADS) void k_pf_attn(const float *__restrict_
         m[k] = -__builtin_huge_valf();
         l[k] = 0.f;
     }
-    for (int f0 = 0; f0 < kend; f0 += PA_KF) {
+    for (int f0 = k0; f0 < kend; f0 += PA_KF) {
         __syncthreads();   // the previous fill is no longer read
 #pragma unroll
         for (int i = 0; i < NL; i++) {
@@ -287,14 +297,15 @@ __global__ __launch_bounds__(PA_THREADS) void k_pf_attn(const float *__restrict_
                 s[k][j] = c0 + j <= qpos[k] ? a : -__builtin_huge_valf();
                 cm = fmaxf(cm, s[k][j]);
             }
+            // a row that has seen no position yet keeps m = -inf, l = 0, o = 0
             const float mn = fmaxf(m[k], cm);
-            const float corr = __expf(m[k] - mn);   // 0 on the first chunk (m = -inf)
+            const float corr = m[k] == -__builtin_huge_valf() ? 0.f : __expf(m[k] - mn);
             l[k] *= corr;
 #pragma unroll
             for (int i = 0; i < DQ; i++) o[k][i] *= corr;
 #pragma unroll
             for (int j = 0; j < PA_KC; j++) {
-                s[k][j] = __expf(s[k][j] - mn);   // 0 where masked
+                s[k][j] = s[k][j] == -__builtin_huge_valf() ? 0.f : __expf(s[k][j] - mn);   // 0 where masked
                 l[k] += s[k][j];
             }
             m[k] = mn;
@@ -318,31 +329,76 @@ __global__ __launch_bounds__(PA_THREADS) void k_pf_attn(const float *__restrict_
 #pragma unroll
     for (int k = 0; k < PA_R; k++) {
         const int rr = rg * PA_R + k, g = rr % G, t = blockIdx.y * QB + rr / G;
-        if (t < T) {
+        if (t >= T) continue;
+        const long long row = (long long)t * NQ + kvh * G + g;
+        if (nsplit == 1) {
             const float inv = 1.0f / l[k];
-            float *dst = out + ((long long)t * NQ + kvh * G + g) * D + 4 * qq;
+            float *dst = out + row * D + 4 * qq;
 #pragma unroll
             for (int i = 0; i < NI; i++)
                 *reinterpret_cast<float4 *>(dst + 4 * PA_TPR * i) =
                     make_float4(o[k][4 * i] * inv, o[k][4 * i + 1] * inv, o[k][4 * i + 2] * inv, o[k][4 * i + 3] * inv);
+        } else {
+            float *dst = part + (row * nsplit + blockIdx.z) * (D + 2);
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+                *reinterpret_cast<float4 *>(dst + 4 * qq + 4 * PA_TPR * i) =
+                    make_float4(o[k][4 * i], o[k][4 * i + 1], o[k][4 * i + 2], o[k][4 * i + 3]);
+            if (qq == 0) {
+                dst[D] = m[k];
+                dst[D + 1] = l[k];
+            }
         }
     }
 }
 
+// out[row] = sum_z e^(m_z - M) o_z / sum_z e^(m_z - M) l_z over the splits
+// z <= qpos / ks that row (t, h) reaches.  grid = T * NQ, D threads.
+template <int D>
+__global__ __launch_bounds__(D) void k_pf_attn_combine(const float *__restrict__ part, int NQ, int pos0, int ks,
+                                                       int nsplit, float *__restrict__ out) {
+    const long long row = blockIdx.x;
+    const int t = (int)(row / NQ), d = threadIdx.x;
+    const int nz = (pos0 + t) / ks + 1;
+    const float *p = part + row * nsplit * (D + 2);
+    float M = -__builtin_huge_valf();
+    for (int z = 0; z < nz; z++) M = fmaxf(M, p[z * (D + 2) + D]);
+    float num = 0.f, den = 0.f;
+    for (int z = 0; z < nz; z++) {
+        const float f = __expf(p[z * (D + 2) + D] - M);
+        num = fmaf(f, p[z * (D + 2) + d], num);
+        den = fmaf(f, p[z * (D + 2) + D + 1], den);
+    }
+    out[row * D + d] = num / den;
+}
+
+// Split size: PA_PREF_KS positions, larger for long contexts so that at
+// most PA_MAX_SPLIT splits exist (a multiple of PA_KF either way).
+constexpr int PA_PREF_KS = 128, PA_MAX_SPLIT = 8;
+static int pf_split_size(int kmax) {
+    int ks = PA_PREF_KS;
+    if ((kmax + ks - 1) / ks > PA_MAX_SPLIT) ks = ((kmax + PA_MAX_SPLIT - 1) / PA_MAX_SPLIT + PA_KF - 1) / PA_KF * PA_KF;
+    return ks;
+}
+
 template <int D>
 static hipError_t launch_pf_attn(int G, const float *qb, const float *kc, const float *vc, int T, int pos0, int NQ,
-                                 int NKV, int max_ctx, float *out, hipStream_t st) {
-#define TBQ_PFA(GG)                                                                                                   \
-    case GG:                                                                                                          \
-        hipLaunchKernelGGL((k_pf_attn<D, GG>), dim3(NKV, (T + PA_ROWS / GG - 1) / (PA_ROWS / GG)), dim3(PA_THREADS), 0, st, qb, \
-                           kc, vc, T, pos0, NQ, max_ctx, out);                                                        \
-        return hipGetLastError();
+                                 int NKV, int max_ctx, float *part, float *out, hipStream_t st) {
+    const int ks = pf_split_size(pos0 + T), nsplit = (pos0 + T + ks - 1) / ks;
+#define TBQ_PFA(GG)                                                                                                \
+    case GG:                                                                                                       \
+        hipLaunchKernelGGL((k_pf_attn<D, GG>), dim3(NKV, (T + PA_ROWS / GG - 1) / (PA_ROWS / GG), nsplit),         \
+                           dim3(PA_THREADS), 0, st, qb, kc, vc, T, pos0, NQ, max_ctx, ks, nsplit, part, out);      \
+        break;
     switch (G) {
         TBQ_PFA(1) TBQ_PFA(2) TBQ_PFA(4) TBQ_PFA(8)
     default:
         return hipErrorNotSupported;
     }
 #undef TBQ_PFA
+    if (nsplit > 1)
+        hipLaunchKernelGGL(k_pf_attn_combine<D>, dim3(T * NQ), dim3(D), 0, st, part, NQ, pos0, ks, nsplit, out);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -368,7 +424,7 @@ bool dense_prefill_batched(const tbq_dense_model *m) {
 }
 
 struct PfWs {
-    float *x, *y, *qkv, *qb, *att, *act, *hinv;
+    float *x, *y, *qkv, *qb, *att, *act, *hinv, *part;
     _Float16 *h16;
     int *tok;
     void *gemm, *dec;
@@ -399,6 +455,10 @@ static PfWs pf_ws(const tbq_dense_model *m, int T, void *ws, size_t *total) {
         w.h16 = (_Float16 *)take((size_t)T * wide * 2);
         w.hinv = (float *)take((size_t)T * 4);
         w.gemm = take(dense_gemm_scratch_bytes(T));
+        // attention split partials: a prefill reaching position kmax - 1 uses
+        // min(PA_MAX_SPLIT, ceil(kmax / PA_PREF_KS)) splits, and kmax <= max_ctx
+        const int ns = min(PA_MAX_SPLIT, (m->max_ctx + PA_PREF_KS - 1) / PA_PREF_KS);
+        w.part = ns > 1 ? (float *)take((size_t)T * m->n_heads * ns * (m->head_dim + 2) * 4) : nullptr;
     }
     if (total) *total = off;
     return w;
@@ -429,11 +489,11 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
         if (D == 128) {
             hipLaunchKernelGGL(k_pf_qk<128>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, L.q_norm, L.k_norm, NQ, NKV,
                                pos0, m->rope_theta, m->norm_eps, kc, vc, m->max_ctx, w.qb);
-            err = launch_pf_attn<128>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.att, st);
+            err = launch_pf_attn<128>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, st);
         } else {
             hipLaunchKernelGGL(k_pf_qk<64>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, L.q_norm, L.k_norm, NQ, NKV,
                                pos0, m->rope_theta, m->norm_eps, kc, vc, m->max_ctx, w.qb);
-            err = launch_pf_attn<64>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.att, st);
+            err = launch_pf_attn<64>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, st);
         }
         if (err != hipSuccess) break;
         if ((err = launch_rows_f16(w.att, T, QD, w.h16, w.hinv, st)) != hipSuccess) break;
