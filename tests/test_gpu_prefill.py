@@ -1,13 +1,16 @@
 """GPU parity of tbq_dense_prefill, the batched prefill of a dense
 Qwen3-style model (T prompt tokens per layer pass; the reference prefills
 token by token, layer4/tb_infer.c:1068-1075), through the C-ABI:
-  * batched path (Q4_K layers): the last token's logits and the K/V cache
+  * batched path (any format or layout; fused or separate matrices): the
+    last token's logits and the K/V cache
     rows of every prompt position within PREFILL_TOL of the float64 oracle
     run token by token, and of libtbq's own decode steps; prompts of 1, 7,
     130 and 300 tokens (one, two and three 128-token GEMM tiles), from an
     empty cache and after decoded tokens, head_dim 64 and 128, GQA 2, 4, 8;
-  * the per-token path (any other model): bit-identical to T decode calls;
+  * a one-token prefill is the decode step itself (bit-identical);
   * argument checks."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -114,20 +117,66 @@ def test_prefill_long_context_many_splits(oracle, G):
     assert rel_l2(kcg[:, :, P:P + 100], ref.kc[:, :, P:P + 100]) <= PREFILL_TOL
 
 
-def test_prefill_per_token_path_bit_identical():
-    """A Q8_0 model takes the per-token path: the same logits and cache as
-    the decode step run token by token."""
+@pytest.mark.parametrize("ql,qe", [(fm.Q8_0, fm.Q6_K), (fm.Q5_K, fm.Q8_0), (fm.GGML | fm.Q4_K, fm.GGML | fm.Q6_K),
+                                   (fm.GGML | fm.Q3_K, fm.Q4_K)])
+def test_prefill_other_formats(oracle, ql, qe):
+    """Layer matrices of every format and either layout take the batched
+    path (each matrix dequantised to fp16 before its GEMM)."""
+    rng = np.random.default_rng(ql)
+    _check_prefill(oracle, _cfg(qtype_layers=ql, qtype_embd=qe, vocab=256), 47, rng.integers(0, 256, 70))
+
+
+def test_prefill_separate_matrices(oracle):
+    """A mixed-quant layer (separate q, k, v and gate, up matrices of
+    different formats, as a GGUF file assembles them) on the batched path."""
+    import torch
+    from gguf_write import dense_gguf_tensors, write_gguf
+    from oracle.dense import DenseOracle
+    from trailblaze_amd import synth
+    from trailblaze_amd.gguf import GgufFile
+    cfg = _cfg(n_layers=1, vocab=256, max_ctx=128)
+    r = np.random.default_rng(48)
+    norm = lambda n: (1.0 + 0.1 * r.standard_normal(n)).astype(np.float32)
+    mat = lambda qt, M, K: synth.kquant_matrix(qt, M, K, r)
+    l0 = {"attn_norm": norm(256), "q_norm": norm(64), "k_norm": norm(64), "ffn_norm": norm(256),
+          "wq": mat(fm.Q4_K, 256, 256), "wk": mat(fm.Q4_K, 128, 256), "wv": mat(fm.Q6_K, 128, 256),
+          "qt_wq": fm.Q4_K, "qt_wk": fm.Q4_K, "qt_wv": fm.Q6_K, "wo": mat(fm.Q5_K, 256, 256), "qt_wo": fm.Q5_K,
+          "wgate": mat(fm.Q4_K, 512, 256), "wup": mat(fm.Q8_0, 512, 256), "qt_wgate": fm.Q4_K, "qt_wup": fm.Q8_0,
+          "wdown": mat(fm.Q6_K, 256, 512), "qt_wdown": fm.Q6_K}
+    hostd = {"layers": [l0], "lm_head": mat(fm.Q6_K, 256, 256), "output_norm": norm(256)}
+    kv, ts = dense_gguf_tensors(cfg, hostd)
+    import tempfile, os
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "mixed.gguf")
+        write_gguf(path, kv, ts)
+        ref = DenseOracle(oracle, cfg, hostd)
+        with GgufFile(path) as g:
+            m, ws = g.dense_model(cfg.max_ctx)
+            assert not m.layers[0].wqkv and not m.layers[0].wgu
+            toks = np.ascontiguousarray(r.integers(0, 256, 50), dtype=np.int32)
+            n = int(tb.lib().tbq_dense_prefill_workspace_size(C.byref(m), len(toks)))
+            pw = torch.empty(n, dtype=torch.uint8, device="cuda")
+            logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+            print("prefill separate matrices", flush=True)
+            assert tb.lib().tbq_dense_prefill(C.byref(m), toks.ctypes.data, len(toks), 0, C.c_void_p(logits.data_ptr()),
+                                              C.c_void_p(pw.data_ptr()), n, None)
+            for pos, tok in enumerate(toks):
+                want = ref.decode(tok, pos)
+            assert rel_l2(host(logits), want) <= PREFILL_TOL
+
+
+def test_prefill_one_token_is_the_decode_step():
+    """T = 1 runs the decode step itself: the same logits and cache bits."""
     import torch
     from trailblaze_amd.dense import SyntheticDense
-    cfg = _cfg(qtype_layers=fm.Q8_0, qtype_embd=fm.Q8_0, max_ctx=64)
+    cfg = _cfg(max_ctx=64)
     a, b = SyntheticDense(cfg, 44), SyntheticDense(cfg, 44)
-    assert not a.prefill_batched()
-    toks = [5, 6, 7, 500, 1]
     la = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
     lb = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
-    a.prefill(toks, 0, la)
-    for pos, tok in enumerate(toks):
-        b.decode(tok, pos, lb)
+    a.decode(7, 0, la)
+    b.decode(7, 0, lb)
+    a.prefill([500], 1, la)
+    b.decode(500, 1, lb)
     assert bits_equal(host(la), host(lb))
     assert bits_equal(host(a.k_cache), host(b.k_cache)) and bits_equal(host(a.v_cache), host(b.v_cache))
 

@@ -53,7 +53,10 @@ def build(verbose: bool = False) -> str:
                 sys.stderr.write(r.stdout + r.stderr)
     objs = [j[j.index("-o") + 1] for j in jobs]
     tmp = LIB + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-lpthread"])
+    # rocBLAS: the prefill's plain fp16 GEMMs (the process's already-loaded
+    # librocblas.so.5, torch's, is reused when one is present)
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-L/opt/rocm/lib", "-lrocblas",
+          "-lpthread"])
     os.replace(tmp, LIB)
     return LIB
 

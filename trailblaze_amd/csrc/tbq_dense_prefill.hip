@@ -4,26 +4,33 @@
 // (layer4/tb_infer.c:1068-1075: one tb_infer_decode step per prompt token).
 //
 // Per layer (x: fp32 residual rows [T][H]; h16: fp16 rows with per-row
-// power-of-two scales, the MFMA GEMMs' operand format):
-//   k_pf_norm        x += y (the previous sublayer's output), h16 =
-//                    rmsnorm(x) * attn_norm
-//   GEMM (mode 1)    qkv = h16 Wqkv^T                  Q4_K, fp16 MFMA
+// power-of-two scales, the GEMMs' activation operand; each weight matrix
+// is dequantised to fp16 (k_dequant_f16, any format or layout) just before
+// its GEMM, into one reused buffer):
+//   k_pf_norm        x += y (the previous sublayer's output, unscaled by
+//                    its row scales), h16 = rmsnorm(x) * attn_norm
+//   GEMM             qkv = h16 Wqkv^T             rocBLAS fp16, fp32 acc
 //   k_pf_qk          per (token, head): QK-norm + RoPE of q (to qb) and k;
 //                    k and v rows written to the cache at pos0 + t
 //   k_pf_attn        causal GQA attention over cache positions 0 .. pos,
-//                    online softmax over 16-position chunks staged in LDS
-//                    (the next chunk prefetched into registers)
-//   rows to fp16, GEMM (mode 1)   y = att Wo^T
+//                    online softmax, key ranges split over workgroups
+//                    (k_pf_attn_combine merges them)
+//   rows to fp16, GEMM            y = att Wo^T
 //   k_pf_norm        x += y, h16 = rmsnorm(x) * ffn_norm
-//   GEMM (mode 0)    act = silu(h16 Wg^T) * (h16 Wu^T)
-//   rows to fp16, GEMM (mode 1)   y = act Wdown^T
+//   GEMM             gu = h16 [Wg | Wu]^T
+//   k_pf_swiglu_f16  a16 = silu(g) * u (fp16, row scales)
+//   GEMM             y = a16 Wdown^T
 // then the last token's logits = Wlm rmsnorm(x + y) (the decode step's
-// lm_head matvec with its norm prologue).  The GEMMs are the MoE prefill's
-// MFMA kernel with one expert whose tiles are runs of 128 tokens.
+// lm_head matvec with its norm prologue).
 //
-// Accuracy: fp16 GEMM operands (11-bit mantissa) with fp32 accumulation,
-// fp32 norms, RoPE and attention; the logits land within 1e-2 relative L2
-// of the float64 sequential decode.
+// Accuracy: fp16 weights and activations (11-bit mantissa) with fp32
+// accumulation, fp32 norms, RoPE and attention; the logits land within
+// 1e-2 relative L2 of the float64 sequential decode.
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <mutex>
+
 #include "tbq_kernels.h"
 #include "tbq_device.hpp"
 #include "../../include/tbq.h"
@@ -57,15 +64,17 @@ __device__ __forceinline__ float pf_block_max(float v, float *red) {
     return r;
 }
 
-// Row t: v = x[t] + y[t] (y may be null; x[t] = v is stored back when y is
-// not), h = v * rsqrt(mean(v^2) + eps) * w, then h16[t] = h * 2^s in fp16
+// Row t: v = x[t] + y[t] * ys[t] (y may be null; x[t] = v is stored back
+// when y is not; ys, the row scales of a GEMM's fp16 operand, may be null
+// for 1), h = v * rsqrt(mean(v^2) + eps) * w, then h16[t] = h * 2^s in fp16
 // with s putting max |h| in [2^14, 2^15) and hinv[t] = 2^-s.  grid = T.
 // A thread holds up to PN_V float4 of the row (H <= 8192), all loaded
 // before any is used.
 constexpr int PN_V = 8;
 __global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, const float *__restrict__ y,
-                                                        const float *__restrict__ w, int H, float eps,
-                                                        _Float16 *__restrict__ h16, float *__restrict__ hinv) {
+                                                        const float *__restrict__ ys, const float *__restrict__ w,
+                                                        int H, float eps, _Float16 *__restrict__ h16,
+                                                        float *__restrict__ hinv) {
     __shared__ float red[PN_THREADS / 64];
     const int t = blockIdx.x, tid = threadIdx.x, n4 = H / 4;
     float4 *xr = reinterpret_cast<float4 *>(x + (long long)t * H);
@@ -80,10 +89,12 @@ __global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, c
         g[i] = wr[j];
     }
     float ss = 0.f;
+    const float yscale = ys ? ys[t] : 1.f;
 #pragma unroll
     for (int i = 0; i < PN_V; i++) {
         if (y) {
-            v[i].x += b[i].x; v[i].y += b[i].y; v[i].z += b[i].z; v[i].w += b[i].w;
+            v[i].x += b[i].x * yscale; v[i].y += b[i].y * yscale;
+            v[i].z += b[i].z * yscale; v[i].w += b[i].w * yscale;
         }
         if (tid + PN_THREADS * i < n4) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
     }
@@ -150,21 +161,23 @@ __device__ __forceinline__ void pf_norm_rope(float (&x)[D / 64], const float *__
     }
 }
 
-// grid = (T, NQ + NKV), one wave.  Head hh < NQ: q head hh of token t,
+// grid = (T, NQ + NKV), one wave; qkv row t times rs[t] is the true row.
+// Head hh < NQ: q head hh of token t,
 // normed, rotated and scaled by 1/sqrt(D) into qb[t][hh]; else k head
 // hh - NQ, normed and rotated, and the matching v head, written to the
 // layer's cache rows pos0 + t.
 template <int D>
-__global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, const float *__restrict__ qn,
-                                              const float *__restrict__ kn, int NQ, int NKV, int pos0, float theta,
-                                              float eps, float *__restrict__ kc, float *__restrict__ vc, int max_ctx,
-                                              float *__restrict__ qb) {
+__global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, const float *__restrict__ rs,
+                                              const float *__restrict__ qn, const float *__restrict__ kn, int NQ,
+                                              int NKV, int pos0, float theta, float eps, float *__restrict__ kc,
+                                              float *__restrict__ vc, int max_ctx, float *__restrict__ qb) {
     const int t = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
     const int QKVR = (NQ + 2 * NKV) * D, pos = pos0 + t;
+    const float sc = rs[t];   // row t of qkv is scaled by 1 / rs[t]
     const float *src = qkv + (long long)t * QKVR + hh * D;
     float x[D / 64];
 #pragma unroll
-    for (int i = 0; i < D / 64; i++) x[i] = src[lane + 64 * i];
+    for (int i = 0; i < D / 64; i++) x[i] = src[lane + 64 * i] * sc;
     pf_norm_rope<D>(x, hh < NQ ? qn : kn, pos, theta, eps);
     if (hh < NQ) {
         const float scale = 1.0f / sqrtf((float)D);
@@ -177,9 +190,38 @@ __global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, con
 #pragma unroll
         for (int i = 0; i < D / 64; i++) {
             kc[row + lane + 64 * i] = x[i];
-            vc[row + lane + 64 * i] = vsrc[lane + 64 * i];
+            vc[row + lane + 64 * i] = vsrc[lane + 64 * i] * sc;
         }
     }
+}
+
+// Row t: a = silu(g * s) * (u * s) with gu[t] = [g (F) | u (F)] and s =
+// gs[t], then a16[t] = a * 2^e in fp16 (max |a| in [2^14, 2^15)) and
+// ainv[t] = 2^-e.  grid = T, two passes over the row.
+__global__ __launch_bounds__(PN_THREADS) void k_pf_swiglu_f16(const float *__restrict__ gu, const float *__restrict__ gs,
+                                                              int F, _Float16 *__restrict__ a16,
+                                                              float *__restrict__ ainv) {
+    __shared__ float red[PN_THREADS / 64];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float *g = gu + (long long)t * 2 * F, *u = g + F;
+    const float s = gs[t];
+    float mx = 0.f;
+    for (int j = tid; j < F; j += PN_THREADS) mx = fmaxf(mx, fabsf(pro_swiglu(g[j] * s, u[j] * s)));
+    mx = pf_block_max(mx, red);
+    int e = 0;
+    frexpf(mx, &e);
+    int sh = mx > 0.f ? 15 - e : 0;
+    sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
+    const float sc = ldexpf(1.f, sh);
+    _Float16 *ar = a16 + (long long)t * F;
+    for (int j = tid; j < F; j += PN_THREADS) ar[j] = (_Float16)(pro_swiglu(g[j] * s, u[j] * s) * sc);
+    if (tid == 0) ainv[t] = ldexpf(1.f, -sh);
+}
+
+// y[j] *= ys[0] for one row of n floats (the last token's down output
+// before the lm_head).
+__global__ __launch_bounds__(256) void k_pf_scale_row(float *__restrict__ y, const float *__restrict__ ys, int n) {
+    for (int j = threadIdx.x; j < n; j += 256) y[j] *= ys[0];
 }
 
 // Causal attention.  grid = (NKV, ceil(T / QB)), 256 threads: the
@@ -406,35 +448,23 @@ static hipError_t launch_pf_attn(int G, const float *qb, const float *kc, const 
 // ---------------------------------------------------------------------------
 static size_t pf_up(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// The batched path covers models whose layers have fused q|k|v and gate|up
-// matrices, all in the reference's Q4_K layout, with row lengths the MFMA
-// kernel is built for and H <= 8192.
-bool dense_prefill_batched(const tbq_dense_model *m) {
-    const int H = m->hidden, QD = m->n_heads * m->head_dim, F = m->ffn;
-    const int QKVR = (m->n_heads + 2 * m->n_kv_heads) * m->head_dim;
-    if (H > 8192 || !gemm_k_supported(H) || !gemm_k_supported(QD) || !gemm_k_supported(F) ||
-        QKVR % 256 || H % 256 || F % 128)
-        return false;
-    auto q4k = [m](int q) { return canon_qt(q ? q : m->qtype_layers) == QT_Q4_K; };
-    for (int l = 0; l < m->n_layers; l++) {
-        const tbq_dense_layer &L = m->layers[l];
-        if (!L.wqkv || !L.wgu || !q4k(L.qt_qkv) || !q4k(L.qt_o) || !q4k(L.qt_gu) || !q4k(L.qt_down)) return false;
-    }
-    return true;
-}
+// Every model with hidden <= 8192 (the norm kernel's row) takes the batched
+// path for T >= 2; its matrices, of any format and layout, are dequantised
+// to fp16 one at a time and multiplied by rocBLAS.
+bool dense_prefill_batched(const tbq_dense_model *m) { return m->hidden <= PN_THREADS * PN_V * 4; }
 
 struct PfWs {
-    float *x, *y, *qkv, *qb, *att, *act, *hinv, *part;
-    _Float16 *h16;
+    float *x, *y, *qkv, *qb, *att, *gu, *sa, *sb, *part;
+    _Float16 *h16, *wh;
     int *tok;
-    void *gemm, *dec;
+    void *dec;
 };
 
 static PfWs pf_ws(const tbq_dense_model *m, int T, void *ws, size_t *total) {
     const size_t H = m->hidden, QD = (size_t)m->n_heads * m->head_dim, F = m->ffn;
     const size_t QKVR = (size_t)(m->n_heads + 2 * m->n_kv_heads) * m->head_dim;
-    size_t wide = H > QD ? H : QD;
-    wide = wide > F ? wide : F;
+    const size_t wide = std::max(std::max(H, QD), F);
+    const size_t wmax = std::max(std::max(QKVR * H, H * QD), std::max(2 * F * H, H * F));
     char *p = (char *)ws;
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -442,22 +472,23 @@ static PfWs pf_ws(const tbq_dense_model *m, int T, void *ws, size_t *total) {
         off += pf_up(bytes);
         return r;
     };
-    PfWs w;
+    PfWs w{};
     w.dec = take(dense_workspace_bytes(m));
     w.tok = (int *)take((size_t)T * 4);
-    if (dense_prefill_batched(m)) {
+    if (dense_prefill_batched(m) && T >= 2) {
         w.x = (float *)take((size_t)T * H * 4);
         w.y = (float *)take((size_t)T * H * 4);
         w.qkv = (float *)take((size_t)T * QKVR * 4);
         w.qb = (float *)take((size_t)T * QD * 4);
         w.att = (float *)take((size_t)T * QD * 4);
-        w.act = (float *)take((size_t)T * F * 4);
+        w.gu = (float *)take((size_t)T * 2 * F * 4);
         w.h16 = (_Float16 *)take((size_t)T * wide * 2);
-        w.hinv = (float *)take((size_t)T * 4);
-        w.gemm = take(dense_gemm_scratch_bytes(T));
+        w.sa = (float *)take((size_t)T * 4);
+        w.sb = (float *)take((size_t)T * 4);
+        w.wh = (_Float16 *)take(wmax * 2);
         // attention split partials: a prefill reaching position kmax - 1 uses
         // min(PA_MAX_SPLIT, ceil(kmax / PA_PREF_KS)) splits, and kmax <= max_ctx
-        const int ns = min(PA_MAX_SPLIT, (m->max_ctx + PA_PREF_KS - 1) / PA_PREF_KS);
+        const int ns = std::min(PA_MAX_SPLIT, (m->max_ctx + PA_PREF_KS - 1) / PA_PREF_KS);
         w.part = ns > 1 ? (float *)take((size_t)T * m->n_heads * ns * (m->head_dim + 2) * 4) : nullptr;
     }
     if (total) *total = off;
@@ -470,54 +501,86 @@ size_t dense_prefill_workspace_bytes(const tbq_dense_model *m, int T) {
     return t;
 }
 
-// tokens: T device ints (in range); the batched path only.
+// rocBLAS for the prefill's fp16 GEMMs: one handle per process, used under
+// a mutex (its stream is set per call).
+static std::mutex g_rb_mu;
+static rocblas_handle g_rb = nullptr;
+
+// C[T][M] = X[T][K] . W[M][K]^T, row-major, fp16 operands, fp32 accumulate
+// and output (column-major: C'[M x T] = W'^T[M x K] X'[K x T]).
+static hipError_t pf_gemm(const _Float16 *W, const _Float16 *X, int T, int M, int K, float *C) {
+    const float alpha = 1.f, beta = 0.f;
+    const rocblas_status r =
+        rocblas_gemm_ex(g_rb, rocblas_operation_transpose, rocblas_operation_none, M, T, K, &alpha, W,
+                        rocblas_datatype_f16_r, K, X, rocblas_datatype_f16_r, K, &beta, C, rocblas_datatype_f32_r, M, C,
+                        rocblas_datatype_f32_r, M, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    return r == rocblas_status_success ? hipSuccess : hipErrorUnknown;
+}
+
+// tokens: T device ints (in range); T >= 2.
 static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int pos0, float *logits,
                              hipStream_t st) {
     const int H = m->hidden, D = m->head_dim, NQ = m->n_heads, NKV = m->n_kv_heads, G = NQ / NKV, F = m->ffn;
-    const int QD = NQ * D, QKVR = (NQ + 2 * NKV) * D;
-    const long long rbh = (long long)(H / 256) * 144;   // Q4_K row bytes at K = H
-    DenseGemmPlan plan;
-    hipError_t err = dense_gemm_plan(T, w.gemm, &plan, st);
-    if (err == hipSuccess) err = launch_dequant_rows(canon_qt(m->qtype_embd), m->tok_embd, w.tok, T, H, w.x, st);
+    const int QD = NQ * D, KD = NKV * D, QKVR = QD + 2 * KD;
+    auto qt_of = [m](int q) { return canon_qt(q ? q : m->qtype_layers); };
+    auto dq = [&](int qt, const void *W, long long rows, int K, _Float16 *dst) {
+        return launch_dequant_f16(qt, W, rows * K, dst, st);
+    };
+    std::lock_guard<std::mutex> lk(g_rb_mu);
+    if (!g_rb && rocblas_create_handle(&g_rb) != rocblas_status_success) return hipErrorUnknown;
+    if (rocblas_set_stream(g_rb, st) != rocblas_status_success) return hipErrorUnknown;
+    hipError_t err = launch_dequant_rows(canon_qt(m->qtype_embd), m->tok_embd, w.tok, T, H, w.x, st);
     for (int l = 0; l < m->n_layers && err == hipSuccess; l++) {
         const tbq_dense_layer &L = m->layers[l];
         const size_t kvoff = (size_t)l * NKV * m->max_ctx * D;
         float *kc = m->k_cache + kvoff, *vc = m->v_cache + kvoff;
-        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, l ? w.y : nullptr, L.attn_norm, H,
-                           m->norm_eps, w.h16, w.hinv);
-        if ((err = launch_dense_gemm(1, plan, L.wqkv, nullptr, w.h16, T, w.hinv, QKVR, H, w.qkv, st)) != hipSuccess) break;
+        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, l ? w.y : nullptr, l ? w.sb : nullptr,
+                           L.attn_norm, H, m->norm_eps, w.h16, w.sa);
+        if (L.wqkv) {
+            err = dq(qt_of(L.qt_qkv), L.wqkv, QKVR, H, w.wh);
+        } else {
+            err = dq(qt_of(L.qt_q), L.wq, QD, H, w.wh);
+            if (err == hipSuccess) err = dq(qt_of(L.qt_k), L.wk, KD, H, w.wh + (size_t)QD * H);
+            if (err == hipSuccess) err = dq(qt_of(L.qt_v), L.wv, KD, H, w.wh + (size_t)(QD + KD) * H);
+        }
+        if (err != hipSuccess || (err = pf_gemm(w.wh, w.h16, T, QKVR, H, w.qkv)) != hipSuccess) break;
         if (D == 128) {
-            hipLaunchKernelGGL(k_pf_qk<128>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, L.q_norm, L.k_norm, NQ, NKV,
-                               pos0, m->rope_theta, m->norm_eps, kc, vc, m->max_ctx, w.qb);
+            hipLaunchKernelGGL(k_pf_qk<128>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, w.sa, L.q_norm, L.k_norm, NQ,
+                               NKV, pos0, m->rope_theta, m->norm_eps, kc, vc, m->max_ctx, w.qb);
             err = launch_pf_attn<128>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, st);
         } else {
-            hipLaunchKernelGGL(k_pf_qk<64>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, L.q_norm, L.k_norm, NQ, NKV,
-                               pos0, m->rope_theta, m->norm_eps, kc, vc, m->max_ctx, w.qb);
+            hipLaunchKernelGGL(k_pf_qk<64>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, w.sa, L.q_norm, L.k_norm, NQ,
+                               NKV, pos0, m->rope_theta, m->norm_eps, kc, vc, m->max_ctx, w.qb);
             err = launch_pf_attn<64>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, st);
         }
-        if (err != hipSuccess) break;
-        if ((err = launch_rows_f16(w.att, T, QD, w.h16, w.hinv, st)) != hipSuccess) break;
-        if ((err = launch_dense_gemm(1, plan, L.wo, nullptr, w.h16, T, w.hinv, H, QD, w.y, st)) != hipSuccess) break;
-        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, w.y, L.ffn_norm, H, m->norm_eps, w.h16,
-                           w.hinv);
-        const uint8_t *wg = (const uint8_t *)L.wgu;
-        if ((err = launch_dense_gemm(0, plan, wg, wg + (long long)F * rbh, w.h16, T, w.hinv, F, H, w.act, st)) !=
-            hipSuccess)
-            break;
-        if ((err = launch_rows_f16(w.act, T, F, w.h16, w.hinv, st)) != hipSuccess) break;
-        err = launch_dense_gemm(1, plan, L.wdown, nullptr, w.h16, T, w.hinv, H, F, w.y, st);
+        if (err != hipSuccess || (err = launch_rows_f16(w.att, T, QD, w.h16, w.sb, st)) != hipSuccess) break;
+        if ((err = dq(qt_of(L.qt_o), L.wo, H, QD, w.wh)) != hipSuccess) break;
+        if ((err = pf_gemm(w.wh, w.h16, T, H, QD, w.y)) != hipSuccess) break;
+        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, w.y, w.sb, L.ffn_norm, H, m->norm_eps,
+                           w.h16, w.sa);
+        if (L.wgu) {
+            err = dq(qt_of(L.qt_gu), L.wgu, 2 * F, H, w.wh);
+        } else {
+            err = dq(qt_of(L.qt_gate), L.wgate, F, H, w.wh);
+            if (err == hipSuccess) err = dq(qt_of(L.qt_up), L.wup, F, H, w.wh + (size_t)F * H);
+        }
+        if (err != hipSuccess || (err = pf_gemm(w.wh, w.h16, T, 2 * F, H, w.gu)) != hipSuccess) break;
+        hipLaunchKernelGGL(k_pf_swiglu_f16, dim3(T), dim3(PN_THREADS), 0, st, w.gu, w.sa, F, w.h16, w.sb);
+        if ((err = dq(qt_of(L.qt_down), L.wdown, H, F, w.wh)) != hipSuccess) break;
+        err = pf_gemm(w.wh, w.h16, T, H, F, w.y);
     }
     if (err != hipSuccess) return err;
-    err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    return dense_final_logits(m, w.x + (size_t)(T - 1) * H, w.y + (size_t)(T - 1) * H, logits, w.dec, st);
+    float *ylast = w.y + (size_t)(T - 1) * H;
+    hipLaunchKernelGGL(k_pf_scale_row, dim3(1), dim3(256), 0, st, ylast, w.sb + (T - 1), H);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    return dense_final_logits(m, w.x + (size_t)(T - 1) * H, ylast, logits, w.dec, st);
 }
 
 hipError_t launch_dense_prefill(const tbq_dense_model *m, const int *tokens_host, int T, int pos0, float *logits,
                                 void *ws, hipStream_t st) {
     const PfWs w = pf_ws(m, T, ws, nullptr);
-    if (!dense_prefill_batched(m)) {
-        // every other model: the decode step once per token, in order
+    if (!dense_prefill_batched(m) || T < 2) {
+        // one token, or a row wider than the norm kernel: the decode step per token
         for (int t = 0; t < T; t++) {
             const hipError_t err = launch_dense_decode(m, tokens_host[t], pos0 + t, logits, w.dec, st);
             if (err != hipSuccess) return err;

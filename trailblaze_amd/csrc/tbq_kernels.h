@@ -41,6 +41,7 @@ struct MoeArgs {
 
 hipError_t launch_dequant(int qt, const void *W, long long nweights, float *out, hipStream_t s);
 hipError_t launch_dequant_rows(int qt, const void *W, const int *idx, int nrows, int K, float *out, hipStream_t s);
+hipError_t launch_dequant_f16(int qt, const void *W, long long nweights, _Float16 *out, hipStream_t s);
 hipError_t launch_matvec_generic(int qt, const void *W, int M, int K, const float *x, float *y,
                                  hipStream_t s, int n_cu);
 // The Q4_K kernels read the reference's layout, or ggml's (QT_GQ4_K) when ggml.
@@ -64,19 +65,7 @@ hipError_t launch_router(const float *xn, const float *router, const float *bias
 // a.qtype QT_Q4_K or QT_GQ4_K
 hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st);
 size_t prefill_workspace_bytes(int T, int k, int E, int H, int F);
-// Dense GEMMs on the prefill MFMA kernel (Q4_K weights, fp16 activations
-// with per-row power-of-two scales): a tile plan over T rows, then
-// out[T][M] = X W^T (mode 1) or silu(X Wg^T) * (X Wu^T) (mode 0).
-struct DenseGemmPlan {
-    void *tiles;
-    int *ntiles, *tpair, *ttok;
-    int nt;
-};
 bool gemm_k_supported(int K);
-size_t dense_gemm_scratch_bytes(int T);
-hipError_t dense_gemm_plan(int T, void *scratch, DenseGemmPlan *p, hipStream_t st);
-hipError_t launch_dense_gemm(int mode, const DenseGemmPlan &p, const void *W0, const void *W1, const _Float16 *X,
-                             int T, const float *xinv, int M, int K, float *out, hipStream_t st);
 // rows of n floats to fp16 with per-row power-of-two scales (inv = 1 / scale)
 hipError_t launch_rows_f16(const float *in, int rows, int n, _Float16 *out, float *inv, hipStream_t st);
 hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t st, bool x16_done = false);

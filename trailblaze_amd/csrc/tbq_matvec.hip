@@ -97,6 +97,42 @@ __global__ __launch_bounds__(256) void k_dequant_rows(const uint8_t *__restrict_
     }
 }
 
+// W[nrows][K] in format qt to fp16 (the fp32 weight rounded once), for the
+// prefill's library GEMMs.  Thread t writes weights 8t..8t+7.
+template <int QT>
+__global__ __launch_bounds__(256) void k_dequant_f16(const uint8_t *__restrict__ W, long long n8,
+                                                     _Float16 *__restrict__ out) {
+    constexpr int BW = block_weights(QT), BB = block_bytes(QT);
+    for (long long t = blockIdx.x * 256ll + threadIdx.x; t < n8; t += (long long)gridDim.x * 256) {
+        const long long e = t * 8;
+        float w[8];
+        if constexpr (BW == 1) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint8_t *p = W + (e + i) * BB;
+                w[i] = QT == QT_F32 ? __builtin_bit_cast(float, ldu32(p))
+                     : QT == QT_F16 ? f16_ref(ldu16(p)) : QT == QT_GF16 ? f16_ieee(ldu16(p))
+                     : bf16_ref(ldu16(p));
+            }
+        } else {
+            const long long blk = e / BW;
+            decode8<QT>(W + blk * BB, (int)(e - blk * BW), w);
+        }
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        const h8 v = {(_Float16)w[0], (_Float16)w[1], (_Float16)w[2], (_Float16)w[3],
+                      (_Float16)w[4], (_Float16)w[5], (_Float16)w[6], (_Float16)w[7]};
+        *reinterpret_cast<h8 *>(out + e) = v;
+    }
+}
+
+template <int QT>
+static hipError_t launch_dequant_f16_t(const void *W, long long nweights, _Float16 *out, hipStream_t s) {
+    const long long n8 = nweights / 8, blocks = (n8 + 255) / 256;
+    const int grid = (int)(blocks < 65536 ? blocks : 65536);
+    hipLaunchKernelGGL((k_dequant_f16<QT>), dim3(grid), dim3(256), 0, s, (const uint8_t *)W, n8, out);
+    return hipGetLastError();
+}
+
 template <int QT>
 static hipError_t launch_dequant_rows_t(const void *W, const int *idx, int nrows, int K, float *out, hipStream_t s) {
     const long long rb = (long long)(K / block_weights(QT)) * block_bytes(QT);
@@ -165,6 +201,32 @@ hipError_t launch_dequant(int qt, const void *W, long long nweights, float *out,
     case QT_GQ4_K: return launch_dequant_t<QT_GQ4_K>(W, nweights, out, s);
     case QT_GQ5_K: return launch_dequant_t<QT_GQ5_K>(W, nweights, out, s);
     case QT_GQ6_K: return launch_dequant_t<QT_GQ6_K>(W, nweights, out, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// nweights (a multiple of 8 and of the block size) of format qt to fp16.
+hipError_t launch_dequant_f16(int qt, const void *W, long long nweights, _Float16 *out, hipStream_t s) {
+    switch (qt) {
+    case QT_F32: return launch_dequant_f16_t<QT_F32>(W, nweights, out, s);
+    case QT_F16: return launch_dequant_f16_t<QT_F16>(W, nweights, out, s);
+    case QT_BF16: return launch_dequant_f16_t<QT_BF16>(W, nweights, out, s);
+    case QT_Q4_0: return launch_dequant_f16_t<QT_Q4_0>(W, nweights, out, s);
+    case QT_Q8_0: return launch_dequant_f16_t<QT_Q8_0>(W, nweights, out, s);
+    case QT_Q2_K: return launch_dequant_f16_t<QT_Q2_K>(W, nweights, out, s);
+    case QT_Q3_K: return launch_dequant_f16_t<QT_Q3_K>(W, nweights, out, s);
+    case QT_Q4_K: return launch_dequant_f16_t<QT_Q4_K>(W, nweights, out, s);
+    case QT_Q5_K: return launch_dequant_f16_t<QT_Q5_K>(W, nweights, out, s);
+    case QT_Q6_K: return launch_dequant_f16_t<QT_Q6_K>(W, nweights, out, s);
+    case QT_Q8_K: return launch_dequant_f16_t<QT_Q8_K>(W, nweights, out, s);
+    case QT_GF16: return launch_dequant_f16_t<QT_GF16>(W, nweights, out, s);
+    case QT_GQ4_0: return launch_dequant_f16_t<QT_GQ4_0>(W, nweights, out, s);
+    case QT_GQ8_0: return launch_dequant_f16_t<QT_GQ8_0>(W, nweights, out, s);
+    case QT_GQ2_K: return launch_dequant_f16_t<QT_GQ2_K>(W, nweights, out, s);
+    case QT_GQ3_K: return launch_dequant_f16_t<QT_GQ3_K>(W, nweights, out, s);
+    case QT_GQ4_K: return launch_dequant_f16_t<QT_GQ4_K>(W, nweights, out, s);
+    case QT_GQ5_K: return launch_dequant_f16_t<QT_GQ5_K>(W, nweights, out, s);
+    case QT_GQ6_K: return launch_dequant_f16_t<QT_GQ6_K>(W, nweights, out, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -428,7 +428,7 @@ static hipError_t launch_moe_f16(int ns, unsigned nwg, hipStream_t st, const uin
         break;                                                                                                     \
     }
     switch (ns) {
-        TBQ_NS(2) TBQ_NS(4) TBQ_NS(6) TBQ_NS(8) TBQ_NS(12) TBQ_NS(16) TBQ_NS(20) TBQ_NS(24) TBQ_NS(32) TBQ_NS(76)
+        TBQ_NS(2) TBQ_NS(4) TBQ_NS(6) TBQ_NS(8) TBQ_NS(12) TBQ_NS(16) TBQ_NS(24) TBQ_NS(32)
     default:
         return hipErrorNotSupported;
     }
@@ -439,68 +439,12 @@ static hipError_t launch_moe_f16(int ns, unsigned nwg, hipStream_t st, const uin
 // K values the MFMA kernel is instantiated for (K = 128 * NS).
 bool gemm_k_supported(int K) {
     const int n = K / PF_KC;
-    return K % 256 == 0 && (n == 2 || n == 4 || n == 6 || n == 8 || n == 12 || n == 16 || n == 20 || n == 24 ||
-                            n == 32 || n == 76);
-}
-
-// ---------------------------------------------------------------------------
-// Dense GEMMs out[T][M] = X[T][K] . W[M][K]^T (Q4_K W) on the same kernel:
-// one "expert" whose tiles are ceil(T / 128) runs of consecutive rows.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_pf_tiles(int T, PfTile *__restrict__ tiles, int *__restrict__ ntiles,
-                                                  int *__restrict__ tpair, int *__restrict__ ttok) {
-    const int nt = (T + PF_MT - 1) / PF_MT;
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < nt * PF_MT; i += gridDim.x * 256) {
-        const int t = i / PF_MT;
-        if (i % PF_MT == 0) tiles[t] = PfTile{0, min(PF_MT, T - t * PF_MT)};
-        const int r = i < T ? i : -1;
-        tpair[i] = r;
-        ttok[i] = r;
-    }
-    if (blockIdx.x == 0 && threadIdx.x == 0) *ntiles = nt;
+    return K % 256 == 0 && (n == 2 || n == 4 || n == 6 || n == 8 || n == 12 || n == 16 || n == 24 || n == 32);
 }
 
 hipError_t launch_rows_f16(const float *in, int rows, int n, _Float16 *out, float *inv, hipStream_t st) {
     hipLaunchKernelGGL(k_rows_f16, dim3(rows), dim3(256), 0, st, in, n, out, inv);
     return hipGetLastError();
-}
-
-size_t dense_gemm_scratch_bytes(int T) {
-    const size_t nt = (size_t)(T + PF_MT - 1) / PF_MT;
-    auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
-    return up(nt * sizeof(PfTile)) + 256 + 2 * up(nt * PF_MT * 4);
-}
-
-hipError_t dense_gemm_plan(int T, void *scratch, DenseGemmPlan *p, hipStream_t st) {
-    const size_t nt = (size_t)(T + PF_MT - 1) / PF_MT;
-    auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
-    char *w = (char *)scratch;
-    p->tiles = w; w += up(nt * sizeof(PfTile));
-    p->ntiles = (int *)w; w += 256;
-    p->tpair = (int *)w; w += up(nt * PF_MT * 4);
-    p->ttok = (int *)w;
-    p->nt = (int)nt;
-    const int grid = (int)((nt * PF_MT + 255) / 256);
-    hipLaunchKernelGGL(k_pf_tiles, dim3(grid), dim3(256), 0, st, T, (PfTile *)p->tiles, p->ntiles, p->tpair, p->ttok);
-    return hipGetLastError();
-}
-
-// mode 1: out[T][M] = X W^T, K = the row length of W.  mode 0: W0, W1 are
-// gate and up ([M][K] each) and out[T][M] = silu(X Wg^T) * (X Wu^T).  X is
-// fp16 [T][K] with per-row scales xinv (k_rows_f16's convention).  M a
-// multiple of 256 (mode 1) or 128 (mode 0); gemm_k_supported(K).
-hipError_t launch_dense_gemm(int mode, const DenseGemmPlan &p, const void *W0, const void *W1, const _Float16 *X,
-                             int T, const float *xinv, int M, int K, float *out, hipStream_t st) {
-    if (!gemm_k_supported(K) || M % (mode ? PF_ROWS : PF_COLS)) return hipErrorNotSupported;
-    const PfTile *tiles = (const PfTile *)p.tiles;
-    if (mode == 0) {
-        const int ncb = M / PF_COLS;
-        return launch_moe_f16<0>(K / PF_KC, (unsigned)(p.nt * ncb), st, (const uint8_t *)W0, (const uint8_t *)W1, X,
-                                 T, xinv, p.tpair, p.ttok, tiles, p.ntiles, ncb, K, M, out);
-    }
-    const int ncb = M / PF_ROWS;
-    return launch_moe_f16<1>(K / PF_KC, (unsigned)(p.nt * ncb), st, (const uint8_t *)W0, nullptr, X, T, xinv,
-                             p.tpair, p.ttok, tiles, p.ntiles, ncb, M, K, out);
 }
 
 // Experts on MFMA for Q4_K weights; routing already in a.sel_idx/a.sel_w.
