@@ -12,9 +12,9 @@
 //   GEMM             qkv = h16 Wqkv^T             rocBLAS fp16, fp32 acc
 //   k_pf_qk          per (token, head): QK-norm + RoPE of q (to qb) and k;
 //                    k and v rows written to the cache at pos0 + t
-//   k_pf_attn        causal GQA attention over cache positions 0 .. pos,
-//                    online softmax, key ranges split over workgroups
-//                    (k_pf_attn_combine merges them)
+//   k_pf_attn        causal GQA attention over cache positions 0 .. pos on
+//                    fp16 MFMA, online softmax, key ranges split over
+//                    workgroups (k_pf_attn_combine merges them)
 //   rows to fp16, GEMM            y = att Wo^T
 //   k_pf_norm        x += y, h16 = rmsnorm(x) * ffn_norm
 //   GEMM             gu = h16 [Wg | Wu]^T
@@ -23,8 +23,9 @@
 // then the last token's logits = Wlm rmsnorm(x + y) (the decode step's
 // lm_head matvec with its norm prologue).
 //
-// Accuracy: fp16 weights and activations (11-bit mantissa) with fp32
-// accumulation, fp32 norms, RoPE and attention; the logits land within
+// Accuracy: fp16 weights, activations, attention scores' operands and
+// probabilities (11-bit mantissa) with fp32 accumulation, fp32 norms, RoPE
+// and softmax; the logits land within
 // 1e-2 relative L2 of the float64 sequential decode.
 #include <rocblas/rocblas.h>
 
@@ -38,9 +39,7 @@
 namespace tbq {
 
 constexpr int PN_THREADS = 256;
-constexpr int PA_THREADS = 256;
-constexpr int PA_KC = 8;      // cache positions per attention step
-constexpr int PA_KF = 32;     // cache positions per LDS fill (PA_KF / PA_KC steps)
+constexpr int PA_KF = 32;     // split sizes are multiples of this many positions
 
 __device__ __forceinline__ float pf_block_sum(float v, float *red) {
     v = group_sum<64>(v);
@@ -224,173 +223,135 @@ __global__ __launch_bounds__(256) void k_pf_scale_row(float *__restrict__ y, con
     for (int j = threadIdx.x; j < n; j += 256) y[j] *= ys[0];
 }
 
-// Causal attention.  grid = (NKV, ceil(T / QB)), 256 threads: the
-// workgroup owns QB = 64 / G tokens x the G query heads of kv head kvh = 64
-// query rows.  PA_TPR = 16 lanes share PA_R = 4 rows, each lane holding a
-// sixteenth of the head dimension of all four (dims 4qq + 4 PA_TPR i + c,
-// so a row group's lanes read one contiguous LDS run), so every K and V
-// value read from LDS serves four rows.  Cache positions 0 .. the block's
-// last position pass through LDS PA_KF at a time, the next fill's rows
-// loaded into registers while the current one is used; per PA_KC step each row
-// forms its scores (partial dots summed over the 16 lanes), masks
-// positions past its own, and updates its running max, denominator and
-// output (online softmax).  Position 0 is in every row's range, so the
-// running maxima are finite after the first chunk.
-constexpr int PA_TPR = 16, PA_R = 4;
-constexpr int PA_ROWS = PA_THREADS / PA_TPR * PA_R;
-
+// Causal attention on MFMA (v_mfma_f32_32x32x16_f16, fp16 operands, fp32
+// accumulate).  grid = (NKV, ceil(T / QB), nsplit), 4 waves: the workgroup
+// owns QB = 128 / G tokens x the G query heads of kv head kvh = 128 query
+// columns, 32 per wave (query c of a wave: token c / G, head c % G).  Cache
+// positions pass through LDS 32 at a time in fp16: K as [position][dim],
+// V transposed as [dim][position].  Per chunk a wave forms S^T = K Q^T (32
+// positions x its 32 queries), so a lane holds 16 scores of one query:
+// lane l, register r: query l % 32, position 8(r/4) + 4(l/32) + r%4.  The
+// query's max and denominator need one exchange with lane l ^ 32.  The
+// probabilities, rounded to fp16, are already the B operand of
+// O^T += V^T P^T when the 16 positions of a step are taken in the order
+// k-slot 8h + i <-> position 8(i/4) + 4h + i%4 (h = l / 32), which V^T's A
+// operand follows; O^T's accumulators hold dims 32j + 8(r/4) + 4h + r%4
+// of the lane's query.  Online softmax over chunks; positions past a
+// query's own are masked.
 //
-// Key splits: grid.z = nsplit workgroups per block, split z taking cache
-// positions [z ks, (z + 1) ks) (ks a multiple of PA_KF), so the heavy
-// blocks of a causal prompt (whose rows see every earlier position) are
-// spread over several workgroups.  With nsplit > 1 each writes its rows'
-// unnormalised output, running max and denominator to part[(row * nsplit
-// + z) * (D + 2)], and k_pf_attn_combine merges the splits a row reaches.
+// Key splits: split z takes positions [z ks, (z + 1) ks) (ks a multiple of
+// PA_KF), so the heavy blocks of a causal prompt (whose queries see every
+// earlier position) spread over several workgroups.  With nsplit > 1 each
+// writes its queries' unnormalised output, running max and denominator to
+// part[(row * nsplit + z) * (D + 2)], and k_pf_attn_combine merges the
+// splits a row reaches.
+constexpr int PM_THREADS = 256, PM_Q = 128, PM_KC = 32;
+typedef _Float16 pm_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 pm_h4 __attribute__((ext_vector_type(4)));
+typedef float pm_f16 __attribute__((ext_vector_type(16)));
+
 template <int D, int G>
-__global__ __launch_bounds__(PA_THREADS) void k_pf_attn(const float *__restrict__ qb, const float *__restrict__ kc,
+__global__ __launch_bounds__(PM_THREADS) void k_pf_attn(const float *__restrict__ qb, const float *__restrict__ kc,
                                                         const float *__restrict__ vc, int T, int pos0, int NQ,
                                                         int max_ctx, int ks, int nsplit, float *__restrict__ part,
                                                         float *__restrict__ out) {
-    constexpr int QB = PA_ROWS / G, DQ = D / PA_TPR, NI = DQ / 4;
-    constexpr int NF = PA_KF * D / 4;                  // float4 of K (and of V) per fill
-    constexpr int NL = (NF + PA_THREADS - 1) / PA_THREADS;
-    static_assert(NI >= 1, "shape");
-    __shared__ __attribute__((aligned(16))) float Ks[PA_KF][D];
-    __shared__ __attribute__((aligned(16))) float Vs[PA_KF][D];
-    const int kvh = blockIdx.x, tid = threadIdx.x, rg = tid / PA_TPR, qq = tid % PA_TPR;
+    constexpr int QB = PM_Q / G, KLD = D + 8, VLD = PM_KC + 8, NT = D / 32, NS = D / 16;
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[PM_KC * KLD];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VLD];
+    const int kvh = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, h = lane >> 5;
+    const int qc = wave * 32 + li, g = qc % G;
+    const int t = blockIdx.y * QB + qc / G;
+    const int tt = t < T ? t : T - 1;
+    const int qpos = pos0 + tt;
     const int tend = min(T, (int)(blockIdx.y + 1) * QB);
     const int k0 = blockIdx.z * ks;                  // this split's positions k0 .. kend - 1
     const int kend = min(pos0 + tend, k0 + ks);
     if (k0 >= kend) return;   // no position of the split is seen by the block (uniform)
+    // Q^T's B fragments: dim step s, lane half h supplies dims 16s + 8h .. + 8
+    pm_h8 qf[NS];
+    const float *qsrc = qb + ((long long)tt * NQ + kvh * G + g) * D;
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+#pragma unroll
+        for (int c = 0; c < 8; c++) qf[s][c] = (_Float16)qsrc[16 * s + 8 * h + c];
+    pm_f16 o[NT];
+#pragma unroll
+    for (int j = 0; j < NT; j++) o[j] = pm_f16{};
+    float m = -__builtin_huge_valf(), l = 0.f;
     const float *kb = kc + (long long)kvh * max_ctx * D;
     const float *vb = vc + (long long)kvh * max_ctx * D;
-    // native vectors: arrays of HIP's float4 struct carried across loop
-    // iterations are kept in scratch memory
-    typedef float f32x4 __attribute__((ext_vector_type(4)));
-    f32x4 kn[NL], vn[NL];
-    auto fetch = [&](int c0) {
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const int f = tid + PA_THREADS * i, row = f / (D / 4), c4 = f % (D / 4);
-            const long long p = min(c0 + row, kend - 1);
-            kn[i] = *reinterpret_cast<const f32x4 *>(kb + p * D + 4 * c4);
-            vn[i] = *reinterpret_cast<const f32x4 *>(vb + p * D + 4 * c4);
-        }
-    };
-    fetch(k0);
-    int qpos[PA_R];
-    float q[PA_R][DQ], o[PA_R][DQ], m[PA_R], l[PA_R];
-#pragma unroll
-    for (int k = 0; k < PA_R; k++) {
-        const int rr = rg * PA_R + k, g = rr % G, t = min((int)blockIdx.y * QB + rr / G, T - 1);
-        qpos[k] = pos0 + t;
-        const float *qsrc = qb + ((long long)t * NQ + kvh * G + g) * D + 4 * qq;
-#pragma unroll
-        for (int i = 0; i < NI; i++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                q[k][4 * i + c] = qsrc[4 * PA_TPR * i + c];
-                o[k][4 * i + c] = 0.f;
-            }
-        m[k] = -__builtin_huge_valf();
-        l[k] = 0.f;
-    }
-    for (int f0 = k0; f0 < kend; f0 += PA_KF) {
-        __syncthreads();   // the previous fill is no longer read
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const int f = tid + PA_THREADS * i, row = f / (D / 4), c4 = f % (D / 4);
-            if (NF % PA_THREADS == 0 || f < NF) {
-                *reinterpret_cast<f32x4 *>(&Ks[row][4 * c4]) = kn[i];
-                *reinterpret_cast<f32x4 *>(&Vs[row][4 * c4]) = vn[i];
-            }
+    for (int c0 = k0; c0 < kend; c0 += PM_KC) {
+        __syncthreads();   // the previous chunk is no longer read
+        for (int f = tid; f < PM_KC * D / 4; f += PM_THREADS) {
+            const int key = f / (D / 4), c4 = f % (D / 4);
+            const long long p = min(c0 + key, kend - 1);
+            const float4 kv = *reinterpret_cast<const float4 *>(kb + p * D + 4 * c4);
+            const float4 vv = *reinterpret_cast<const float4 *>(vb + p * D + 4 * c4);
+            *reinterpret_cast<pm_h4 *>(&Ks[key * KLD + 4 * c4]) =
+                pm_h4{(_Float16)kv.x, (_Float16)kv.y, (_Float16)kv.z, (_Float16)kv.w};
+            Vt[(4 * c4) * VLD + key] = (_Float16)vv.x;
+            Vt[(4 * c4 + 1) * VLD + key] = (_Float16)vv.y;
+            Vt[(4 * c4 + 2) * VLD + key] = (_Float16)vv.z;
+            Vt[(4 * c4 + 3) * VLD + key] = (_Float16)vv.w;
         }
         __syncthreads();
-        fetch(f0 + PA_KF < kend ? f0 + PA_KF : f0);   // the next fill (the last one again at the end)
+        pm_f16 sc = pm_f16{};
 #pragma unroll
-        for (int sub = 0; sub < PA_KF / PA_KC; sub++) {
-        const int c0 = f0 + sub * PA_KC;
-        if (c0 >= kend) break;   // uniform
-        float s[PA_R][PA_KC];
-#pragma unroll
-        for (int k = 0; k < PA_R; k++)
-#pragma unroll
-            for (int j = 0; j < PA_KC; j++) s[k][j] = 0.f;
-#pragma unroll
-        for (int i = 0; i < NI; i++) {
-#pragma unroll
-            for (int j = 0; j < PA_KC; j++) {
-                const float4 k4 = *reinterpret_cast<const float4 *>(&Ks[sub * PA_KC + j][4 * qq + 4 * PA_TPR * i]);
-#pragma unroll
-                for (int k = 0; k < PA_R; k++) {
-                    s[k][j] = fmaf(q[k][4 * i], k4.x, s[k][j]);
-                    s[k][j] = fmaf(q[k][4 * i + 1], k4.y, s[k][j]);
-                    s[k][j] = fmaf(q[k][4 * i + 2], k4.z, s[k][j]);
-                    s[k][j] = fmaf(q[k][4 * i + 3], k4.w, s[k][j]);
-                }
-            }
+        for (int s = 0; s < NS; s++) {
+            const pm_h8 a = *reinterpret_cast<const pm_h8 *>(&Ks[li * KLD + 16 * s + 8 * h]);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sc, 0, 0, 0);
         }
+        float mx = -__builtin_huge_valf();
 #pragma unroll
-        for (int k = 0; k < PA_R; k++) {
-            float cm = -__builtin_huge_valf();
-#pragma unroll
-            for (int j = 0; j < PA_KC; j++) {
-                const float a = group_sum<PA_TPR>(s[k][j]);
-                s[k][j] = c0 + j <= qpos[k] ? a : -__builtin_huge_valf();
-                cm = fmaxf(cm, s[k][j]);
-            }
-            // a row that has seen no position yet keeps m = -inf, l = 0, o = 0
-            const float mn = fmaxf(m[k], cm);
-            const float corr = m[k] == -__builtin_huge_valf() ? 0.f : __expf(m[k] - mn);
-            l[k] *= corr;
-#pragma unroll
-            for (int i = 0; i < DQ; i++) o[k][i] *= corr;
-#pragma unroll
-            for (int j = 0; j < PA_KC; j++) {
-                s[k][j] = s[k][j] == -__builtin_huge_valf() ? 0.f : __expf(s[k][j] - mn);   // 0 where masked
-                l[k] += s[k][j];
-            }
-            m[k] = mn;
+        for (int r = 0; r < 16; r++) {
+            const int key = c0 + 8 * (r / 4) + 4 * h + r % 4;
+            const float v = key <= qpos ? sc[r] : -__builtin_huge_valf();
+            sc[r] = v;
+            mx = fmaxf(mx, v);
         }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // a query that has seen no position yet keeps m = -inf, l = 0, o = 0
+        const float mn = fmaxf(m, mx);
+        const float corr = m == -__builtin_huge_valf() ? 0.f : __expf(m - mn);
+        float ls = 0.f;
 #pragma unroll
-        for (int j = 0; j < PA_KC; j++) {
-#pragma unroll
-            for (int i = 0; i < NI; i++) {
-                const float4 v4 = *reinterpret_cast<const float4 *>(&Vs[sub * PA_KC + j][4 * qq + 4 * PA_TPR * i]);
-#pragma unroll
-                for (int k = 0; k < PA_R; k++) {
-                    o[k][4 * i] = fmaf(s[k][j], v4.x, o[k][4 * i]);
-                    o[k][4 * i + 1] = fmaf(s[k][j], v4.y, o[k][4 * i + 1]);
-                    o[k][4 * i + 2] = fmaf(s[k][j], v4.z, o[k][4 * i + 2]);
-                    o[k][4 * i + 3] = fmaf(s[k][j], v4.w, o[k][4 * i + 3]);
-                }
-            }
+        for (int r = 0; r < 16; r++) {
+            const float p = sc[r] == -__builtin_huge_valf() ? 0.f : __expf(sc[r] - mn);
+            sc[r] = p;
+            ls += p;
         }
+        ls += __shfl_xor(ls, 32);
+        l = l * corr + ls;
+        m = mn;
+        pm_h8 pb[2];
+#pragma unroll
+        for (int r = 0; r < 16; r++) pb[r / 8][r % 8] = (_Float16)sc[r];
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            o[j] *= corr;
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const _Float16 *vr = &Vt[(32 * j + li) * VLD + 16 * k + 4 * h];
+                const pm_h4 lo = *reinterpret_cast<const pm_h4 *>(vr);
+                const pm_h4 hi = *reinterpret_cast<const pm_h4 *>(vr + 8);
+                const pm_h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[k], o[j], 0, 0, 0);
+            }
         }
     }
+    if (t >= T) return;
+    const long long row = (long long)t * NQ + kvh * G + g;
+    const float inv = nsplit == 1 ? 1.0f / l : 1.f;
+    float *dst = nsplit == 1 ? out + row * D : part + (row * nsplit + blockIdx.z) * (D + 2);
 #pragma unroll
-    for (int k = 0; k < PA_R; k++) {
-        const int rr = rg * PA_R + k, g = rr % G, t = blockIdx.y * QB + rr / G;
-        if (t >= T) continue;
-        const long long row = (long long)t * NQ + kvh * G + g;
-        if (nsplit == 1) {
-            const float inv = 1.0f / l[k];
-            float *dst = out + row * D + 4 * qq;
+    for (int j = 0; j < NT; j++)
 #pragma unroll
-            for (int i = 0; i < NI; i++)
-                *reinterpret_cast<float4 *>(dst + 4 * PA_TPR * i) =
-                    make_float4(o[k][4 * i] * inv, o[k][4 * i + 1] * inv, o[k][4 * i + 2] * inv, o[k][4 * i + 3] * inv);
-        } else {
-            float *dst = part + (row * nsplit + blockIdx.z) * (D + 2);
-#pragma unroll
-            for (int i = 0; i < NI; i++)
-                *reinterpret_cast<float4 *>(dst + 4 * qq + 4 * PA_TPR * i) =
-                    make_float4(o[k][4 * i], o[k][4 * i + 1], o[k][4 * i + 2], o[k][4 * i + 3]);
-            if (qq == 0) {
-                dst[D] = m[k];
-                dst[D + 1] = l[k];
-            }
-        }
+        for (int r4 = 0; r4 < 4; r4++)
+            *reinterpret_cast<float4 *>(dst + 32 * j + 8 * r4 + 4 * h) =
+                make_float4(o[j][4 * r4] * inv, o[j][4 * r4 + 1] * inv, o[j][4 * r4 + 2] * inv, o[j][4 * r4 + 3] * inv);
+    if (nsplit > 1 && h == 0) {
+        dst[D] = m;
+        dst[D + 1] = l;
     }
 }
 
@@ -429,8 +390,8 @@ static hipError_t launch_pf_attn(int G, const float *qb, const float *kc, const 
     const int ks = pf_split_size(pos0 + T), nsplit = (pos0 + T + ks - 1) / ks;
 #define TBQ_PFA(GG)                                                                                                \
     case GG:                                                                                                       \
-        hipLaunchKernelGGL((k_pf_attn<D, GG>), dim3(NKV, (T + PA_ROWS / GG - 1) / (PA_ROWS / GG), nsplit),         \
-                           dim3(PA_THREADS), 0, st, qb, kc, vc, T, pos0, NQ, max_ctx, ks, nsplit, part, out);      \
+        hipLaunchKernelGGL((k_pf_attn<D, GG>), dim3(NKV, (T + PM_Q / GG - 1) / (PM_Q / GG), nsplit),               \
+                           dim3(PM_THREADS), 0, st, qb, kc, vc, T, pos0, NQ, max_ctx, ks, nsplit, part, out);      \
         break;
     switch (G) {
         TBQ_PFA(1) TBQ_PFA(2) TBQ_PFA(4) TBQ_PFA(8)
