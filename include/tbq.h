@@ -182,16 +182,14 @@ int tbq_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits
  * pos0 + T - 1 in one batched pass per layer, replacing the reference's
  * token-by-token prefill (layer4/tb_infer.c:1068-1075, one tb_infer_decode
  * step per prompt token).  Writes the K/V rows of every position and the
- * logits of the last token.  Models whose layers have fused q|k|v and
- * gate|up matrices, all Q4_K in the reference's layout, with hidden,
- * n_heads*head_dim and ffn among the MFMA kernel's row lengths (256..4096
- * in steps it is built for, 2560 and 9728 included) and hidden <= 8192,
- * take the batched path (fp16-operand MFMA GEMMs, fp32 accumulate: logits
- * within 1e-2 relative L2 of the sequential decode); every other model
- * runs the decode step once per token (identical to T tbq_dense_decode
- * calls).  tokens_host is read by an asynchronous copy on `stream`: keep it
- * valid until the stream has run the call.  1 <= T <= 65536,
- * pos0 + T <= max_ctx. */
+ * logits of the last token.  Models with hidden <= 8192 take the batched
+ * path for T >= 2, whatever their formats or layouts: each weight matrix
+ * dequantised to fp16 and multiplied by rocBLAS, attention on fp16 MFMA,
+ * fp32 accumulation (logits within 1e-2 relative L2 of the sequential
+ * decode); otherwise, and for T = 1, the decode step runs once per token
+ * (identical to T tbq_dense_decode calls).  tokens_host is read by an
+ * asynchronous copy on `stream`: keep it valid until the stream has run
+ * the call.  1 <= T <= 65536, pos0 + T <= max_ctx. */
 size_t tbq_dense_prefill_workspace_size(const tbq_dense_model *m, int T);
 int tbq_dense_prefill(const tbq_dense_model *m, const int *tokens_host, int T, int pos0, float *logits,
                       void *workspace, size_t ws_bytes, void *stream);
