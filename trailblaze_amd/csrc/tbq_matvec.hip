@@ -125,8 +125,65 @@ __global__ __launch_bounds__(256) void k_dequant_f16(const uint8_t *__restrict__
     }
 }
 
+// Q4_K to fp16: thread t writes weights 8t .. 8t + 7 (16 contiguous bytes,
+// so a wave's stores are one contiguous run): 64-weight unit u = t / 8
+// (super-block u / 4, quant bytes 32p .. 32p + 31, p = u % 4), part
+// k = t % 8; the unit's header is read by its 8 threads (cache hits) and
+// each reads only its quant dwords.  Values as decode8 rounds them
+// (fl(fl(d*s)*q) - fl(dmin*m)), then fp16.  GG: ggml's layout (byte i of
+// the run: element i of sub-block 2p low, of 2p+1 high; get_scale_min_k4;
+// IEEE fp16 d).
+template <bool GG>
+__global__ __launch_bounds__(256) void k_dequant_f16_q4k(const uint8_t *__restrict__ W, long long n8,
+                                                         _Float16 *__restrict__ out) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    for (long long t = blockIdx.x * 256ll + threadIdx.x; t < n8; t += (long long)gridDim.x * 256) {
+        const long long u = t >> 3;
+        const int k = (int)(t & 7), p = (int)(u & 3);
+        const uint8_t *b = W + (u >> 2) * 144;
+        const uint4 hdr = *reinterpret_cast<const uint4 *>(b);
+        const uint8_t *run = b + 16 + 32 * p;
+        int si, mi;
+        float d, dmin;
+        uint32_t q[2];
+        int sh = 0;
+        if constexpr (GG) {   // weights 8k + i: bytes 8(k % 4) + i, nibble k / 4
+            d = f16_ieee(hdr.x & 0xFFFFu);
+            dmin = f16_ieee(hdr.x >> 16);
+            gq4k_sm(hdr, p, k >> 2, si, mi);
+            const uint2 v = *reinterpret_cast<const uint2 *>(run + 8 * (k & 3));
+            q[0] = v.x;
+            q[1] = v.y;
+            sh = 4 * (k >> 2);
+        } else {              // weights 8k + i: byte 4k + i / 2, nibble i % 2
+            d = f16_ref(hdr.x & 0xFFFFu);
+            dmin = f16_ref(hdr.x >> 16);
+            q4k_scale_min(b, 2 * p + (k >> 2), si, mi);
+            q[0] = *reinterpret_cast<const uint32_t *>(run + 4 * k);
+            q[1] = 0;
+        }
+        const float S = d * (float)si, Mn = dmin * (float)mi;
+        h8 v;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int qq = GG ? (int)((q[i >> 2] >> (8 * (i & 3) + sh)) & 15)
+                              : (int)((q[0] >> (8 * (i >> 1) + 4 * (i & 1))) & 15);
+            const float tt = S * (float)qq;
+            v[i] = (_Float16)(tt - Mn);
+        }
+        *reinterpret_cast<h8 *>(out + t * 8) = v;
+    }
+}
+
 template <int QT>
 static hipError_t launch_dequant_f16_t(const void *W, long long nweights, _Float16 *out, hipStream_t s) {
+    if constexpr (QT == QT_Q4_K || QT == QT_GQ4_K) {
+        const long long n8 = nweights / 8, blocks = (n8 + 255) / 256;
+        const int grid = (int)(blocks < 65536 ? blocks : 65536);
+        hipLaunchKernelGGL((k_dequant_f16_q4k<QT == QT_GQ4_K>), dim3(grid), dim3(256), 0, s, (const uint8_t *)W, n8,
+                           out);
+        return hipGetLastError();
+    }
     const long long n8 = nweights / 8, blocks = (n8 + 255) / 256;
     const int grid = (int)(blocks < 65536 ? blocks : 65536);
     hipLaunchKernelGGL((k_dequant_f16<QT>), dim3(grid), dim3(256), 0, s, (const uint8_t *)W, n8, out);
