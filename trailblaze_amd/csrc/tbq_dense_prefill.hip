@@ -196,24 +196,49 @@ __global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, con
 
 // Row t: a = silu(g * s) * (u * s) with gu[t] = [g (F) | u (F)] and s =
 // gs[t], then a16[t] = a * 2^e in fp16 (max |a| in [2^14, 2^15)) and
-// ainv[t] = 2^-e.  grid = T, two passes over the row.
-__global__ __launch_bounds__(PN_THREADS) void k_pf_swiglu_f16(const float *__restrict__ gu, const float *__restrict__ gs,
+// ainv[t] = 2^-e.  grid = T, 1024 threads, the row read once (up to PS_V
+// float4 of g and of u per thread: F <= 16384).
+constexpr int PS_THREADS = 1024, PS_V = 4;
+__global__ __launch_bounds__(PS_THREADS) void k_pf_swiglu_f16(const float *__restrict__ gu, const float *__restrict__ gs,
                                                               int F, _Float16 *__restrict__ a16,
                                                               float *__restrict__ ainv) {
-    __shared__ float red[PN_THREADS / 64];
-    const int t = blockIdx.x, tid = threadIdx.x;
-    const float *g = gu + (long long)t * 2 * F, *u = g + F;
+    __shared__ float red[PS_THREADS / 64];
+    const int t = blockIdx.x, tid = threadIdx.x, n4 = F / 4;
+    const float4 *g = reinterpret_cast<const float4 *>(gu + (long long)t * 2 * F), *u = g + n4;
     const float s = gs[t];
+    float4 a[PS_V];
+#pragma unroll
+    for (int i = 0; i < PS_V; i++) {
+        const int j = min(tid + PS_THREADS * i, n4 - 1);   // clamped: loads stay unconditional
+        const float4 gv = g[j], uv = u[j];
+        a[i] = make_float4(pro_swiglu(gv.x * s, uv.x * s), pro_swiglu(gv.y * s, uv.y * s),
+                           pro_swiglu(gv.z * s, uv.z * s), pro_swiglu(gv.w * s, uv.w * s));
+    }
     float mx = 0.f;
-    for (int j = tid; j < F; j += PN_THREADS) mx = fmaxf(mx, fabsf(pro_swiglu(g[j] * s, u[j] * s)));
-    mx = pf_block_max(mx, red);
+#pragma unroll
+    for (int i = 0; i < PS_V; i++)
+        if (tid + PS_THREADS * i < n4)
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a[i].x), fabsf(a[i].y)), fmaxf(fabsf(a[i].z), fabsf(a[i].w))));
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < PS_THREADS / 64; i++) mx = fmaxf(mx, red[i]);
     int e = 0;
     frexpf(mx, &e);
     int sh = mx > 0.f ? 15 - e : 0;
     sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
     const float sc = ldexpf(1.f, sh);
-    _Float16 *ar = a16 + (long long)t * F;
-    for (int j = tid; j < F; j += PN_THREADS) ar[j] = (_Float16)(pro_swiglu(g[j] * s, u[j] * s) * sc);
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 *ar = reinterpret_cast<h4 *>(a16 + (long long)t * F);
+#pragma unroll
+    for (int i = 0; i < PS_V; i++) {
+        const int j = tid + PS_THREADS * i;
+        if (j < n4)
+            ar[j] = h4{(_Float16)(a[i].x * sc), (_Float16)(a[i].y * sc), (_Float16)(a[i].z * sc),
+                       (_Float16)(a[i].w * sc)};
+    }
     if (tid == 0) ainv[t] = ldexpf(1.f, -sh);
 }
 
@@ -409,10 +434,12 @@ static hipError_t launch_pf_attn(int G, const float *qb, const float *kc, const 
 // ---------------------------------------------------------------------------
 static size_t pf_up(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Every model with hidden <= 8192 (the norm kernel's row) takes the batched
-// path for T >= 2; its matrices, of any format and layout, are dequantised
+// Every model with hidden <= 8192 and ffn <= 16384 (the rows the norm and
+// SwiGLU kernels hold) takes the batched path for T >= 2; its matrices, of any format and layout, are dequantised
 // to fp16 one at a time and multiplied by rocBLAS.
-bool dense_prefill_batched(const tbq_dense_model *m) { return m->hidden <= PN_THREADS * PN_V * 4; }
+bool dense_prefill_batched(const tbq_dense_model *m) {
+    return m->hidden <= PN_THREADS * PN_V * 4 && m->ffn <= PS_THREADS * PS_V * 4;
+}
 
 struct PfWs {
     float *x, *y, *qkv, *qb, *att, *gu, *sa, *sb, *part;
@@ -526,7 +553,7 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
             if (err == hipSuccess) err = dq(qt_of(L.qt_up), L.wup, F, H, w.wh + (size_t)F * H);
         }
         if (err != hipSuccess || (err = pf_gemm(w.wh, w.h16, T, 2 * F, H, w.gu)) != hipSuccess) break;
-        hipLaunchKernelGGL(k_pf_swiglu_f16, dim3(T), dim3(PN_THREADS), 0, st, w.gu, w.sa, F, w.h16, w.sb);
+        hipLaunchKernelGGL(k_pf_swiglu_f16, dim3(T), dim3(PS_THREADS), 0, st, w.gu, w.sa, F, w.h16, w.sb);
         if ((err = dq(qt_of(L.qt_down), L.wdown, H, F, w.wh)) != hipSuccess) break;
         err = pf_gemm(w.wh, w.h16, T, H, F, w.y);
     }
