@@ -132,12 +132,25 @@ __global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, c
     if (tid == 0) hinv[t] = ldexpf(1.f, -sh);
 }
 
+// RoPE tables of the prompt's positions, shared by every layer: rc[t][j] =
+// cos, rc[t][D/2 + j] = sin of (pos0 + t) * theta^(-2j/D), formed and
+// reduced in fp64 exactly as the decode step's k_rope_table.  grid = T.
+__global__ __launch_bounds__(64) void k_pf_rope(int pos0, float theta, int D, float *__restrict__ rc) {
+    const int t = blockIdx.x, j = threadIdx.x;
+    if (j < D / 2) {
+        double sd, cd;
+        sincos((double)(pos0 + t) * pow((double)theta, -2.0 * j / D), &sd, &cd);
+        rc[(long long)t * D + j] = (float)cd;
+        rc[(long long)t * D + D / 2 + j] = (float)sd;
+    }
+}
+
 // Head vector (one wave; lane l holds elements l and l + 64, or l for
-// D = 64): RMSNorm with the head's weights, then rotate-half RoPE at
-// position pos, the angle formed as the decode step's table forms it.
+// D = 64): RMSNorm with the head's weights, then rotate-half RoPE with the
+// position's table row rc (cos | sin).
 template <int D>
-__device__ __forceinline__ void pf_norm_rope(float (&x)[D / 64], const float *__restrict__ w, int pos, float theta,
-                                             float eps) {
+__device__ __forceinline__ void pf_norm_rope(float (&x)[D / 64], const float *__restrict__ w,
+                                             const float *__restrict__ rc, float eps) {
     const int lane = threadIdx.x & 63;
     float ss = 0.f;
 #pragma unroll
@@ -147,9 +160,7 @@ __device__ __forceinline__ void pf_norm_rope(float (&x)[D / 64], const float *__
 #pragma unroll
     for (int i = 0; i < D / 64; i++) x[i] = x[i] * r * w[lane + 64 * i];
     const int j = lane % (D / 2);
-    double sd, cd;
-    sincos((double)pos * pow((double)theta, -2.0 * j / D), &sd, &cd);
-    const float cs = (float)cd, sn = (float)sd;
+    const float cs = rc[j], sn = rc[D / 2 + j];
     if constexpr (D == 128) {
         const float a = x[0], b = x[1];
         x[0] = a * cs - b * sn;
@@ -168,8 +179,9 @@ __device__ __forceinline__ void pf_norm_rope(float (&x)[D / 64], const float *__
 template <int D>
 __global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, const float *__restrict__ rs,
                                               const float *__restrict__ qn, const float *__restrict__ kn, int NQ,
-                                              int NKV, int pos0, float theta, float eps, float *__restrict__ kc,
-                                              float *__restrict__ vc, int max_ctx, float *__restrict__ qb) {
+                                              int NKV, int pos0, const float *__restrict__ rope, float eps,
+                                              float *__restrict__ kc, float *__restrict__ vc, int max_ctx,
+                                              float *__restrict__ qb) {
     const int t = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
     const int QKVR = (NQ + 2 * NKV) * D, pos = pos0 + t;
     const float sc = rs[t];   // row t of qkv is scaled by 1 / rs[t]
@@ -177,7 +189,7 @@ __global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, con
     float x[D / 64];
 #pragma unroll
     for (int i = 0; i < D / 64; i++) x[i] = src[lane + 64 * i] * sc;
-    pf_norm_rope<D>(x, hh < NQ ? qn : kn, pos, theta, eps);
+    pf_norm_rope<D>(x, hh < NQ ? qn : kn, rope + (long long)t * D, eps);
     if (hh < NQ) {
         const float scale = 1.0f / sqrtf((float)D);
 #pragma unroll
@@ -442,7 +454,7 @@ bool dense_prefill_batched(const tbq_dense_model *m) {
 }
 
 struct PfWs {
-    float *x, *y, *qkv, *qb, *att, *gu, *sa, *sb, *part;
+    float *x, *y, *qkv, *qb, *att, *gu, *sa, *sb, *part, *rope;
     _Float16 *h16, *wh;
     int *tok;
     void *dec;
@@ -474,6 +486,7 @@ static PfWs pf_ws(const tbq_dense_model *m, int T, void *ws, size_t *total) {
         w.sa = (float *)take((size_t)T * 4);
         w.sb = (float *)take((size_t)T * 4);
         w.wh = (_Float16 *)take(wmax * 2);
+        w.rope = (float *)take((size_t)T * m->head_dim * 4);
         // attention split partials: a prefill reaching position kmax - 1 uses
         // min(PA_MAX_SPLIT, ceil(kmax / PA_PREF_KS)) splits, and kmax <= max_ctx
         const int ns = std::min(PA_MAX_SPLIT, (m->max_ctx + PA_PREF_KS - 1) / PA_PREF_KS);
@@ -517,6 +530,7 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
     std::lock_guard<std::mutex> lk(g_rb_mu);
     if (!g_rb && rocblas_create_handle(&g_rb) != rocblas_status_success) return hipErrorUnknown;
     if (rocblas_set_stream(g_rb, st) != rocblas_status_success) return hipErrorUnknown;
+    hipLaunchKernelGGL(k_pf_rope, dim3(T), dim3(64), 0, st, pos0, m->rope_theta, D, w.rope);
     hipError_t err = launch_dequant_rows(canon_qt(m->qtype_embd), m->tok_embd, w.tok, T, H, w.x, st);
     for (int l = 0; l < m->n_layers && err == hipSuccess; l++) {
         const tbq_dense_layer &L = m->layers[l];
@@ -534,11 +548,11 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
         if (err != hipSuccess || (err = pf_gemm(w.wh, w.h16, T, QKVR, H, w.qkv)) != hipSuccess) break;
         if (D == 128) {
             hipLaunchKernelGGL(k_pf_qk<128>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, w.sa, L.q_norm, L.k_norm, NQ,
-                               NKV, pos0, m->rope_theta, m->norm_eps, kc, vc, m->max_ctx, w.qb);
+                               NKV, pos0, w.rope, m->norm_eps, kc, vc, m->max_ctx, w.qb);
             err = launch_pf_attn<128>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, st);
         } else {
             hipLaunchKernelGGL(k_pf_qk<64>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, w.sa, L.q_norm, L.k_norm, NQ,
-                               NKV, pos0, m->rope_theta, m->norm_eps, kc, vc, m->max_ctx, w.qb);
+                               NKV, pos0, w.rope, m->norm_eps, kc, vc, m->max_ctx, w.qb);
             err = launch_pf_attn<64>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, st);
         }
         if (err != hipSuccess || (err = launch_rows_f16(w.att, T, QD, w.h16, w.sb, st)) != hipSuccess) break;
