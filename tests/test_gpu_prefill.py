@@ -9,8 +9,6 @@ token by token, layer4/tb_infer.c:1068-1075), through the C-ABI:
     empty cache and after decoded tokens, head_dim 64 and 128, GQA 2, 4, 8;
   * a one-token prefill is the decode step itself (bit-identical);
   * argument checks."""
-import ctypes as C
-
 import numpy as np
 import pytest
 
@@ -133,7 +131,7 @@ def test_prefill_separate_matrices(oracle):
     from gguf_write import dense_gguf_tensors, write_gguf
     from oracle.dense import DenseOracle
     from trailblaze_amd import synth
-    from trailblaze_amd.gguf import GgufFile
+    from trailblaze_amd.gguf import GgufFile, dense_prefill
     cfg = _cfg(n_layers=1, vocab=256, max_ctx=128)
     r = np.random.default_rng(48)
     norm = lambda n: (1.0 + 0.1 * r.standard_normal(n)).astype(np.float32)
@@ -153,13 +151,10 @@ def test_prefill_separate_matrices(oracle):
         with GgufFile(path) as g:
             m, ws = g.dense_model(cfg.max_ctx)
             assert not m.layers[0].wqkv and not m.layers[0].wgu
-            toks = np.ascontiguousarray(r.integers(0, 256, 50), dtype=np.int32)
-            n = int(tb.lib().tbq_dense_prefill_workspace_size(C.byref(m), len(toks)))
-            pw = torch.empty(n, dtype=torch.uint8, device="cuda")
+            toks = r.integers(0, 256, 50)
             logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
             print("prefill separate matrices", flush=True)
-            assert tb.lib().tbq_dense_prefill(C.byref(m), toks.ctypes.data, len(toks), 0, C.c_void_p(logits.data_ptr()),
-                                              C.c_void_p(pw.data_ptr()), n, None)
+            dense_prefill(m, toks, 0, logits)
             for pos, tok in enumerate(toks):
                 want = ref.decode(tok, pos)
             assert rel_l2(host(logits), want) <= PREFILL_TOL

@@ -116,3 +116,19 @@ def dense_decode(m, ws, token: int, pos: int, logits, stream=None):
     _check(lib().tbq_dense_decode(C.byref(m), token, pos, _ptr(logits), _ptr(ws), ws.numel(), _stream(stream)),
            "tbq_dense_decode")
     return logits
+
+
+def dense_prefill(m, tokens, pos0: int, logits, stream=None):
+    """tbq_dense_prefill on a model from ``GgufFile.dense_model``: the last
+    token's logits; the workspace is allocated per call."""
+    import numpy as np
+    import torch
+    toks = np.ascontiguousarray(tokens, dtype=np.int32)
+    n = int(lib().tbq_dense_prefill_workspace_size(C.byref(m), len(toks)))
+    _check(n > 0, "tbq_dense_prefill_workspace_size")
+    ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+    _check(lib().tbq_dense_prefill(C.byref(m), toks.ctypes.data, len(toks), pos0, _ptr(logits), _ptr(ws), n,
+                                   _stream(stream)), "tbq_dense_prefill")
+    torch.cuda.synchronize()   # the token copy has run before `toks` goes away
+    return logits
+
