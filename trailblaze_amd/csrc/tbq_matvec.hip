@@ -158,7 +158,13 @@ __global__ __launch_bounds__(256) void k_dequant_f16_q4k(const uint8_t *__restri
         } else {              // weights 8k + i: byte 4k + i / 2, nibble i % 2
             d = f16_ref(hdr.x & 0xFFFFu);
             dmin = f16_ref(hdr.x >> 16);
-            q4k_scale_min(b, 2 * p + (k >> 2), si, mi);
+            // sub-block j = 2p + k / 4: j < 4 scale byte 4 + j (hdr.y), min
+            // byte 8 + j (hdr.z); j >= 4 scale byte 8 + j (hdr.w), min byte
+            // 12 + j (the block's first quant dword)
+            const int j = 2 * p + (k >> 2), jb = 8 * (j & 3);
+            const uint32_t mind = j < 4 ? hdr.z : *reinterpret_cast<const uint32_t *>(b + 16);
+            si = (int)(((j < 4 ? hdr.y : hdr.w) >> jb) & 63);
+            mi = (int)((mind >> jb) & 63);
             q[0] = *reinterpret_cast<const uint32_t *>(run + 4 * k);
             q[1] = 0;
         }
