@@ -269,7 +269,19 @@ def dense_leg(torch, stream):
         f"{T * us / 1e3:.0f} ms)")
     del m
     torch.cuda.empty_cache()
-    return dict(us_per_token=us, tokens_per_s=1e6 / us, matvec_us=mv_us, matvec_gbs=wbytes / mv_us / 1e3,
+    # the same model in ggml's layouts (Q4_K layers, Q6_K embedding), as a
+    # llama.cpp file holds it
+    from dataclasses import replace
+    mg = SyntheticDense(replace(c, qtype_layers=fm.GGML | fm.Q4_K, qtype_embd=fm.GGML | fm.Q6_K), seed=4)
+    mg.k_cache.normal_()
+    mg.v_cache.normal_()
+    sg = time_region(lambda: mg.decode(1234, pos, logits), reps, 3, stream)
+    ggml_us = sg / reps * 1e6
+    log(f"dense Qwen3-4B decode, ggml layouts: {ggml_us:.0f} us/token = {1e6 / ggml_us:.0f} tok/s")
+    del mg
+    torch.cuda.empty_cache()
+    return dict(us_per_token=us, tokens_per_s=1e6 / us, ggml_us_per_token=ggml_us,
+                matvec_us=mv_us, matvec_gbs=wbytes / mv_us / 1e3,
                 other_us=us - mv_us, weight_bytes=wbytes, kv_bytes=kv_bytes, hbm_bound_us=bound_us,
                 frac_of_bound=bound_us / us,
                 prefill_512=dict(ms=pf_ms, tokens_per_s=T / pf_ms * 1e3, layer_gemm_tflops=gemm_tflops))
