@@ -67,7 +67,8 @@ int tbq_dequant(const void *W, int qtype, int nrows, int K, float *out, void *st
 /* y[M] = dequant(W[M][K]) . x[K], fp32 accumulate (tb_gguf_dequant_matvec,
  * layer4/tb_gguf.h:95-96; device-resident form of tb_cuda_matvec_device,
  * layer4/tb_gguf_dequant.h:36-37).  K a multiple of 256 for super-block
- * formats, of 32 otherwise; W and x 16-byte aligned. */
+ * formats, of 32 otherwise, at most 32768 (x is staged in LDS; F32, F16 and
+ * BF16 rows at most 15360); W and x 16-byte aligned. */
 int tbq_matvec(const void *W, int qtype, int M, int K, const float *x, float *y, void *stream);
 
 /* Kernel choice for tbq_matvec (no counterpart in the reference: it has one
@@ -75,7 +76,7 @@ int tbq_matvec(const void *W, int qtype, int M, int K, const float *x, float *y,
  * FMA is the byte->fp32 fma kernel every format has; INTDOT is the Q4_K
  * v_dot4 kernel specialised for K <= 16384; KQ is the v_dot4 kernel shared
  * by Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 and Q8_K (K a multiple of 64,
- * at most 16384).  INTDOT and KQ fail for shapes they do not cover. */
+ * at most 32768).  INTDOT and KQ fail for shapes they do not cover. */
 #define TBQ_MV_AUTO 0
 #define TBQ_MV_FMA 1
 #define TBQ_MV_INTDOT 2
@@ -91,6 +92,8 @@ int tbq_matvec_variant(const void *W, int qtype, int M, int K, const float *x, f
  * -1 / 0.  E <= 256, top_k clamped to 8. */
 int tbq_route(const float *xn, const float *router, const float *bias, int T, int H, int E,
               int top_k, int *sel_idx, float *sel_w, void *stream);
+/* (tbq_route keeps its logits and arrival counters in a library-owned
+ * buffer: calls must be ordered on one stream.) */
 
 /* One MoE layer in the reference's packed expert layout
  * (layer4/tb_infer.c:780-806): gate/up are [E*F rows][H], down [E*H rows][F],
@@ -113,10 +116,14 @@ typedef struct {
 size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode);
 /* out[T][H] = resid + sum_slots w_slot * expert_slot(xn) for every token
  * (layer4/tb_infer.c:753-833,876).  sel_idx/sel_w ([T][8]) may be NULL.
- * workspace: device buffer of tbq_moe_workspace_size() bytes, zero-filled
- * before its first use (its first 256 KiB hold router arrival counters that
- * every call leaves at zero), or NULL to use a library-owned buffer (grown
- * on demand).  Calls that share a workspace must not overlap. */
+ * workspace: device buffer of tbq_moe_workspace_size() bytes whose first
+ * 256 KiB (router arrival counters, at the same offset whatever T and mode
+ * are) are zero before its first use; every call leaves them at zero.  Or
+ * NULL: one library-owned buffer, shared by every NULL-workspace call in the
+ * process and grown (freed and reallocated) on demand -- such calls must all
+ * be ordered on one stream, as a grow can free memory that a call still
+ * queued on another stream uses.  Calls that share a workspace must not
+ * overlap. */
 int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float *resid, float *out,
                     int *sel_idx, float *sel_w, void *workspace, size_t workspace_bytes, int mode,
                     void *stream);
@@ -173,7 +180,8 @@ size_t tbq_dense_workspace_size(const tbq_dense_model *m);
 /* logits[vocab] for `token` at position `pos` (0 <= pos < max_ctx); appends
  * the token's K and V at `pos` of every layer's cache and attends over
  * positions 0..pos.  head_dim 64 or 128; n_heads / n_kv_heads in {1, 2, 4,
- * 8}; hidden, ffn and n_heads*head_dim multiples of 256; max_ctx <= 131072.
+ * 8}; hidden, ffn and n_heads*head_dim multiples of 256 and at most 32768
+ * (the matvec row limit); max_ctx <= 131072.
  * Calls that share a workspace must not overlap. */
 int tbq_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *workspace,
                      size_t workspace_bytes, void *stream);

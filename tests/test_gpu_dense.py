@@ -147,6 +147,62 @@ def test_dense_decode_wide_hidden(oracle, qt):
         assert rel_l2(host(logits), ref.decode(tok, pos)) <= DENSE_TOL, pos
 
 
+def test_dense_decode_configs2_context_4096(oracle):
+    """BASELINE configs[2] at its context: two layers at the Qwen3-4B widths
+    (hidden 2560, 32 query / 8 kv heads of 128, ffn 9728, max_ctx 4096)
+    with every layer's cache filled N(0,1) up to position 4094; the step at
+    position 4095 attends over all 4096 positions, i.e. 32 attention chunks
+    merged by the combine kernel, in both layers (the cache's layer stride
+    at max_ctx 4096)."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=2, hidden=2560, n_heads=32, n_kv_heads=8, head_dim=128, ffn=9728, vocab=1024,
+                      max_ctx=4096)
+    m = _model(cfg, 40)
+    ref = DenseOracle(oracle, cfg, m.host)
+    rng = np.random.default_rng(4096)
+    P = 4095
+    kc = np.zeros(ref.kc.shape, np.float32)
+    vc = np.zeros(ref.vc.shape, np.float32)
+    kc[:, :, :P] = rng.standard_normal(kc[:, :, :P].shape, dtype=np.float32)
+    vc[:, :, :P] = rng.standard_normal(vc[:, :, :P].shape, dtype=np.float32)
+    m.k_cache.copy_(torch.from_numpy(kc))
+    m.v_cache.copy_(torch.from_numpy(vc))
+    ref.kc[:] = kc
+    ref.vc[:] = vc
+    del kc, vc
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    print("dense configs[2] step at position", P, flush=True)
+    m.decode(123, P, logits)
+    err = rel_l2(host(logits), ref.decode(123, P))
+    assert err <= DENSE_TOL, err
+    # the appended K/V rows of both layers
+    kcg = host(m.k_cache).reshape(ref.kc.shape)
+    vcg = host(m.v_cache).reshape(ref.vc.shape)
+    assert rel_l2(kcg[:, :, P], ref.kc[:, :, P]) <= DENSE_TOL
+    assert rel_l2(vcg[:, :, P], ref.vc[:, :, P]) <= DENSE_TOL
+
+
+@pytest.mark.parametrize("qt", [fm.Q4_K, fm.Q6_K])
+def test_dense_decode_ffn_beyond_16384(oracle, qt):
+    """ffn 17408 (Qwen3-14B's): the down matvec's rows are longer than 16384
+    weights, which the fused kernels do not stage; the step runs SwiGLU and
+    the down matvec (x over 6 wave slices) as launches of their own."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=1, hidden=512, n_heads=4, n_kv_heads=2, head_dim=128, ffn=17408, vocab=256,
+                      max_ctx=32, qtype_layers=qt)
+    m = _model(cfg, 17)
+    ref = DenseOracle(oracle, cfg, m.host)
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    for pos, tok in enumerate([3, 250]):
+        print("dense ffn 17408 step", pos, flush=True)
+        m.decode(tok, pos, logits)
+        assert rel_l2(host(logits), ref.decode(tok, pos)) <= DENSE_TOL, pos
+
+
 def test_dense_decode_rejects_bad_position():
     import torch
     from trailblaze_amd.dense import DenseConfig

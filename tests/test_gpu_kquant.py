@@ -145,6 +145,27 @@ def test_matvec_kq_kernel(oracle, qt, M, K):
     assert rel_l2(gpu_matvec(W, qt, M, K, x, tb.TBQ_MV_KQ), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
 
 
+@pytest.mark.parametrize("qt", KQ_FORMATS)
+@pytest.mark.parametrize("M,K", [(70, 17408), (129, 24576), (33, 32768)])
+def test_matvec_long_rows(oracle, qt, M, K):
+    """Rows longer than 16384 weights (FFN-down of models with FFN 17408 ..
+    32768): x staged over 6 or 8 wave slices with more than 64 KiB of LDS."""
+    print(f"long rows qt={qt} M={M} K={K}", flush=True)
+    rng = np.random.default_rng(M * 7 + K + qt)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, qt, M, K, x), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+
+
+def test_matvec_rejects_rows_beyond_limit():
+    import torch
+    W = empty(4096, torch.uint8)
+    x = empty(32768 + 256, torch.float32)
+    y = empty(4, torch.float32)
+    with pytest.raises(tb.TbqError):
+        tb.matvec(W, fm.Q4_K, 4, 32768 + 256, x, y)
+
+
 @pytest.mark.parametrize("qt", [fm.Q8_0, fm.Q4_0])
 @pytest.mark.parametrize("K", [64, 128, 192])
 def test_matvec_kq_short_rows(oracle, qt, K):
@@ -214,7 +235,7 @@ def test_reference_abi_matvec_device(oracle):
     L = tb.lib()
     assert L.tb_cuda_init() == 1
     rng = np.random.default_rng(9)
-    for qt, M, K in ((fm.Q4_K, 1000, 4096), (fm.Q2_K, 64, 768), (fm.Q6_K, 33, 2048)):
+    for qt, M, K in ((fm.Q4_K, 1000, 4096), (fm.Q2_K, 64, 768), (fm.Q6_K, 33, 2048), (fm.Q4_K, 40, 17408)):
         W = synth.kquant_matrix(qt, M, K, rng)
         x = synth.activations(K, rng)
         d = L.tb_cuda_upload_tensor(W.ctypes.data, W.nbytes)

@@ -264,6 +264,39 @@ def test_moe_host_block(oracle):
     assert rel_l2(out, g["out"]) <= TOL
 
 
+@pytest.mark.parametrize("H", [512, 2048])
+def test_moe_host_block_varying_batches(oracle, H):
+    """tbq_moe_block_host over a sequence of calls whose T and mode change,
+    so its cached buffer is reused at a smaller T and regrown at a larger
+    one: every call routes exactly and stays within tolerance.  H = 512 and
+    2048 take the router whose per-token arrival counters live in the
+    workspace (T < 32), the path a misplaced or unzeroed counter area
+    breaks."""
+    F, E, k = 256, 16, 4
+    router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=H + 7)
+    L = tb.moe_layer(H, F, E, k, fm.Q4_K, dev(router), dev(gate), dev(up), dev(down))
+    import torch
+    torch.cuda.synchronize()
+    for i, (T, mode) in enumerate([(5, tb.TBQ_MOE_FP32), (1, tb.TBQ_MOE_FP32), (16, tb.TBQ_MOE_FP32),
+                                   (1, tb.TBQ_MOE_FP32), (40, tb.TBQ_MOE_BF16), (1, tb.TBQ_MOE_FP32),
+                                   (3, tb.TBQ_MOE_BF16), (2, tb.TBQ_MOE_FP32)]):
+        print(f"host block H={H} call {i}: T={T} mode={mode}", flush=True)
+        rng = np.random.default_rng(1000 * H + i)
+        xn = synth.activations((T, H), rng)
+        resid = synth.activations((T, H), rng)
+        out = np.zeros((T, H), np.float32)
+        idx = np.full((T, 8), 77, np.int32)
+        w = np.zeros((T, 8), np.float32)
+        ok = tb.lib().tbq_moe_block_host(C.byref(L), T, xn.ctypes.data, resid.ctypes.data, out.ctypes.data,
+                                         idx.ctypes.data, w.ctypes.data, mode)
+        assert ok == 1, tb.lib().tbq_last_error()
+        ref, ridx, rw = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
+        assert np.array_equal(idx, ridx), (T, mode)
+        assert bits_equal(w, rw), (T, mode)
+        tol = TOL if mode == tb.TBQ_MOE_FP32 else 1e-2
+        assert rel_l2(out - resid, ref - resid) <= tol, (T, mode)
+
+
 # ---------------------------------------------------------------------------
 # Prefill: grouped fp16 MFMA experts (tolerance 1e-2 rel-L2, routing exact)
 # ---------------------------------------------------------------------------

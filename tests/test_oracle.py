@@ -297,6 +297,143 @@ def test_route_vs_compiled_reference(oracle, reference):
 
 
 # --------------------------------------------------------------------------
+# The CPU timing baseline's restatement (tbo_matvec_q4k_avx512s): the
+# oracle's Q4_K decode with tb_dot_q4k_avx512's per-super-block partial sums
+# (src/tb_analog_dispatch.c:486-524) -- a different summation order only.
+# --------------------------------------------------------------------------
+def _q4k_integer_matrix(M, K, rng):
+    """Q4_K rows whose weights are their nibbles: d = 1, dmin = 0, every
+    scale = 1 (scale bytes sc[0..3] and sc[8..11], block offsets 4..7 and
+    12..15; the mins are multiplied by dmin = 0)."""
+    W = synth.kquant_matrix(fm.Q4_K, M, K, rng).reshape(M, K // 256, 144)
+    W[:, :, 0:2] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)
+    W[:, :, 2:4] = 0
+    W[:, :, 4:8] = 1
+    W[:, :, 8:12] = 0
+    W[:, :, 12:16] = 1
+    return W.reshape(M, -1)
+
+
+def _q4k_nibbles(W, M, K):
+    qs = W.reshape(M, K // 256, 144)[:, :, 16:].astype(np.int64)
+    out = np.empty((M, K // 256, 256), np.int64)
+    out[:, :, 0::2] = qs & 15
+    out[:, :, 1::2] = qs >> 4
+    return out.reshape(M, K)
+
+
+def test_avx512_restatement_exact_on_integers(oracle):
+    """Integer weights (the nibbles) and integer x: every product and
+    partial sum is exact in fp32, so both summation orders give the exact
+    integer dot; a dropped block, a wrong nibble order or a misplaced x
+    index fails.  One-hot x picks one dequantised column exactly."""
+    rng = np.random.default_rng(44)
+    M, K = 64, 4096
+    W = _q4k_integer_matrix(M, K, rng)
+    q = _q4k_nibbles(W, M, K)
+    assert np.array_equal(oracle.dequant_rows(W, fm.Q4_K, M, K), q.astype(np.float32))
+    x = rng.integers(-8, 9, K).astype(np.float32)
+    exact = (q @ x.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(oracle.matvec_q4k_avx512s(W, M, K, x), exact)
+    assert np.array_equal(oracle.matvec(W, fm.Q4_K, M, K, x), exact)
+    Wr = synth.kquant_matrix(fm.Q4_K, M, K, rng)
+    deq = oracle.dequant_rows(Wr, fm.Q4_K, M, K)
+    for k in (0, 31, 32, 255, 256, 1000, 4095):
+        e = np.zeros(K, np.float32)
+        e[k] = 1.0
+        assert bits_equal(oracle.matvec_q4k_avx512s(Wr, M, K, e), deq[:, k])
+
+
+def test_avx512_restatement_close_to_sequential_at_config0(oracle):
+    """BASELINE configs[0] (Q4_K 4096 x 4096): the restatement's blocked sum
+    is within the matvec tolerance of the sequential reference sum."""
+    from conftest import rel_l2
+    rng = np.random.default_rng(0)
+    M = K = 4096
+    W = synth.kquant_matrix(fm.Q4_K, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(oracle.matvec_q4k_avx512s(W, M, K, x), oracle.matvec(W, fm.Q4_K, M, K, x)) <= 1e-5
+
+
+# --------------------------------------------------------------------------
+# Q8_K activation quantiser (tbo_quantize_q8k).  The reference fixes only
+# the block layout (layer4/tb_gguf.c:281-288: f32 d at 0, int8 qs[256] at 4,
+# int16 bsums[16] at 260); what a max-abs quantiser must satisfy is fixed by
+# the mathematics, and the reference's own Q8_K decoder reads its blocks.
+# --------------------------------------------------------------------------
+def _q8k_fields(blocks):
+    b = blocks.reshape(-1, 292)
+    d = b[:, 0:4].copy().view(np.float32)[:, 0]
+    q = b[:, 4:260].view(np.int8).astype(np.int64)
+    bs = b[:, 260:292].copy().view(np.int16).astype(np.int64)
+    return d, q, bs
+
+
+def _q8k_inputs(rng):
+    x = [rng.standard_normal(1024).astype(np.float32),
+         (rng.standard_normal(512) * 1e-30).astype(np.float32),
+         (rng.standard_normal(512) * 1e30).astype(np.float32),
+         np.zeros(256, np.float32),
+         np.full(256, -3.25, np.float32)]
+    o = rng.standard_normal(768).astype(np.float32)
+    o[rng.choice(768, 5, replace=False)] *= 1000.0   # outlier channels
+    x.append(o)
+    return np.concatenate(x)
+
+
+def test_q8k_quantiser_invariants(oracle):
+    rng = np.random.default_rng(8)
+    x = _q8k_inputs(rng)
+    d, q, bs = _q8k_fields(oracle.quantize_q8k(x))
+    xb = x.reshape(-1, 256).astype(np.float64)
+    amax = np.abs(x.reshape(-1, 256)).max(1)
+    # d = fl(max|x| / 127)
+    assert bits_equal(d, amax / np.float32(127.0))
+    assert np.all(np.abs(q) <= 127)
+    # every value within half a step (plus the rounding of 1/d and x/d)
+    err = np.abs(xb - d[:, None].astype(np.float64) * q)
+    assert np.all(err <= d[:, None].astype(np.float64) * (0.5 + 1e-4))
+    # the largest |x| of a block maps to +-127 with its sign
+    nz = amax > 0
+    j = np.abs(xb).argmax(1)
+    rows = np.arange(len(j))
+    assert np.all(np.abs(q[rows, j])[nz] == 127)
+    assert np.all(np.sign(q[rows, j])[nz] == np.sign(xb[rows, j])[nz])
+    # the all-zero block quantises to zeros with d = 0
+    assert np.all(d[~nz] == 0) and not q[~nz].any()
+    # bsums = sums of the quants over each 16-element group
+    assert np.array_equal(bs, q.reshape(-1, 16, 16).sum(-1))
+    # rint: an x exactly halfway between two steps rounds to even
+    h = np.zeros(256, np.float32)
+    h[0] = 127.0
+    h[1] = 2.5
+    h[2] = -3.5
+    _, qh, _ = _q8k_fields(oracle.quantize_q8k(h))
+    assert (qh[0, 0], qh[0, 1], qh[0, 2]) == (127, 2, -4)
+
+
+def test_q8k_blocks_decode_with_reference_layout(oracle):
+    """The quantised blocks decode, through the oracle's Q8_K decoder (bit-
+    exact to the reference's, pinned by the golden vectors), to d * q."""
+    rng = np.random.default_rng(9)
+    x = _q8k_inputs(rng)
+    blocks = oracle.quantize_q8k(x)
+    d, q, _ = _q8k_fields(blocks)
+    n = x.size
+    w = oracle.dequant_rows(blocks, fm.Q8_K, 1, n)[0]
+    assert bits_equal(w, (d[:, None] * q.astype(np.float32)).reshape(-1))
+
+
+def test_q8k_blocks_decode_with_compiled_reference(oracle, reference):
+    rng = np.random.default_rng(10)
+    x = _q8k_inputs(rng)
+    blocks = oracle.quantize_q8k(x)
+    d, q, _ = _q8k_fields(blocks)
+    w = reference.dequant_rows(blocks, fm.Q8_K, 1, x.size, blocks.size)[0]
+    assert bits_equal(w, (d[:, None] * q.astype(np.float32)).reshape(-1))
+
+
+# --------------------------------------------------------------------------
 # Dense decode oracle (oracle/dense.py): closed forms that a wrong index,
 # sign or pairing breaks.
 # --------------------------------------------------------------------------

@@ -5,6 +5,7 @@
 
 #include <mutex>
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -60,7 +61,19 @@ bool known_qtype(int qt) {
 
 hipStream_t S(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
+// TBQ_FORCE_NO_DEVICE=1 in the environment (read at the first call) makes
+// libtbq behave as on a host without a GPU: tbq_init and every call that
+// needs the device return 0, so tb_cuda_init returns 0, uploads return NULL
+// and tb_cuda_matvec_device returns 0 -- the caller's CPU fallback
+// (layer4/tb_gguf.c:444-451) -- without any HIP call.
+bool forced_no_device() {
+    const char *v = getenv("TBQ_FORCE_NO_DEVICE");
+    return v && *v && strcmp(v, "0") != 0;
+}
+
 int ensure_init() {
+    static const bool forced = forced_no_device();
+    if (forced) return fail("no HIP device available (TBQ_FORCE_NO_DEVICE is set)");
     std::call_once(g_init_once, [] {
         int n = 0;
         if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return;
@@ -84,6 +97,11 @@ const char *tbq_last_error(void) { return g_err; }
 
 // Error setter for libtbq's C11 host files (hidden: not part of the ABI).
 __attribute__((visibility("hidden"))) int tbq_host_fail(const char *msg) { return fail("%s", msg); }
+// Synchronous zero fill for the C11 host files (hidden).
+__attribute__((visibility("hidden"))) int tbq_host_zero(void *dev, size_t bytes) {
+    if (!dev) return fail("tbq_host_zero: null pointer");
+    return hip_ok(hipMemset(dev, 0, bytes), "hipMemset");
+}
 const char *tbq_device_name(void) { return g_name; }
 int tbq_cu_count(void) { return g_cu; }
 
@@ -125,7 +143,7 @@ static int check_matvec(const void *W, int qt, int M, int K, const float *x, con
     if (!known_qtype(qt)) return fail("unsupported qtype %d", qt);
     int chunk = block_weights(qt) == 256 ? 256 : 32;
     if (M < 0 || K <= 0 || K % chunk) return fail("K=%d must be a positive multiple of %d for qtype %d", K, chunk, qt);
-    if (K > 16384) return fail("K=%d exceeds the LDS-resident x limit (16384)", K);
+    if (K > TBQ_MAX_K) return fail("K=%d exceeds the LDS-resident x limit (%d)", K, TBQ_MAX_K);
     if (!W || !x || !y) return fail("null pointer");
     if (!aligned16(x)) return fail("x must be 16-byte aligned");
     if (((qt & 0xFF) == QT_Q4_K || (qt & 0xFF) == QT_Q5_K || qt == QT_F32) && !aligned16(W))
@@ -169,6 +187,9 @@ int tbq_matvec(const void *W, int qt, int M, int K, const float *x, float *y, vo
 // entry to every call and left zero on exit.
 constexpr int MAX_TOKENS = 65536;
 constexpr size_t COUNTER_BYTES = (size_t)MAX_TOKENS * 4;
+
+// For the C11 host files (hidden): the counter area of a MoE workspace.
+__attribute__((visibility("hidden"))) size_t tbq_moe_counter_bytes(void) { return COUNTER_BYTES; }
 
 int tbq_route(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
               int *sel_idx, float *sel_w, void *s) {
@@ -287,6 +308,9 @@ static int check_dense(const tbq_dense_model *m) {
     if (m->max_ctx > 131072) return fail("tbq_dense: max_ctx above 131072");
     if (m->hidden % 256 || m->ffn % 256 || (m->n_heads * m->head_dim) % 256)
         return fail("tbq_dense: hidden, ffn and n_heads*head_dim must be multiples of 256");
+    if (m->hidden > TBQ_MAX_K || m->ffn > TBQ_MAX_K || m->n_heads * m->head_dim > TBQ_MAX_K)
+        return fail("tbq_dense: hidden, ffn and n_heads*head_dim must be at most %d (the matvec row limit)",
+                    TBQ_MAX_K);
     if (!tbq_qtype_supported(m->qtype_layers) || !tbq_qtype_supported(m->qtype_embd))
         return fail("tbq_dense: unsupported qtype");
     if (!m->tok_embd || !m->lm_head || !m->output_norm || !m->k_cache || !m->v_cache)

@@ -280,9 +280,12 @@ __global__ __launch_bounds__(256) void k_pf_scale_row(float *__restrict__ y, con
 // PA_KF), so the heavy blocks of a causal prompt (whose queries see every
 // earlier position) spread over several workgroups.  With nsplit > 1 each
 // writes its queries' unnormalised output, running max and denominator to
-// part[(row * nsplit + z) * (D + 2)], and k_pf_attn_combine merges the
-// splits a row reaches.
+// the record part[(row * nsplit + z) * pf_rec(D)] (D outputs, max,
+// denominator, two floats of padding so that every record starts 16-byte
+// aligned for the float4 stores), and k_pf_attn_combine merges the splits a
+// row reaches.
 constexpr int PM_THREADS = 256, PM_Q = 128, PM_KC = 32;
+__host__ __device__ constexpr int pf_rec(int D) { return D + 4; }
 typedef _Float16 pm_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 pm_h4 __attribute__((ext_vector_type(4)));
 typedef float pm_f16 __attribute__((ext_vector_type(16)));
@@ -379,7 +382,7 @@ __global__ __launch_bounds__(PM_THREADS) void k_pf_attn(const float *__restrict_
     if (t >= T) return;
     const long long row = (long long)t * NQ + kvh * G + g;
     const float inv = nsplit == 1 ? 1.0f / l : 1.f;
-    float *dst = nsplit == 1 ? out + row * D : part + (row * nsplit + blockIdx.z) * (D + 2);
+    float *dst = nsplit == 1 ? out + row * D : part + (row * nsplit + blockIdx.z) * pf_rec(D);
 #pragma unroll
     for (int j = 0; j < NT; j++)
 #pragma unroll
@@ -400,14 +403,15 @@ __global__ __launch_bounds__(D) void k_pf_attn_combine(const float *__restrict__
     const long long row = blockIdx.x;
     const int t = (int)(row / NQ), d = threadIdx.x;
     const int nz = (pos0 + t) / ks + 1;
-    const float *p = part + row * nsplit * (D + 2);
+    constexpr int RS = pf_rec(D);
+    const float *p = part + row * nsplit * RS;
     float M = -__builtin_huge_valf();
-    for (int z = 0; z < nz; z++) M = fmaxf(M, p[z * (D + 2) + D]);
+    for (int z = 0; z < nz; z++) M = fmaxf(M, p[z * RS + D]);
     float num = 0.f, den = 0.f;
     for (int z = 0; z < nz; z++) {
-        const float f = __expf(p[z * (D + 2) + D] - M);
-        num = fmaf(f, p[z * (D + 2) + d], num);
-        den = fmaf(f, p[z * (D + 2) + D + 1], den);
+        const float f = __expf(p[z * RS + D] - M);
+        num = fmaf(f, p[z * RS + d], num);
+        den = fmaf(f, p[z * RS + D + 1], den);
     }
     out[row * D + d] = num / den;
 }
@@ -490,7 +494,7 @@ static PfWs pf_ws(const tbq_dense_model *m, int T, void *ws, size_t *total) {
         // attention split partials: a prefill reaching position kmax - 1 uses
         // min(PA_MAX_SPLIT, ceil(kmax / PA_PREF_KS)) splits, and kmax <= max_ctx
         const int ns = std::min(PA_MAX_SPLIT, (m->max_ctx + PA_PREF_KS - 1) / PA_PREF_KS);
-        w.part = ns > 1 ? (float *)take((size_t)T * m->n_heads * ns * (m->head_dim + 2) * 4) : nullptr;
+        w.part = ns > 1 ? (float *)take((size_t)T * m->n_heads * ns * pf_rec(m->head_dim) * 4) : nullptr;
     }
     if (total) *total = off;
     return w;

@@ -8,6 +8,10 @@
 
 namespace tbq {
 
+// Longest row (K) tbq_matvec takes: the int-dot kernel stages all of x in
+// LDS (224 bytes per 64 elements).
+constexpr int TBQ_MAX_K = 32768;
+
 // Fusions of the dense decode's elementwise steps into a matvec, so they
 // need no launch of their own.  Staging prologue (how x is formed):
 //   PRO_NONE    x

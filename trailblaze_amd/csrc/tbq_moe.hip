@@ -108,11 +108,16 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ xn, con
 template <int QT, int LPR>
 __global__ __launch_bounds__(256) void k_gate_up(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
                                                  const float *__restrict__ xn, const int *__restrict__ sel_idx,
-                                                 int H, int F, int k, int rows_per_block, float *__restrict__ act) {
+                                                 int H, int F, int E, int k, int rows_per_block,
+                                                 float *__restrict__ act) {
     extern __shared__ float lds[];
     float *xl = lds, *xs = lds + H;
     const int pair = blockIdx.y, t = pair / k, s = pair % k;
-    const int e = sel_idx[t * 8 + s];
+    // an index outside [0, E) (never produced by the router) reads expert 0
+    // and contributes 0
+    const int e_sel = sel_idx[t * 8 + s];
+    const bool ev = (unsigned)e_sel < (unsigned)E;
+    const int e = ev ? e_sel : 0;
     stage_x_swizzled<256>(xn + (long long)t * H, H, xl, xs);
     __syncthreads();
     constexpr int GROUPS = 256 / LPR;   // dot products per iteration
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(256) void k_gate_up(const uint8_t *__restrict__ gat
                 float g = res[2 * threadIdx.x], u = res[2 * threadIdx.x + 1];
                 float den = 1.0f + expf_glibc(-g);
                 float sg = g / den;
-                act[(long long)pair * F + rr] = sg * u;
+                act[(long long)pair * F + rr] = ev ? sg * u : 0.f;
             }
         }
         __syncthreads();
@@ -154,12 +159,14 @@ __global__ __launch_bounds__(256) void k_gate_up(const uint8_t *__restrict__ gat
 // ---------------------------------------------------------------------------
 template <int QT, int LPR>
 __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, const float *__restrict__ act,
-                                              const int *__restrict__ sel_idx, int H, int F, int k,
+                                              const int *__restrict__ sel_idx, int H, int F, int E, int k,
                                               int rows_per_block, float *__restrict__ yout) {
     extern __shared__ float lds[];
     float *xl = lds, *xs = lds + F;
     const int pair = blockIdx.y, t = pair / k, s = pair % k;
-    const int e = sel_idx[t * 8 + s];
+    const int e_sel = sel_idx[t * 8 + s];
+    const bool ev = (unsigned)e_sel < (unsigned)E;
+    const int e = ev ? e_sel : 0;   // out of range: y = 0
     stage_x_swizzled<256>(act + (long long)pair * F, F, xl, xs);
     __syncthreads();
     constexpr int GROUPS = 256 / LPR;
@@ -179,19 +186,22 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, 
             }
         }
         acc = group_sum<LPR>(acc);
-        if (lane == 0 && r < H) yout[(long long)pair * H + r] = acc;
+        if (lane == 0 && r < H) yout[(long long)pair * H + r] = ev ? acc : 0.f;
     }
 }
 
-// out[t][i] = resid[t][i] + (((0 + w0*y0) + w1*y1) + ...) in slot order.
-__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const float *__restrict__ sel_w,
-                                                 const float *__restrict__ resid, int T, int H, int k,
-                                                 float *__restrict__ out) {
+// out[t][i] = resid[t][i] + (((0 + w0*y0) + w1*y1) + ...) in slot order;
+// a slot whose expert index is outside [0, E) (never produced by the
+// router; its y may be unwritten) is skipped.
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const int *__restrict__ sel_idx,
+                                                 const float *__restrict__ sel_w, const float *__restrict__ resid,
+                                                 int T, int H, int E, int k, float *__restrict__ out) {
     long long n = (long long)T * H;
     for (long long i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
         int t = (int)(i / H), h = (int)(i - (long long)t * H);
         float acc = 0.f;
         for (int s = 0; s < k; s++) {
+            if ((unsigned)sel_idx[t * 8 + s] >= (unsigned)E) continue;
             float p = sel_w[t * 8 + s] * y[((long long)t * k + s) * H + h];
             acc = acc + p;
         }
@@ -215,7 +225,7 @@ static hipError_t launch_moe_experts_t(const MoeArgs &a, hipStream_t st) {
         dim3 grid((a.F + rpb - 1) / rpb, pairs);
         size_t lds = (size_t)a.H * 4 + (size_t)(a.H / 16) * 4;
         hipLaunchKernelGGL((k_gate_up<QT, LPR>), grid, dim3(256), lds, st, (const uint8_t *)a.gate,
-                           (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.k, rpb, a.act);
+                           (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.E, a.k, rpb, a.act);
     }
     return hipGetLastError();
 }
@@ -228,7 +238,7 @@ static hipError_t launch_moe_down_t(const MoeArgs &a, hipStream_t st) {
     dim3 grid((a.H + rpb - 1) / rpb, pairs);
     size_t lds = (size_t)a.F * 4 + (size_t)(a.F / 16) * 4;
     hipLaunchKernelGGL((k_down<QT, LPR>), grid, dim3(256), lds, st, (const uint8_t *)a.down, a.act, a.sel_idx,
-                       a.H, a.F, a.k, rpb, a.y);
+                       a.H, a.F, a.E, a.k, rpb, a.y);
     return hipGetLastError();
 }
 
@@ -287,7 +297,8 @@ hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
     if (err != hipSuccess) return err;
     long long n = (long long)a.T * a.H;
     int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-    hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_w, a.resid, a.T, a.H, a.k, a.out);
+    hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_idx, a.sel_w, a.resid, a.T, a.H, a.E, a.k,
+                       a.out);
     return hipGetLastError();
 }
 
@@ -308,7 +319,8 @@ hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st) {
     if (err != hipSuccess) return err;
     long long n = (long long)a.T * a.H;
     int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-    hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_w, a.resid, a.T, a.H, a.k, a.out);
+    hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_idx, a.sel_w, a.resid, a.T, a.H, a.E, a.k,
+                       a.out);
     return hipGetLastError();
 }
 

@@ -88,7 +88,12 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
     if (tid < 256) { hist[tid] = 0; cur[tid] = 0; }
     if (tid <= NQ) qcnt[tid] = 0;
     __syncthreads();
-    for (int p = tid; p < P; p += 1024) atomicAdd(&hist[sel_idx[(p / k) * 8 + p % k]], 1);
+    // a pair whose expert index is outside [0, E) (never produced by the
+    // router) joins no tile; the combine skips its slot
+    for (int p = tid; p < P; p += 1024) {
+        const int e = sel_idx[(p / k) * 8 + p % k];
+        if ((unsigned)e < (unsigned)E) atomicAdd(&hist[e], 1);
+    }
     __syncthreads();
     // exclusive prefix sum of hist over 256 experts (Hillis-Steele in LDS);
     // tiles counted per sub-tile class
@@ -129,7 +134,7 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
     }
     for (int p = tid; p < P; p += 1024) {
         const int e = sel_idx[(p / k) * 8 + p % k];
-        perm[off[e] + atomicAdd(&cur[e], 1)] = p;
+        if ((unsigned)e < (unsigned)E) perm[off[e] + atomicAdd(&cur[e], 1)] = p;
     }
     __syncthreads();
     const int nt = qbase[0];

@@ -313,11 +313,15 @@ constexpr int GU_ROWS = TBQ_GU_ROWS;   // output rows per wave
 template <int UPL, bool GG>
 __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
                                                             const float *__restrict__ xn, const int *__restrict__ sel_idx,
-                                                            int H, int F, int k, float *__restrict__ act) {
+                                                            int H, int F, int E, int k, float *__restrict__ act) {
     extern __shared__ uint32_t xd[];
     constexpr int LPR = 32;
     const int pair = blockIdx.y, t = pair / k, s = pair % k;
-    const int e = sel_idx[t * 8 + s];
+    // an index outside [0, E) (never produced by the router) reads expert 0
+    // and contributes 0: no weight read leaves the expert tensors
+    const int e_sel = sel_idx[t * 8 + s];
+    const bool ev = (unsigned)e_sel < (unsigned)E;
+    const int e = ev ? e_sel : 0;
     const long long rb = (long long)(H / 256) * 144;
     const int U = H / 64;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -355,7 +359,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
             const float g = acc;
             const float den = 1.0f + expf_glibc(-g);
             const float sg = g / den;
-            act[(long long)pair * F + r] = sg * u_val;
+            act[(long long)pair * F + r] = ev ? sg * u_val : 0.f;
         }
     }
 }
@@ -373,8 +377,8 @@ constexpr int DC_ROWS = 8;   // rows per workgroup
 template <int UPL, bool GG>
 __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *__restrict__ down, const float *__restrict__ act,
                                                                  const int *__restrict__ sel_idx, const float *__restrict__ sel_w,
-                                                                 const float *__restrict__ resid, int H, int F, int k,
-                                                                 float *__restrict__ out) {
+                                                                 const float *__restrict__ resid, int H, int F, int E,
+                                                                 int k, float *__restrict__ out) {
     extern __shared__ uint32_t xd[];                  // k act vectors' digits
     __shared__ float yv[8][DC_ROWS];
     constexpr int LPR = 16, RPP = 4;
@@ -393,7 +397,8 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
         const int d = RPP * (wave + (DC_THREADS / 64) * p) + rsub;
         if (d < DC_ROWS * k) {
             const int rd = d / k, sd = d % k;
-            const int e = sel_idx[t * 8 + sd];
+            const int e_sel = sel_idx[t * 8 + sd];
+            const int e = (unsigned)e_sel < (unsigned)E ? e_sel : 0;   // out of range: contributes 0 below
             const uint8_t *row = down + ((long long)e * H + r0 + rd) * rb;
 #pragma unroll
             for (int i = 0; i < UPL; i++) {
@@ -418,13 +423,14 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
             }
         }
         acc = group_sum<16>(acc);
-        if (dv && lr == 0) yv[sd][rd] = acc;
+        if (dv && lr == 0) yv[sd][rd] = (unsigned)sel_idx[t * 8 + sd] < (unsigned)E ? acc : 0.f;
     }
     __syncthreads();
     if (threadIdx.x < DC_ROWS) {
         const int rd = threadIdx.x, r = r0 + rd;
         float a = 0.f;
         for (int s = 0; s < k; s++) {
+            if ((unsigned)sel_idx[t * 8 + s] >= (unsigned)E) continue;   // never produced by the router
             const float pr = sel_w[t * 8 + s] * yv[s][rd];
             a = a + pr;
         }
@@ -689,14 +695,14 @@ static hipError_t launch_experts_q4k(const MoeArgs &a, hipStream_t st) {
         dim3 grid((a.F + out_per_wg - 1) / out_per_wg, pairs);
         size_t lds = (size_t)(a.H / 32) * XD_PER_SB * 4;
         hipLaunchKernelGGL((k_gate_up_q4k<UPL_GU, GG>), grid, dim3(GU_THREADS), lds, st, (const uint8_t *)a.gate,
-                           (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.k, a.act);
+                           (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.E, a.k, a.act);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
     }
     dim3 grid(a.H / DC_ROWS, a.T);
     size_t lds = (size_t)a.k * (a.F / 32) * XD_PER_SB * 4;
     hipLaunchKernelGGL((k_down_combine_q4k<UPL_DC, GG>), grid, dim3(DC_THREADS), lds, st, (const uint8_t *)a.down, a.act,
-                       a.sel_idx, a.sel_w, a.resid, a.H, a.F, a.k, a.out);
+                       a.sel_idx, a.sel_w, a.resid, a.H, a.F, a.E, a.k, a.out);
     return hipGetLastError();
 }
 

@@ -1010,6 +1010,14 @@ static hipError_t launch_kq(const void *W, int M, int K, const float *x, float *
     const long long rb = (long long)(K / block_weights(QT)) * block_bytes(QT);
     constexpr int RP = GLU ? 2 : R;
     const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (S > 1 ? (size_t)2 * G * S * RP * RPP * 4 : 0);
+    if constexpr (S > 4) {
+        // rows of more than 256 units stage more than 64 KiB of x: opted
+        // into once per instantiation (gfx950 has 160 KiB of LDS per CU)
+        static const hipError_t attr = hipFuncSetAttribute(
+            (const void *)k_mv_kq<QT, LPR, S, G, R, D, PRO, GLU>, hipFuncAttributeMaxDynamicSharedMemorySize,
+            (int)((size_t)S * 64 * (KQ_UNIT * 4 + 16) + 2 * G * S * RP * RPP * 4));
+        if (attr != hipSuccess) return attr;
+    }
     hipLaunchKernelGGL((k_mv_kq<QT, LPR, S, G, R, D, PRO, GLU>), dim3(grid), dim3(S * G * 64), lds, st,
                        (const uint8_t *)W, M, K, rb, x, y, rpw, pro);
     return hipGetLastError();
@@ -1043,15 +1051,22 @@ static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float
     if (U <= 128) return launch_kq_shape<QT, 64, 2, NW / 2, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 192) return launch_kq_shape<QT, 64, 3, G3, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 256) return launch_kq_shape<QT, 64, 4, NW / 4, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    // K up to 32768 for plain matvecs (the fused prologue's registers do not
+    // fit 8 slices): 6 or 8 slices of 64 units, two row groups
+    if constexpr (PRO == PRO_NONE && !GLU) {
+        if (U <= 384) return launch_kq_shape<QT, 64, 6, 2, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+        if (U <= 512) return launch_kq_shape<QT, 64, 8, 2, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    }
     return hipErrorNotSupported;
 }
 
 // Returns hipErrorNotSupported for formats or shapes this kernel does not
-// cover (K must be a multiple of 64 and at most 16384).
+// cover (K must be a multiple of 64 and at most 32768; at most 16384 with a
+// prologue or the GLU epilogue).
 template <int PRO, bool GLU>
 static hipError_t launch_matvec_kq_p(int qt, const void *W, int M, int K, const float *x, float *y, hipStream_t st,
                                      int n_cu, const MvPro &pro) {
-    if (K % 64 || K > 16384 || K <= 0) return hipErrorNotSupported;
+    if (K % 64 || K > TBQ_MAX_K || K <= 0) return hipErrorNotSupported;
     const bool sb256 = block_weights(qt) == 256;
     if (sb256 && K % 256) return hipErrorNotSupported;
     switch (qt) {

@@ -88,7 +88,9 @@ int tb_cuda_matvec_device(const void *W_device, int qtype, int M, int K, const f
     return ok;
 }
 
-void tb_cuda_sync_all(void) { tbq_device_sync(); }
+void tb_cuda_sync_all(void) {
+    if (tbq_init()) tbq_device_sync();
+}
 
 void tb_cuda_cleanup(void) {
     pthread_mutex_lock(&g_mu);
