@@ -128,6 +128,20 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
                     int *sel_idx, float *sel_w, void *workspace, size_t workspace_bytes, int mode,
                     void *stream);
 
+/* tbq_moe_forward with no workspace argument and no allocation of any kind
+ * (no hipMalloc/hipFree, no allocating library call): the workspace is a
+ * static device array of TBQ_NOALLOC_SCRATCH_BYTES per GPU, held until the
+ * process ends.  No counterpart in the reference; for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  Returns 0 with a message when T and mode need a larger
+ * workspace than the array (tbq_moe_workspace_size > the limit: at the
+ * Qwen3-30B-A3B shape, T <= 182 in TBQ_MOE_FP32).  Every call on a GPU
+ * shares that GPU's array, so calls that overlap on one GPU (other streams
+ * or threads) race; calls ordered on one stream do not. */
+#define TBQ_NOALLOC_SCRATCH_BYTES (16u << 20)
+int tbq_moe_forward_noalloc(const tbq_moe_layer *L, int T, const float *xn, const float *resid, float *out,
+                            int *sel_idx, float *sel_w, int mode, void *stream);
+
 /* Host-memory MoE block: the substitution for the MoE branch of
  * tb_layer_forward (layer4/tb_infer.c:753-833,876).  Weights in L are device
  * pointers (e.g. from tb_cuda_upload_tensor); xn, resid, out, sel_idx and

@@ -47,6 +47,7 @@ SYMBOLS = {
     "tbq_moe_workspace_size": (_sz, [_vp, _i, _i]),
     "tbq_moe_forward": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _vp]),
     "tbq_moe_block_host": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _i]),
+    "tbq_moe_forward_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
     "tbq_dense_workspace_size": (_sz, [_vp]),
     "tbq_dense_decode": (_i, [_vp, _i, _i, _vp, _vp, _sz, _vp]),
     "tbq_dense_prefill_workspace_size": (_sz, [_vp, _i]),
@@ -175,10 +176,19 @@ def moe_forward(L: MoeLayer, T, xn, resid, out, sel_idx=None, sel_w=None, worksp
     return out
 
 
+def moe_forward_noalloc(L: MoeLayer, T, xn, resid, out, sel_idx=None, sel_w=None, mode: int = TBQ_MOE_FP32,
+                        stream=None):
+    """tbq_moe_forward with the library's static per-GPU workspace (no
+    allocation anywhere on the call's path)."""
+    _check(lib().tbq_moe_forward_noalloc(C.byref(L), T, _ptr(xn), _ptr(resid), _ptr(out), _ptr(sel_idx),
+                                         _ptr(sel_w), mode, _stream(stream)), "tbq_moe_forward_noalloc")
+    return out
+
+
 def expf_device(x, out, stream=None):
     _check(lib().tbq_expf_device(_ptr(x), _ptr(out), x.numel(), _stream(stream)), "tbq_expf_device")
     return out
 
 
 __all__ = ["formats", "row_bytes", "lib", "init", "dequant", "matvec", "route", "moe_layer", "moe_forward",
-           "moe_workspace_size", "expf_device", "MoeLayer", "TbqError", "SYMBOLS", "TBQ_MOE_FP32", "TBQ_MOE_BF16"]
+           "moe_forward_noalloc", "moe_workspace_size", "expf_device", "MoeLayer", "TbqError", "SYMBOLS", "TBQ_MOE_FP32", "TBQ_MOE_BF16"]

@@ -26,7 +26,8 @@ HIP_FLAGS = [
 C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-ffp-contract=off",
            "-I", os.path.join(ROOT, "include")]
 
-HIP_SOURCES = ["tbq_matvec.hip", "tbq_mv_q4k.hip", "tbq_mv_kq.hip", "tbq_moe.hip", "tbq_moe_q4k.hip", "tbq_moe_prefill.hip", "tbq_dense.hip", "tbq_dense_prefill.hip", "tbq_api.hip"]
+HIP_SOURCES = ["tbq_matvec.hip", "tbq_mv_q4k.hip", "tbq_mv_kq.hip", "tbq_moe.hip", "tbq_moe_q4k.hip", "tbq_moe_prefill.hip", "tbq_dense.hip", "tbq_dense_prefill.hip", "tbq_api.hip",
+               "tbq_noalloc.hip"]
 C_SOURCES = ["tb_cuda_abi.c", "tbq_moe_host.c", "tbq_gguf.c"]
 
 
