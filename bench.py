@@ -27,7 +27,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "int8": 5000.0}   # MI355X dense, per GPU
 PMC_COPY_BYTES = 256 << 20
+PROFILES = ("q4k", "q4k_big", "sweep", "moe_b1", "moe_b16", "moe_prefill")
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "q4k_matvec_4096x4096_pmc.txt")
 
 
@@ -55,10 +57,15 @@ def parse():
     p.add_argument("--moe-only", action="store_true", help="only the MoE leg (profiling)")
     p.add_argument("--dense-only", action="store_true", help="only the dense decode leg (profiling)")
     p.add_argument("--no-dense", action="store_true", help="skip the dense decode leg")
-    p.add_argument("--pmc-calib", action="store_true",
-                   help="counter-collection run: the headline matvec as direct launches, then a plain "
-                        "copy of PMC_COPY_BYTES (the HBM-byte calibration of FETCH_SIZE / WRITE_SIZE)")
-    return p.parse_args()
+    p.add_argument("--pmc-calib", action="store_true", help="same as --profile q4k")
+    p.add_argument("--profile", choices=sorted(PROFILES),
+                   help="counter-collection run for rocprofv3: one workload as direct launches (no graph), "
+                        "then a plain copy of PMC_COPY_BYTES (the HBM-byte calibration of FETCH_SIZE / "
+                        "WRITE_SIZE); prints nothing on stdout")
+    a = p.parse_args()
+    if a.pmc_calib:
+        a.profile = "q4k"
+    return a
 
 
 def log(*a):
@@ -110,6 +117,9 @@ def gpu_leg(args):
     log("device", dev_name)
     stream = torch.cuda.current_stream()
     res = {"device": dev_name}
+    if args.profile:
+        profile_leg(args.profile, tb, fm, synth, torch)
+        return res
 
     # ---- headline: Q4_K 4096x4096, cold HBM via rotated copies ----------
     qt, M, K = fm.Q4_K, 4096, 4096
@@ -126,19 +136,8 @@ def gpu_leg(args):
         for i in range(ncopy):
             tb.matvec(copies[i], qt, M, K, x, ys[i])
 
-    if args.pmc_calib:
-        # direct launches (no graph) so every dispatch carries its counters
-        for _ in range(3):
-            step()
-        src = torch.empty(PMC_COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"pmc calibration: {3 * ncopy} headline launches, 5 copies of {PMC_COPY_BYTES} B")
-        res["headline"] = None
-        return res
-
+    # the kernel's own average duration over the timed region, from HIP
+    # events on the stream it runs on (graph replay, one event pair)
     secs = time_region(step, args.steps, args.warmup, stream)
     per_launch = secs / (args.steps * ncopy)
     bpl = matvec_bytes(qt, M, K)
@@ -180,11 +179,11 @@ def gpu_leg(args):
     if args.moe_only:
         res["moe"] = moe_leg(tb, fm, synth, torch, rng, stream)
         return res
+    # ---- steady-state Q4_K stream: a matrix larger than the MALL --------
+    res["q4k_steady"] = sweep_leg(tb, fm, synth, torch, rng, stream, [(fm.Q4_K, 151936, 4096),
+                                                                      (fm.Q4_K, 65536, 4096)])
     # ---- configs[1] sweep ------------------------------------------------
-    res["sweep"] = sweep_leg(tb, fm, synth, torch, rng, stream, [
-        (fm.Q2_K, 12288, 4096), (fm.Q2_K, 4096, 12288), (fm.Q3_K, 12288, 4096), (fm.Q3_K, 4096, 12288),
-        (fm.Q5_K, 12288, 4096), (fm.Q5_K, 4096, 12288), (fm.Q8_0, 12288, 4096), (fm.Q8_0, 4096, 12288),
-        (fm.Q6_K, 151936, 4096)])
+    res["sweep"] = sweep_leg(tb, fm, synth, torch, rng, stream, SWEEP_SHAPES)
     # the same formats in ggml's on-disk layouts (TBQ_GGML ids)
     G = fm.GGML
     res["ggml_sweep"] = sweep_leg(tb, fm, synth, torch, rng, stream, [
@@ -196,6 +195,73 @@ def gpu_leg(args):
     if not args.no_dense and not args.quick:
         res["dense"] = dense_leg(torch, stream)
     return res
+
+
+def _sweep_shapes():
+    from trailblaze_amd import formats as fm
+    return [(fm.Q2_K, 12288, 4096), (fm.Q2_K, 4096, 12288), (fm.Q3_K, 12288, 4096), (fm.Q3_K, 4096, 12288),
+            (fm.Q5_K, 12288, 4096), (fm.Q5_K, 4096, 12288), (fm.Q8_0, 12288, 4096), (fm.Q8_0, 4096, 12288),
+            (fm.Q6_K, 151936, 4096)]
+
+
+SWEEP_SHAPES = None   # filled in main() (formats import)
+
+
+def hbm_roofline(nbytes, secs):
+    gbs = nbytes / secs / 1e9
+    return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(gbs / HBM_PEAK_GBS, 4))
+
+
+def profile_leg(name, tb, fm, synth, torch):
+    """One workload as direct launches for rocprofv3 (kernel trace or
+    counters per dispatch), then the copy that calibrates FETCH_SIZE and
+    WRITE_SIZE.  Weights are rotated over copies larger than the MALL where
+    one matrix is smaller, as in the timed legs."""
+    rng = np.random.default_rng(0)
+    reps = 3
+    if name in ("q4k", "q4k_big", "sweep"):
+        shapes = {"q4k": [(fm.Q4_K, 4096, 4096)], "q4k_big": [(fm.Q4_K, 151936, 4096)],
+                  "sweep": _sweep_shapes()}[name]
+        for qt, M, K in shapes:
+            W = torch.from_numpy(synth.kquant_matrix(qt, M, K, rng)).cuda()
+            nc = max(1, int(np.ceil(2 * 256e6 / fm.weight_bytes(qt, M, K))) + (1 if M * K < 2 ** 26 else 0))
+            cps = [W] + [W.clone() for _ in range(nc - 1)]
+            x = torch.from_numpy(synth.activations(K, rng)).cuda()
+            y = torch.empty(M, dtype=torch.float32, device="cuda")
+            for _ in range(reps):
+                for c in cps:
+                    tb.matvec(c, qt, M, K, x, y)
+            torch.cuda.synchronize()
+            log(f"profile {name}: {fm.NAMES[qt]} {M}x{K}, {reps} x {nc} launches")
+            del cps, W
+            torch.cuda.empty_cache()
+    else:
+        H, F, E, k = 2048, 768, 128, 8
+        layers, keep = moe_layers(tb, fm, synth, torch, H, F, E, k, 3 if name != "moe_prefill" else 1)
+        T = {"moe_b1": 1, "moe_b16": 16, "moe_prefill": 512}[name]
+        mode = tb.TBQ_MOE_BF16 if name == "moe_prefill" else tb.TBQ_MOE_FP32
+        L = layers[0]
+        if name == "moe_prefill":
+            bias = torch.from_numpy(synth.zipf_router_bias(E, 1.1, 1.0, rng)).cuda()
+            L = tb.moe_layer(H, F, E, k, fm.Q4_K, *L._keep[:4], bias=bias)
+            layers = [L]
+        n = 8 if name == "moe_prefill" else 24
+        xs = torch.from_numpy(synth.activations((n, T, H), rng)).cuda()
+        out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+        ws = torch.zeros(tb.moe_workspace_size(L, T, mode), dtype=torch.uint8, device="cuda")
+        for i in range(n):
+            tb.moe_forward(layers[i % len(layers)], T, xs[i], xs[(i + 1) % n], out, workspace=ws, mode=mode)
+        torch.cuda.synchronize()
+        log(f"profile {name}: {n} MoE layer calls at T={T} over {len(layers)} layer copies")
+        del keep
+    torch.cuda.empty_cache()
+    src = torch.empty(PMC_COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"profile {name}: calibration copies 5 x {PMC_COPY_BYTES} B")
 
 
 def sweep_leg(tb, fm, synth, torch, rng, stream, shapes):
@@ -217,8 +283,10 @@ def sweep_leg(tb, fm, synth, torch, rng, stream, shapes):
         s = time_region(st, reps, 2, stream)
         pl = s / (reps * nc)
         b = matvec_bytes(qt2, M2, K2)
-        out.append(dict(qt=fm.NAMES[qt2], M=M2, K=K2, us=pl * 1e6, gbs=b / pl / 1e9))
-        log(f"{fm.NAMES[qt2]} {M2}x{K2}: {pl * 1e6:.2f} us  {b / pl / 1e9:.0f} GB/s")
+        out.append(dict(qt=fm.NAMES[qt2], M=M2, K=K2, us=pl * 1e6, gbs=b / pl / 1e9,
+                        frac=round(b / pl / 1e9 / HBM_PEAK_GBS, 4), copies=nc))
+        log(f"{fm.NAMES[qt2]} {M2}x{K2}: {pl * 1e6:.2f} us  {b / pl / 1e9:.0f} GB/s "
+            f"({b / pl / 1e9 / HBM_PEAK_GBS:.1%})")
         del cps, Wm
         torch.cuda.empty_cache()
     return out
@@ -292,54 +360,121 @@ def tb_matvec(W, qt, M, K, x, y):
     tb.matvec(W, qt, M, K, x, y)
 
 
-def moe_leg(tb, fm, synth, torch, rng, stream):
-    """MoE layer (configs[3] decode at batch 1 and 16, configs[4] prefill)."""
-    H, F, E, k = 2048, 768, 128, 8
+def moe_layers(tb, fm, synth, torch, H, F, E, k, n):
+    """n distinct copies of one random-init MoE layer on the device (the
+    first from the seeded recipe, the others device clones): rotating over
+    them keeps every call's experts out of the 256 MB MALL."""
     router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=3)
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
-    L = tb.moe_layer(H, F, E, k, fm.Q4_K, d(router), d(gate), d(up), d(down))
+    base = [d(router), d(gate), d(up), d(down)]
+    keep, layers = [base], [tb.moe_layer(H, F, E, k, fm.Q4_K, *base)]
+    for _ in range(n - 1):
+        c = [t.clone() for t in base]
+        keep.append(c)
+        layers.append(tb.moe_layer(H, F, E, k, fm.Q4_K, *c))
+    return layers, keep
+
+
+EXPERT_BYTES = 3 * 768 * 2048 // 256 * 144   # one Q4_K expert at the Qwen3-30B-A3B shape: 2,654,208 B
+
+
+def moe_leg(tb, fm, synth, torch, rng, stream):
+    """MoE layer (configs[3] decode at batch 1 and 16, configs[4] prefill).
+    Decode is timed cold: consecutive calls go to different copies of the
+    layer (3 copies, 1 GB), so an expert's weights come from HBM, not from
+    the MALL; the warm number repeats one layer.  Algorithmic bytes per call
+    = router + U distinct experts x 2,654,208 B + xn, resid, out."""
+    H, F, E, k = 2048, 768, 128, 8
+    NL = 3
+    layers, keep = moe_layers(tb, fm, synth, torch, H, F, E, k, NL)
+    router_bytes = E * H * 4
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     moe = {}
 
-    def decode(Lx, T, name):
-        # 64 different token batches per step, so consecutive layers route to
-        # different experts (the 340 MB of experts exceed the MALL)
+    def distinct_experts(Lx, xs, T):
+        idx = torch.empty(T * 8, dtype=torch.int32, device="cuda")
+        w = torch.empty(T * 8, dtype=torch.float32, device="cuda")
+        us = []
+        for i in range(xs.shape[0]):
+            tb.route(xs[i], Lx._keep[0], Lx._keep[4], T, H, E, k, idx, w)
+            us.append(len(np.unique(idx.cpu().numpy().reshape(T, 8)[:, :k])))
+        return float(np.mean(us))
+
+    def decode(lx, T, name):
+        # 64 different token batches per step
         ntok = 64
         xs = d(synth.activations((ntok, T, H), rng))
         rs = d(synth.activations((ntok, T, H), rng))
         out = torch.empty((T, H), dtype=torch.float32, device="cuda")
-        ws_t = torch.zeros(tb.moe_workspace_size(Lx, T), dtype=torch.uint8, device="cuda")
-
-        def mstep():
-            for i in range(ntok):
-                tb.moe_forward(Lx, T, xs[i], rs[i], out, workspace=ws_t)
-        reps = 20
-        s = time_region(mstep, reps, 2, stream)
-        us = s / (reps * ntok) * 1e6
-        moe[name] = dict(us_per_layer=us, us_per_token=us / T)
-        log(f"MoE {name}: {us:.1f} us/layer  {us / T:.2f} us/token")
+        ws_t = torch.zeros(tb.moe_workspace_size(lx[0], T), dtype=torch.uint8, device="cuda")
+        U = distinct_experts(lx[0], xs, T)
+        nbytes = router_bytes + U * EXPERT_BYTES + 3 * T * H * 4
+        r = {}
+        for temp, ls in (("cold", lx), ("warm", lx[:1])):
+            def mstep():
+                for i in range(ntok):
+                    tb.moe_forward(ls[i % len(ls)], T, xs[i], rs[i], out, workspace=ws_t)
+            reps = 20
+            sec = time_region(mstep, reps, 2, stream) / (reps * ntok)
+            r[temp] = dict(us_per_layer=round(sec * 1e6, 2), us_per_token=round(sec * 1e6 / T, 3),
+                           roofline=hbm_roofline(nbytes, sec))
+        moe[name] = dict(us_per_layer=r["cold"]["us_per_layer"], us_per_token=r["cold"]["us_per_token"],
+                         distinct_experts=U, algorithmic_bytes=int(nbytes), layer_copies=len(lx), **r)
+        log(f"MoE {name}: cold {r['cold']['us_per_layer']:.1f} us/layer ({r['cold']['roofline']['frac']:.1%} of "
+            f"HBM, U={U:.1f}), warm {r['warm']['us_per_layer']:.1f} us/layer")
     for T in (1, 16):
-        decode(L, T, f"decode_b{T}")
+        decode(layers, T, f"decode_b{T}")
     # the same expert bytes read in ggml's Q4_K layout
-    Lg = tb.moe_layer(H, F, E, k, fm.GGML | fm.Q4_K, L._keep[0], L._keep[1], L._keep[2], L._keep[3])
-    decode(Lg, 1, "decode_b1_ggml_q4k")
-    # prefill, Zipf-skewed routing, grouped fp16 MFMA experts (configs[4])
+    lg = [tb.moe_layer(H, F, E, k, fm.GGML | fm.Q4_K, *c) for c in keep]
+    decode(lg, 1, "decode_b1_ggml_q4k")
+    del lg
+    # prefill, Zipf-skewed routing, grouped MFMA experts (configs[4])
     T = 512
-    bias = synth.zipf_router_bias(E, 1.1, 1.0, rng)
-    Lb = tb.moe_layer(H, F, E, k, fm.Q4_K, L._keep[0], L._keep[1], L._keep[2], L._keep[3], bias=d(bias))
+    bias = d(synth.zipf_router_bias(E, 1.1, 1.0, rng))
+    Lb = tb.moe_layer(H, F, E, k, fm.Q4_K, *keep[0], bias=bias)
     xs = d(synth.activations((T, H), rng))
     rs = d(synth.activations((T, H), rng))
     out = torch.empty((T, H), dtype=torch.float32, device="cuda")
-    ws_t = torch.zeros(tb.moe_workspace_size(Lb, T, tb.TBQ_MOE_BF16), dtype=torch.uint8, device="cuda")
-    s = time_region(lambda: tb.moe_forward(Lb, T, xs, rs, out, workspace=ws_t, mode=tb.TBQ_MOE_BF16), 20, 3, stream)
-    us = s / 20 * 1e6
-    moe["prefill_512_bf16_mfma"] = dict(us_per_layer=us, us_per_token=us / T)
-    log(f"MoE prefill T=512 (fp16 MFMA): {us:.1f} us/layer  {us / T:.3f} us/token")
+    U = distinct_experts(Lb, xs[None], T)
+    nbytes = router_bytes + U * EXPERT_BYTES + 3 * T * H * 4
+    flops = 2.0 * T * k * 3 * H * F + 2.0 * T * E * H
+    for name, mode, peak in (("prefill_512_fp16_mfma", tb.TBQ_MOE_BF16, MFMA_PEAK_TFLOPS["fp16"]),):
+        ws_t = torch.zeros(tb.moe_workspace_size(Lb, T, mode), dtype=torch.uint8, device="cuda")
+        sec = time_region(lambda: tb.moe_forward(Lb, T, xs, rs, out, workspace=ws_t, mode=mode), 20, 3,
+                          stream) / 20
+        tf = flops / sec / 1e12
+        moe[name] = dict(us_per_layer=round(sec * 1e6, 2), us_per_token=round(sec * 1e6 / T, 4),
+                         distinct_experts=U, algorithmic_bytes=int(nbytes), flops=flops,
+                         roofline_hbm=hbm_roofline(nbytes, sec),
+                         roofline_mfma=dict(bound="mfma", achieved=round(tf, 1), peak=peak, unit="TFLOP/s",
+                                            frac=round(tf / peak, 4)),
+                         bound_us=round(max(nbytes / HBM_PEAK_GBS / 1e3, flops / peak / 1e6), 2))
+        log(f"MoE {name} T=512: {sec * 1e6:.1f} us/layer; HBM {moe[name]['roofline_hbm']['frac']:.1%}, "
+            f"MFMA {tf:.0f} TFLOP/s ({tf / peak:.1%}); bound {moe[name]['bound_us']:.1f} us")
+    del keep, layers
+    torch.cuda.empty_cache()
     return moe
 
 
-def cpu_leg(budget_s=12.0):
-    """The reference CPU path on this host, one pinned core, on a bounded
-    sample of the headline workload (whole Q4_K 4096x4096 matvecs)."""
+def _time_cpu(fn, budget_s):
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    return (time.perf_counter() - t0) / n, n
+
+
+def cpu_leg(budget_s=10.0, row_budget_s=0.8):
+    """The reference CPU path on this host, one pinned core: (i) the headline
+    workload (whole Q4_K 4096x4096 matvecs) through tb_dispatch_matvec's
+    AVX-512 kernels and the scalar tb_gguf_dequant_matvec, on a bounded
+    sample; (ii) one row per configs[1] shape through the scalar matvec
+    (tb_dispatch_matvec zero-fills Q2_K/Q5_K/Q6_K), plus the AVX dispatch
+    for Q3_K and Q8_0; (iii) the MoE block at batch 1 (the reference's MoE
+    branch composed of its own functions)."""
     from oracle.pyoracle import Oracle, Reference, host_has_avx512
     from trailblaze_amd import formats as fm
     from trailblaze_amd import synth
@@ -353,26 +488,48 @@ def cpu_leg(budget_s=12.0):
     W = synth.kquant_matrix(fm.Q4_K, M, K, rng)
     x = synth.activations(K, rng)
     b = matvec_bytes(fm.Q4_K, M, K)
-    if Reference.available() and host_has_avx512():
+    use_ref = Reference.available() and host_has_avx512()
+    if use_ref:
         ref = Reference()
         kind = "reference"
-        fns = {"tb_dispatch_matvec (AVX-512 class)": lambda: ref.dispatch_matvec_avx512(W, fm.Q4_K, M, K, x),
-               "tb_gguf_dequant_matvec (scalar)": lambda: ref.matvec(W, fm.Q4_K, M, K, x)}
+        mv, avx = ref.matvec, ref.dispatch_matvec_avx512
+        moe_fn = lambda *a, **kw: ref.moe_block(*a, **kw)
+        fns = {"tb_dispatch_matvec (AVX-512 class)": lambda: avx(W, fm.Q4_K, M, K, x),
+               "tb_gguf_dequant_matvec (scalar)": lambda: mv(W, fm.Q4_K, M, K, x)}
     else:
         orc = Oracle()
         kind = "port"
+        mv = orc.matvec
+        avx = None
+        moe_fn = lambda *a, **kw: orc.moe(*a, **kw)[0]
         fns = {"AVX-512-structured restatement": lambda: orc.matvec_q4k_avx512s(W, M, K, x),
                "scalar restatement": lambda: orc.matvec(W, fm.Q4_K, M, K, x)}
     out = {}
     for name, fn in fns.items():
-        fn()
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < budget_s / len(fns):
-            fn()
-            n += 1
-        dt = (time.perf_counter() - t0) / n
+        dt, n = _time_cpu(fn, budget_s / len(fns))
         out[name] = dict(ms_per_matvec=dt * 1e3, gbs=b / dt / 1e9, reps=n)
         log(f"CPU {name}: {dt * 1e3:.1f} ms/matvec {b / dt / 1e9:.2f} GB/s")
+    rows = []
+    for qt, M2, K2 in _sweep_shapes():
+        W2 = synth.kquant_matrix(qt, M2, K2, rng)
+        x2 = synth.activations(K2, rng)
+        b2 = matvec_bytes(qt, M2, K2)
+        paths = [("scalar", lambda: mv(W2, qt, M2, K2, x2))]
+        if avx is not None and qt in (fm.Q3_K, fm.Q8_0):
+            paths.append(("avx", lambda: avx(W2, qt, M2, K2, x2)))
+        for pname, fn in paths:
+            dt, n = _time_cpu(fn, row_budget_s)
+            rows.append(dict(qt=fm.NAMES[qt], M=M2, K=K2, path=pname, ms=round(dt * 1e3, 3),
+                             gbs=round(b2 / dt / 1e9, 3), reps=n))
+            log(f"CPU {fm.NAMES[qt]} {M2}x{K2} {pname}: {dt * 1e3:.1f} ms {b2 / dt / 1e9:.2f} GB/s")
+        del W2
+    H, F, E, k = 2048, 768, 128, 8
+    router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=3)
+    xn = synth.activations((1, H), rng)
+    rs = synth.activations((1, H), rng)
+    dt, n = _time_cpu(lambda: moe_fn(xn, rs, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K), 2 * row_budget_s)
+    moe = dict(us_per_layer=round(dt * 1e6, 1), reps=n)
+    log(f"CPU MoE block b=1: {dt * 1e3:.2f} ms/layer")
     best = max(out, key=lambda k: out[k]["gbs"])
     cpu_model = ""
     try:
@@ -385,7 +542,24 @@ def cpu_leg(budget_s=12.0):
     return dict(value=out[best]["gbs"], unit="GB/s", cores=1, kind=kind,
                 sample=f"{out[best]['reps']} whole Q4_K 4096x4096 matvecs via {best}, 1 pinned thread "
                        f"({cpu_model}, nproc={os.cpu_count()})",
-                detail=out)
+                detail=out, rows=rows, moe_b1=moe)
+
+
+def _reap_children():
+    """Wait for any child process of this one (the bench starts none itself;
+    a library may) and name it on stderr, so the run ends with nothing left."""
+    try:
+        import psutil
+    except ImportError:
+        return
+    kids = psutil.Process().children(recursive=True)
+    for c in kids:
+        try:
+            log(f"child process left at exit: pid {c.pid} {c.name()} {' '.join(c.cmdline()[:4])}")
+            c.terminate()
+        except psutil.Error:
+            pass
+    psutil.wait_procs(kids, timeout=5)
 
 
 def main():
@@ -394,10 +568,13 @@ def main():
         print("bench.py: this build runs on one GPU only (single-GPU hot path); --gpus must be 1",
               file=sys.stderr)
         sys.exit(2)
+    global SWEEP_SHAPES
+    SWEEP_SHAPES = _sweep_shapes()
     res = gpu_leg(args)
-    h = res["headline"]
-    if args.pmc_calib:
+    if args.profile:
+        _reap_children()
         return
+    h = res["headline"]
     cpu = None
     if not args.no_cpu and not args.quick:
         cpu = cpu_leg()
@@ -425,11 +602,29 @@ def main():
         "extra": {"device": res["device"], "warm_mall_gbs": round(h["warm_gbs"], 1),
                   "warm_us_per_launch": round(h["warm_us_per_launch"], 3),
                   "abi_matvec_us": None if res.get("abi_matvec_us") is None else round(res["abi_matvec_us"], 2),
+                  "q4k_steady": res.get("q4k_steady"),
                   "sweep": res.get("sweep"), "ggml_sweep": res.get("ggml_sweep"), "moe": res.get("moe"),
                   "dense": res.get("dense"),
-                  "cpu_detail": None if cpu is None else cpu["detail"]},
+                  "cpu_detail": None if cpu is None else cpu["detail"],
+                  "cpu_rows": None if cpu is None else cpu_rows_vs_gpu(cpu, res)},
     }
     print(json.dumps(line), flush=True)
+    _reap_children()
+
+
+def cpu_rows_vs_gpu(cpu, res):
+    """The CPU rows with the GPU time of the same workload beside them."""
+    gpu = {(r["qt"], r["M"], r["K"]): r["us"] for r in (res.get("sweep") or [])}
+    rows = []
+    for r in cpu["rows"]:
+        g = gpu.get((r["qt"], r["M"], r["K"]))
+        rows.append(dict(r, gpu_us=None if g is None else round(g, 2),
+                         gpu_speedup=None if g is None else round(r["ms"] * 1e3 / g, 1)))
+    m = (res.get("moe") or {}).get("decode_b1")
+    moe = dict(cpu["moe_b1"], gpu_us_cold=None if m is None else m["us_per_layer"])
+    if m is not None:
+        moe["gpu_speedup"] = round(moe["us_per_layer"] / m["us_per_layer"], 1)
+    return dict(matvec=rows, moe_b1=moe, cores=1, kind=cpu["kind"])
 
 
 if __name__ == "__main__":

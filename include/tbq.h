@@ -111,6 +111,10 @@ typedef struct {
 #define TBQ_MOE_BF16 1      /* prefill: grouped 16-bit MFMA (fp16 operands with
                                power-of-two row scaling, fp32 accumulate);
                                within 1e-2 rel-L2 */
+#define TBQ_MOE_I8 2        /* prefill: grouped int8 MFMA, activations quantised to
+                               Q8_K blocks (d = max|x|/127 per 256), the Q4_K
+                               nibbles with their 6-bit scales folded in; fp32
+                               accumulate; within 1e-2 rel-L2 */
 
 /* Workspace bytes tbq_moe_forward needs for T tokens in `mode` (T <= 65536). */
 size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode);
@@ -217,6 +221,16 @@ int tbq_dense_prefill(const tbq_dense_model *m, const int *tokens_host, int T, i
                       void *workspace, size_t ws_bytes, void *stream);
 /* 1 if tbq_dense_prefill takes the batched path for this model. */
 int tbq_dense_prefill_batched(const tbq_dense_model *m);
+
+/* ---- activations to Q8_K ----------------------------------------------- */
+/* blocks[n / 256] = x quantised to Q8_K blocks of 292 bytes in the
+ * reference's layout (layer4/tb_gguf.c:281-288: f32 d, int8 qs[256], int16
+ * bsums[16]); the reference defines the layout and its decoder but no
+ * quantiser.  Per block d = max|x| / 127, q = rint(x * (1 / d)) clamped to
+ * +-127 (0 for an all-zero block), bsums = sums of q over 16 elements: the
+ * activation form of the TBQ_MOE_I8 prefill.  n a multiple of 256; x 16-byte
+ * and blocks 4-byte aligned. */
+int tbq_quantize_q8k(const float *x, long long n, void *blocks, void *stream);
 
 /* ---- test hooks -------------------------------------------------------- */
 /* out[i] = expf(in[i]) evaluated by the device code the router uses. */

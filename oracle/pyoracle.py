@@ -165,6 +165,7 @@ class Reference:
         L.tbref_route.argtypes = [_f32p, C.c_int, C.c_int, _i32p, _f32p]
         L.tbref_swiglu.argtypes = [_f32p, _f32p, _f32p, C.c_int]
         L.tbref_dispatch_matvec_avx512.argtypes = [_u8p, C.c_int, C.c_int, C.c_int, _f32p, _f32p]
+        L.tbref_moe_block.argtypes = [C.c_int] * 6 + [_f32p, _f32p, _f32p, _u8p, _u8p, _u8p, _f32p]
 
     def dequant_rows(self, W, qtype, M, K, row_bytes):
         out = np.empty((M, K), np.float32)
@@ -185,6 +186,19 @@ class Reference:
         out = np.empty(M, np.float32)
         self.lib.tbref_dispatch_matvec_avx512(np.ascontiguousarray(W).reshape(-1), qtype, M, K,
                                               np.ascontiguousarray(x, np.float32), out)
+        return out
+
+    def moe_block(self, xn, resid, router, gate, up, down, *, F, top_k, qtype):
+        """The reference's MoE branch (layer4/tb_infer.c:753-833,876) composed
+        of its own functions, per token (no router bias)."""
+        T, H = xn.shape
+        E = router.shape[0]
+        out = np.empty((T, H), np.float32)
+        self.lib.tbref_moe_block(T, H, F, E, top_k, qtype, np.ascontiguousarray(xn, np.float32).reshape(-1),
+                                 np.ascontiguousarray(resid, np.float32).reshape(-1),
+                                 np.ascontiguousarray(router, np.float32).reshape(-1),
+                                 np.ascontiguousarray(gate).reshape(-1), np.ascontiguousarray(up).reshape(-1),
+                                 np.ascontiguousarray(down).reshape(-1), out.reshape(-1))
         return out
 
     def route(self, logits, top_k):

@@ -9,6 +9,8 @@
  *   tb_route_experts   layer4/tb_infer.h:120-122 (use_hdgl=0 context)
  *   tb_swiglu          layer4/tb_infer.c:130-135 (no prototype in a header)
  *   tb_dispatch_matvec src/tb_analog_dispatch.h:102-105 (AVX-512 class)
+ *   the MoE branch of tb_layer_forward (layer4/tb_infer.c:753-833), composed
+ *   of tb_gguf_dequant_matvec, tb_route_experts and tb_swiglu
  * tb_gguf_dequant_row / tb_gguf_dequant_matvec (layer4/tb_gguf.h:90,95) are
  * exported by the reference objects themselves and called directly.
  */
@@ -18,6 +20,14 @@
 #include "tb_infer.h"
 
 void tb_swiglu(const float *gate, const float *up, float *out, int dim);
+
+/* Row bytes of the packed expert tensors, as the _RB macro of
+ * layer4/tb_infer.c:806 computes them. */
+static long tb_gguf_row_bytes_ref(int qt, int K) {
+    return qt == 12 ? (long)(K / 256) * 144 : qt == 11 ? (long)(K / 256) * 110 : qt == 13 ? (long)(K / 256) * 176
+         : qt == 14 ? (long)(K / 256) * 210 : qt == 15 ? (long)(K / 256) * 292 : qt == 8 ? (long)(K / 32) * 34
+         : qt == 2 ? (long)(K / 32) * 18 : (long)K * 4;
+}
 
 int tbref_route(const float *logits, int n_experts, int top_k, int idx[8], float w[8]) {
     TB_GGUFModel *m = (TB_GGUFModel *)calloc(1, sizeof(TB_GGUFModel));
@@ -59,3 +69,47 @@ void tbref_dispatch_matvec_avx512(const void *W, int qtype, int M, int K,
 }
 
 int tbref_sizeof_selection(void) { return (int)sizeof(TB_ExpertSelection); }
+
+/* The MoE branch of tb_layer_forward (layer4/tb_infer.c:753-833, residual
+ * :876) for T tokens, composed of the reference's own functions as that
+ * branch calls them: router logits by tb_gguf_dequant_matvec on the fp32
+ * router (the 4-bit-compat router call at :759-763 cannot read an fp32
+ * ffn_gate_inp), tb_route_experts, two tb_gguf_dequant_matvec + tb_swiglu +
+ * one tb_gguf_dequant_matvec per slot on the packed expert rows (:794-820,
+ * with the three mallocs per slot), the weighted accumulate (:829-831) and
+ * the residual add.  The CPU baseline of the MoE block (one thread). */
+void tbref_moe_block(int T, int H, int F, int E, int top_k, int qtype, const float *xn, const float *resid,
+                     const float *router, const void *gate, const void *up, const void *down, float *out) {
+    TB_GGUFModel *m = (TB_GGUFModel *)calloc(1, sizeof(TB_GGUFModel));
+    TB_InferCtx *ctx = (TB_InferCtx *)calloc(1, sizeof(TB_InferCtx));
+    m->n_experts_per_tok = top_k;
+    ctx->model = m;
+    const size_t rb_h = (size_t)tb_gguf_row_bytes_ref(qtype, H), rb_f = (size_t)tb_gguf_row_bytes_ref(qtype, F);
+    for (int t = 0; t < T; t++) {
+        const float *x = xn + (size_t)t * H;
+        float *lg = (float *)calloc(E, sizeof(float));
+        tb_gguf_dequant_matvec(router, 0, E, H, x, lg);
+        TB_ExpertSelection sel = tb_route_experts(ctx, 0, 0, lg, E);
+        free(lg);
+        float *ffn = (float *)calloc(H, sizeof(float));
+        float *eo = (float *)calloc(H, sizeof(float));
+        for (int ei = 0; ei < sel.k; ei++) {
+            const int e = sel.expert_indices[ei];
+            float *g = (float *)malloc(F * sizeof(float));
+            float *u = (float *)malloc(F * sizeof(float));
+            float *a = (float *)malloc(F * sizeof(float));
+            tb_gguf_dequant_matvec((const char *)gate + (size_t)e * F * rb_h, qtype, F, H, x, g);
+            tb_gguf_dequant_matvec((const char *)up + (size_t)e * F * rb_h, qtype, F, H, x, u);
+            tb_swiglu(g, u, a, F);
+            tb_gguf_dequant_matvec((const char *)down + (size_t)e * H * rb_f, qtype, H, F, a, eo);
+            free(g); free(u); free(a);
+            const float w = sel.expert_weights[ei];
+            for (int i = 0; i < H; i++) ffn[i] += w * eo[i];
+        }
+        for (int i = 0; i < H; i++) out[(size_t)t * H + i] = resid[(size_t)t * H + i] + ffn[i];
+        free(ffn);
+        free(eo);
+    }
+    free(ctx);
+    free(m);
+}

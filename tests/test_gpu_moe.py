@@ -279,7 +279,8 @@ def test_moe_host_block_varying_batches(oracle, H):
     torch.cuda.synchronize()
     for i, (T, mode) in enumerate([(5, tb.TBQ_MOE_FP32), (1, tb.TBQ_MOE_FP32), (16, tb.TBQ_MOE_FP32),
                                    (1, tb.TBQ_MOE_FP32), (40, tb.TBQ_MOE_BF16), (1, tb.TBQ_MOE_FP32),
-                                   (3, tb.TBQ_MOE_BF16), (2, tb.TBQ_MOE_FP32)]):
+                                   (3, tb.TBQ_MOE_BF16), (2, tb.TBQ_MOE_FP32), (24, tb.TBQ_MOE_I8),
+                                   (1, tb.TBQ_MOE_FP32)]):
         print(f"host block H={H} call {i}: T={T} mode={mode}", flush=True)
         rng = np.random.default_rng(1000 * H + i)
         xn = synth.activations((T, H), rng)
@@ -345,6 +346,72 @@ def test_moe_prefill_mfma_small_batches(oracle):
         xn = synth.activations((T, H), rng)
         resid = synth.activations((T, H), rng)
         out, idx, w = gpu_moe(xn, resid, router, gate, up, down, F, k, fm.Q4_K, mode=tb.TBQ_MOE_BF16)
+        ref, ridx, rw = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
+        assert np.array_equal(idx, ridx)
+        assert rel_l2(out - resid, ref - resid) <= PREFILL_TOL
+
+
+# ---------------------------------------------------------------------------
+# Prefill on int8 MFMA with Q8_K activations (TBQ_MOE_I8): routing exact,
+# outputs within 1e-2 rel-L2 (8-bit activations)
+# ---------------------------------------------------------------------------
+def test_quantize_q8k_device_matches_oracle(oracle):
+    """tbq_quantize_q8k writes the Q8_K blocks the pinned oracle quantiser
+    writes (d, every int8 quant, every 16-element sum), byte for byte, on
+    N(0,1) blocks, tiny and huge scales, 1000x outliers, an all-zero block,
+    a constant block and exact rounding ties."""
+    import torch
+    rng = np.random.default_rng(81)
+    parts = [rng.standard_normal(4096).astype(np.float32),
+             (rng.standard_normal(512) * 1e-30).astype(np.float32),
+             (rng.standard_normal(512) * 1e30).astype(np.float32),
+             np.zeros(256, np.float32), np.full(256, -3.25, np.float32)]
+    o = rng.standard_normal(1024).astype(np.float32)
+    o[rng.choice(1024, 9, replace=False)] *= 1000.0
+    ties = np.zeros(256, np.float32)
+    ties[0], ties[1], ties[2] = 127.0, 2.5, -3.5
+    x = np.concatenate(parts + [o, ties])
+    blocks = empty(x.size // 256 * 292, torch.uint8)
+    assert tb.lib().tbq_quantize_q8k(dev(x).data_ptr(), x.size, blocks.data_ptr(), None) == 1
+    got = host(blocks)
+    want = oracle.quantize_q8k(x)
+    assert np.array_equal(got, want), np.flatnonzero(got != want)[:10]
+
+
+def test_moe_prefill_i8_config(oracle, qwen_layer):
+    """BASELINE configs[4] on the int8 path: 512 tokens, Zipf(1.1)-skewed
+    router bias."""
+    H, F, E, router, gate, up, down = qwen_layer
+    T = 512
+    rng = np.random.default_rng(512)
+    bias = synth.zipf_router_bias(E, 1.1, 1.0, rng)
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    out, idx, w = gpu_moe(xn, resid, router, gate, up, down, F, 8, fm.Q4_K, bias=bias, mode=tb.TBQ_MOE_I8)
+    lg = oracle.router_logits(xn, router, bias)
+    for t in range(T):
+        ri, rw = oracle.route(lg[t], 8)
+        assert np.array_equal(idx[t], ri), t
+        assert bits_equal(w[t], rw), t
+    sample = np.sort(rng.choice(T, 32, replace=False))
+    ref, _, _ = oracle.moe(xn[sample], resid[sample], router, gate, up, down, F=F, top_k=8, qtype=fm.Q4_K, bias=bias)
+    e = rel_l2(out[sample] - resid[sample], ref - resid[sample])
+    print("int8 prefill delta rel-L2", e, flush=True)
+    assert e <= PREFILL_TOL
+    assert rel_l2(out[sample], ref) <= PREFILL_TOL
+
+
+@pytest.mark.parametrize("H,F,E,k", [(512, 256, 8, 4), (2048, 768, 16, 8), (1024, 512, 6, 2)])
+def test_moe_prefill_i8_small_batches(oracle, H, F, E, k):
+    """Tiles of 1..70 pairs (one and two 64-pair halves), experts with no
+    tokens, several tiles per expert, K of 2..16 chunks."""
+    router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=H + E)
+    for T in (1, 3, 17, 70):
+        print(f"int8 prefill H={H} F={F} E={E} k={k} T={T}", flush=True)
+        rng = np.random.default_rng(T + H)
+        xn = synth.activations((T, H), rng)
+        resid = synth.activations((T, H), rng)
+        out, idx, w = gpu_moe(xn, resid, router, gate, up, down, F, k, fm.Q4_K, mode=tb.TBQ_MOE_I8)
         ref, ridx, rw = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
         assert np.array_equal(idx, ridx)
         assert rel_l2(out - resid, ref - resid) <= PREFILL_TOL

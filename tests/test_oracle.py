@@ -283,6 +283,19 @@ def test_oracle_vs_compiled_reference(oracle, reference, qt):
     assert bits_equal(oracle.matvec(Wf, qt, M, K, x), reference.matvec(Wf, qt, M, K, x))
 
 
+def test_moe_vs_compiled_reference_block(oracle, reference):
+    """tbo_moe_forward against the reference's MoE branch composed of its own
+    functions (oracle/ref_harness.c tbref_moe_block): bit-identical outputs."""
+    H, F, E, k, T = 512, 256, 16, 4, 3
+    router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=12)
+    rng = np.random.default_rng(12)
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    out, _, _ = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
+    ref = reference.moe_block(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
+    assert bits_equal(out, ref)
+
+
 def test_route_vs_compiled_reference(oracle, reference):
     rng = np.random.default_rng(7)
     for t in range(2000):

@@ -38,7 +38,7 @@ def _with_workspace(L, T, xn, resid, mode):
 
 
 @pytest.mark.parametrize("mode,Ts", [(tb.TBQ_MOE_FP32, (16, 1)), (tb.TBQ_MOE_BF16, (40, 3)),
-                                     (tb.TBQ_MOE_FP32, (5, 2))])
+                                     (tb.TBQ_MOE_I8, (40, 3)), (tb.TBQ_MOE_FP32, (5, 2))])
 def test_noalloc_matches_workspace_entry_point(oracle, mode, Ts):
     H, F, E, k = 2048, 768, 128, 8
     router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=77)

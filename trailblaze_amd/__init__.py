@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(HERE, "libtbq.so")
 
 TBQ_MOE_FP32 = 0
 TBQ_MOE_BF16 = 1
+TBQ_MOE_I8 = 2
 TBQ_MV_AUTO, TBQ_MV_FMA, TBQ_MV_INTDOT, TBQ_MV_KQ = 0, 1, 2, 3
 
 # (name, restype, argtypes) for every symbol declared in include/tbq.h,
@@ -53,6 +54,7 @@ SYMBOLS = {
     "tbq_dense_prefill_workspace_size": (_sz, [_vp, _i]),
     "tbq_dense_prefill": (_i, [_vp, _vp, _i, _i, _vp, _vp, _sz, _vp]),
     "tbq_dense_prefill_batched": (_i, [_vp]),
+    "tbq_quantize_q8k": (_i, [_vp, C.c_longlong, _vp, _vp]),
     "tbq_expf_device": (_i, [_vp, _vp, _sz, _vp]),
     "tbq_expf_host": (_f, [_f]),
     # include/tbq_gguf.h
@@ -191,4 +193,5 @@ def expf_device(x, out, stream=None):
 
 
 __all__ = ["formats", "row_bytes", "lib", "init", "dequant", "matvec", "route", "moe_layer", "moe_forward",
-           "moe_forward_noalloc", "moe_workspace_size", "expf_device", "MoeLayer", "TbqError", "SYMBOLS", "TBQ_MOE_FP32", "TBQ_MOE_BF16"]
+           "moe_forward_noalloc", "moe_workspace_size", "expf_device", "MoeLayer", "TbqError", "SYMBOLS", "TBQ_MOE_FP32", "TBQ_MOE_BF16",
+           "TBQ_MOE_I8"]

@@ -230,6 +230,7 @@ size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode) {
     n += align256((size_t)T * k * L->F * 4);                 // act
     n += align256((size_t)T * k * L->H * 4);                 // y
     if (mode == TBQ_MOE_BF16) n += align256(prefill_workspace_bytes(T, k, L->E, L->H, L->F));
+    if (mode == TBQ_MOE_I8) n += align256(prefill_i8_workspace_bytes(T, k, L->E, L->H, L->F));
     return n;
 }
 
@@ -253,10 +254,11 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
                     float *sel_w, void *workspace, size_t ws_bytes, int mode, void *s) {
     if (!ensure_init()) return 0;
     if (!check_moe(L, T)) return 0;
-    if (mode != TBQ_MOE_FP32 && mode != TBQ_MOE_BF16) return fail("tbq_moe_forward: unknown mode %d", mode);
-    if (mode == TBQ_MOE_BF16 && (L->qtype != QT_Q4_K || L->F % 128 || L->H % 128))
-        return fail("tbq_moe_forward: the prefill MFMA path takes Q4_K experts (reference layout) with H, F "
-                    "multiples of 256");
+    if (mode != TBQ_MOE_FP32 && mode != TBQ_MOE_BF16 && mode != TBQ_MOE_I8)
+        return fail("tbq_moe_forward: unknown mode %d", mode);
+    if (mode != TBQ_MOE_FP32 && (L->qtype != QT_Q4_K || !gemm_k_supported(L->H) || !gemm_k_supported(L->F)))
+        return fail("tbq_moe_forward: the prefill MFMA paths take Q4_K experts (reference layout) with H and F "
+                    "in {256, 512, 768, 1024, 1536, 2048, 3072, 4096}");
     if (!xn || !resid || !out || !aligned16(xn) || !aligned16(resid) || !aligned16(out))
         return fail("tbq_moe_forward: null or misaligned activation pointer");
     if (T == 0) return 1;
@@ -293,6 +295,7 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     a.sel_idx = sel_idx ? sel_idx : ws_idx;
     a.sel_w = sel_w ? sel_w : ws_w;
     if (mode == TBQ_MOE_BF16) return hip_ok(launch_moe_bf16(a, ws + off, S(s)), "moe launch (prefill MFMA)");
+    if (mode == TBQ_MOE_I8) return hip_ok(launch_moe_i8(a, ws + off, S(s)), "moe launch (prefill int8 MFMA)");
     return hip_ok(launch_moe_fp32(a, S(s)), "moe launch");
 }
 
@@ -366,6 +369,15 @@ int tbq_dense_prefill(const tbq_dense_model *m, const int *tokens_host, int T, i
             return fail("tbq_dense_prefill: token %d at %d out of range", tokens_host[t], t);
     if (ws_bytes < dense_prefill_workspace_bytes(m, T)) return fail("tbq_dense_prefill: workspace too small");
     return hip_ok(launch_dense_prefill(m, tokens_host, T, pos0, logits, workspace, S(s)), "dense prefill launch");
+}
+
+int tbq_quantize_q8k(const float *x, long long n, void *blocks, void *s) {
+    if (!ensure_init()) return 0;
+    if (n < 0 || n % 256) return fail("tbq_quantize_q8k: n=%lld must be a multiple of 256", n);
+    if (!x || !blocks || !aligned16(x) || ((uintptr_t)blocks & 3u))
+        return fail("tbq_quantize_q8k: null or misaligned pointer");
+    if (n == 0) return 1;
+    return hip_ok(launch_quantize_q8k(x, n, blocks, S(s)), "quantize_q8k launch");
 }
 
 int tbq_expf_device(const float *in, float *out, size_t n, void *s) {

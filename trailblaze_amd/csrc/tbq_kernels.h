@@ -77,6 +77,13 @@ hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t s
 // scales (so the router can write them).
 void prefill_x16(const MoeArgs &a, void *scratch, _Float16 **x16, float **xinv);
 hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st);
+// int8 MFMA prefill (TBQ_MOE_I8): Q8_K activations against the Q4_K nibbles
+size_t prefill_i8_workspace_bytes(int T, int k, int E, int H, int F);
+hipError_t launch_rows_q8(const float *in, long long rows, int n, int8_t *q8, float *dq, _Float16 *bs16,
+                          hipStream_t st);
+hipError_t launch_moe_prefill_q4k_i8(const MoeArgs &a, void *scratch, hipStream_t st);
+hipError_t launch_quantize_q8k(const float *in, long long n, void *blocks, hipStream_t st);
+hipError_t launch_moe_i8(const MoeArgs &a, void *scratch, hipStream_t st);
 size_t dense_workspace_bytes(const tbq_dense_model *m);
 hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,
                                hipStream_t st);

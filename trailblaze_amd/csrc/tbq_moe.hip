@@ -193,19 +193,28 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, 
 // out[t][i] = resid[t][i] + (((0 + w0*y0) + w1*y1) + ...) in slot order;
 // a slot whose expert index is outside [0, E) (never produced by the
 // router; its y may be unwritten) is skipped.
+// Four consecutive outputs per thread (H is a multiple of 4), each summed
+// exactly as the scalar form.
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const int *__restrict__ sel_idx,
                                                  const float *__restrict__ sel_w, const float *__restrict__ resid,
                                                  int T, int H, int E, int k, float *__restrict__ out) {
-    long long n = (long long)T * H;
-    for (long long i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
-        int t = (int)(i / H), h = (int)(i - (long long)t * H);
-        float acc = 0.f;
+    const long long n4 = (long long)T * H / 4;
+    const int H4 = H / 4;
+    for (long long i = blockIdx.x * 256ll + threadIdx.x; i < n4; i += (long long)gridDim.x * 256) {
+        const int t = (int)(i / H4), h4 = (int)(i - (long long)t * H4);
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int s = 0; s < k; s++) {
             if ((unsigned)sel_idx[t * 8 + s] >= (unsigned)E) continue;
-            float p = sel_w[t * 8 + s] * y[((long long)t * k + s) * H + h];
-            acc = acc + p;
+            const float w = sel_w[t * 8 + s];
+            const float4 v = reinterpret_cast<const float4 *>(y + ((long long)t * k + s) * H)[h4];
+            const float px = w * v.x, py = w * v.y, pz = w * v.z, pw = w * v.w;
+            acc.x = acc.x + px;
+            acc.y = acc.y + py;
+            acc.z = acc.z + pz;
+            acc.w = acc.w + pw;
         }
-        out[i] = resid[i] + acc;
+        const float4 r = reinterpret_cast<const float4 *>(resid)[i];
+        reinterpret_cast<float4 *>(out)[i] = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
     }
 }
 
@@ -295,7 +304,7 @@ hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
     default: return hipErrorInvalidValue;
     }
     if (err != hipSuccess) return err;
-    long long n = (long long)a.T * a.H;
+    long long n = (long long)a.T * a.H / 4;
     int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
     hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_idx, a.sel_w, a.resid, a.T, a.H, a.E, a.k,
                        a.out);
@@ -317,7 +326,24 @@ hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st) {
     if (err != hipSuccess) return err;
     err = launch_moe_prefill_q4k(a, scratch, st, x16_done);
     if (err != hipSuccess) return err;
-    long long n = (long long)a.T * a.H;
+    long long n = (long long)a.T * a.H / 4;
+    int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+    hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_idx, a.sel_w, a.resid, a.T, a.H, a.E, a.k,
+                       a.out);
+    return hipGetLastError();
+}
+
+// Prefill on int8 MFMA: exact routing, Q8_K activations, grouped int8
+// expert GEMMs, the slot-ordered combine.
+hipError_t launch_moe_i8(const MoeArgs &a, void *scratch, hipStream_t st) {
+    hipError_t err = launch_router(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.logits,
+                                   a.T >= 32 ? nullptr : a.counters, a.sel_idx, a.sel_w, st);
+    if (err == hipErrorNotSupported)
+        err = launch_route(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.sel_idx, a.sel_w, st);
+    if (err != hipSuccess) return err;
+    err = launch_moe_prefill_q4k_i8(a, scratch, st);
+    if (err != hipSuccess) return err;
+    long long n = (long long)a.T * a.H / 4;
     int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
     hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_idx, a.sel_w, a.resid, a.T, a.H, a.E, a.k,
                        a.out);

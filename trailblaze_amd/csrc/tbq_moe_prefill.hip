@@ -239,8 +239,12 @@ __device__ __forceinline__ void q4pair_frags(const Q4Pair &r, int j0, int u, f16
 }
 
 // ---------------------------------------------------------------------------
-// Expert tile GEMM.  1-D grid of max tiles x ncb row blocks (ncb = F/PF_COLS
-// for MODE 0, H/PF_ROWS for MODE 1); K = NS * 128.
+// Expert tile GEMM.  Work items are (tile, row block) pairs, tile-major
+// (ncb = F/PF_COLS row blocks for MODE 0, H/PF_ROWS for MODE 1), the tiles
+// heaviest first; K = NS * 128.  The grid is persistent (one workgroup
+// per CU): workgroup b takes items b, b + grid, b + 2 grid, ..., so the
+// heavy items are spread over the whole GPU first and no CU idles while
+// another finishes a second round of one-item workgroups.
 //   MODE 0: wave w, lane row i = l % 32 is gate (i < 16) or up (i >= 16)
 //   column PF_COLS*cb + 16w + i % 16, so a lane's accumulator registers r
 //   and r + 8 hold gate and up of the same (column, pair) and SwiGLU needs
@@ -261,10 +265,11 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
     constexpr int K = NS * PF_KC;
     constexpr int XPT = PF_MT * PF_KC / 8 / PF_THREADS;   // 16-byte activation segments per thread per chunk
     extern __shared__ __attribute__((aligned(16))) _Float16 pf_lds[];   // [2][PF_MT][PF_LD]
-    // workgroup -> (tile, row block), tile-major so the heavy tiles, listed
-    // first, start first.  The tile record and its row lists are loaded
-    // together (the row lists of a tile past the end are never used).
-    const int tix = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+    const int nitems = *ntiles * ncb;
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+    // item -> (tile, row block).  The tile record and its row lists are
+    // loaded together.
+    const int tix = item / ncb, cb = item % ncb;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, lh = lane >> 5;
     const int *xrows = (MODE == 0 ? ttok : tpair) + tix * PF_MT;
     int px[XPT];
@@ -272,7 +277,6 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
     for (int m = 0; m < XPT; m++) px[m] = xrows[(tid + PF_THREADS * m) >> 4];
     const int po = tid < PF_MT ? tpair[tix * PF_MT + tid] : -1;
     const int pxo = tid < PF_MT ? xrows[tid] : -1;
-    if (tix >= *ntiles) return;
     const PfTile tl = tiles[tix];
     const long long rb = (long long)(K / 256) * 144;
 
@@ -407,6 +411,319 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
             }
         }
     }
+    // the next item rewrites the activation buffers and the pair lists
+    __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// int8 MFMA variant (TBQ_MOE_I8): Q8_K-quantised activations against the
+// Q4_K nibbles on v_mfma_i32_32x32x32_i8.
+//
+// Activations.  k_rows_q8 quantises rows of n floats per 256-element block
+// as the Q8_K activation quantiser (tbo_quantize_q8k): d = max|x| / 127,
+// q1 = rint(x / d) clamped to +-127 (computed as x * (1/d)).  For the
+// prefill it adds a second int8 level for the residual, q2 = rint((x - q1 d)
+// * 256 / d) clamped to +-127, so x = d (q1 + q2 / 256) to 2^-16 of the
+// block's max: with the first level alone the layer's MoE delta lands 1-2%
+// from the fp32 reference on N(0,1) activations (the SwiGLU outputs are
+// heavy-tailed), above the 1e-2 bound.  Each level keeps Q8_K's 16-element
+// sums (fp16: |sum| <= 2032 is exact).  The int8 rows store the elements of
+// every 16-element group in the order 0,2,4,6,1,3,5,7,8,10,12,14,9,11,13,15:
+// the order in which one Q4_K quant dword unpacks with two AND masks and a
+// shift (the reference's layout puts weights 2i and 2i+1 in the low and high
+// nibbles of byte i, layer4/tb_gguf.c:148-180).  The sum over k does not
+// depend on the order, which both operands share.
+//
+// Weights.  Per 32-weight sub-block j of a row the 6-bit scale is split
+// sc_j = 8 a_j + b_j (a_j, b_j < 8) and folded into the int8 operands q a_j
+// and q b_j (<= 105), so int8 MFMAs accumulate a whole super-block in int32
+// with no per-output scaling: four per sub-block, (q a, q b) x (q1, q2).  The
+// mins enter once per super-block through two fp16 MFMAs of the row's m_j
+// (each twice) against the pair's 16-element sums of q1 and q2 (exact
+// integers in fp32).  Per super-block and output, with F_l = 8 acc_a,l +
+// acc_b,l and M_l = sum_j m_j S_j,l:
+//   y += d dx (F_1 + F_2 / 256) - dmin dx (M_1 + M_2 / 256)
+// with d, dmin the row's fp16 super-block scales (a1's reading of the
+// scale bytes) and dx the pair's block scale; fp32 accumulation.
+//
+// Items: (tile, 32-pair sub-tile, row block), otherwise the layout of
+// k_moe_f16 (8 waves x 32 weight rows, MODE 0 gate/up interleaved per wave,
+// activation tile double-buffered in LDS, one barrier per chunk).
+// ---------------------------------------------------------------------------
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int I8_MT = 32;                 // pairs per item
+constexpr int I8_LD = PF_KC + 16;         // LDS row stride in bytes (one activation level)
+constexpr size_t I8_LDS_BYTES = (size_t)2 * I8_MT * 2 * I8_LD + I8_MT * 8;
+
+// Position of element e (< 16) of a 16-element group in the stored order.
+__device__ __forceinline__ int q8_pos(int e) {
+    const int h = e & 8, r = e & 7;
+    return h + ((r & 1) << 2) + (r >> 1);
+}
+
+// One wave per 256-element block of a float array (blocks of 256
+// consecutive floats).  BLOCKS = false: the prefill operand form of a row of
+// n floats (int8 levels [row][2][n] in the MFMA order above, block scales
+// [row][n/256], fp16 group sums [row][2][n/16]); BLOCKS = true: the
+// reference's Q8_K block of the first level only (layer4/tb_gguf.c:281-288:
+// f32 d at 0, int8 qs[256] in element order at 4, int16 bsums[16] at 260;
+// 292 bytes), written to q8 with n, dq and bs16 unused.
+template <bool BLOCKS>
+__global__ __launch_bounds__(256) void k_rows_q8(const float *__restrict__ in, int n, long long nblocks,
+                                                 int8_t *__restrict__ q8, float *__restrict__ dq,
+                                                 _Float16 *__restrict__ bs16) {
+    __shared__ int8_t stage[4][2][256];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long long b0 = (long long)blockIdx.x * 4 + wave;
+    const bool valid = b0 < nblocks;   // past the end: redo the last block, store nothing
+    const long long b = valid ? b0 : nblocks - 1;
+    const float4 v = reinterpret_cast<const float4 *>(in + b * 256)[lane];
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = wave_max(amax);
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    const float xs[4] = {v.x, v.y, v.z, v.w};
+    int s1 = 0, s2 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float r = rintf(xs[i] * id);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        const int q1 = (int)r;
+        float r2 = rintf((xs[i] - r * d) * (id * 256.0f));
+        r2 = fminf(fmaxf(r2, -127.0f), 127.0f);
+        const int q2 = (int)r2;
+        s1 += q1;
+        s2 += q2;
+        const int e = 4 * (lane & 3) + i;   // element within the lane's 16-element group
+        const int pos = 16 * (lane >> 2) + (BLOCKS ? e : q8_pos(e));
+        stage[wave][0][pos] = (int8_t)q1;
+        stage[wave][1][pos] = (int8_t)q2;
+    }
+    // the group's sums over its four lanes
+    s1 += __shfl_xor(s1, 1);
+    s1 += __shfl_xor(s1, 2);
+    s2 += __shfl_xor(s2, 1);
+    s2 += __shfl_xor(s2, 2);
+    __syncthreads();
+    if (!valid) return;
+    if constexpr (BLOCKS) {
+        uint8_t *blk = reinterpret_cast<uint8_t *>(q8) + b * 292;   // 4-byte aligned
+        reinterpret_cast<int *>(blk + 4)[lane] = reinterpret_cast<const int *>(stage[wave][0])[lane];
+        if ((lane & 3) == 0) reinterpret_cast<int16_t *>(blk + 260)[lane >> 2] = (int16_t)s1;
+        if (lane == 0) *reinterpret_cast<float *>(blk) = d;
+    } else {
+        const int nb = n / 256;
+        const long long row = b / nb, blk = b % nb;
+        int8_t *qr = q8 + row * 2 * n + blk * 256;
+        reinterpret_cast<int *>(qr)[lane] = reinterpret_cast<const int *>(stage[wave][0])[lane];
+        reinterpret_cast<int *>(qr + n)[lane] = reinterpret_cast<const int *>(stage[wave][1])[lane];
+        if ((lane & 3) == 0) {
+            _Float16 *sr = bs16 + row * 2 * (n / 16) + blk * 16 + (lane >> 2);
+            sr[0] = (_Float16)(float)s1;
+            sr[n / 16] = (_Float16)(float)s2;
+        }
+        if (lane == 0) dq[b] = d;
+    }
+}
+
+// One lane's Q4_K data for a 128-column chunk c of its row: d/dmin, the
+// chunk's four scale bytes, the four mins of its half of the super-block
+// (for the min MFMA), and 8 quant bytes of each of the chunk's four
+// sub-blocks (elements 16 lh .. 16 lh + 15 of sub-block 4 (c & 1) + ks).
+struct Q4I8 {
+    unsigned dd, sw, mw;
+    uint2 q[4];
+};
+
+__device__ __forceinline__ void q4i8_load(const uint8_t *sb, int c, int lh, Q4I8 &r) {
+    r.dd = *reinterpret_cast<const unsigned *>(sb);
+    r.sw = *reinterpret_cast<const unsigned *>(sb + ((c & 1) ? 12 : 4));
+    r.mw = *reinterpret_cast<const unsigned *>(sb + (lh ? 16 : 8));   // mins 4..7 sit in quant bytes 0..3
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+        r.q[ks] = *reinterpret_cast<const uint2 *>(sb + 16 + 16 * (4 * (c & 1) + ks) + 8 * lh);
+}
+
+template <int MODE, int NS>
+__global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1,
+                                                       const int8_t *__restrict__ X, const float *__restrict__ XD,
+                                                       const _Float16 *__restrict__ XB, int x_rows,
+                                                       const int *__restrict__ tpair, const int *__restrict__ ttok,
+                                                       const PfTile *__restrict__ tiles, const int *__restrict__ ntiles,
+                                                       int ncb, int H, int F, float *__restrict__ out) {
+    constexpr int K = NS * PF_KC;
+    constexpr int NSB = K / 256;
+    constexpr int NQ = PF_MT / I8_MT;   // sub-tiles per tile
+    extern __shared__ __attribute__((aligned(16))) int8_t i8_lds[];   // [2][I8_MT][2][I8_LD]
+    int *po_s = reinterpret_cast<int *>(i8_lds + 2 * I8_MT * 2 * I8_LD);
+    int *px_s = po_s + I8_MT;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, lh = lane >> 5;
+    const long long rb = (long long)(K / 256) * 144;
+    const int xbytes = x_rows * 2 * K;
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *)X, (short)0, xbytes, 0x00020000);
+    const int nitems = *ntiles * NQ * ncb;
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+        const int tix = item / (NQ * ncb), qt = (item / ncb) % NQ, cb = item % ncb;
+        const PfTile tl = tiles[tix];
+        const int n = min(tl.n - I8_MT * qt, I8_MT);   // pairs of this sub-tile (uniform)
+        if (n <= 0) continue;                         // uniform: no barrier skipped by part of the group
+        const int *xrows = (MODE == 0 ? ttok : tpair) + tix * PF_MT + I8_MT * qt;
+        // activation staging: thread -> (pair slot tid >> 4, level (tid >> 3) & 1, 16 bytes at 16 (tid & 7))
+        const int xr = xrows[tid >> 4];
+        const int xoff = xr >= 0 ? (xr * 2 + ((tid >> 3) & 1)) * K + 16 * (tid & 7) : xbytes;
+        if (tid < I8_MT) {
+            po_s[tid] = tpair[tix * PF_MT + I8_MT * qt + tid];
+            px_s[tid] = xrows[tid];
+        }
+        const uint8_t *wrow;
+        if (MODE == 0) {
+            const int col = cb * PF_COLS + 16 * wave + (li & 15);
+            wrow = (li < 16 ? W0 : W1) + ((long long)tl.e * F + col) * rb;
+        } else {
+            wrow = W0 + ((long long)tl.e * H + cb * PF_ROWS + 32 * wave + li) * rb;
+        }
+        auto wload = [&](Q4I8 &w, int c) {
+            c = min(c, NS - 1);
+            q4i8_load(wrow + (long long)(c >> 1) * 144, c, lh, w);
+        };
+        u32x4 xv;
+        auto xload = [&](int c) {
+            c = min(c, NS - 1);
+            xv = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff < xbytes ? xoff + c * PF_KC : xbytes, 0, 0);
+        };
+        auto xstore = [&](int buf) {
+            *reinterpret_cast<u32x4 *>(i8_lds + ((buf * I8_MT + (tid >> 4)) * 2 + ((tid >> 3) & 1)) * I8_LD +
+                                       16 * (tid & 7)) = xv;
+        };
+        Q4I8 w0, w1, w2;
+        wload(w0, 0);
+        wload(w1, min(1, NS - 1));
+        xload(0);
+        __syncthreads();   // po_s / px_s written
+        xstore(0);
+        xload(1);
+        __syncthreads();
+        const int pa = px_s[min(li, n - 1)];   // this lane's pair's activation row
+        i32x16 aa1 = {}, ab1 = {}, aa2 = {}, ab2 = {};
+        f32x16 y = {};
+        // super-block flush: y += d dx (F1 + F2/256) - dmin dx (M1 + M2/256)
+        auto flush = [&](const Q4I8 &w, int sb) {
+            f16x8 am;   // this lane's row's mins m_{4 lh + i}, each twice
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const _Float16 m = (_Float16)(float)((w.mw >> (8 * i)) & 63u);
+                am[2 * i] = m;
+                am[2 * i + 1] = m;
+            }
+            const float dx = XD[(long long)pa * NSB + sb];
+            const _Float16 *bsr = XB + (long long)pa * 2 * (K / 16) + 16 * sb + 8 * lh;
+            const f16x8 b1 = *reinterpret_cast<const f16x8 *>(bsr);
+            const f16x8 b2 = *reinterpret_cast<const f16x8 *>(bsr + K / 16);
+            const f32x16 m1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, b1, f32x16{}, 0, 0, 0);
+            const f32x16 m2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, b2, f32x16{}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                // d and dmin of accumulator r's row, from the lane that loads that row
+                const int row = 8 * (r >> 2) + 4 * lh + (r & 3);
+                const unsigned ddr = (unsigned)__shfl((int)w.dd, row);
+                const float dw = f16_ref((uint16_t)(ddr & 0xFFFFu)) * dx;
+                const float mw = f16_ref((uint16_t)(ddr >> 16)) * dx;
+                const float f = fmaf((float)(8 * aa2[r] + ab2[r]), 1.0f / 256.0f, (float)(8 * aa1[r] + ab1[r]));
+                const float mm = fmaf(m2[r], 1.0f / 256.0f, m1[r]);
+                y[r] = fmaf(dw, f, y[r]);
+                y[r] = fmaf(-mw, mm, y[r]);
+            }
+            aa1 = i32x16{};
+            ab1 = i32x16{};
+            aa2 = i32x16{};
+            ab2 = i32x16{};
+        };
+        auto chunk = [&](int s, const Q4I8 &wc, Q4I8 &wn) {
+            wload(wn, s + 2);
+            if (s < NS) {
+                const int8_t *xb = i8_lds + ((s & 1) * I8_MT + li) * 2 * I8_LD + 16 * lh;
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) {
+                    const uint2 q = wc.q[ks];
+                    const unsigned sc = (wc.sw >> (8 * ks)) & 63u;
+                    const unsigned short a = (unsigned short)(sc >> 3), b = (unsigned short)(sc & 7u);
+                    const unsigned n0 = q.x & 0x0F0F0F0Fu, n1 = (q.x >> 4) & 0x0F0F0F0Fu;
+                    const unsigned n2 = q.y & 0x0F0F0F0Fu, n3 = (q.y >> 4) & 0x0F0F0F0Fu;
+                    const u16x2 va = {a, a}, vb = {b, b};
+                    auto mul = [](unsigned v, u16x2 f) {
+                        return __builtin_bit_cast(unsigned, __builtin_bit_cast(u16x2, v) * f);
+                    };
+                    const i32x4 Aa = {(int)mul(n0, va), (int)mul(n1, va), (int)mul(n2, va), (int)mul(n3, va)};
+                    const i32x4 Ab = {(int)mul(n0, vb), (int)mul(n1, vb), (int)mul(n2, vb), (int)mul(n3, vb)};
+                    const i32x4 bv1 = *reinterpret_cast<const i32x4 *>(xb + 32 * ks);
+                    const i32x4 bv2 = *reinterpret_cast<const i32x4 *>(xb + I8_LD + 32 * ks);
+                    aa1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(Aa, bv1, aa1, 0, 0, 0);
+                    ab1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ab, bv1, ab1, 0, 0, 0);
+                    aa2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(Aa, bv2, aa2, 0, 0, 0);
+                    ab2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ab, bv2, ab2, 0, 0, 0);
+                }
+                if (s & 1) flush(wc, s >> 1);
+                if (s + 1 < NS) xstore((s + 1) & 1);
+            }
+            xload(s + 2);
+            if (s < NS) __syncthreads();
+        };
+        for (int s = 0; s < NS; s += 3) {
+            chunk(s, w0, w2);
+            chunk(s + 1, w1, w0);
+            chunk(s + 2, w2, w1);
+        }
+        // accumulator register r of lane l: row 8(r/4) + 4 lh + r%4 of the
+        // wave's 32, pair li of the sub-tile
+        if (li < n) {
+            const int p = po_s[li];
+            if (MODE == 0) {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    float o[4];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const int r = 4 * h + c;
+                        const float g = y[r], u = y[r + 8];
+                        o[c] = g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+                    }
+                    const int col = cb * PF_COLS + 16 * wave + 8 * h + 4 * lh;
+                    *reinterpret_cast<float4 *>(out + (long long)p * F + col) = make_float4(o[0], o[1], o[2], o[3]);
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    const int row = cb * PF_ROWS + 32 * wave + 8 * h + 4 * lh;
+                    *reinterpret_cast<float4 *>(out + (long long)p * H + row) =
+                        make_float4(y[4 * h], y[4 * h + 1], y[4 * h + 2], y[4 * h + 3]);
+                }
+            }
+        }
+        __syncthreads();   // the next item rewrites the pair lists and the activation buffers
+    }
+}
+
+template <int MODE>
+static hipError_t launch_moe_i8(int ns, unsigned nwg, hipStream_t st, const uint8_t *W0, const uint8_t *W1,
+                                const int8_t *X, const float *XD, const _Float16 *XB, int x_rows, const int *tpair,
+                                const int *ttok, const PfTile *tiles, const int *ntiles, int ncb, int H, int F,
+                                float *out) {
+#define TBQ_NS(N)                                                                                                   \
+    case N:                                                                                                         \
+        hipLaunchKernelGGL((k_moe_i8<MODE, N>), dim3(nwg), dim3(PF_THREADS), I8_LDS_BYTES, st, W0, W1, X, XD, XB,   \
+                           x_rows, tpair, ttok, tiles, ntiles, ncb, H, F, out);                                     \
+        break;
+    switch (ns) {
+        TBQ_NS(2) TBQ_NS(4) TBQ_NS(6) TBQ_NS(8) TBQ_NS(12) TBQ_NS(16) TBQ_NS(24) TBQ_NS(32)
+    default:
+        return hipErrorNotSupported;
+    }
+#undef TBQ_NS
+    return hipGetLastError();
 }
 
 size_t prefill_workspace_bytes(int T, int k, int E, int H, int F) {
@@ -415,6 +732,15 @@ size_t prefill_workspace_bytes(int T, int k, int E, int H, int F) {
     auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
     return up(P * 4) + up(max_tiles * sizeof(PfTile)) + 256 + 2 * up(max_tiles * PF_MT * 4) + up(P * F * 2) +
            up((size_t)T * H * 2) + up(P * 4) + up((size_t)T * 4);
+}
+
+// Persistent grid of the expert GEMMs: one workgroup per CU (about 200
+// VGPRs per lane hold two of the eight waves per SIMD, so a second
+// workgroup would only queue behind the first), never more than the item
+// count bound.
+static unsigned pf_grid(unsigned max_items) {
+    const unsigned g = (unsigned)(tbq_cu_count() > 0 ? tbq_cu_count() : 256);
+    return max_items < g ? max_items : g;
 }
 
 template <int MODE>
@@ -445,6 +771,71 @@ static hipError_t launch_moe_f16(int ns, unsigned nwg, hipStream_t st, const uin
 bool gemm_k_supported(int K) {
     const int n = K / PF_KC;
     return K % 256 == 0 && (n == 2 || n == 4 || n == 6 || n == 8 || n == 12 || n == 16 || n == 24 || n == 32);
+}
+
+// int8 mode workspace: the dispatch lists of the fp16 mode, then the
+// two-level Q8_K activations of x ([T][2][H] int8, block scales [T][H/256],
+// fp16 16-element sums [T][2][H/16]) and of the SwiGLU output ([P][2][F],
+// the same three).
+size_t prefill_i8_workspace_bytes(int T, int k, int E, int H, int F) {
+    const size_t P = (size_t)T * k;
+    const size_t max_tiles = (P + PF_MT - 1) / PF_MT + E;
+    auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    return up(P * 4) + up(max_tiles * sizeof(PfTile)) + 256 + 2 * up(max_tiles * PF_MT * 4) +
+           up((size_t)T * H * 2) + up((size_t)T * H / 256 * 4) + up((size_t)T * H / 16 * 4) + up(P * F * 2) +
+           up(P * F / 256 * 4) + up(P * F / 16 * 4);
+}
+
+// Rows of n floats (n a multiple of 256) to Q8_K blocks in the int8 MFMA
+// operand order (k_rows_q8).
+hipError_t launch_rows_q8(const float *in, long long rows, int n, int8_t *q8, float *dq, _Float16 *bs16,
+                          hipStream_t st) {
+    const long long nb = rows * (n / 256);
+    hipLaunchKernelGGL(k_rows_q8<false>, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, st, in, n, nb, q8, dq, bs16);
+    return hipGetLastError();
+}
+
+// n floats (a multiple of 256) to n / 256 Q8_K blocks of 292 bytes.
+hipError_t launch_quantize_q8k(const float *in, long long n, void *blocks, hipStream_t st) {
+    const long long nb = n / 256;
+    hipLaunchKernelGGL(k_rows_q8<true>, dim3((unsigned)((nb + 3) / 4)), dim3(256), 0, st, in, 256, nb,
+                       (int8_t *)blocks, nullptr, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_prefill_q4k_i8(const MoeArgs &a, void *scratch, hipStream_t st) {
+    if (a.qtype != QT_Q4_K || !gemm_k_supported(a.H) || !gemm_k_supported(a.F) || a.H % PF_ROWS ||
+        a.F % PF_COLS || a.T > 65536 || a.E > 256)
+        return hipErrorNotSupported;
+    const size_t P = (size_t)a.T * a.k;
+    const int max_tiles = (int)((P + PF_MT - 1) / PF_MT + a.E);
+    auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    char *w = (char *)scratch;
+    int *perm = (int *)w; w += up(P * 4);
+    PfTile *tiles = (PfTile *)w; w += up((size_t)max_tiles * sizeof(PfTile));
+    int *ntiles = (int *)w; w += 256;
+    int *tpair = (int *)w; w += up((size_t)max_tiles * PF_MT * 4);
+    int *ttok = (int *)w; w += up((size_t)max_tiles * PF_MT * 4);
+    int8_t *x8 = (int8_t *)w; w += up((size_t)a.T * a.H * 2);
+    float *xd = (float *)w; w += up((size_t)a.T * a.H / 256 * 4);
+    _Float16 *xb = (_Float16 *)w; w += up((size_t)a.T * a.H / 16 * 4);
+    int8_t *a8 = (int8_t *)w; w += up(P * a.F * 2);
+    float *ad = (float *)w; w += up(P * a.F / 256 * 4);
+    _Float16 *ab = (_Float16 *)w;
+    hipError_t err = launch_rows_q8(a.xn, a.T, a.H, x8, xd, xb, st);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, st, a.sel_idx, a.T, a.k, a.E, perm, tiles, ntiles, tpair,
+                       ttok);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const int ncb0 = a.F / PF_COLS, ncb1 = a.H / PF_ROWS;
+    err = launch_moe_i8<0>(a.H / PF_KC, pf_grid((unsigned)(PF_MT / I8_MT * max_tiles * ncb0)), st, (const uint8_t *)a.gate,
+                           (const uint8_t *)a.up, x8, xd, xb, a.T, tpair, ttok, tiles, ntiles, ncb0, a.H, a.F, a.act);
+    if (err != hipSuccess) return err;
+    err = launch_rows_q8(a.act, (long long)P, a.F, a8, ad, ab, st);
+    if (err != hipSuccess) return err;
+    return launch_moe_i8<1>(a.F / PF_KC, pf_grid((unsigned)(PF_MT / I8_MT * max_tiles * ncb1)), st, (const uint8_t *)a.down,
+                            nullptr, a8, ad, ab, (int)P, tpair, ttok, tiles, ntiles, ncb1, a.H, a.F, a.y);
 }
 
 hipError_t launch_rows_f16(const float *in, int rows, int n, _Float16 *out, float *inv, hipStream_t st) {
@@ -494,14 +885,14 @@ hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t s
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     const int ncb0 = a.F / PF_COLS, ncb1 = a.H / PF_ROWS;
-    err = launch_moe_f16<0>(a.H / PF_KC, (unsigned)(max_tiles * ncb0), st, (const uint8_t *)a.gate,
+    err = launch_moe_f16<0>(a.H / PF_KC, pf_grid((unsigned)(max_tiles * ncb0)), st, (const uint8_t *)a.gate,
                             (const uint8_t *)a.up, x16, a.T, xinv, tpair, ttok, tiles, ntiles, ncb0, a.H, a.F, a.act);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_rows_f16, dim3((unsigned)P), dim3(256), 0, st, a.act, a.F, act16, ainv);
     err = hipGetLastError();
     if (err != hipSuccess) return err;
-    return launch_moe_f16<1>(a.F / PF_KC, (unsigned)(max_tiles * ncb1), st, (const uint8_t *)a.down, nullptr, act16,
-                             (int)P, ainv, tpair, ttok, tiles, ntiles, ncb1, a.H, a.F, a.y);
+    return launch_moe_f16<1>(a.F / PF_KC, pf_grid((unsigned)(max_tiles * ncb1)), st, (const uint8_t *)a.down, nullptr,
+                             act16, (int)P, ainv, tpair, ttok, tiles, ntiles, ncb1, a.H, a.F, a.y);
 }
 
 }  // namespace tbq
