@@ -29,7 +29,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "int8": 5000.0}   # MI355X dense, per GPU
 PMC_COPY_BYTES = 256 << 20
-PROFILES = ("q4k", "q4k_big", "sweep", "moe_b1", "moe_b16", "moe_prefill")
+PROFILES = ("q4k", "q4k_big", "sweep", "moe_b1", "moe_b16", "moe_prefill", "moe_prefill_i8")
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "q4k_matvec_4096x4096_pmc.txt")
 
 
@@ -179,6 +179,9 @@ def gpu_leg(args):
     if args.moe_only:
         res["moe"] = moe_leg(tb, fm, synth, torch, rng, stream)
         return res
+    # ---- HBM ceiling on this box: torch's read reduction and copy over
+    # buffers larger than the MALL (a reference point for the fractions) --
+    res["hbm_ceiling"] = hbm_ceiling(torch, stream)
     # ---- steady-state Q4_K stream: a matrix larger than the MALL --------
     res["q4k_steady"] = sweep_leg(tb, fm, synth, torch, rng, stream, [(fm.Q4_K, 151936, 4096),
                                                                       (fm.Q4_K, 65536, 4096)])
@@ -205,6 +208,31 @@ def _sweep_shapes():
 
 
 SWEEP_SHAPES = None   # filled in main() (formats import)
+
+
+def hbm_ceiling(torch, stream):
+    """Read and copy bandwidth of torch's own kernels on 512 MiB buffers
+    (two alternating, so neither fits the 256 MB MALL)."""
+    n = 512 << 20
+    bufs = [torch.ones(n // 4, dtype=torch.float32, device="cuda") for _ in range(2)]
+    dst = torch.empty(n // 4, dtype=torch.float32, device="cuda")
+    acc = torch.zeros((), dtype=torch.float32, device="cuda")
+
+    def rd():
+        for b in bufs:
+            torch.sum(b, dim=0, out=acc)
+
+    def cp():
+        for b in bufs:
+            dst.copy_(b)
+    r = time_region(rd, 10, 2, stream, graph=False) / 20
+    c = time_region(cp, 10, 2, stream, graph=False) / 20
+    out = dict(read_gbs=round(n / r / 1e9, 1), copy_gbs=round(2 * n / c / 1e9, 1), bytes=n,
+               kernels="torch.sum (read), Tensor.copy_ (read + write)")
+    log(f"HBM ceiling: torch.sum read {out['read_gbs']:.0f} GB/s, copy_ {out['copy_gbs']:.0f} GB/s (read+write)")
+    del bufs, dst
+    torch.cuda.empty_cache()
+    return out
 
 
 def hbm_roofline(nbytes, secs):
@@ -238,15 +266,16 @@ def profile_leg(name, tb, fm, synth, torch):
             torch.cuda.empty_cache()
     else:
         H, F, E, k = 2048, 768, 128, 8
-        layers, keep = moe_layers(tb, fm, synth, torch, H, F, E, k, 3 if name != "moe_prefill" else 1)
-        T = {"moe_b1": 1, "moe_b16": 16, "moe_prefill": 512}[name]
-        mode = tb.TBQ_MOE_BF16 if name == "moe_prefill" else tb.TBQ_MOE_FP32
+        prefill = name.startswith("moe_prefill")
+        layers, keep = moe_layers(tb, fm, synth, torch, H, F, E, k, 1 if prefill else 3)
+        T = 512 if prefill else {"moe_b1": 1, "moe_b16": 16}[name]
+        mode = {"moe_prefill": tb.TBQ_MOE_BF16, "moe_prefill_i8": tb.TBQ_MOE_I8}.get(name, tb.TBQ_MOE_FP32)
         L = layers[0]
-        if name == "moe_prefill":
+        if prefill:
             bias = torch.from_numpy(synth.zipf_router_bias(E, 1.1, 1.0, rng)).cuda()
             L = tb.moe_layer(H, F, E, k, fm.Q4_K, *L._keep[:4], bias=bias)
             layers = [L]
-        n = 8 if name == "moe_prefill" else 24
+        n = 8 if prefill else 24
         xs = torch.from_numpy(synth.activations((n, T, H), rng)).cuda()
         out = torch.empty((T, H), dtype=torch.float32, device="cuda")
         ws = torch.zeros(tb.moe_workspace_size(L, T, mode), dtype=torch.uint8, device="cuda")
@@ -438,7 +467,8 @@ def moe_leg(tb, fm, synth, torch, rng, stream):
     U = distinct_experts(Lb, xs[None], T)
     nbytes = router_bytes + U * EXPERT_BYTES + 3 * T * H * 4
     flops = 2.0 * T * k * 3 * H * F + 2.0 * T * E * H
-    for name, mode, peak in (("prefill_512_fp16_mfma", tb.TBQ_MOE_BF16, MFMA_PEAK_TFLOPS["fp16"]),):
+    for name, mode, peak in (("prefill_512_fp16_mfma", tb.TBQ_MOE_BF16, MFMA_PEAK_TFLOPS["fp16"]),
+                             ("prefill_512_int8_mfma", tb.TBQ_MOE_I8, MFMA_PEAK_TFLOPS["int8"])):
         ws_t = torch.zeros(tb.moe_workspace_size(Lb, T, mode), dtype=torch.uint8, device="cuda")
         sec = time_region(lambda: tb.moe_forward(Lb, T, xs, rs, out, workspace=ws_t, mode=mode), 20, 3,
                           stream) / 20
@@ -602,7 +632,7 @@ def main():
         "extra": {"device": res["device"], "warm_mall_gbs": round(h["warm_gbs"], 1),
                   "warm_us_per_launch": round(h["warm_us_per_launch"], 3),
                   "abi_matvec_us": None if res.get("abi_matvec_us") is None else round(res["abi_matvec_us"], 2),
-                  "q4k_steady": res.get("q4k_steady"),
+                  "hbm_ceiling": res.get("hbm_ceiling"), "q4k_steady": res.get("q4k_steady"),
                   "sweep": res.get("sweep"), "ggml_sweep": res.get("ggml_sweep"), "moe": res.get("moe"),
                   "dense": res.get("dense"),
                   "cpu_detail": None if cpu is None else cpu["detail"],
