@@ -164,6 +164,33 @@ def test_moe_decode_config(oracle, qwen_layer, T):
     assert rel_l2(out - resid, ref - resid) <= TOL
 
 
+@pytest.mark.parametrize("T,H,F,E,k,qt,skew", [
+    (8, 2048, 768, 128, 8, fm.Q4_K, False),
+    (24, 1024, 512, 64, 6, fm.Q4_K, True),
+    (32, 2048, 768, 128, 8, fm.Q4_K, True),
+    (12, 4096, 1536, 256, 8, fm.Q4_K, False),
+    (16, 2048, 768, 128, 8, fm.GGML | fm.Q4_K, True),
+])
+def test_moe_decode_expert_order(oracle, T, H, F, E, k, qt, skew):
+    """Decode batches of 8..32 tokens run their expert kernels in expert
+    order (a sorted pair list, down per pair, slot-ordered combine).  With a
+    skewed router bias many tokens share an expert; every index and weight
+    equals the reference's and the output is within tolerance."""
+    router, gate, up, down = synth.moe_layer(H, F, E, qt, seed=T + E)
+    rng = np.random.default_rng(T * 7 + k)
+    bias = synth.zipf_router_bias(E, 1.1, 2.0, rng) if skew else None
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    print("moe expert order T=", T, "H=", H, "E=", E, "k=", k, "qt=", qt, flush=True)
+    out, idx, w = gpu_moe(xn, resid, router, gate, up, down, F, k, qt, bias=bias)
+    ref, ridx, rw = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=qt, bias=bias)
+    assert np.array_equal(idx, ridx)
+    assert bits_equal(w, rw)
+    if skew:   # the bias concentrates the selections: some expert has several tokens
+        assert np.bincount(idx[:, :k].ravel(), minlength=E).max() >= 3
+    assert rel_l2(out - resid, ref - resid) <= TOL
+
+
 def test_moe_decode_router_many_tokens(oracle):
     """Routing inside tbq_moe_forward over 512 decode tokens (32 batches of
     16): every index, slot and weight equal to the reference's."""

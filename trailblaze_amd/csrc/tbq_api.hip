@@ -229,6 +229,7 @@ size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode) {
     n += align256((size_t)T * L->E * 4);                     // router logits
     n += align256((size_t)T * k * L->F * 4);                 // act
     n += align256((size_t)T * k * L->H * 4);                 // y
+    n += align256((size_t)(2 + 3 * L->E + T * k) * 4);       // decode order by expert
     if (mode == TBQ_MOE_BF16) n += align256(prefill_workspace_bytes(T, k, L->E, L->H, L->F));
     if (mode == TBQ_MOE_I8) n += align256(prefill_i8_workspace_bytes(T, k, L->E, L->H, L->F));
     return n;
@@ -292,6 +293,7 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     a.logits = (float *)(ws + off); off += align256((size_t)T * a.E * 4);
     a.act = (float *)(ws + off); off += align256((size_t)T * a.k * a.F * 4);
     a.y = (float *)(ws + off); off += align256((size_t)T * a.k * a.H * 4);
+    a.grp = (int *)(ws + off); off += align256((size_t)(2 + 3 * a.E + T * a.k) * 4);
     a.sel_idx = sel_idx ? sel_idx : ws_idx;
     a.sel_w = sel_w ? sel_w : ws_w;
     if (mode == TBQ_MOE_BF16) return hip_ok(launch_moe_bf16(a, ws + off, S(s)), "moe launch (prefill MFMA)");

@@ -41,6 +41,7 @@ struct MoeArgs {
     float *sel_w;      // [T][8]
     float *act;        // [T*k][F]
     float *y;          // [T*k][H]
+    int *grp;          // decode order by expert: 2 + 3E + T*k ints (null: the per-pair order)
 };
 
 hipError_t launch_dequant(int qt, const void *W, long long nweights, float *out, hipStream_t s);
@@ -63,6 +64,8 @@ hipError_t launch_expf(const float *in, float *out, long long n, hipStream_t s);
 hipError_t launch_route(const float *xn, const float *router, const float *bias, int T, int H, int E,
                         int top_k, int *sel_idx, float *sel_w, hipStream_t st);
 hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st);
+// out = resid + sum over slots, in slot order, of sel_w * y[t*k + s]
+hipError_t launch_combine(const MoeArgs &a, hipStream_t st);
 hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
                          float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st,
                          _Float16 *x16 = nullptr, float *xinv = nullptr, bool *x16_done = nullptr);

@@ -194,26 +194,39 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, 
 // a slot whose expert index is outside [0, E) (never produced by the
 // router; its y may be unwritten) is skipped.
 // Four consecutive outputs per thread (H is a multiple of 4), each summed
-// exactly as the scalar form.
-__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, const int *__restrict__ sel_idx,
-                                                 const float *__restrict__ sel_w, const float *__restrict__ resid,
-                                                 int T, int H, int E, int k, float *__restrict__ out) {
+// exactly as the scalar form.  A thread's k slot loads are all issued before
+// its adds (unwritten y of a skipped slot is read and not used).
+template <int NT>
+__global__ __launch_bounds__(NT) void k_combine(const float *__restrict__ y, const int *__restrict__ sel_idx,
+                                                const float *__restrict__ sel_w, const float *__restrict__ resid,
+                                                int T, int H, int E, int k, float *__restrict__ out) {
     const long long n4 = (long long)T * H / 4;
     const int H4 = H / 4;
-    for (long long i = blockIdx.x * 256ll + threadIdx.x; i < n4; i += (long long)gridDim.x * 256) {
+    for (long long i = blockIdx.x * (long long)NT + threadIdx.x; i < n4; i += (long long)gridDim.x * NT) {
         const int t = (int)(i / H4), h4 = (int)(i - (long long)t * H4);
+        float4 v[8];
+        float w[8];
+        bool ok[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            ok[s] = false;
+            if (s < k) {
+                ok[s] = (unsigned)sel_idx[t * 8 + s] < (unsigned)E;
+                w[s] = sel_w[t * 8 + s];
+                v[s] = reinterpret_cast<const float4 *>(y + ((long long)t * k + s) * H)[h4];
+            }
+        }
+        const float4 r = reinterpret_cast<const float4 *>(resid)[i];
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s = 0; s < k; s++) {
-            if ((unsigned)sel_idx[t * 8 + s] >= (unsigned)E) continue;
-            const float w = sel_w[t * 8 + s];
-            const float4 v = reinterpret_cast<const float4 *>(y + ((long long)t * k + s) * H)[h4];
-            const float px = w * v.x, py = w * v.y, pz = w * v.z, pw = w * v.w;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            if (!ok[s]) continue;
+            const float px = w[s] * v[s].x, py = w[s] * v[s].y, pz = w[s] * v[s].z, pw = w[s] * v[s].w;
             acc.x = acc.x + px;
             acc.y = acc.y + py;
             acc.z = acc.z + pz;
             acc.w = acc.w + pw;
         }
-        const float4 r = reinterpret_cast<const float4 *>(resid)[i];
         reinterpret_cast<float4 *>(out)[i] = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
     }
 }
@@ -304,10 +317,19 @@ hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
     default: return hipErrorInvalidValue;
     }
     if (err != hipSuccess) return err;
-    long long n = (long long)a.T * a.H / 4;
-    int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-    hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_idx, a.sel_w, a.resid, a.T, a.H, a.E, a.k,
-                       a.out);
+    return launch_combine(a, st);
+}
+
+hipError_t launch_combine(const MoeArgs &a, hipStream_t st) {
+    const long long n = (long long)a.T * a.H / 4;
+    if (n <= 65536) {   // decode batches: small workgroups, one float4 per thread
+        hipLaunchKernelGGL(k_combine<64>, dim3((int)((n + 63) / 64)), dim3(64), 0, st, a.y, a.sel_idx, a.sel_w,
+                           a.resid, a.T, a.H, a.E, a.k, a.out);
+    } else {
+        const int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+        hipLaunchKernelGGL(k_combine<256>, dim3(grid), dim3(256), 0, st, a.y, a.sel_idx, a.sel_w, a.resid, a.T, a.H,
+                           a.E, a.k, a.out);
+    }
     return hipGetLastError();
 }
 
@@ -326,11 +348,7 @@ hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st) {
     if (err != hipSuccess) return err;
     err = launch_moe_prefill_q4k(a, scratch, st, x16_done);
     if (err != hipSuccess) return err;
-    long long n = (long long)a.T * a.H / 4;
-    int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-    hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_idx, a.sel_w, a.resid, a.T, a.H, a.E, a.k,
-                       a.out);
-    return hipGetLastError();
+    return launch_combine(a, st);
 }
 
 // Prefill on int8 MFMA: exact routing, Q8_K activations, grouped int8
@@ -343,11 +361,7 @@ hipError_t launch_moe_i8(const MoeArgs &a, void *scratch, hipStream_t st) {
     if (err != hipSuccess) return err;
     err = launch_moe_prefill_q4k_i8(a, scratch, st);
     if (err != hipSuccess) return err;
-    long long n = (long long)a.T * a.H / 4;
-    int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-    hipLaunchKernelGGL(k_combine, dim3(grid), dim3(256), 0, st, a.y, a.sel_idx, a.sel_w, a.resid, a.T, a.H, a.E, a.k,
-                       a.out);
-    return hipGetLastError();
+    return launch_combine(a, st);
 }
 
 }  // namespace tbq

@@ -254,6 +254,28 @@ __device__ __forceinline__ void router_dpp_chunks(const float4 *w4, const float4
     }
 }
 
+// H <= 64 * RD_CH * RD_ALL_NC: every load of the workgroup's slice is
+// issued up front (256 VGPRs at H = 2048), so only the first load's latency
+// is exposed and the chain consumes the chunks as they arrive.
+#ifndef TBQ_RD_ALL_NC
+#define TBQ_RD_ALL_NC 4
+#endif
+constexpr int RD_ALL_NC = TBQ_RD_ALL_NC;
+
+template <int NC>
+__device__ __forceinline__ float router_dpp_all(const float4 *w4, const float4 *x4, int j) {
+    float4 wb[NC * RD_CH], xb[NC * RD_CH];
+#pragma unroll
+    for (int i = 0; i < NC * RD_CH; i++) {
+        wb[i] = w4[16 * i + j];
+        xb[i] = x4[16 * i + j];
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC * RD_CH; i++) acc = chain_block64(acc, wb[i], xb[i]);
+    return acc;
+}
+
 template <int M, int NJ>
 __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn, const float *__restrict__ Wr,
                                                    const float *__restrict__ bias, int E, int top_k,
@@ -267,14 +289,18 @@ __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn,
     const bool ev = e < E;
     const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (long long)(ev ? e : 0) * H);
     const float4 *x4 = reinterpret_cast<const float4 *>(xn + (long long)t * H);
-    float4 wb[2][RD_CH], xb[2][RD_CH];
-#pragma unroll
-    for (int i = 0; i < RD_CH; i++) {
-        wb[0][i] = w4[16 * i + j];
-        xb[0][i] = x4[16 * i + j];
-    }
     float acc = 0.f;
-    router_dpp_chunks<0, NC>(w4, x4, j, wb, xb, acc);
+    if constexpr (NC <= RD_ALL_NC) {
+        acc = router_dpp_all<NC>(w4, x4, j);
+    } else {
+        float4 wb[2][RD_CH], xb[2][RD_CH];
+#pragma unroll
+        for (int i = 0; i < RD_CH; i++) {
+            wb[0][i] = w4[16 * i + j];
+            xb[0][i] = x4[16 * i + j];
+        }
+        router_dpp_chunks<0, NC>(w4, x4, j, wb, xb, acc);
+    }
     if (j == 15 && ev) {
         if (bias) acc = acc + bias[e];
         __hip_atomic_store(logits + (long long)t * E + e, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -310,13 +336,16 @@ __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn,
 constexpr int GU_THREADS = 64 * TBQ_GU_WAVES;
 constexpr int GU_ROWS = TBQ_GU_ROWS;   // output rows per wave
 
-template <int UPL, bool GG>
+template <int UPL, bool GG, int ROWS = GU_ROWS>
 __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
                                                             const float *__restrict__ xn, const int *__restrict__ sel_idx,
+                                                            const int *__restrict__ order, const int *__restrict__ nvalid,
                                                             int H, int F, int E, int k, float *__restrict__ act) {
     extern __shared__ uint32_t xd[];
     constexpr int LPR = 32;
-    const int pair = blockIdx.y, t = pair / k, s = pair % k;
+    // with an order list (expert-ordered valid pairs), column y runs pair order[y]
+    if (order && (int)blockIdx.y >= *nvalid) return;   // workgroup-uniform
+    const int pair = order ? order[blockIdx.y] : blockIdx.y, t = pair / k, s = pair % k;
     // an index outside [0, E) (never produced by the router) reads expert 0
     // and contributes 0: no weight read leaves the expert tensors
     const int e_sel = sel_idx[t * 8 + s];
@@ -327,13 +356,13 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int lr = lane & 31, half = lane >> 5;
     const uint8_t *Wb = (half ? up : gate) + (long long)e * F * rb;
-    const int r0 = (blockIdx.x * (GU_THREADS / 64) + wave) * GU_ROWS;
+    const int r0 = (blockIdx.x * (GU_THREADS / 64) + wave) * ROWS;
 
     XStager<GU_THREADS, (1024 + GU_THREADS - 1) / GU_THREADS> xs;   // H <= 8192
     xs.load(xn + (long long)t * H, H);
-    Q4KUnit raw[GU_ROWS][UPL];
+    Q4KUnit raw[ROWS][UPL];
 #pragma unroll
-    for (int rr = 0; rr < GU_ROWS; rr++) {
+    for (int rr = 0; rr < ROWS; rr++) {
         const int r = r0 + rr;
 #pragma unroll
         for (int i = 0; i < UPL; i++) {
@@ -344,7 +373,7 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
     xs.store(xd, H);
     __syncthreads();
 #pragma unroll
-    for (int rr = 0; rr < GU_ROWS; rr++) {
+    for (int rr = 0; rr < ROWS; rr++) {
         const int r = r0 + rr;
         if (r >= F) break;   // wave-uniform
         float acc = 0.f;
@@ -361,6 +390,133 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
             const float sg = g / den;
             act[(long long)pair * F + r] = ev ? sg * u_val : 0.f;
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode batches (2 <= T <= 32) in expert order.  k_group sorts the batch's
+// T*k selections by expert:
+//   grp[0]                U, the number of distinct experts
+//   grp[1 + u]            expert of group u (ascending)
+//   grp[1 + E + u]        first position of group u in the pair list
+//   grp[1 + 2E + u]       number of pairs in group u
+//   grp[1 + 3E + i]       pair list (t*k + s), by expert, then by token
+//   grp[1 + 3E + T*k]     number of valid pairs in the list
+// One workgroup of 256 threads; T*k <= 256, T <= 32, E <= 256.
+// The per-pair expert kernels then take their grid's pair column from the
+// list, so the workgroups of the pairs that share an expert run back to
+// back on the same XCDs (a workgroup's XCD follows its row block) and the
+// later ones read the expert's rows from L2 instead of HBM.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_group(const int *__restrict__ sel_idx, int T, int E, int k,
+                                               int *__restrict__ grp) {
+    __shared__ int cnt[256];
+    __shared__ unsigned tokmask[256];   // bit t: token t chose the expert (T <= 32)
+    __shared__ int wc[4], wg[4];
+    const int i = threadIdx.x, n = T * k;
+    const int t = i / k, s = i - t * k;
+    int e = -1;
+    if (i < n) {
+        e = sel_idx[t * 8 + s];
+        if ((unsigned)e >= (unsigned)E) e = -1;   // never produced by the router: left out
+    }
+    cnt[i] = 0;
+    tokmask[i] = 0u;
+    __syncthreads();
+    if (e >= 0) {
+        atomicAdd(&cnt[e], 1);
+        atomicOr(&tokmask[e], 1u << t);
+    }
+    __syncthreads();
+    // thread j = expert j: exclusive scans of the pair counts (list offsets)
+    // and of the non-empty flags (group ranks)
+    const int c = i < E ? cnt[i] : 0, g = c > 0;
+    int ic = c, ig = g;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int a = __shfl_up(ic, d), b = __shfl_up(ig, d);
+        if ((i & 63) >= d) {
+            ic += a;
+            ig += b;
+        }
+    }
+    if ((i & 63) == 63) {
+        wc[i >> 6] = ic;
+        wg[i >> 6] = ig;
+    }
+    __syncthreads();
+    int bc = 0, bg = 0;
+    for (int w = 0; w < (i >> 6); w++) {
+        bc += wc[w];
+        bg += wg[w];
+    }
+    const int off = bc + ic - c, rank = bg + ig - g;
+    if (g) {
+        grp[1 + rank] = i;
+        grp[1 + E + rank] = off;
+        grp[1 + 2 * E + rank] = c;
+    }
+    if (i == 255) {
+        grp[0] = bg + ig;
+        grp[1 + 3 * E + n] = bc + ic;
+    }
+    __syncthreads();
+    cnt[i] = off;   // list offset of expert i
+    __syncthreads();
+    if (e >= 0) grp[1 + 3 * E + cnt[e] + __popc(tokmask[e] & ((1u << t) - 1u))] = i;
+}
+
+// down for one pair: y[p][r] = W_down[e] act[p] over DG_ROWS rows, p taken
+// from the expert-ordered pair list (k_combine then adds the slots in slot
+// order).  grid = (H / DG_ROWS, T*k).
+constexpr int DG_THREADS = 512;
+#ifndef TBQ_DG_ROWS
+#define TBQ_DG_ROWS 128
+#endif
+constexpr int DG_ROWS = TBQ_DG_ROWS;   // rows per workgroup: passes of 32 (16 lanes per row)
+
+template <int UPL, bool GG>
+__global__ __launch_bounds__(DG_THREADS) void k_down_pair_q4k(const uint8_t *__restrict__ down,
+                                                              const float *__restrict__ act,
+                                                              const int *__restrict__ sel_idx,
+                                                              const int *__restrict__ order,
+                                                              const int *__restrict__ nvalid, int H, int F, int E,
+                                                              int k, float *__restrict__ y) {
+    extern __shared__ uint32_t xd[];   // the pair's act digits
+    constexpr int LPR = 16, PASSES = DG_ROWS / (DG_THREADS / LPR);
+    if ((int)blockIdx.y >= *nvalid) return;   // workgroup-uniform
+    const int pair = order[blockIdx.y];
+    const int e = sel_idx[(pair / k) * 8 + pair % k];
+    if ((unsigned)e >= (unsigned)E) return;   // the list holds valid pairs only
+    const long long rb = (long long)(F / 256) * 144;
+    const int U = F / 64;
+    const int lr = threadIdx.x & 15, rl = threadIdx.x >> 4;   // row of the pass
+    const int r0 = blockIdx.x * DG_ROWS;
+    XStager<DG_THREADS, 1> xs;   // F <= 4096
+    xs.load(act + (long long)pair * F, F);
+    Q4KUnit raw[PASSES][UPL];
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const uint8_t *row = down + ((long long)e * H + r0 + (DG_THREADS / LPR) * p + rl) * rb;
+#pragma unroll
+        for (int i = 0; i < UPL; i++) {
+            const int u = lr + LPR * i;
+            if (u < U) q4k_load<GG>(row, u, raw[p][i]);
+        }
+    }
+    xs.store(xd, F);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int r = r0 + (DG_THREADS / LPR) * p + rl;
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < UPL; i++) {
+            const int u = lr + LPR * i;
+            if (u < U) acc = q4k_unit_dot<GG>(raw[p][i], u, xd, acc);
+        }
+        acc = group_sum<16>(acc);
+        if (lr == 0) y[(long long)pair * H + r] = acc;
     }
 }
 
@@ -687,17 +843,46 @@ hipError_t launch_router(const float *xn, const float *router, const float *bias
     return launch_topk(logits, T, E, top_k, sel_idx, sel_w, st);
 }
 
+// Batches of at least this many tokens run in expert order.
+#ifndef TBQ_GRP_MIN_T
+#define TBQ_GRP_MIN_T 8
+#endif
+#ifndef TBQ_GU_ROWS_B
+#define TBQ_GU_ROWS_B 4
+#endif
+
 template <int UPL_GU, int UPL_DC, bool GG>
 static hipError_t launch_experts_q4k(const MoeArgs &a, hipStream_t st) {
     const int pairs = a.T * a.k;
+    const bool grouped = a.T >= TBQ_GRP_MIN_T && pairs <= 256 && a.T <= 32 && a.E <= 256 && a.H % DG_ROWS == 0 &&
+                         a.grp;
+    const int *order = grouped ? a.grp + 1 + 3 * a.E : nullptr, *nvalid = grouped ? order + pairs : nullptr;
+    hipError_t err;
+    if (grouped) {
+        hipLaunchKernelGGL(k_group, dim3(1), dim3(256), 0, st, a.sel_idx, a.T, a.E, a.k, a.grp);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
     {
-        const int out_per_wg = (GU_THREADS / 64) * GU_ROWS;
+        // batches: more rows per workgroup, fewer workgroups
+        const int rows = grouped ? TBQ_GU_ROWS_B : GU_ROWS;
+        const int out_per_wg = (GU_THREADS / 64) * rows;
         dim3 grid((a.F + out_per_wg - 1) / out_per_wg, pairs);
         size_t lds = (size_t)(a.H / 32) * XD_PER_SB * 4;
-        hipLaunchKernelGGL((k_gate_up_q4k<UPL_GU, GG>), grid, dim3(GU_THREADS), lds, st, (const uint8_t *)a.gate,
-                           (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.E, a.k, a.act);
-        hipError_t err = hipGetLastError();
-        if (err != hipSuccess) return err;
+        if (rows == GU_ROWS)
+            hipLaunchKernelGGL((k_gate_up_q4k<UPL_GU, GG>), grid, dim3(GU_THREADS), lds, st, (const uint8_t *)a.gate,
+                               (const uint8_t *)a.up, a.xn, a.sel_idx, order, nvalid, a.H, a.F, a.E, a.k, a.act);
+        else
+            hipLaunchKernelGGL((k_gate_up_q4k<UPL_GU, GG, TBQ_GU_ROWS_B>), grid, dim3(GU_THREADS), lds, st,
+                               (const uint8_t *)a.gate, (const uint8_t *)a.up, a.xn, a.sel_idx, order, nvalid, a.H,
+                               a.F, a.E, a.k, a.act);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
+    if (grouped) {
+        hipLaunchKernelGGL((k_down_pair_q4k<UPL_DC, GG>), dim3(a.H / DG_ROWS, pairs), dim3(DG_THREADS),
+                           (size_t)(a.F / 32) * XD_PER_SB * 4, st, (const uint8_t *)a.down, a.act, a.sel_idx, order,
+                           nvalid, a.H, a.F, a.E, a.k, a.y);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+        return launch_combine(a, st);
     }
     dim3 grid(a.H / DC_ROWS, a.T);
     size_t lds = (size_t)a.k * (a.F / 32) * XD_PER_SB * 4;
