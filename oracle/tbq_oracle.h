@@ -24,10 +24,18 @@
  *                          vectors from the compiled reference (bit-exact)
  *   tbo_swiglu             closed form + golden vectors
  *   tbo_moe_forward        golden vectors from the compiled reference
- *   tbo_quantize_q8k       no reference counterpart (the reference has no
- *                          Q8_K activation quantiser): parity unpinned;
- *                          closed-form round-trip bound only
- *   tbo_dot_q4k_avx512s    timing baseline only (never a parity target)
+ *   tbo_quantize_q8k       the reference has no Q8_K activation quantiser
+ *                          (it fixes the block layout, layer4/tb_gguf.c:
+ *                          281-288); pinned by what a max-abs quantiser
+ *                          must satisfy: d bit-equal to fl(max|x|/127),
+ *                          |x - d q| <= d/2, the extremal element at +-127
+ *                          with its sign, the zero block, bsums, round half
+ *                          to even; and its blocks decode through the
+ *                          reference-pinned Q8_K decoder to d q
+ *   tbo_dot_q4k_avx512s    the CPU timing baseline's restatement: exact on
+ *                          integer-valued matrices (bit-equal to the exact
+ *                          sum) and within 1e-5 of tbo_dequant_matvec at
+ *                          configs[0] (same decode, another sum order)
  *   tbo_f16_ieee,          ggml's layouts (qtype | 0x100, ggml_layout.c):
  *   tbo_ggml_dequant_row   f16 against numpy on all 65536 inputs; decoders
  *                          against an independent block packer and closed
