@@ -209,8 +209,9 @@ int tbq_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits
  * token-by-token prefill (layer4/tb_infer.c:1068-1075, one tb_infer_decode
  * step per prompt token).  Writes the K/V rows of every position and the
  * logits of the last token.  Models with hidden <= 8192 and ffn <= 16384
- * take the batched path for T >= 2, whatever their formats or layouts: each weight matrix
- * dequantised to fp16 and multiplied by rocBLAS, attention on fp16 MFMA,
+ * take the batched path for T >= 2, whatever their formats or layouts: the
+ * weight products on tbq_gemm's kernel (Q4_K dequantised inside it, other
+ * formats to fp16 first), attention on fp16 MFMA,
  * fp32 accumulation (logits within 1e-2 relative L2 of the sequential
  * decode); otherwise, and for T = 1, the decode step runs once per token
  * (identical to T tbq_dense_decode calls).  tokens_host is read by an
@@ -231,6 +232,19 @@ int tbq_dense_prefill_batched(const tbq_dense_model *m);
  * activation form of the TBQ_MOE_I8 prefill.  n a multiple of 256; x 16-byte
  * and blocks 4-byte aligned. */
 int tbq_quantize_q8k(const float *x, long long n, void *blocks, void *stream);
+
+/* ---- prefill GEMM --------------------------------------------------------- */
+/* C[T][N] (row stride ldc >= N floats) = X[T][K] . W[N][K]^T with the batched
+ * prefill's GEMM (hand-written fp16 MFMA, fp32 accumulate): X fp16 rows (IEEE
+ * halves); W rows of IEEE fp16 halves (wqt = 1, TBQ's F16 id, taken as IEEE
+ * halves here) or Q4_K in the reference's layout (wqt = 12), dequantised
+ * inside the GEMM to the fp16 values the prefill's fp16 weights hold.  N a
+ * multiple of 4, K of 256, T >= 1.  workspace: tbq_gemm_workspace_size()
+ * bytes (split-K partial sums; may be 0).  No counterpart in the reference
+ * (it prefills token by token, layer4/tb_infer.c:1068-1075). */
+size_t tbq_gemm_workspace_size(int T, int N, int K);
+int tbq_gemm(int wqt, const void *W, const void *X16, int T, int N, int K, float *C, int ldc, void *workspace,
+             size_t workspace_bytes, void *stream);
 
 /* ---- test hooks -------------------------------------------------------- */
 /* out[i] = expf(in[i]) evaluated by the device code the router uses. */

@@ -55,6 +55,8 @@ SYMBOLS = {
     "tbq_dense_prefill": (_i, [_vp, _vp, _i, _i, _vp, _vp, _sz, _vp]),
     "tbq_dense_prefill_batched": (_i, [_vp]),
     "tbq_quantize_q8k": (_i, [_vp, C.c_longlong, _vp, _vp]),
+    "tbq_gemm_workspace_size": (_sz, [_i, _i, _i]),
+    "tbq_gemm": (_i, [_i, _vp, _vp, _i, _i, _i, _vp, _i, _vp, _sz, _vp]),
     "tbq_expf_device": (_i, [_vp, _vp, _sz, _vp]),
     "tbq_expf_host": (_f, [_f]),
     # include/tbq_gguf.h
@@ -187,11 +189,24 @@ def moe_forward_noalloc(L: MoeLayer, T, xn, resid, out, sel_idx=None, sel_w=None
     return out
 
 
+def gemm(W, wqt: int, X16, T: int, N: int, K: int, C_out, ldc: int = 0, workspace=None, stream=None):
+    """C_out[T][ldc or N] = X16[T][K] . W[N][K]^T with the batched prefill's
+    GEMM (W fp16 halves, wqt = 1, or Q4_K rows, wqt = 12)."""
+    import torch
+    if workspace is None:
+        nb = int(lib().tbq_gemm_workspace_size(T, N, K))
+        workspace = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda") if nb else None
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(lib().tbq_gemm(wqt, _ptr(W), _ptr(X16), T, N, K, _ptr(C_out), ldc or N, _ptr(workspace), ws_bytes,
+                          _stream(stream)), "tbq_gemm")
+    return C_out
+
+
 def expf_device(x, out, stream=None):
     _check(lib().tbq_expf_device(_ptr(x), _ptr(out), x.numel(), _stream(stream)), "tbq_expf_device")
     return out
 
 
 __all__ = ["formats", "row_bytes", "lib", "init", "dequant", "matvec", "route", "moe_layer", "moe_forward",
-           "moe_forward_noalloc", "moe_workspace_size", "expf_device", "MoeLayer", "TbqError", "SYMBOLS", "TBQ_MOE_FP32", "TBQ_MOE_BF16",
+           "moe_forward_noalloc", "moe_workspace_size", "gemm", "expf_device", "MoeLayer", "TbqError", "SYMBOLS", "TBQ_MOE_FP32", "TBQ_MOE_BF16",
            "TBQ_MOE_I8"]

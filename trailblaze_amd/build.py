@@ -26,7 +26,7 @@ HIP_FLAGS = [
 C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-ffp-contract=off",
            "-I", os.path.join(ROOT, "include")]
 
-HIP_SOURCES = ["tbq_matvec.hip", "tbq_mv_q4k.hip", "tbq_mv_kq.hip", "tbq_moe.hip", "tbq_moe_q4k.hip", "tbq_moe_prefill.hip", "tbq_dense.hip", "tbq_dense_prefill.hip", "tbq_api.hip",
+HIP_SOURCES = ["tbq_matvec.hip", "tbq_mv_q4k.hip", "tbq_mv_kq.hip", "tbq_moe.hip", "tbq_moe_q4k.hip", "tbq_moe_prefill.hip", "tbq_dense.hip", "tbq_dense_prefill.hip", "tbq_gemm.hip", "tbq_api.hip",
                "tbq_noalloc.hip"]
 C_SOURCES = ["tb_cuda_abi.c", "tbq_moe_host.c", "tbq_gguf.c"]
 
@@ -54,10 +54,7 @@ def build(verbose: bool = False) -> str:
                 sys.stderr.write(r.stdout + r.stderr)
     objs = [j[j.index("-o") + 1] for j in jobs]
     tmp = LIB + ".tmp"
-    # rocBLAS: the prefill's plain fp16 GEMMs (the process's already-loaded
-    # librocblas.so.5, torch's, is reused when one is present)
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-L/opt/rocm/lib", "-lrocblas",
-          "-lpthread"])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-lpthread"])
     os.replace(tmp, LIB)
     return LIB
 

@@ -382,6 +382,27 @@ int tbq_quantize_q8k(const float *x, long long n, void *blocks, void *s) {
     return hip_ok(launch_quantize_q8k(x, n, blocks, S(s)), "quantize_q8k launch");
 }
 
+size_t tbq_gemm_workspace_size(int T, int N, int K) {
+    if (T <= 0 || N <= 0 || K <= 0) return 0;
+    return hgemm_partial_bytes(T, N, K, hgemm_cus());
+}
+
+int tbq_gemm(int wqt, const void *W, const void *X16, int T, int N, int K, float *C, int ldc, void *ws,
+             size_t ws_bytes, void *s) {
+    if (!ensure_init()) return 0;
+    if (wqt != QT_F16 && wqt != QT_Q4_K) return fail("tbq_gemm: weight format %d (F16 or Q4_K only)", wqt);
+    if (T <= 0 || N <= 0 || K <= 0 || !hgemm_supported(wqt, N, K) || ldc < N || ldc % 4)
+        return fail("tbq_gemm: bad shape T=%d N=%d K=%d ldc=%d (N a multiple of 4, K of 256, ldc >= N)", T, N, K,
+                    ldc);
+    if ((long long)T * K * 2 >= (1ll << 31)) return fail("tbq_gemm: X above 2 GiB");
+    if (!W || !X16 || !C || !aligned16(W) || !aligned16(X16) || !aligned16(C))
+        return fail("tbq_gemm: null or misaligned pointer");
+    const size_t need = tbq_gemm_workspace_size(T, N, K);
+    if (need && (!ws || ws_bytes < need)) return fail("tbq_gemm: workspace %zu < %zu bytes", ws_bytes, need);
+    return hip_ok(launch_hgemm(wqt, W, (const _Float16 *)X16, T, N, K, C, ldc, (float *)ws, hgemm_cus(), S(s)),
+                  "gemm launch");
+}
+
 int tbq_expf_device(const float *in, float *out, size_t n, void *s) {
     if (!ensure_init()) return 0;
     if (!in || !out) return fail("tbq_expf_device: null pointer");

@@ -4,12 +4,12 @@
 // (layer4/tb_infer.c:1068-1075: one tb_infer_decode step per prompt token).
 //
 // Per layer (x: fp32 residual rows [T][H]; h16: fp16 rows with per-row
-// power-of-two scales, the GEMMs' activation operand; each weight matrix
-// is dequantised to fp16 (k_dequant_f16, any format or layout) just before
-// its GEMM, into one reused buffer):
+// power-of-two scales, the GEMMs' activation operand; the GEMMs are
+// k_hgemm (tbq_gemm.hip): Q4_K weights are dequantised inside it, any other
+// format to fp16 first (k_dequant_f16, one reused buffer)):
 //   k_pf_norm        x += y (the previous sublayer's output, unscaled by
 //                    its row scales), h16 = rmsnorm(x) * attn_norm
-//   GEMM             qkv = h16 Wqkv^T             rocBLAS fp16, fp32 acc
+//   GEMM             qkv = h16 Wqkv^T             fp16 MFMA, fp32 acc
 //   k_pf_qk          per (token, head): QK-norm + RoPE of q (to qb) and k;
 //                    k and v rows written to the cache at pos0 + t
 //   k_pf_attn        causal GQA attention over cache positions 0 .. pos on
@@ -27,10 +27,8 @@
 // probabilities (11-bit mantissa) with fp32 accumulation, fp32 norms, RoPE
 // and softmax; the logits land within
 // 1e-2 relative L2 of the float64 sequential decode.
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
-#include <mutex>
 
 #include "tbq_kernels.h"
 #include "tbq_device.hpp"
@@ -451,14 +449,16 @@ static hipError_t launch_pf_attn(int G, const float *qb, const float *kc, const 
 static size_t pf_up(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Every model with hidden <= 8192 and ffn <= 16384 (the rows the norm and
-// SwiGLU kernels hold) takes the batched path for T >= 2; its matrices, of any format and layout, are dequantised
-// to fp16 one at a time and multiplied by rocBLAS.
+// SwiGLU kernels hold) takes the batched path for T >= 2.  Q4_K matrices go
+// straight into the GEMM (dequantised on the way into LDS); every other
+// format and layout is dequantised to fp16 first (one matrix at a time) and
+// multiplied by the same GEMM.
 bool dense_prefill_batched(const tbq_dense_model *m) {
     return m->hidden <= PN_THREADS * PN_V * 4 && m->ffn <= PS_THREADS * PS_V * 4;
 }
 
 struct PfWs {
-    float *x, *y, *qkv, *qb, *att, *gu, *sa, *sb, *part, *rope;
+    float *x, *y, *qkv, *qb, *att, *gu, *sa, *sb, *part, *rope, *gpart;
     _Float16 *h16, *wh;
     int *tok;
     void *dec;
@@ -490,6 +490,15 @@ static PfWs pf_ws(const tbq_dense_model *m, int T, void *ws, size_t *total) {
         w.sa = (float *)take((size_t)T * 4);
         w.sb = (float *)take((size_t)T * 4);
         w.wh = (_Float16 *)take(wmax * 2);
+        // split-K partials of the largest product that splits
+        const int cu = hgemm_cus(), Ti = T;
+        const size_t gp = std::max(
+            std::max(std::max(hgemm_partial_bytes(Ti, (int)QKVR, (int)H, cu), hgemm_partial_bytes(Ti, (int)QD, (int)H, cu)),
+                     std::max(hgemm_partial_bytes(Ti, m->n_kv_heads * m->head_dim, (int)H, cu),
+                              hgemm_partial_bytes(Ti, (int)H, (int)QD, cu))),
+            std::max(std::max(hgemm_partial_bytes(Ti, (int)(2 * F), (int)H, cu), hgemm_partial_bytes(Ti, (int)F, (int)H, cu)),
+                     hgemm_partial_bytes(Ti, (int)H, (int)F, cu)));
+        w.gpart = gp ? (float *)take(gp) : nullptr;
         w.rope = (float *)take((size_t)T * m->head_dim * 4);
         // attention split partials: a prefill reaching position kmax - 1 uses
         // min(PA_MAX_SPLIT, ceil(kmax / PA_PREF_KS)) splits, and kmax <= max_ctx
@@ -506,34 +515,21 @@ size_t dense_prefill_workspace_bytes(const tbq_dense_model *m, int T) {
     return t;
 }
 
-// rocBLAS for the prefill's fp16 GEMMs: one handle per process, used under
-// a mutex (its stream is set per call).
-static std::mutex g_rb_mu;
-static rocblas_handle g_rb = nullptr;
-
-// C[T][M] = X[T][K] . W[M][K]^T, row-major, fp16 operands, fp32 accumulate
-// and output (column-major: C'[M x T] = W'^T[M x K] X'[K x T]).
-static hipError_t pf_gemm(const _Float16 *W, const _Float16 *X, int T, int M, int K, float *C) {
-    const float alpha = 1.f, beta = 0.f;
-    const rocblas_status r =
-        rocblas_gemm_ex(g_rb, rocblas_operation_transpose, rocblas_operation_none, M, T, K, &alpha, W,
-                        rocblas_datatype_f16_r, K, X, rocblas_datatype_f16_r, K, &beta, C, rocblas_datatype_f32_r, M, C,
-                        rocblas_datatype_f32_r, M, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    return r == rocblas_status_success ? hipSuccess : hipErrorUnknown;
-}
-
 // tokens: T device ints (in range); T >= 2.
 static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int pos0, float *logits,
                              hipStream_t st) {
     const int H = m->hidden, D = m->head_dim, NQ = m->n_heads, NKV = m->n_kv_heads, G = NQ / NKV, F = m->ffn;
     const int QD = NQ * D, KD = NKV * D, QKVR = QD + 2 * KD;
     auto qt_of = [m](int q) { return canon_qt(q ? q : m->qtype_layers); };
-    auto dq = [&](int qt, const void *W, long long rows, int K, _Float16 *dst) {
-        return launch_dequant_f16(qt, W, rows * K, dst, st);
+    const int cu = hgemm_cus();
+    // C[T][rows] (row stride ldc) = h16 . W^T: Q4_K rows directly, any other
+    // format through its fp16 form in wh
+    auto gemm = [&](int qt, const void *W, int rows, int K, float *C, int ldc) {
+        if (qt == QT_Q4_K) return launch_hgemm(QT_Q4_K, W, w.h16, T, rows, K, C, ldc, w.gpart, cu, st);
+        const hipError_t e = launch_dequant_f16(qt, W, (long long)rows * K, w.wh, st);
+        if (e != hipSuccess) return e;
+        return launch_hgemm(QT_F16, w.wh, w.h16, T, rows, K, C, ldc, w.gpart, cu, st);
     };
-    std::lock_guard<std::mutex> lk(g_rb_mu);
-    if (!g_rb && rocblas_create_handle(&g_rb) != rocblas_status_success) return hipErrorUnknown;
-    if (rocblas_set_stream(g_rb, st) != rocblas_status_success) return hipErrorUnknown;
     hipLaunchKernelGGL(k_pf_rope, dim3(T), dim3(64), 0, st, pos0, m->rope_theta, D, w.rope);
     hipError_t err = launch_dequant_rows(canon_qt(m->qtype_embd), m->tok_embd, w.tok, T, H, w.x, st);
     for (int l = 0; l < m->n_layers && err == hipSuccess; l++) {
@@ -543,13 +539,13 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
         hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, l ? w.y : nullptr, l ? w.sb : nullptr,
                            L.attn_norm, H, m->norm_eps, w.h16, w.sa);
         if (L.wqkv) {
-            err = dq(qt_of(L.qt_qkv), L.wqkv, QKVR, H, w.wh);
+            err = gemm(qt_of(L.qt_qkv), L.wqkv, QKVR, H, w.qkv, QKVR);
         } else {
-            err = dq(qt_of(L.qt_q), L.wq, QD, H, w.wh);
-            if (err == hipSuccess) err = dq(qt_of(L.qt_k), L.wk, KD, H, w.wh + (size_t)QD * H);
-            if (err == hipSuccess) err = dq(qt_of(L.qt_v), L.wv, KD, H, w.wh + (size_t)(QD + KD) * H);
+            err = gemm(qt_of(L.qt_q), L.wq, QD, H, w.qkv, QKVR);
+            if (err == hipSuccess) err = gemm(qt_of(L.qt_k), L.wk, KD, H, w.qkv + QD, QKVR);
+            if (err == hipSuccess) err = gemm(qt_of(L.qt_v), L.wv, KD, H, w.qkv + QD + KD, QKVR);
         }
-        if (err != hipSuccess || (err = pf_gemm(w.wh, w.h16, T, QKVR, H, w.qkv)) != hipSuccess) break;
+        if (err != hipSuccess) break;
         if (D == 128) {
             hipLaunchKernelGGL(k_pf_qk<128>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, w.sa, L.q_norm, L.k_norm, NQ,
                                NKV, pos0, w.rope, m->norm_eps, kc, vc, m->max_ctx, w.qb);
@@ -560,20 +556,18 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
             err = launch_pf_attn<64>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, st);
         }
         if (err != hipSuccess || (err = launch_rows_f16(w.att, T, QD, w.h16, w.sb, st)) != hipSuccess) break;
-        if ((err = dq(qt_of(L.qt_o), L.wo, H, QD, w.wh)) != hipSuccess) break;
-        if ((err = pf_gemm(w.wh, w.h16, T, H, QD, w.y)) != hipSuccess) break;
+        if ((err = gemm(qt_of(L.qt_o), L.wo, H, QD, w.y, H)) != hipSuccess) break;
         hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, w.y, w.sb, L.ffn_norm, H, m->norm_eps,
                            w.h16, w.sa);
         if (L.wgu) {
-            err = dq(qt_of(L.qt_gu), L.wgu, 2 * F, H, w.wh);
+            err = gemm(qt_of(L.qt_gu), L.wgu, 2 * F, H, w.gu, 2 * F);
         } else {
-            err = dq(qt_of(L.qt_gate), L.wgate, F, H, w.wh);
-            if (err == hipSuccess) err = dq(qt_of(L.qt_up), L.wup, F, H, w.wh + (size_t)F * H);
+            err = gemm(qt_of(L.qt_gate), L.wgate, F, H, w.gu, 2 * F);
+            if (err == hipSuccess) err = gemm(qt_of(L.qt_up), L.wup, F, H, w.gu + F, 2 * F);
         }
-        if (err != hipSuccess || (err = pf_gemm(w.wh, w.h16, T, 2 * F, H, w.gu)) != hipSuccess) break;
+        if (err != hipSuccess) break;
         hipLaunchKernelGGL(k_pf_swiglu_f16, dim3(T), dim3(PS_THREADS), 0, st, w.gu, w.sa, F, w.h16, w.sb);
-        if ((err = dq(qt_of(L.qt_down), L.wdown, H, F, w.wh)) != hipSuccess) break;
-        err = pf_gemm(w.wh, w.h16, T, H, F, w.y);
+        err = gemm(qt_of(L.qt_down), L.wdown, H, F, w.y, H);
     }
     if (err != hipSuccess) return err;
     float *ylast = w.y + (size_t)(T - 1) * H;

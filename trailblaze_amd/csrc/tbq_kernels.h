@@ -87,6 +87,14 @@ hipError_t launch_rows_q8(const float *in, long long rows, int n, int8_t *q8, fl
 hipError_t launch_moe_prefill_q4k_i8(const MoeArgs &a, void *scratch, hipStream_t st);
 hipError_t launch_quantize_q8k(const float *in, long long n, void *blocks, hipStream_t st);
 hipError_t launch_moe_i8(const MoeArgs &a, void *scratch, hipStream_t st);
+// Prefill weight products (tbq_gemm.hip): C[T][N] (row stride ldc) =
+// X[T][K] . W[N][K]^T, X fp16, W fp16 (QT_F16) or Q4_K rows; N % 4 == 0,
+// K % 256 == 0; part = hgemm_partial_bytes() of scratch.
+int hgemm_cus();
+bool hgemm_supported(int wqt, int N, int K);
+size_t hgemm_partial_bytes(int T, int N, int K, int n_cu);
+hipError_t launch_hgemm(int wqt, const void *W, const _Float16 *X, int T, int N, int K, float *C, int ldc,
+                        float *part, int n_cu, hipStream_t st);
 size_t dense_workspace_bytes(const tbq_dense_model *m);
 hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,
                                hipStream_t st);
