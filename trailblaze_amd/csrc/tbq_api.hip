@@ -158,11 +158,12 @@ int tbq_matvec_variant(const void *W, int qt, int M, int K, const float *x, floa
     if (!check_matvec(W, qt, M, K, x, y)) return 0;
     if (variant < TBQ_MV_AUTO || variant > TBQ_MV_KQ) return fail("tbq_matvec_variant: unknown variant %d", variant);
     if (M == 0) return 1;
-    // The specialised Q4_K kernel takes one row per wave in a single pass
-    // (rows of up to 64 units keep x's digits in registers); taller
-    // matrices stream better through the shared kernel's row passes.
+    // The specialised Q4_K kernels keep x's digits in registers for rows of
+    // up to 64 units: one pass of two rows per wave up to 8192 rows,
+    // persistent waves walking the rows of taller matrices; longer rows
+    // stream through the shared K-quant kernel.
     const bool q4k_special = (qt == QT_Q4_K || qt == QT_GQ4_K) &&
-                             (variant == TBQ_MV_INTDOT || (variant == TBQ_MV_AUTO && K <= 4096 && M <= 8192));
+                             (variant == TBQ_MV_INTDOT || (variant == TBQ_MV_AUTO && K <= 4096));
     if (q4k_special) {
         hipError_t e = launch_matvec_q4k(W, M, K, x, y, S(s), g_cu, qt == QT_GQ4_K);
         if (e != hipErrorNotSupported) return hip_ok(e, "matvec launch (Q4_K int-dot)");

@@ -80,6 +80,32 @@ __host__ __device__ __forceinline__ float f16_of(uint32_t h) {
     else return f16_ref(h);
 }
 
+// The same decoders for arithmetic kernels, on both halves of a dword (lo =
+// bits 0-15).  The hardware conversion (v_cvt_f32_f16) gives exactly the
+// decoders' bits for zero and normal halves, the fields real scales hold;
+// when any active lane of the wave holds a subnormal, inf or nan half
+// (exponent 0 with a nonzero mantissa, or exponent 31) the whole wave takes
+// the integer decoders instead.  The branch is wave-uniform.
+template <bool IEEE = false>
+__device__ __forceinline__ void f16x2_dec(uint32_t h, float &lo, float &hi) {
+    const uint32_t a = h & 0x7FFFu, b = (h >> 16) & 0x7FFFu;
+    const bool odd = (a - 1u < 0x3FFu) | (a >= 0x7C00u) | (b - 1u < 0x3FFu) | (b >= 0x7C00u);
+    if (__builtin_amdgcn_ballot_w64(odd) != 0) {
+        lo = IEEE ? f16_ieee(h & 0xFFFFu) : f16_ref(h & 0xFFFFu);
+        hi = IEEE ? f16_ieee(h >> 16) : f16_ref(h >> 16);
+    } else {
+        lo = (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
+        hi = (float)__builtin_bit_cast(_Float16, (uint16_t)(h >> 16));
+    }
+}
+template <bool IEEE = false>
+__device__ __forceinline__ float f16_dec(uint32_t h) {
+    const uint32_t a = h & 0x7FFFu;
+    const bool odd = (a - 1u < 0x3FFu) | (a >= 0x7C00u);
+    if (__builtin_amdgcn_ballot_w64(odd) != 0) return IEEE ? f16_ieee(h & 0xFFFFu) : f16_ref(h & 0xFFFFu);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
+}
+
 __host__ __device__ __forceinline__ float bf16_ref(uint32_t b) {
     return __builtin_bit_cast(float, b << 16);
 }

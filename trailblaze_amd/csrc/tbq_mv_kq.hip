@@ -98,10 +98,25 @@ __device__ __forceinline__ void ld_dw(const uint8_t *p, uint32_t *out) {
 
 // Loads of the per-format unit loaders: wide loads at 4-byte-aligned
 // addresses, ld_dw for runs that are only 2-byte aligned.
+#ifdef TBQ_NT
+typedef unsigned tbq_v4u __attribute__((ext_vector_type(4)));
+typedef unsigned tbq_v2u __attribute__((ext_vector_type(2)));
+struct GMem {
+    static __device__ __forceinline__ uint4 ld128(const uint8_t *p) {
+        const tbq_v4u v = __builtin_nontemporal_load(reinterpret_cast<const tbq_v4u *>(p));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    }
+    static __device__ __forceinline__ uint2 ld64(const uint8_t *p) {
+        const tbq_v2u v = __builtin_nontemporal_load(reinterpret_cast<const tbq_v2u *>(p));
+        return make_uint2(v.x, v.y);
+    }
+    static __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p)); }
+#else
 struct GMem {
     static __device__ __forceinline__ uint4 ld128(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
     static __device__ __forceinline__ uint2 ld64(const uint8_t *p) { return *reinterpret_cast<const uint2 *>(p); }
     static __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+#endif
     static __device__ __forceinline__ uint32_t ld16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
     template <int N>
     static __device__ __forceinline__ void ldw(const uint8_t *p, uint32_t *out) { ld_dw<N>(p, out); }
@@ -219,7 +234,8 @@ struct KqStager {
             uint32_t dh = 0, dm = 0, dl = 0;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
-                const int X = (int)rintf(e[b] * sc);
+                // rint(x * 2^s): low bits of fl(x * 2^s + 1.5 * 2^23), |x * 2^s| < 2^22
+                const int X = (int)(__builtin_bit_cast(uint32_t, fmaf(e[b], sc, 12582912.f)) - 0x4B400000u);
                 const int l = (int)(int8_t)(X & 0xFF);
                 const int X1 = (X - l) >> 8;
                 const int m = (int)(int8_t)(X1 & 0xFF);
@@ -332,7 +348,8 @@ template <> struct KqFmt<QT_Q2_K> {
             L = mad24(s, al, L);
             mn = fmaf((float)m, x.gs[g], mn);
         }
-        const float d = f16_ref(w.dd & 0xFFFFu), dmin = f16_ref(w.dd >> 16);
+        float d, dmin;
+        f16x2_dec<false>(w.dd, d, dmin);
         return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
     }
 };
@@ -384,7 +401,7 @@ template <> struct KqFmt<QT_Q3_K> {
             L = mad24(s, al, L);
             mn = fmaf((float)s, x.gs[g], mn);
         }
-        const float d = f16_ref(w.hi.y >> 16);
+        const float d = f16_dec<false>(w.hi.y >> 16);
         return d * fmaf(x.isc, kq_combine(H, Mm, L), -4.f * mn);
     }
 };
@@ -427,7 +444,8 @@ template <> struct KqFmt<QT_Q4_K> {
             L = mad24(s, al, L);
             mn = fmaf((float)m, x.gs[2 * j] + x.gs[2 * j + 1], mn);
         }
-        const float d = f16_ref(w.hdr.x & 0xFFFFu), dmin = f16_ref(w.hdr.x >> 16);
+        float d, dmin;
+        f16x2_dec<false>(w.hdr.x, d, dmin);
         return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
     }
 };
@@ -481,7 +499,8 @@ template <> struct KqFmt<QT_Q5_K> {
             L = mad24(s, al, L);
             mn = fmaf((float)m, x.gs[2 * j] + x.gs[2 * j + 1], mn);
         }
-        const float d = f16_ref(w.hdr.x & 0xFFFFu), dmin = f16_ref(w.hdr.x >> 16);
+        float d, dmin;
+        f16x2_dec<false>(w.hdr.x, d, dmin);
         return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
     }
 };
@@ -529,7 +548,7 @@ template <> struct KqFmt<QT_Q6_K> {
             L = mad24(s, al, L);
             mn = fmaf((float)s, x.gs[g], mn);
         }
-        const float d = f16_ref(w.d);
+        const float d = f16_dec<false>(w.d);
         return d * fmaf(x.isc, kq_combine(H, Mm, L), -32.f * mn);
     }
 };
@@ -559,8 +578,8 @@ template <int QT> struct KqQ80 {
         int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
         kq_dots<8>(q0, x, 0, h0, m0, l0);
         kq_dots<8>(q1, x, 8, h1, m1, l1);
-        const float f0 = f16_of<QT>(w.d0) * kq_combine(h0, m0, l0);
-        return fmaf(f16_of<QT>(w.d1), kq_combine(h1, m1, l1), f0) * x.isc;
+        const float f0 = f16_dec<(QT & QT_GGML) != 0>(w.d0) * kq_combine(h0, m0, l0);
+        return fmaf(f16_dec<(QT & QT_GGML) != 0>(w.d1), kq_combine(h1, m1, l1), f0) * x.isc;
     }
 };
 
@@ -585,6 +604,7 @@ template <> struct KqFmt<QT_Q4_0> {
         w.b = make_uint4(t[0], t[1], t[2], t[3]);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
+        const float d0 = f16_dec<false>(w.d0), d1 = f16_dec<false>(w.d1);
         float r = 0.f;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
@@ -599,7 +619,7 @@ template <> struct KqFmt<QT_Q4_0> {
             int ah = 0, am = 0, al = 0;
             kq_dots<8>(q, x, 8 * j, ah, am, al);
             const float sx = x.gs[2 * j] + x.gs[2 * j + 1];
-            r = fmaf(f16_ref(j ? w.d1 : w.d0), fmaf(x.isc, kq_combine(ah, am, al), -8.f * sx), r);
+            r = fmaf(j ? d1 : d0, fmaf(x.isc, kq_combine(ah, am, al), -8.f * sx), r);
         }
         return r;
     }
@@ -668,7 +688,8 @@ template <> struct KqFmt<QT_GQ4_K> {
             L = mad24(s, al, L);
             mn = fmaf((float)m, x.gs[2 * j] + x.gs[2 * j + 1], mn);
         }
-        const float d = f16_ieee(w.hdr.x & 0xFFFFu), dmin = f16_ieee(w.hdr.x >> 16);
+        float d, dmin;
+        f16x2_dec<true>(w.hdr.x, d, dmin);
         return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
     }
 };
@@ -709,7 +730,8 @@ template <> struct KqFmt<QT_GQ5_K> {
             L = mad24(s, al, L);
             mn = fmaf((float)m, x.gs[2 * j] + x.gs[2 * j + 1], mn);
         }
-        const float d = f16_ieee(w.hdr.x & 0xFFFFu), dmin = f16_ieee(w.hdr.x >> 16);
+        float d, dmin;
+        f16x2_dec<true>(w.hdr.x, d, dmin);
         return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
     }
 };
@@ -765,7 +787,7 @@ template <> struct KqFmt<QT_GQ6_K> {
             L = mad24(s, al, L);
             mn = fmaf((float)s, x.gs[g], mn);
         }
-        return f16_ieee(w.d) * fmaf(x.isc, kq_combine(H, Mm, L), -32.f * mn);
+        return f16_dec<true>(w.d) * fmaf(x.isc, kq_combine(H, Mm, L), -32.f * mn);
     }
 };
 
@@ -810,7 +832,7 @@ template <> struct KqFmt<QT_GQ3_K> {
             L = mad24(s, al, L);
             mn = fmaf((float)s, x.gs[g], mn);
         }
-        return f16_ieee(w.d) * fmaf(x.isc, kq_combine(H, Mm, L), -4.f * mn);
+        return f16_dec<true>(w.d) * fmaf(x.isc, kq_combine(H, Mm, L), -4.f * mn);
     }
 };
 
@@ -848,7 +870,8 @@ template <> struct KqFmt<QT_GQ2_K> {
             L = mad24(s, al, L);
             mn = fmaf((float)m, x.gs[g], mn);
         }
-        const float d = f16_ieee(w.dd & 0xFFFFu), dmin = f16_ieee(w.dd >> 16);
+        float d, dmin;
+        f16x2_dec<true>(w.dd, d, dmin);
         return fmaf(d * x.isc, kq_combine(H, Mm, L), -dmin * mn);
     }
 };
@@ -869,6 +892,7 @@ template <> struct KqFmt<QT_GQ4_0> {
         w.b = make_uint4(t[0], t[1], t[2], t[3]);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
+        const float d0 = f16_dec<true>(w.d0), d1 = f16_dec<true>(w.d1);
         float r = 0.f;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
@@ -883,7 +907,7 @@ template <> struct KqFmt<QT_GQ4_0> {
             int ah = 0, am = 0, al = 0;
             kq_dots<8>(q, x, 8 * j, ah, am, al);
             const float sx = x.gs[2 * j] + x.gs[2 * j + 1];
-            r = fmaf(f16_ieee(j ? w.d1 : w.d0), fmaf(x.isc, kq_combine(ah, am, al), -8.f * sx), r);
+            r = fmaf(j ? d1 : d0, fmaf(x.isc, kq_combine(ah, am, al), -8.f * sx), r);
         }
         return r;
     }

@@ -3,14 +3,16 @@
 //
 // (Digit representation and its accuracy: tbq_q4k.hpp.)
 //
-// Work split: a 1024-thread workgroup (16 waves, one staging of x per CU)
-// stores x's digits in LDS (XD_UNIT layout: 52 dwords per 64 elements, read
-// free of bank conflicts); x's loads are issued before the weight loads so
-// they do not queue behind them; each lane owns "units" of two consecutive sub-blocks of one
-// super-block (64 weights, 4 lanes per super-block), LPR lanes share a row,
-// and a wave issues its first row's loads before staging x and the next
-// row's loads before reducing the current one, so HBM latency overlaps the
-// staging and the arithmetic.
+// Work split: a workgroup stores x's digits in LDS (XD_UNIT layout: 52
+// dwords per 64 elements, read free of bank conflicts); x's loads are
+// issued before the weight loads so they do not queue behind them; each
+// lane owns "units" of two consecutive sub-blocks of one super-block (64
+// weights, 4 lanes per super-block) and LPR lanes share a row.  Three
+// kernels: k_mv_q4k_xr (K <= 4096, up to 8192 rows: one pass, R rows per
+// wave, all weight loads issued before x is staged), k_mv_q4k_xp (K <=
+// 4096, taller: persistent waves, the next row's loads in flight while the
+// current one is reduced), k_mv_q4k (longer rows: digits read from LDS per
+// row, grid-strided rows).
 #include "tbq_kernels.h"
 #include "tbq_q4k.hpp"
 
@@ -18,11 +20,15 @@ namespace tbq {
 
 constexpr int WG = 1024;        // threads per workgroup (16 waves share one x staging)
 #ifndef Q4K_XR_R
-#define Q4K_XR_R 1               // rows per lane of the register-x kernel
+#define Q4K_XR_R 2               // rows per lane of the register-x kernel
 #endif
 #ifndef Q4K_XR_NW
-#define Q4K_XR_NW 16             // waves per workgroup of the register-x kernel
+#define Q4K_XR_NW 8              // waves per workgroup of the register-x kernel
 #endif
+#ifndef Q4K_XP_NW
+#define Q4K_XP_NW 16             // waves per workgroup of the persistent kernel (one per CU)
+#endif
+constexpr int Q4K_XR_MAX_M = 8192;   // taller matrices take the persistent kernel
 
 // One pass of a wave covers RPP = 64/LPR rows; each lane owns UPL units of
 // its row.  Rows are grid-strided over all waves; the next pass's loads are
@@ -119,6 +125,62 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
     }
 }
 
+// Tall matrices (rows of up to 64 units): persistent waves.  Each
+// workgroup stages x once; each wave keeps its lanes' x digits in
+// registers (fixed unit per lane, as above) and walks rows gridDim.x * NW *
+// RPP apart, with the weights of the next D rows in flight while it reduces
+// the current one.  Prefetches past the last row re-read row M-1 and are
+// discarded, so every load is unconditional.
+template <int LPR, int D, int NW, bool GG>
+__global__ __launch_bounds__(NW * 64) void k_mv_q4k_xp(const uint8_t *__restrict__ W, int M, int K, long long rb,
+                                                      const float *__restrict__ x, float *__restrict__ y) {
+    extern __shared__ uint32_t xd[];
+    constexpr int NT = NW * 64, RPP = 64 / LPR;
+    const int U = K / 64;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lr = lane % LPR, rsub = lane / LPR;
+    const bool lv = lr < U;
+    const int ul = lv ? lr : 0;
+    XStager<NT, (4 * 128 + NT - 1) / NT> xs;   // K <= 4096
+    xs.load(x, K);
+    __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
+    const int stride = gridDim.x * NW * RPP;
+    const int row0 = (blockIdx.x * NW + wave) * RPP + rsub;
+    Q4KUnit buf[D + 1];
+#pragma unroll
+    for (int i = 0; i < D; i++) q4k_load<GG>(W + (long long)min(row0 + i * stride, M - 1) * rb, ul, buf[i]);
+    xs.store(xd, K);
+    __syncthreads();
+    XUnit xu;
+    xunit_load(xd, ul, xu);
+    // every lane of a wave runs the same number of passes (bound from the
+    // wave's first row), so the reductions always see a full wave
+    const int wrow0 = (blockIdx.x * NW + wave) * RPP;
+    for (int r0 = wrow0; r0 < M; r0 += stride) {
+        const int r = r0 + rsub;
+        q4k_load<GG>(W + (long long)min(r + D * stride, M - 1) * rb, ul, buf[D]);
+        const float v = q4k_unit_dot<GG>(buf[0], ul, xu, 0.f);
+        const float acc = group_sum<LPR>((r < M && lv) ? v : 0.f);
+        if (lr == 0 && r < M) y[r] = acc;
+#pragma unroll
+        for (int i = 0; i < D; i++) buf[i] = buf[i + 1];
+    }
+}
+
+template <int LPR, int D, int NW, bool GG>
+static hipError_t launch_q4k_xp(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu,
+                                int wpc) {
+    constexpr int RPW = NW * (64 / LPR);
+    const long long need = ((long long)M + RPW - 1) / RPW;
+    const long long cap = (long long)n_cu * wpc;
+    const int grid = (int)(need < cap ? need : cap);
+    const long long rb = (long long)(K / 256) * 144;
+    const size_t lds = (size_t)(K / 32) * XD_PER_SB * 4;
+    hipLaunchKernelGGL((k_mv_q4k_xp<LPR, D, NW, GG>), dim3(grid), dim3(NW * 64), lds, s, (const uint8_t *)W, M, K,
+                       rb, x, y);
+    return hipGetLastError();
+}
+
 template <int LPR, int R, int NW, int PRO, bool GG>
 static hipError_t launch_q4k_xr(const void *W, int M, int K, const float *x, float *y, hipStream_t s,
                                 const MvPro &pro) {
@@ -155,8 +217,20 @@ static hipError_t launch_q4k_t(const void *W, int M, int K, const float *x, floa
 }
 
 template <bool GG>
+static hipError_t launch_q4k_xp_k(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu) {
+    const int U = K / 64;
+    constexpr int NW = Q4K_XP_NW;
+    if (U <= 4) return launch_q4k_xp<4, 1, NW, GG>(W, M, K, x, y, s, n_cu, 1);
+    if (U <= 8) return launch_q4k_xp<8, 1, NW, GG>(W, M, K, x, y, s, n_cu, 1);
+    if (U <= 16) return launch_q4k_xp<16, 1, NW, GG>(W, M, K, x, y, s, n_cu, 1);
+    if (U <= 32) return launch_q4k_xp<32, 1, NW, GG>(W, M, K, x, y, s, n_cu, 1);
+    return launch_q4k_xp<64, 1, NW, GG>(W, M, K, x, y, s, n_cu, 1);
+}
+
+template <bool GG>
 static hipError_t launch_matvec_q4k_g(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu) {
     const int U = K / 64;
+    if (U <= 64 && M > Q4K_XR_MAX_M) return launch_q4k_xp_k<GG>(W, M, K, x, y, s, n_cu);
     if (U <= 64) return launch_q4k_xr_k<PRO_NONE, GG>(W, M, K, x, y, s, MvPro{});
     if (U <= 128) return launch_q4k_t<64, 2, GG>(W, M, K, x, y, s, n_cu);
     if (U <= 192) return launch_q4k_t<64, 3, GG>(W, M, K, x, y, s, n_cu);

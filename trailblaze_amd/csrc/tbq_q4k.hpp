@@ -150,7 +150,10 @@ struct XStager {
             const float sc = ldexpf(1.f, s);
             uint32_t X[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) X[j] = (uint32_t)(int)rintf(e8[j] * sc);
+            // rint(x * 2^s) as the low bits of fl(x * 2^s + 1.5 * 2^23): the
+            // sum lies in [2^23, 2^24) (|x * 2^s| < 2^22), where one ulp is 1,
+            // so the single rounding of the fma is round-to-nearest-even
+            for (int j = 0; j < 8; j++) X[j] = __builtin_bit_cast(uint32_t, fmaf(e8[j], sc, 12582912.f)) - 0x4B400000u;
             uint32_t dig[6];
 #pragma unroll
             for (int par = 0; par < 2; par++) {
@@ -199,7 +202,9 @@ __device__ __forceinline__ float q4_subblock(uint4 q, const uint4 *D, float sx, 
         al = __builtin_amdgcn_udot4(lo, D32[o * 6 + 4], al, false);
         al = __builtin_amdgcn_udot4(hi, D32[o * 6 + 5], al, false);
     }
-    const float f = fmaf((float)ah, 65536.f, fmaf((float)am, 256.f, (float)al));
+    // 256*am + al < 2^31 (|q| <= 15, 32 elements): one integer add, then
+    // the same single rounding to fp32 as fmaf(am, 256, al)
+    const float f = fmaf((float)ah, 65536.f, (float)(am * 256u + al));
     acc = fmaf(S * isc, f, acc);
     return fmaf(-Mn, sx, acc);
 }
@@ -258,7 +263,9 @@ __device__ __forceinline__ float gq4_subblock(const uint32_t *ev, const uint32_t
         al = __builtin_amdgcn_udot4(lo, D32[o * 6 + 4], al, false);
         al = __builtin_amdgcn_udot4(hi, D32[o * 6 + 5], al, false);
     }
-    const float f = fmaf((float)ah, 65536.f, fmaf((float)am, 256.f, (float)al));
+    // 256*am + al < 2^31 (|q| <= 15, 32 elements): one integer add, then
+    // the same single rounding to fp32 as fmaf(am, 256, al)
+    const float f = fmaf((float)ah, 65536.f, (float)(am * 256u + al));
     acc = fmaf(S * isc, f, acc);
     return fmaf(-Mn, sx, acc);
 }
@@ -271,7 +278,8 @@ template <bool GG = false>
 __device__ __forceinline__ float q4k_unit_dot(const Q4KUnit &r, int u, const XUnit &x, float acc) {
     const int p = u & 3;
     if constexpr (GG) {
-        const float d = f16_ieee(r.hdr.x & 0xFFFFu), dmin = f16_ieee(r.hdr.x >> 16);
+        float d, dmin;
+        f16x2_dec<true>(r.hdr.x, d, dmin);
         int s0, m0, s1, m1;
         gq4k_sm(r.hdr, p, 0, s0, m0);
         gq4k_sm(r.hdr, p, 1, s1, m1);
@@ -285,7 +293,8 @@ __device__ __forceinline__ float q4k_unit_dot(const Q4KUnit &r, int u, const XUn
         acc = gq4_subblock(ev, od, 0, x.d, x.meta.x, x.meta.z, d * (float)s0, dmin * (float)m0, acc);
         return gq4_subblock(ev, od, 4, x.d + 6, x.meta.y, x.meta.w, d * (float)s1, dmin * (float)m1, acc);
     }
-    const float d = f16_ref(r.hdr.x & 0xFFFFu), dmin = f16_ref(r.hdr.x >> 16);
+    float d, dmin;
+    f16x2_dec<false>(r.hdr.x, d, dmin);
     const uint32_t sw = p < 2 ? r.hdr.y : r.hdr.w;
     const uint32_t mw = p < 2 ? r.hdr.z : r.mind;
     const int sh = 16 * (p & 1);
