@@ -75,11 +75,14 @@ __device__ __forceinline__ uint32_t mulu24(uint32_t a, uint32_t b) { return (uin
 // width.  The reads cover [p - 2, p + 4N + 2) when p is 2 mod 4 and exactly
 // [p, p + 4N) otherwise, so a run that ends where its block ends (always
 // 4-byte aligned in the layouts below when p is) never reads past it.
+// The aligned base is formed by pointer arithmetic on p (not through an
+// integer), so the compiler keeps the global address space and emits
+// global loads: flat loads would share the LDS wait counter, and every LDS
+// wait would then also wait for the prefetched weights.
 template <int N>
 __device__ __forceinline__ void ld_dw(const uint8_t *p, uint32_t *out) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t sh = (uint32_t)(a & 3u);
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(a - sh);
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p - sh);
     uint32_t w[N + 1];
     int i = 0;
     for (; i + 4 <= N; i += 4) {
@@ -91,7 +94,7 @@ __device__ __forceinline__ void ld_dw(const uint8_t *p, uint32_t *out) {
         w[i] = v.x; w[i + 1] = v.y;
     }
     for (; i < N; i++) w[i] = q[i];
-    w[N] = *reinterpret_cast<const uint32_t *>((a + 4 * N - 1) & ~(uintptr_t)3);
+    w[N] = q[(sh + 4 * N - 1) >> 2];
 #pragma unroll
     for (int j = 0; j < N; j++) out[j] = __builtin_amdgcn_alignbyte(w[j + 1], w[j], sh);
 }
