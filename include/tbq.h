@@ -208,8 +208,8 @@ int tbq_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits
  * pos0 + T - 1 in one batched pass per layer, replacing the reference's
  * token-by-token prefill (layer4/tb_infer.c:1068-1075, one tb_infer_decode
  * step per prompt token).  Writes the K/V rows of every position and the
- * logits of the last token.  Models with hidden <= 8192 and ffn <= 16384
- * take the batched path for T >= 2, whatever their formats or layouts: the
+ * logits of the last token.  Models with hidden <= 8192, n_heads *
+ * head_dim <= 8192 and ffn <= 16384 take the batched path for T >= 2, whatever their formats or layouts: the
  * weight products on tbq_gemm's kernel (Q4_K dequantised inside it, other
  * formats to fp16 first), attention on fp16 MFMA,
  * fp32 accumulation (logits within 1e-2 relative L2 of the sequential

@@ -14,8 +14,10 @@
 //                    k and v rows written to the cache at pos0 + t
 //   k_pf_attn        causal GQA attention over cache positions 0 .. pos on
 //                    fp16 MFMA, online softmax, key ranges split over
-//                    workgroups (k_pf_attn_combine merges them)
-//   rows to fp16, GEMM            y = att Wo^T
+//                    workgroups
+//   k_pf_attn_rows   merges the splits of each token's row and writes it
+//                    as fp16 rows with row scales (the o GEMM's operand)
+//   GEMM             y = att Wo^T
 //   k_pf_norm        x += y, h16 = rmsnorm(x) * ffn_norm
 //   GEMM             gu = h16 [Wg | Wu]^T
 //   k_pf_swiglu_f16  a16 = silu(g) * u (fp16, row scales)
@@ -65,13 +67,14 @@ __device__ __forceinline__ float pf_block_max(float v, float *red) {
 // when y is not; ys, the row scales of a GEMM's fp16 operand, may be null
 // for 1), h = v * rsqrt(mean(v^2) + eps) * w, then h16[t] = h * 2^s in fp16
 // with s putting max |h| in [2^14, 2^15) and hinv[t] = 2^-s.  grid = T.
-// A thread holds up to PN_V float4 of the row (H <= 8192), all loaded
-// before any is used.
+// y may be a GEMM's ny split-K slices (slice z at y + z * ystride), added
+// here in slice order.  A thread holds up to PN_V float4 of the row (H <=
+// 8192), all loaded before any is used.
 constexpr int PN_V = 8;
-__global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, const float *__restrict__ y,
-                                                        const float *__restrict__ ys, const float *__restrict__ w,
-                                                        int H, float eps, _Float16 *__restrict__ h16,
-                                                        float *__restrict__ hinv) {
+__global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, const float *__restrict__ y, int ny,
+                                                        long long ystride, const float *__restrict__ ys,
+                                                        const float *__restrict__ w, int H, float eps,
+                                                        _Float16 *__restrict__ h16, float *__restrict__ hinv) {
     __shared__ float red[PN_THREADS / 64];
     const int t = blockIdx.x, tid = threadIdx.x, n4 = H / 4;
     float4 *xr = reinterpret_cast<float4 *>(x + (long long)t * H);
@@ -84,6 +87,16 @@ __global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, c
         v[i] = xr[j];
         b[i] = yr[j];
         g[i] = wr[j];
+    }
+    if (y) {
+        for (int z = 1; z < ny; z++) {
+            const float4 *yz = yr + z * (ystride / 4);
+#pragma unroll
+            for (int i = 0; i < PN_V; i++) {
+                const float4 c = yz[min(tid + PN_THREADS * i, n4 - 1)];
+                b[i].x = b[i].x + c.x; b[i].y = b[i].y + c.y; b[i].z = b[i].z + c.z; b[i].w = b[i].w + c.w;
+            }
+        }
     }
     float ss = 0.f;
     const float yscale = ys ? ys[t] : 1.f;
@@ -175,18 +188,25 @@ __device__ __forceinline__ void pf_norm_rope(float (&x)[D / 64], const float *__
 // hh - NQ, normed and rotated, and the matching v head, written to the
 // layer's cache rows pos0 + t.
 template <int D>
-__global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, const float *__restrict__ rs,
-                                              const float *__restrict__ qn, const float *__restrict__ kn, int NQ,
-                                              int NKV, int pos0, const float *__restrict__ rope, float eps,
-                                              float *__restrict__ kc, float *__restrict__ vc, int max_ctx,
-                                              float *__restrict__ qb) {
+__global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, int nq, long long qstride,
+                                              const float *__restrict__ rs, const float *__restrict__ qn,
+                                              const float *__restrict__ kn, int NQ, int NKV, int pos0,
+                                              const float *__restrict__ rope, float eps, float *__restrict__ kc,
+                                              float *__restrict__ vc, int max_ctx, float *__restrict__ qb) {
     const int t = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x;
     const int QKVR = (NQ + 2 * NKV) * D, pos = pos0 + t;
     const float sc = rs[t];   // row t of qkv is scaled by 1 / rs[t]
-    const float *src = qkv + (long long)t * QKVR + hh * D;
+    // qkv may be a GEMM's nq split-K slices (slice z at qkv + z * qstride),
+    // added in slice order
+    auto elem = [&](long long off) {
+        float a = qkv[off];
+        for (int z = 1; z < nq; z++) a = a + qkv[off + z * qstride];
+        return a;
+    };
+    const long long src = (long long)t * QKVR + hh * D;
     float x[D / 64];
 #pragma unroll
-    for (int i = 0; i < D / 64; i++) x[i] = src[lane + 64 * i] * sc;
+    for (int i = 0; i < D / 64; i++) x[i] = elem(src + lane + 64 * i) * sc;
     pf_norm_rope<D>(x, hh < NQ ? qn : kn, rope + (long long)t * D, eps);
     if (hh < NQ) {
         const float scale = 1.0f / sqrtf((float)D);
@@ -195,11 +215,11 @@ __global__ __launch_bounds__(64) void k_pf_qk(const float *__restrict__ qkv, con
     } else {
         const int kvh = hh - NQ;
         const long long row = ((long long)kvh * max_ctx + pos) * D;
-        const float *vsrc = qkv + (long long)t * QKVR + (NQ + NKV + kvh) * D;
+        const long long vsrc = (long long)t * QKVR + (NQ + NKV + kvh) * D;
 #pragma unroll
         for (int i = 0; i < D / 64; i++) {
             kc[row + lane + 64 * i] = x[i];
-            vc[row + lane + 64 * i] = vsrc[lane + 64 * i] * sc;
+            vc[row + lane + 64 * i] = elem(vsrc + lane + 64 * i) * sc;
         }
     }
 }
@@ -252,10 +272,16 @@ __global__ __launch_bounds__(PS_THREADS) void k_pf_swiglu_f16(const float *__res
     if (tid == 0) ainv[t] = ldexpf(1.f, -sh);
 }
 
-// y[j] *= ys[0] for one row of n floats (the last token's down output
-// before the lm_head).
-__global__ __launch_bounds__(256) void k_pf_scale_row(float *__restrict__ y, const float *__restrict__ ys, int n) {
-    for (int j = threadIdx.x; j < n; j += 256) y[j] *= ys[0];
+// out[j] = (sum over the ny slices, in slice order, of y[z * ystride + j])
+// * ys[0] for one row of n floats (the last token's down output before the
+// lm_head).
+__global__ __launch_bounds__(256) void k_pf_scale_row(const float *__restrict__ y, int ny, long long ystride,
+                                                      const float *__restrict__ ys, int n, float *__restrict__ out) {
+    for (int j = threadIdx.x; j < n; j += 256) {
+        float a = y[j];
+        for (int z = 1; z < ny; z++) a = a + y[z * ystride + j];
+        out[j] = a * ys[0];
+    }
 }
 
 // Causal attention on MFMA (v_mfma_f32_32x32x16_f16, fp16 operands, fp32
@@ -280,7 +306,7 @@ __global__ __launch_bounds__(256) void k_pf_scale_row(float *__restrict__ y, con
 // writes its queries' unnormalised output, running max and denominator to
 // the record part[(row * nsplit + z) * pf_rec(D)] (D outputs, max,
 // denominator, two floats of padding so that every record starts 16-byte
-// aligned for the float4 stores), and k_pf_attn_combine merges the splits a
+// aligned for the float4 stores), and k_pf_attn_rows merges the splits a
 // row reaches.
 constexpr int PM_THREADS = 256, PM_Q = 128, PM_KC = 32;
 __host__ __device__ constexpr int pf_rec(int D) { return D + 4; }
@@ -393,30 +419,87 @@ __global__ __launch_bounds__(PM_THREADS) void k_pf_attn(const float *__restrict_
     }
 }
 
-// out[row] = sum_z e^(m_z - M) o_z / sum_z e^(m_z - M) l_z over the splits
-// z <= qpos / ks that row (t, h) reaches.  grid = T * NQ, D threads.
+// Attention rows to the o GEMM's operand in one pass: row t (all NQ heads,
+// QD = NQ * D floats) is the attention output -- att[t] itself when the
+// keys were not split, else the merge of the splits z <= (pos0 + t) / ks
+// with e^(m_z - M) weights and fmaf sums in z order -- and is written as fp16 scaled by
+// the power of two that puts its max |value| in [2^14, 2^15), with
+// hinv[t] = the inverse scale (k_rows_f16's arithmetic).  grid = T,
+// PN_THREADS threads, up to PR_V float4 of the row per thread (QD <= 8192).
+constexpr int PR_V = 8;
+constexpr int PA_PREF_KS = 128, PA_MAX_SPLIT = 8;   // preferred split size, most splits
 template <int D>
-__global__ __launch_bounds__(D) void k_pf_attn_combine(const float *__restrict__ part, int NQ, int pos0, int ks,
-                                                       int nsplit, float *__restrict__ out) {
-    const long long row = blockIdx.x;
-    const int t = (int)(row / NQ), d = threadIdx.x;
-    const int nz = (pos0 + t) / ks + 1;
+__global__ __launch_bounds__(PN_THREADS) void k_pf_attn_rows(const float *__restrict__ part,
+                                                             const float *__restrict__ att, int NQ, int pos0, int ks,
+                                                             int nsplit, _Float16 *__restrict__ h16,
+                                                             float *__restrict__ hinv) {
+    __shared__ float red[PN_THREADS / 64];
     constexpr int RS = pf_rec(D);
-    const float *p = part + row * nsplit * RS;
-    float M = -__builtin_huge_valf();
-    for (int z = 0; z < nz; z++) M = fmaxf(M, p[z * RS + D]);
-    float num = 0.f, den = 0.f;
-    for (int z = 0; z < nz; z++) {
-        const float f = __expf(p[z * RS + D] - M);
-        num = fmaf(f, p[z * RS + d], num);
-        den = fmaf(f, p[z * RS + D + 1], den);
+    const int t = blockIdx.x, tid = threadIdx.x, n4 = NQ * D / 4;
+    const int nz = (pos0 + t) / ks + 1;
+    float4 v[PR_V];
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < PR_V; i++) {
+        const int j = tid + PN_THREADS * i;
+        if (j >= n4) continue;
+        const int hh = 4 * j / D, d = 4 * j % D;
+        const long long row = (long long)t * NQ + hh;
+        if (nsplit == 1) {
+            v[i] = *reinterpret_cast<const float4 *>(att + row * D + d);
+        } else {
+            // every split's record loaded at once (splits past nz re-read the
+            // last one and are skipped), then merged in z order
+            const float *p = part + row * nsplit * RS;
+            float ml[PA_MAX_SPLIT], ll[PA_MAX_SPLIT];
+            float4 o[PA_MAX_SPLIT];
+#pragma unroll
+            for (int z = 0; z < PA_MAX_SPLIT; z++) {
+                const float *r = p + min(z, nz - 1) * RS;
+                ml[z] = r[D];
+                ll[z] = r[D + 1];
+                o[z] = *reinterpret_cast<const float4 *>(r + d);
+            }
+            float M = -__builtin_huge_valf();
+#pragma unroll
+            for (int z = 0; z < PA_MAX_SPLIT; z++)
+                if (z < nz) M = fmaxf(M, ml[z]);
+            float n0 = 0.f, n1 = 0.f, n2 = 0.f, n3 = 0.f, den = 0.f;
+#pragma unroll
+            for (int z = 0; z < PA_MAX_SPLIT; z++) {
+                if (z < nz) {
+                    const float f = __expf(ml[z] - M);
+                    n0 = fmaf(f, o[z].x, n0);
+                    n1 = fmaf(f, o[z].y, n1);
+                    n2 = fmaf(f, o[z].z, n2);
+                    n3 = fmaf(f, o[z].w, n3);
+                    den = fmaf(f, ll[z], den);
+                }
+            }
+            v[i] = make_float4(n0 / den, n1 / den, n2 / den, n3 / den);
+        }
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
     }
-    out[row * D + d] = num / den;
+    mx = pf_block_max(mx, red);
+    int e = 0;
+    frexpf(mx, &e);
+    int sh = mx > 0.f ? 15 - e : 0;
+    sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
+    const float sc = ldexpf(1.f, sh);
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 *hr = reinterpret_cast<h4 *>(h16 + (long long)t * NQ * D);
+#pragma unroll
+    for (int i = 0; i < PR_V; i++) {
+        const int j = tid + PN_THREADS * i;
+        if (j < n4)
+            hr[j] = h4{(_Float16)(v[i].x * sc), (_Float16)(v[i].y * sc), (_Float16)(v[i].z * sc),
+                       (_Float16)(v[i].w * sc)};
+    }
+    if (tid == 0) hinv[t] = ldexpf(1.f, -sh);
 }
 
 // Split size: PA_PREF_KS positions, larger for long contexts so that at
 // most PA_MAX_SPLIT splits exist (a multiple of PA_KF either way).
-constexpr int PA_PREF_KS = 128, PA_MAX_SPLIT = 8;
 static int pf_split_size(int kmax) {
     int ks = PA_PREF_KS;
     if ((kmax + ks - 1) / ks > PA_MAX_SPLIT) ks = ((kmax + PA_MAX_SPLIT - 1) / PA_MAX_SPLIT + PA_KF - 1) / PA_KF * PA_KF;
@@ -425,7 +508,8 @@ static int pf_split_size(int kmax) {
 
 template <int D>
 static hipError_t launch_pf_attn(int G, const float *qb, const float *kc, const float *vc, int T, int pos0, int NQ,
-                                 int NKV, int max_ctx, float *part, float *out, hipStream_t st) {
+                                 int NKV, int max_ctx, float *part, float *out, _Float16 *h16, float *hinv,
+                                 hipStream_t st) {
     const int ks = pf_split_size(pos0 + T), nsplit = (pos0 + T + ks - 1) / ks;
 #define TBQ_PFA(GG)                                                                                                \
     case GG:                                                                                                       \
@@ -438,8 +522,8 @@ static hipError_t launch_pf_attn(int G, const float *qb, const float *kc, const 
         return hipErrorNotSupported;
     }
 #undef TBQ_PFA
-    if (nsplit > 1)
-        hipLaunchKernelGGL(k_pf_attn_combine<D>, dim3(T * NQ), dim3(D), 0, st, part, NQ, pos0, ks, nsplit, out);
+    hipLaunchKernelGGL(k_pf_attn_rows<D>, dim3(T), dim3(PN_THREADS), 0, st, part, out, NQ, pos0, ks, nsplit, h16,
+                       hinv);
     return hipGetLastError();
 }
 
@@ -448,13 +532,14 @@ static hipError_t launch_pf_attn(int G, const float *qb, const float *kc, const 
 // ---------------------------------------------------------------------------
 static size_t pf_up(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Every model with hidden <= 8192 and ffn <= 16384 (the rows the norm and
-// SwiGLU kernels hold) takes the batched path for T >= 2.  Q4_K matrices go
+// Every model with hidden <= 8192, n_heads * head_dim <= 8192 and ffn <=
+// 16384 (the rows the norm, attention-row and SwiGLU kernels hold) takes the batched path for T >= 2.  Q4_K matrices go
 // straight into the GEMM (dequantised on the way into LDS); every other
 // format and layout is dequantised to fp16 first (one matrix at a time) and
 // multiplied by the same GEMM.
 bool dense_prefill_batched(const tbq_dense_model *m) {
-    return m->hidden <= PN_THREADS * PN_V * 4 && m->ffn <= PS_THREADS * PS_V * 4;
+    return m->hidden <= PN_THREADS * PN_V * 4 && m->ffn <= PS_THREADS * PS_V * 4 &&
+           m->n_heads * m->head_dim <= PN_THREADS * PR_V * 4;
 }
 
 struct PfWs {
@@ -524,41 +609,48 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
     const int cu = hgemm_cus();
     // C[T][rows] (row stride ldc) = h16 . W^T: Q4_K rows directly, any other
     // format through its fp16 form in wh
-    auto gemm = [&](int qt, const void *W, int rows, int K, float *C, int ldc) {
-        if (qt == QT_Q4_K) return launch_hgemm(QT_Q4_K, W, w.h16, T, rows, K, C, ldc, w.gpart, cu, st);
+    // (with ns set, the K slices' partial sums stay in w.gpart for the
+    // consumer to add: k_pf_qk, k_pf_norm and k_pf_scale_row take them)
+    auto gemm = [&](int qt, const void *W, int rows, int K, float *C, int ldc, int *ns = nullptr) {
+        if (qt == QT_Q4_K) return launch_hgemm(QT_Q4_K, W, w.h16, T, rows, K, C, ldc, w.gpart, cu, st, ns);
         const hipError_t e = launch_dequant_f16(qt, W, (long long)rows * K, w.wh, st);
         if (e != hipSuccess) return e;
-        return launch_hgemm(QT_F16, w.wh, w.h16, T, rows, K, C, ldc, w.gpart, cu, st);
+        return launch_hgemm(QT_F16, w.wh, w.h16, T, rows, K, C, ldc, w.gpart, cu, st, ns);
     };
+    const float *ysrc = w.y;   // the previous sublayer's output, as yns slices
+    int yns = 1;
     hipLaunchKernelGGL(k_pf_rope, dim3(T), dim3(64), 0, st, pos0, m->rope_theta, D, w.rope);
     hipError_t err = launch_dequant_rows(canon_qt(m->qtype_embd), m->tok_embd, w.tok, T, H, w.x, st);
     for (int l = 0; l < m->n_layers && err == hipSuccess; l++) {
         const tbq_dense_layer &L = m->layers[l];
         const size_t kvoff = (size_t)l * NKV * m->max_ctx * D;
         float *kc = m->k_cache + kvoff, *vc = m->v_cache + kvoff;
-        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, l ? w.y : nullptr, l ? w.sb : nullptr,
-                           L.attn_norm, H, m->norm_eps, w.h16, w.sa);
+        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, l ? ysrc : nullptr, yns,
+                           (long long)T * H, l ? w.sb : nullptr, L.attn_norm, H, m->norm_eps, w.h16, w.sa);
+        int qns = 1;
         if (L.wqkv) {
-            err = gemm(qt_of(L.qt_qkv), L.wqkv, QKVR, H, w.qkv, QKVR);
+            err = gemm(qt_of(L.qt_qkv), L.wqkv, QKVR, H, w.qkv, QKVR, &qns);
         } else {
             err = gemm(qt_of(L.qt_q), L.wq, QD, H, w.qkv, QKVR);
             if (err == hipSuccess) err = gemm(qt_of(L.qt_k), L.wk, KD, H, w.qkv + QD, QKVR);
             if (err == hipSuccess) err = gemm(qt_of(L.qt_v), L.wv, KD, H, w.qkv + QD + KD, QKVR);
         }
         if (err != hipSuccess) break;
+        const float *qsrc = qns > 1 ? w.gpart : w.qkv;
         if (D == 128) {
-            hipLaunchKernelGGL(k_pf_qk<128>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, w.sa, L.q_norm, L.k_norm, NQ,
-                               NKV, pos0, w.rope, m->norm_eps, kc, vc, m->max_ctx, w.qb);
-            err = launch_pf_attn<128>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, st);
+            hipLaunchKernelGGL(k_pf_qk<128>, dim3(T, NQ + NKV), dim3(64), 0, st, qsrc, qns, (long long)T * QKVR, w.sa,
+                               L.q_norm, L.k_norm, NQ, NKV, pos0, w.rope, m->norm_eps, kc, vc, m->max_ctx, w.qb);
+            err = launch_pf_attn<128>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, w.h16, w.sb, st);
         } else {
-            hipLaunchKernelGGL(k_pf_qk<64>, dim3(T, NQ + NKV), dim3(64), 0, st, w.qkv, w.sa, L.q_norm, L.k_norm, NQ,
-                               NKV, pos0, w.rope, m->norm_eps, kc, vc, m->max_ctx, w.qb);
-            err = launch_pf_attn<64>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, st);
+            hipLaunchKernelGGL(k_pf_qk<64>, dim3(T, NQ + NKV), dim3(64), 0, st, qsrc, qns, (long long)T * QKVR, w.sa,
+                               L.q_norm, L.k_norm, NQ, NKV, pos0, w.rope, m->norm_eps, kc, vc, m->max_ctx, w.qb);
+            err = launch_pf_attn<64>(G, w.qb, kc, vc, T, pos0, NQ, NKV, m->max_ctx, w.part, w.att, w.h16, w.sb, st);
         }
-        if (err != hipSuccess || (err = launch_rows_f16(w.att, T, QD, w.h16, w.sb, st)) != hipSuccess) break;
-        if ((err = gemm(qt_of(L.qt_o), L.wo, H, QD, w.y, H)) != hipSuccess) break;
-        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, w.y, w.sb, L.ffn_norm, H, m->norm_eps,
-                           w.h16, w.sa);
+        if (err != hipSuccess) break;
+        if ((err = gemm(qt_of(L.qt_o), L.wo, H, QD, w.y, H, &yns)) != hipSuccess) break;
+        ysrc = yns > 1 ? w.gpart : w.y;
+        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, ysrc, yns, (long long)T * H, w.sb,
+                           L.ffn_norm, H, m->norm_eps, w.h16, w.sa);
         if (L.wgu) {
             err = gemm(qt_of(L.qt_gu), L.wgu, 2 * F, H, w.gu, 2 * F);
         } else {
@@ -567,11 +659,13 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
         }
         if (err != hipSuccess) break;
         hipLaunchKernelGGL(k_pf_swiglu_f16, dim3(T), dim3(PS_THREADS), 0, st, w.gu, w.sa, F, w.h16, w.sb);
-        err = gemm(qt_of(L.qt_down), L.wdown, H, F, w.y, H);
+        err = gemm(qt_of(L.qt_down), L.wdown, H, F, w.y, H, &yns);
+        ysrc = yns > 1 ? w.gpart : w.y;
     }
     if (err != hipSuccess) return err;
     float *ylast = w.y + (size_t)(T - 1) * H;
-    hipLaunchKernelGGL(k_pf_scale_row, dim3(1), dim3(256), 0, st, ylast, w.sb + (T - 1), H);
+    hipLaunchKernelGGL(k_pf_scale_row, dim3(1), dim3(256), 0, st, ysrc + (size_t)(T - 1) * H, yns, (long long)T * H,
+                       w.sb + (T - 1), H, ylast);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     return dense_final_logits(m, w.x + (size_t)(T - 1) * H, ylast, logits, w.dec, st);
 }

@@ -400,7 +400,7 @@ bool hgemm_supported(int wqt, int N, int K) {
 // C: T rows of N floats at row stride ldc.  part: hgemm_partial_bytes() of
 // device memory (unused with one slice).
 hipError_t launch_hgemm(int wqt, const void *W, const _Float16 *X, int T, int N, int K, float *C, int ldc,
-                        float *part, int n_cu, hipStream_t st) {
+                        float *part, int n_cu, hipStream_t st, int *nslices) {
     if (!hgemm_supported(wqt, N, K) || T <= 0 || (long long)T * K * 2 >= (1ll << 31)) return hipErrorNotSupported;
     const int S = hgemm_slices(T, N, K, n_cu);
     const int steps = K / HG_BK, per = (steps + S - 1) / S;
@@ -408,6 +408,7 @@ hipError_t launch_hgemm(int wqt, const void *W, const _Float16 *X, int T, int N,
     dim3 grid((N + HG_BN - 1) / HG_BN, (T + HG_BT - 1) / HG_BT, Sx);
     float *out = Sx > 1 ? part : C;
     if (Sx > 1 && !part) return hipErrorInvalidValue;
+    if (nslices && Sx > 1 && ldc != N) return hipErrorInvalidValue;   // slices are packed at row stride N
     // more than 64 KiB of dynamic LDS is opted into once per kernel
     constexpr size_t lds = 2 * sizeof(HgStage);
     static const hipError_t a0 =
@@ -423,7 +424,8 @@ hipError_t launch_hgemm(int wqt, const void *W, const _Float16 *X, int T, int N,
         hipLaunchKernelGGL(k_hgemm<1>, grid, dim3(HG_THREADS), lds, st, W, X, T, N, K, per * HG_BK, out,
                            Sx > 1 ? N : ldc);
     hipError_t err = hipGetLastError();
-    if (err != hipSuccess || Sx == 1) return err;
+    if (nslices) *nslices = Sx;
+    if (err != hipSuccess || Sx == 1 || nslices) return err;
     const long long n4 = (long long)T * N / 4;
     const int g = (int)std::min<long long>((n4 + 255) / 256, 4096);
     hipLaunchKernelGGL(k_gemm_reduce, dim3(g), dim3(256), 0, st, part, Sx, T, N, C, ldc);

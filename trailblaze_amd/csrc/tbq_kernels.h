@@ -93,8 +93,11 @@ hipError_t launch_moe_i8(const MoeArgs &a, void *scratch, hipStream_t st);
 int hgemm_cus();
 bool hgemm_supported(int wqt, int N, int K);
 size_t hgemm_partial_bytes(int T, int N, int K, int n_cu);
+// With nslices set, the K slices' partial sums are left for the consumer to
+// add (in slice order): *nslices = S, and slice z is part + z * T * N (row
+// stride N) when S > 1; with S = 1 the product is in C as usual.
 hipError_t launch_hgemm(int wqt, const void *W, const _Float16 *X, int T, int N, int K, float *C, int ldc,
-                        float *part, int n_cu, hipStream_t st);
+                        float *part, int n_cu, hipStream_t st, int *nslices = nullptr);
 size_t dense_workspace_bytes(const tbq_dense_model *m);
 hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,
                                hipStream_t st);
