@@ -19,8 +19,10 @@
 //                    as fp16 rows with row scales (the o GEMM's operand)
 //   GEMM             y = att Wo^T
 //   k_pf_norm        x += y, h16 = rmsnorm(x) * ffn_norm
-//   GEMM             gu = h16 [Wg | Wu]^T
-//   k_pf_swiglu_f16  a16 = silu(g) * u (fp16, row scales)
+//   GEMM             a = silu(h16 Wg^T) * (h16 Wu^T) (SwiGLU in the GEMM's
+//                    epilogue for a fused gate|up matrix; else the two
+//                    products and k_pf_swiglu_f16), then a16 = fp16 rows
+//                    with row scales
 //   GEMM             y = a16 Wdown^T
 // then the last token's logits = Wlm rmsnorm(x + y) (the decode step's
 // lm_head matvec with its norm prologue).
@@ -651,14 +653,29 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
         ysrc = yns > 1 ? w.gpart : w.y;
         hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, ysrc, yns, (long long)T * H, w.sb,
                            L.ffn_norm, H, m->norm_eps, w.h16, w.sa);
+        // a fused gate|up matrix: SwiGLU in the GEMM's epilogue, then the
+        // activation rows to fp16; otherwise the gate and up products and
+        // k_pf_swiglu_f16
+        bool glu = false;
         if (L.wgu) {
-            err = gemm(qt_of(L.qt_gu), L.wgu, 2 * F, H, w.gu, 2 * F);
+            const int qt = qt_of(L.qt_gu);
+            const void *Wg = L.wgu;
+            if (qt != QT_Q4_K && (err = launch_dequant_f16(qt, L.wgu, (long long)2 * F * H, w.wh, st)) != hipSuccess)
+                break;
+            if (qt != QT_Q4_K) Wg = w.wh;
+            err = launch_hgemm_glu(qt == QT_Q4_K ? QT_Q4_K : QT_F16, Wg, w.h16, w.sa, T, F, H, w.gu, F, cu, st);
+            if (err == hipSuccess) glu = true;
+            else if (err == hipErrorNotSupported) err = gemm(qt, L.wgu, 2 * F, H, w.gu, 2 * F);
         } else {
             err = gemm(qt_of(L.qt_gate), L.wgate, F, H, w.gu, 2 * F);
             if (err == hipSuccess) err = gemm(qt_of(L.qt_up), L.wup, F, H, w.gu + F, 2 * F);
         }
         if (err != hipSuccess) break;
-        hipLaunchKernelGGL(k_pf_swiglu_f16, dim3(T), dim3(PS_THREADS), 0, st, w.gu, w.sa, F, w.h16, w.sb);
+        if (glu)
+            err = launch_rows_f16(w.gu, T, F, w.h16, w.sb, st);
+        else
+            hipLaunchKernelGGL(k_pf_swiglu_f16, dim3(T), dim3(PS_THREADS), 0, st, w.gu, w.sa, F, w.h16, w.sb);
+        if (err != hipSuccess) break;
         err = gemm(qt_of(L.qt_down), L.wdown, H, F, w.y, H, &yns);
         ysrc = yns > 1 ? w.gpart : w.y;
     }

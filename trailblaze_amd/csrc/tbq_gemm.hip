@@ -150,10 +150,17 @@ __device__ __forceinline__ void q4sub_f16(const Q4Sub &r, int j, hg_f16x8 (&o)[H
 // AF: 0 = W fp16 rows, 1 = W Q4_K rows (reference layout).  kper = K columns
 // per slice (a multiple of HG_BK); out = C with row stride ldo (gridDim.z ==
 // 1) or the slice partials P[z][T][N] (ldo = N).
-template <int AF>
+// GLU (one slice only): W holds N = 2F rows, gate rows then up rows, and
+// out[t][c] = silu(g xs[t]) (u xs[t]) with g, u = rows c and F + c of the
+// product (xs: the row scales of X).  The A tile's 32-row blocks alternate
+// gate and up rows of the same 32 outputs (tile n-block b holds outputs
+// 64 b .. 64 b + 63), so a lane's accumulators of blocks 0 and 1 hold the
+// gate and up of the same (output, token).
+template <int AF, bool GLU = false>
 __global__ __launch_bounds__(HG_THREADS) __attribute__((amdgpu_waves_per_eu(TBQ_HG_WPE))) void k_hgemm(const void *__restrict__ Wv, const _Float16 *__restrict__ X,
                                                          int T, int N, int K, int kper, float *__restrict__ out,
-                                                         int ldo) {
+                                                         int ldo, const float *__restrict__ xs = nullptr) {
+    static_assert(!GLU || HG_WI == 2, "GLU pairs the wave's two 32-row blocks");
     extern __shared__ __attribute__((aligned(16))) unsigned char hg_lds[];   // two HgStage (72 KiB)
     HgStage *st = reinterpret_cast<HgStage *>(hg_lds);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, lh = lane >> 5;
@@ -178,6 +185,15 @@ __global__ __launch_bounds__(HG_THREADS) __attribute__((amdgpu_waves_per_eu(TBQ_
     const _Float16 *Wh = reinterpret_cast<const _Float16 *>(Wv);
     const uint8_t *Wq = reinterpret_cast<const uint8_t *>(Wv);
     const long long rbq = (long long)(K / 256) * 144;
+    // weight row of tile row rho (rows past N clamp to the last)
+    auto wrow = [&](int rho) {
+        if constexpr (GLU) {
+            const int F = N / 2, b = rho >> 5;
+            return min((b & 1 ? F : 0) + (n0 >> 1) + 32 * (b >> 1) + (rho & 31), N - 1);
+        } else {
+            return min(n0 + rho, N - 1);
+        }
+    };
     // Q4_K task tk = tid + HG_THREADS i: row tk / (QPS SUBS), sub-block
     // (tk / QPS) % SUBS of the step, piece tk % QPS
     auto qtask = [&](int i, int &row, int &sub, int &pc) {
@@ -204,14 +220,13 @@ __global__ __launch_bounds__(HG_THREADS) __attribute__((amdgpu_waves_per_eu(TBQ_
         if constexpr (AF == 0) {
 #pragma unroll
             for (int i = 0; i < HG_ASEG; i++)
-                r.wr[i] = *reinterpret_cast<const hg_u32x4 *>(Wh + (long long)min(n0 + lrow + RSTEP * i, N - 1) * K +
-                                                              k + lcol);
+                r.wr[i] = *reinterpret_cast<const hg_u32x4 *>(Wh + (long long)wrow(lrow + RSTEP * i) * K + k + lcol);
         } else {
 #pragma unroll
             for (int i = 0; i < HG_QTPT; i++) {
                 int row, sub, pc;
                 qtask(i, row, sub, pc);
-                q4sub_load(Wq + (long long)min(n0 + row, N - 1) * rbq + (long long)(k >> 8) * 144,
+                q4sub_load(Wq + (long long)wrow(row) * rbq + (long long)(k >> 8) * 144,
                            ((k & 255) >> 5) + sub, pc, r.wq[i]);
             }
         }
@@ -331,6 +346,25 @@ __global__ __launch_bounds__(HG_THREADS) __attribute__((amdgpu_waves_per_eu(TBQ_
     }
     // accumulator register r of lane l: weight row 8(r/4) + 4(l/32) + r%4 of
     // the 32-row block, token l % 32 of the 32-token block
+    if constexpr (GLU) {
+        // outputs 64 blockIdx.x + wn / 2 + 8g + 4(l/32) + r%4 of register r
+#pragma unroll
+        for (int jx = 0; jx < HG_WJ; jx++) {
+            const int t = t0 + wt + 32 * jx + li;
+            if (t >= T) continue;
+            const float sx = xs[t];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int c = (n0 >> 1) + (wn >> 1) + 8 * g + 4 * lh;
+                if (c >= N / 2) continue;
+                float a[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) a[r] = pro_swiglu(acc[0][jx][4 * g + r] * sx, acc[1][jx][4 * g + r] * sx);
+                *reinterpret_cast<float4 *>(out + (long long)t * ldo + c) = make_float4(a[0], a[1], a[2], a[3]);
+            }
+        }
+        return;
+    }
     float *o = out + (long long)blockIdx.z * T * N;   // z > 0 only for partials (ldo = N)
 #pragma unroll
     for (int jx = 0; jx < HG_WJ; jx++) {
@@ -394,6 +428,31 @@ size_t hgemm_partial_bytes(int T, int N, int K, int n_cu) {
 
 bool hgemm_supported(int wqt, int N, int K) {
     return (wqt == QT_F16 || wqt == QT_Q4_K) && N > 0 && N % 4 == 0 && K > 0 && K % 256 == 0;
+}
+
+// The gate/up product with SwiGLU in the epilogue (k_hgemm GLU mode): W
+// holds 2F rows (gate then up), A[T][F] (row stride lda) = silu(g xs) (u
+// xs).  hipErrorNotSupported where the product would be split over K (the
+// SwiGLU of partial sums is not defined) or F is not a multiple of 64.
+hipError_t launch_hgemm_glu(int wqt, const void *W, const _Float16 *X, const float *xs, int T, int F, int K,
+                            float *A, int lda, int n_cu, hipStream_t st) {
+    const int N = 2 * F;
+    if (!hgemm_supported(wqt, N, K) || F % 64 || T <= 0 || (long long)T * K * 2 >= (1ll << 31) ||
+        hgemm_slices(T, N, K, n_cu) != 1)
+        return hipErrorNotSupported;
+    dim3 grid(N / HG_BN, (T + HG_BT - 1) / HG_BT, 1);
+    constexpr size_t lds = 2 * sizeof(HgStage);
+    static const hipError_t a0 =
+        hipFuncSetAttribute((const void *)k_hgemm<0, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    static const hipError_t a1 =
+        hipFuncSetAttribute((const void *)k_hgemm<1, true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (a0 != hipSuccess) return a0;
+    if (a1 != hipSuccess) return a1;
+    if (wqt == QT_F16)
+        hipLaunchKernelGGL((k_hgemm<0, true>), grid, dim3(HG_THREADS), lds, st, W, X, T, N, K, K, A, lda, xs);
+    else
+        hipLaunchKernelGGL((k_hgemm<1, true>), grid, dim3(HG_THREADS), lds, st, W, X, T, N, K, K, A, lda, xs);
+    return hipGetLastError();
 }
 
 // wqt: QT_F16 (IEEE fp16 rows, as k_dequant_f16 writes them) or QT_Q4_K.

@@ -98,6 +98,12 @@ size_t hgemm_partial_bytes(int T, int N, int K, int n_cu);
 // stride N) when S > 1; with S = 1 the product is in C as usual.
 hipError_t launch_hgemm(int wqt, const void *W, const _Float16 *X, int T, int N, int K, float *C, int ldc,
                         float *part, int n_cu, hipStream_t st, int *nslices = nullptr);
+// The gate|up product (W: 2F rows, gate then up) with SwiGLU in the
+// epilogue: A[T][F] (row stride lda) = silu(g xs) (u xs), xs = X's row
+// scales; hipErrorNotSupported where it would need split K or F % 64 != 0.
+hipError_t launch_hgemm_glu(int wqt, const void *W, const _Float16 *X, const float *xs, int T, int F, int K,
+                            float *A, int lda, int n_cu, hipStream_t st);
+int hgemm_slices(int T, int N, int K, int n_cu);
 size_t dense_workspace_bytes(const tbq_dense_model *m);
 hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,
                                hipStream_t st);
