@@ -72,7 +72,8 @@ __device__ __forceinline__ float pf_block_max(float v, float *red) {
 // y may be a GEMM's ny split-K slices (slice z at y + z * ystride), added
 // here in slice order.  A thread holds up to PN_V float4 of the row (H <=
 // 8192), all loaded before any is used.
-constexpr int PN_V = 8;
+constexpr int PN_V = 8, PN_MAXY = 8;   // float4 per thread (H <= 8192), slices of y
+template <int PV>   // float4 of the row per thread: ceil(H / 4 / PN_THREADS) <= PV
 __global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, const float *__restrict__ y, int ny,
                                                         long long ystride, const float *__restrict__ ys,
                                                         const float *__restrict__ w, int H, float eps,
@@ -82,28 +83,39 @@ __global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, c
     float4 *xr = reinterpret_cast<float4 *>(x + (long long)t * H);
     const float4 *yr = reinterpret_cast<const float4 *>(y ? y + (long long)t * H : x + (long long)t * H);
     const float4 *wr = reinterpret_cast<const float4 *>(w);
-    float4 v[PN_V], b[PN_V], g[PN_V];
+    float4 v[PV], b[PV], g[PV];
 #pragma unroll
-    for (int i = 0; i < PN_V; i++) {
+    for (int i = 0; i < PV; i++) {
         const int j = min(tid + PN_THREADS * i, n4 - 1);   // clamped: loads stay unconditional
         v[i] = xr[j];
         b[i] = yr[j];
         g[i] = wr[j];
     }
-    if (y) {
-        for (int z = 1; z < ny; z++) {
-            const float4 *yz = yr + z * (ystride / 4);
+    if (y && ny > 1) {
+        // every slice's loads issued at once (slices past ny re-read the
+        // last and are not added), then added in slice order
+        float4 c[PN_MAXY - 1][PV];
 #pragma unroll
-            for (int i = 0; i < PN_V; i++) {
-                const float4 c = yz[min(tid + PN_THREADS * i, n4 - 1)];
-                b[i].x = b[i].x + c.x; b[i].y = b[i].y + c.y; b[i].z = b[i].z + c.z; b[i].w = b[i].w + c.w;
+        for (int z = 1; z < PN_MAXY; z++) {
+            const float4 *yz = yr + min(z, ny - 1) * (ystride / 4);
+#pragma unroll
+            for (int i = 0; i < PV; i++) c[z - 1][i] = yz[min(tid + PN_THREADS * i, n4 - 1)];
+        }
+#pragma unroll
+        for (int z = 1; z < PN_MAXY; z++) {
+            if (z < ny) {
+#pragma unroll
+                for (int i = 0; i < PV; i++) {
+                    b[i].x = b[i].x + c[z - 1][i].x; b[i].y = b[i].y + c[z - 1][i].y;
+                    b[i].z = b[i].z + c[z - 1][i].z; b[i].w = b[i].w + c[z - 1][i].w;
+                }
             }
         }
     }
     float ss = 0.f;
     const float yscale = ys ? ys[t] : 1.f;
 #pragma unroll
-    for (int i = 0; i < PN_V; i++) {
+    for (int i = 0; i < PV; i++) {
         if (y) {
             v[i].x += b[i].x * yscale; v[i].y += b[i].y * yscale;
             v[i].z += b[i].z * yscale; v[i].w += b[i].w * yscale;
@@ -112,14 +124,14 @@ __global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, c
     }
     if (y) {
 #pragma unroll
-        for (int i = 0; i < PN_V; i++)
+        for (int i = 0; i < PV; i++)
             if (tid + PN_THREADS * i < n4) xr[tid + PN_THREADS * i] = v[i];
     }
     ss = pf_block_sum(ss, red);
     const float r = 1.0f / sqrtf(ss / (float)H + eps);
     float mx = 0.f;
 #pragma unroll
-    for (int i = 0; i < PN_V; i++) {
+    for (int i = 0; i < PV; i++) {
         v[i].x = v[i].x * r * g[i].x; v[i].y = v[i].y * r * g[i].y;
         v[i].z = v[i].z * r * g[i].z; v[i].w = v[i].w * r * g[i].w;
         if (tid + PN_THREADS * i < n4)
@@ -133,7 +145,7 @@ __global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, c
     const float s = ldexpf(1.f, sh);
     uint2 *hr = reinterpret_cast<uint2 *>(h16 + (long long)t * H);
 #pragma unroll
-    for (int i = 0; i < PN_V; i++) {
+    for (int i = 0; i < PV; i++) {
         const int j = tid + PN_THREADS * i;
         if (j < n4) {
             const _Float16 a0 = (_Float16)(v[i].x * s), a1 = (_Float16)(v[i].y * s);
@@ -143,6 +155,24 @@ __global__ __launch_bounds__(PN_THREADS) void k_pf_norm(float *__restrict__ x, c
         }
     }
     if (tid == 0) hinv[t] = ldexpf(1.f, -sh);
+}
+
+static hipError_t launch_pf_norm(int T, float *x, const float *y, int ny, long long ystride, const float *ys,
+                                 const float *w, int H, float eps, _Float16 *h16, float *hinv, hipStream_t st) {
+    if (ny > PN_MAXY) return hipErrorNotSupported;
+    const int pv = (H / 4 + PN_THREADS - 1) / PN_THREADS;
+#define TBQ_PN(V)                                                                                                  \
+    case V:                                                                                                        \
+        hipLaunchKernelGGL(k_pf_norm<V>, dim3(T), dim3(PN_THREADS), 0, st, x, y, ny, ystride, ys, w, H, eps, h16,  \
+                           hinv);                                                                                  \
+        break;
+    switch (pv) {
+        TBQ_PN(1) TBQ_PN(2) TBQ_PN(3) TBQ_PN(4) TBQ_PN(5) TBQ_PN(6) TBQ_PN(7) TBQ_PN(8)
+    default:
+        return hipErrorNotSupported;
+    }
+#undef TBQ_PN
+    return hipGetLastError();
 }
 
 // RoPE tables of the prompt's positions, shared by every layer: rc[t][j] =
@@ -627,8 +657,9 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
         const tbq_dense_layer &L = m->layers[l];
         const size_t kvoff = (size_t)l * NKV * m->max_ctx * D;
         float *kc = m->k_cache + kvoff, *vc = m->v_cache + kvoff;
-        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, l ? ysrc : nullptr, yns,
-                           (long long)T * H, l ? w.sb : nullptr, L.attn_norm, H, m->norm_eps, w.h16, w.sa);
+        err = launch_pf_norm(T, w.x, l ? ysrc : nullptr, yns, (long long)T * H, l ? w.sb : nullptr, L.attn_norm, H,
+                             m->norm_eps, w.h16, w.sa, st);
+        if (err != hipSuccess) break;
         int qns = 1;
         if (L.wqkv) {
             err = gemm(qt_of(L.qt_qkv), L.wqkv, QKVR, H, w.qkv, QKVR, &qns);
@@ -651,8 +682,9 @@ static hipError_t pf_batched(const tbq_dense_model *m, const PfWs &w, int T, int
         if (err != hipSuccess) break;
         if ((err = gemm(qt_of(L.qt_o), L.wo, H, QD, w.y, H, &yns)) != hipSuccess) break;
         ysrc = yns > 1 ? w.gpart : w.y;
-        hipLaunchKernelGGL(k_pf_norm, dim3(T), dim3(PN_THREADS), 0, st, w.x, ysrc, yns, (long long)T * H, w.sb,
-                           L.ffn_norm, H, m->norm_eps, w.h16, w.sa);
+        if ((err = launch_pf_norm(T, w.x, ysrc, yns, (long long)T * H, w.sb, L.ffn_norm, H, m->norm_eps, w.h16,
+                                  w.sa, st)) != hipSuccess)
+            break;
         // a fused gate|up matrix: SwiGLU in the GEMM's epilogue, then the
         // activation rows to fp16; otherwise the gate and up products and
         // k_pf_swiglu_f16

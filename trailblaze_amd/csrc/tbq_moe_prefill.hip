@@ -153,15 +153,28 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
 // max |row| = f * 2^e (f in [0.5, 1)), so |row| * s < 2^15; inv[row] = 1/s.
 // n a multiple of 4.
 // ---------------------------------------------------------------------------
+// RV > 0: the row is held in registers (n <= 1024 RV), read once with
+// every load issued before the max; RV = 0: two passes over the row.
+template <int RV>
 __global__ __launch_bounds__(256) void k_rows_f16(const float *__restrict__ in, int n, _Float16 *__restrict__ out,
                                                   float *__restrict__ inv) {
     __shared__ float part[4];
-    const int row = blockIdx.x, tid = threadIdx.x;
+    const int row = blockIdx.x, tid = threadIdx.x, n4 = n / 4;
     const float4 *r = reinterpret_cast<const float4 *>(in + (long long)row * n);
+    float4 v[RV > 0 ? RV : 1];
     float mx = 0.f;
-    for (int i = tid; i < n / 4; i += 256) {
-        const float4 v = r[i];
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    if constexpr (RV > 0) {
+#pragma unroll
+        for (int i = 0; i < RV; i++) v[i] = r[min(tid + 256 * i, n4 - 1)];   // clamped: unconditional
+#pragma unroll
+        for (int i = 0; i < RV; i++)
+            if (tid + 256 * i < n4)
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    } else {
+        for (int i = tid; i < n4; i += 256) {
+            const float4 w = r[i];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(w.x), fabsf(w.y)), fmaxf(fabsf(w.z), fabsf(w.w))));
+        }
     }
     mx = wave_max(mx);
     if ((tid & 63) == 0) part[tid >> 6] = mx;
@@ -173,11 +186,17 @@ __global__ __launch_bounds__(256) void k_rows_f16(const float *__restrict__ in, 
     sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
     const float s = ldexpf(1.f, sh);
     uint2 *o = reinterpret_cast<uint2 *>(out + (long long)row * n);
-    for (int i = tid; i < n / 4; i += 256) {
-        const float4 v = r[i];
-        const f16x2 a = {(_Float16)(v.x * s), (_Float16)(v.y * s)};
-        const f16x2 b = {(_Float16)(v.z * s), (_Float16)(v.w * s)};
+    auto put = [&](int i, float4 w) {
+        const f16x2 a = {(_Float16)(w.x * s), (_Float16)(w.y * s)};
+        const f16x2 b = {(_Float16)(w.z * s), (_Float16)(w.w * s)};
         o[i] = make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+    };
+    if constexpr (RV > 0) {
+#pragma unroll
+        for (int i = 0; i < RV; i++)
+            if (tid + 256 * i < n4) put(tid + 256 * i, v[i]);
+    } else {
+        for (int i = tid; i < n4; i += 256) put(i, r[i]);
     }
     if (tid == 0) inv[row] = ldexpf(1.f, -sh);
 }
@@ -845,7 +864,16 @@ hipError_t launch_moe_prefill_q4k_i8(const MoeArgs &a, void *scratch, hipStream_
 }
 
 hipError_t launch_rows_f16(const float *in, int rows, int n, _Float16 *out, float *inv, hipStream_t st) {
-    hipLaunchKernelGGL(k_rows_f16, dim3(rows), dim3(256), 0, st, in, n, out, inv);
+    const int rv = (n / 4 + 255) / 256;
+    switch (rv) {
+    case 1: hipLaunchKernelGGL(k_rows_f16<1>, dim3(rows), dim3(256), 0, st, in, n, out, inv); break;
+    case 2: hipLaunchKernelGGL(k_rows_f16<2>, dim3(rows), dim3(256), 0, st, in, n, out, inv); break;
+    case 3: case 4: hipLaunchKernelGGL(k_rows_f16<4>, dim3(rows), dim3(256), 0, st, in, n, out, inv); break;
+    case 5: case 6: case 7: case 8: hipLaunchKernelGGL(k_rows_f16<8>, dim3(rows), dim3(256), 0, st, in, n, out, inv); break;
+    case 9: case 10: case 11: case 12: hipLaunchKernelGGL(k_rows_f16<12>, dim3(rows), dim3(256), 0, st, in, n, out, inv); break;
+    case 13: case 14: case 15: case 16: hipLaunchKernelGGL(k_rows_f16<16>, dim3(rows), dim3(256), 0, st, in, n, out, inv); break;
+    default: hipLaunchKernelGGL(k_rows_f16<0>, dim3(rows), dim3(256), 0, st, in, n, out, inv); break;
+    }
     return hipGetLastError();
 }
 
@@ -885,7 +913,10 @@ hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t s
     _Float16 *x16 = (_Float16 *)w; w += up((size_t)a.T * a.H * 2);
     float *ainv = (float *)w; w += up(P * 4);
     float *xinv = (float *)w;
-    if (!x16_done) hipLaunchKernelGGL(k_rows_f16, dim3(a.T), dim3(256), 0, st, a.xn, a.H, x16, xinv);
+    if (!x16_done) {
+        const hipError_t e = launch_rows_f16(a.xn, a.T, a.H, x16, xinv, st);
+        if (e != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, st, a.sel_idx, a.T, a.k, a.E, perm, tiles, ntiles, tpair,
                        ttok);
     hipError_t err = hipGetLastError();
@@ -894,8 +925,7 @@ hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t s
     err = launch_moe_f16<0>(a.H / PF_KC, pf_grid((unsigned)(max_tiles * ncb0)), st, (const uint8_t *)a.gate,
                             (const uint8_t *)a.up, x16, a.T, xinv, tpair, ttok, tiles, ntiles, ncb0, a.H, a.F, a.act);
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_rows_f16, dim3((unsigned)P), dim3(256), 0, st, a.act, a.F, act16, ainv);
-    err = hipGetLastError();
+    err = launch_rows_f16(a.act, (int)P, a.F, act16, ainv, st);
     if (err != hipSuccess) return err;
     return launch_moe_f16<1>(a.F / PF_KC, pf_grid((unsigned)(max_tiles * ncb1)), st, (const uint8_t *)a.down, nullptr,
                              act16, (int)P, ainv, tpair, ttok, tiles, ntiles, ncb1, a.H, a.F, a.y);
