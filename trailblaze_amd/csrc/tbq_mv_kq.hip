@@ -320,6 +320,22 @@ __device__ __forceinline__ uint32_t spread_odd(uint32_t b) {
 // Per-format unit loads and dots.  Unit u of a row: super-block u/4, weights
 // 64*(u%4)..+63 (256-weight formats); blocks 2u, 2u+1 (32-weight formats).
 // ---------------------------------------------------------------------------
+// A Q4_0 unit (two 18-byte blocks, 36 bytes, 4-byte aligned in rows of K %
+// 64 == 0 elements) in three loads: block 0's d (bytes 0-1) and quants
+// (bytes 2-17, realigned by two bytes), block 1's d (bytes 18-19) and quants
+// (bytes 20-35, aligned).
+__device__ __forceinline__ void q40_unit_load(const uint8_t *row, int u, uint4 &a, uint4 &b, uint32_t &d0,
+                                              uint32_t &d1) {
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(row + (size_t)u * 36);
+    const uint4 A = *reinterpret_cast<const uint4 *>(q), B = *reinterpret_cast<const uint4 *>(q + 4);
+    const uint32_t C = q[8];
+    d0 = A.x & 0xFFFFu;
+    a = make_uint4(__builtin_amdgcn_alignbyte(A.y, A.x, 2), __builtin_amdgcn_alignbyte(A.z, A.y, 2),
+                   __builtin_amdgcn_alignbyte(A.w, A.z, 2), __builtin_amdgcn_alignbyte(B.x, A.w, 2));
+    d1 = B.x >> 16;
+    b = make_uint4(B.y, B.z, B.w, C);
+}
+
 template <int QT> struct KqFmt;
 
 // Q2_K (layer4/tb_gguf.c:210-225): sc[16]@0 (scale lo nibble, min hi
@@ -561,19 +577,25 @@ template <> struct KqFmt<QT_Q6_K> {
 template <int QT> struct KqQ80 {
     static constexpr bool PAIR = false;
     struct Unit { uint4 a0, a1, b0, b1; uint32_t d0, d1; };
-    // unit = 68 bytes (4-byte aligned when the row is): block 0's quants
-    // start 2 mod 4 (ld_dw), block 1's are aligned
+    // unit = 68 bytes, 4-byte aligned (rows of K % 64 == 0 elements are):
+    // its 17 dwords in five loads, then block 0's d (bytes 0-1) and quants
+    // (bytes 2-33, realigned by two bytes), block 1's d (bytes 34-35) and
+    // quants (bytes 36-67, aligned)
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
-        const uint8_t *b = row + (size_t)u * 68;
-        uint32_t t[8];
-        w.d0 = GMem::ld16(b);
-        GMem::template ldw<8>(b + 2, t);
-        w.a0 = make_uint4(t[0], t[1], t[2], t[3]);
-        w.a1 = make_uint4(t[4], t[5], t[6], t[7]);
-        w.d1 = GMem::ld16(b + 34);
-        GMem::template ldw<8>(b + 36, t);
-        w.b0 = make_uint4(t[0], t[1], t[2], t[3]);
-        w.b1 = make_uint4(t[4], t[5], t[6], t[7]);
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(row + (size_t)u * 68);
+        const uint4 A = *reinterpret_cast<const uint4 *>(q), B = *reinterpret_cast<const uint4 *>(q + 4);
+        const uint4 C = *reinterpret_cast<const uint4 *>(q + 8), D = *reinterpret_cast<const uint4 *>(q + 12);
+        const uint32_t E = q[16];
+        const uint32_t t[9] = {A.x, A.y, A.z, A.w, B.x, B.y, B.z, B.w, C.x};
+        uint32_t r[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) r[j] = __builtin_amdgcn_alignbyte(t[j + 1], t[j], 2);
+        w.d0 = A.x & 0xFFFFu;
+        w.a0 = make_uint4(r[0], r[1], r[2], r[3]);
+        w.a1 = make_uint4(r[4], r[5], r[6], r[7]);
+        w.d1 = C.x >> 16;
+        w.b0 = make_uint4(C.y, C.z, C.w, D.x);
+        w.b1 = make_uint4(D.y, D.z, D.w, E);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
         const uint32_t q0[8] = {w.a0.x, w.a0.y, w.a0.z, w.a0.w, w.a1.x, w.a1.y, w.a1.z, w.a1.w};
@@ -597,14 +619,7 @@ template <> struct KqFmt<QT_Q4_0> {
     // unit = 36 bytes: block 0's quants start 2 mod 4 when the unit is
     // aligned (ld_dw)
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
-        const uint8_t *b = row + (size_t)u * 36;
-        uint32_t t[4];
-        w.d0 = GMem::ld16(b);
-        GMem::template ldw<4>(b + 2, t);
-        w.a = make_uint4(t[0], t[1], t[2], t[3]);
-        w.d1 = GMem::ld16(b + 18);
-        GMem::template ldw<4>(b + 20, t);
-        w.b = make_uint4(t[0], t[1], t[2], t[3]);
+        q40_unit_load(row, u, w.a, w.b, w.d0, w.d1);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
         const float d0 = f16_dec<false>(w.d0), d1 = f16_dec<false>(w.d1);
@@ -885,14 +900,7 @@ template <> struct KqFmt<QT_GQ4_0> {
     static constexpr bool PAIR = false;
     struct Unit { uint4 a, b; uint32_t d0, d1; };
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
-        const uint8_t *b = row + (size_t)u * 36;
-        uint32_t t[4];
-        w.d0 = GMem::ld16(b);
-        GMem::template ldw<4>(b + 2, t);
-        w.a = make_uint4(t[0], t[1], t[2], t[3]);
-        w.d1 = GMem::ld16(b + 18);
-        GMem::template ldw<4>(b + 20, t);
-        w.b = make_uint4(t[0], t[1], t[2], t[3]);
+        q40_unit_load(row, u, w.a, w.b, w.d0, w.d1);
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int) {
         const float d0 = f16_dec<true>(w.d0), d1 = f16_dec<true>(w.d1);
