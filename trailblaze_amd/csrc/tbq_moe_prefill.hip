@@ -331,25 +331,22 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
         const int it = tid + PF_THREADS * m;
         xoff[m] = px[m] >= 0 ? (px[m] * K + 8 * (it & 15)) * 2 : xbytes;
     }
-    // two register sets of activation segments: chunk s + 2's loads are
-    // issued at the start of chunk s into the set that held chunk s (already
-    // in LDS), chunk s + 1's are stored at its end
-    u32x4 xa[XPT], xb[XPT];
-    auto xload = [&](u32x4 *xr, int s) {
+    u32x4 xr[XPT];
+    auto xload = [&](int s) {
 #pragma unroll
         for (int m = 0; m < XPT; m++)
             xr[m] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[m] < xbytes ? xoff[m] + s * PF_KC * 2 : xbytes, 0, 0);
     };
-    auto xstore = [&](const u32x4 *xr, int buf) {
+    auto xstore = [&](int buf) {
 #pragma unroll
         for (int m = 0; m < XPT; m++) {
             const int it = tid + PF_THREADS * m;
             *reinterpret_cast<u32x4 *>(pf_lds + (buf * PF_MT + (it >> 4)) * PF_LD + 8 * (it & 15)) = xr[m];
         }
     };
-    xload(xa, 0);
-    xstore(xa, 0);
-    xload(xb, min(1, NS - 1));
+    xload(0);
+    xstore(0);
+    xload(min(1, NS - 1));
     __syncthreads();
 
     const int nsub = (tl.n + 31) / 32;   // 1..4, uniform over the workgroup
@@ -372,37 +369,34 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
             }
         }
     };
-    // chunk s: weights of chunk s + 2 into wn (ring of three named slots) and
-    // activations of chunk s + 2 into xl (ring of two), both issued before
-    // the chunk's arithmetic; chunk s + 1's activations (xs) are staged into
-    // LDS after it.  Chunks past the end reload the last one and skip the
-    // work.  Every path through a chunk issues the same global loads (the
-    // compiler merges wait counts over paths, and a path with fewer loads
-    // would make it wait for the prefetches too).
-    auto chunk = [&](int s, const Q4Pair &wc, Q4Pair &wn, u32x4 *xl, const u32x4 *xs) {
+    // chunk s: weights of chunk s + 2 into wn (ring of three named slots, so
+    // the loop need not be unrolled to keep them in registers), activations
+    // of chunk s + 2 into registers after staging chunk s + 1's into LDS.
+    // Chunks past the end reload the last one and skip the work.
+    // Every path through a chunk issues the same global loads (the compiler
+    // merges wait counts over paths, and a path with fewer loads would make
+    // it wait for the prefetches too).
+    auto chunk = [&](int s, const Q4Pair &wc, Q4Pair &wn) {
         wload(wn, min(s + 2, NS - 1));
-        xload(xl, min(s + 2, NS - 1));
         if (s < NS) {
             const int j0 = 4 * (s & 1) + 2 * lh;
-            const _Float16 *xbuf = xfrag + (s & 1) * PF_MT * PF_LD;
+            const _Float16 *xb = xfrag + (s & 1) * PF_MT * PF_LD;
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 f16x8 a[4];
                 q4pair_frags(wc, j0, u, a);
-                mma(a, xbuf, u);
+                mma(a, xb, u);
             }
             // buffer last read in chunk s - 1, before the previous barrier
-            if (s + 1 < NS) xstore(xs, (s + 1) & 1);
-            __syncthreads();
+            if (s + 1 < NS) xstore((s + 1) & 1);
         }
+        xload(min(s + 2, NS - 1));
+        if (s < NS) __syncthreads();
     };
-    for (int s = 0; s < NS; s += 6) {
-        chunk(s, w0, w2, xa, xb);
-        chunk(s + 1, w1, w0, xb, xa);
-        chunk(s + 2, w2, w1, xa, xb);
-        chunk(s + 3, w0, w2, xb, xa);
-        chunk(s + 4, w1, w0, xa, xb);
-        chunk(s + 5, w2, w1, xb, xa);
+    for (int s = 0; s < NS; s += 3) {
+        chunk(s, w0, w2);
+        chunk(s + 1, w1, w0);
+        chunk(s + 2, w2, w1);
     }
     // accumulator register r of lane l: row 8(r/4) + 4(l/32) + r%4 of the
     // wave's 32, pair 32t + l%32 of the tile
