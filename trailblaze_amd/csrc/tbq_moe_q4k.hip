@@ -331,7 +331,7 @@ __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn,
 #define TBQ_GU_WAVES 8
 #endif
 #ifndef TBQ_GU_ROWS
-#define TBQ_GU_ROWS 2
+#define TBQ_GU_ROWS 1
 #endif
 constexpr int GU_THREADS = 64 * TBQ_GU_WAVES;
 constexpr int GU_ROWS = TBQ_GU_ROWS;   // output rows per wave
@@ -527,8 +527,11 @@ __global__ __launch_bounds__(DG_THREADS) void k_down_pair_q4k(const uint8_t *__r
 // loops units).  Results meet in LDS and one lane per row adds them in slot
 // order.
 // ---------------------------------------------------------------------------
+#ifndef TBQ_DC_ROWS
+#define TBQ_DC_ROWS 4
+#endif
 constexpr int DC_THREADS = 512;
-constexpr int DC_ROWS = 8;   // rows per workgroup
+constexpr int DC_ROWS = TBQ_DC_ROWS;   // rows per workgroup
 
 template <int UPL, bool GG>
 __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *__restrict__ down, const float *__restrict__ act,
