@@ -67,6 +67,13 @@ struct PfTile {
     int e, n;
 };
 
+// a tile's count of 32-pair sub-tiles as a type, for the per-count copies of
+// the expert GEMM's chunk loop
+template <int N>
+struct PfSub {
+    static constexpr int value = N;
+};
+
 // ---------------------------------------------------------------------------
 // Dispatch: one workgroup of 1024 threads.  pairs p = t*k + s.  Tiles are
 // listed heaviest first (by 32-pair sub-tile count), so the
@@ -120,6 +127,9 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
             qcnt[q] = 0;
         }
         *ntiles = b;
+        // item tickets of the two expert GEMMs (k_moe_f16), taken from 0
+        ntiles[1] = 0;
+        ntiles[2] = 0;
         qbase[0] = b;
     }
     __syncthreads();
@@ -261,9 +271,12 @@ __device__ __forceinline__ void q4pair_frags(const Q4Pair &r, int j0, int u, f16
 // Expert tile GEMM.  Work items are (tile, row block) pairs, tile-major
 // (ncb = F/PF_COLS row blocks for MODE 0, H/PF_ROWS for MODE 1), the tiles
 // heaviest first; K = NS * 128.  The grid is persistent (one workgroup
-// per CU): workgroup b takes items b, b + grid, b + 2 grid, ..., so the
-// heavy items are spread over the whole GPU first and no CU idles while
-// another finishes a second round of one-item workgroups.
+// per CU): workgroup b starts with item b, then takes tickets from the
+// counter ntiles[1 + MODE] (zeroed by k_dispatch): item grid + ticket, the
+// ticket taken two chunks before the end of the current item.  Items thus
+// go out heaviest first to whichever workgroup is about to be free (greedy
+// list scheduling); a fixed stride over the items left the workgroups that
+// drew heavy items 30% busier than the mean.
 //   MODE 0: wave w, lane row i = l % 32 is gate (i < 16) or up (i >= 16)
 //   column PF_COLS*cb + 16w + i % 16, so a lane's accumulator registers r
 //   and r + 8 hold gate and up of the same (column, pair) and SwiGLU needs
@@ -279,13 +292,14 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
                                                         const _Float16 *__restrict__ X, int x_rows,
                                                         const float *__restrict__ xinv, const int *__restrict__ tpair,
                                                         const int *__restrict__ ttok, const PfTile *__restrict__ tiles,
-                                                        const int *__restrict__ ntiles, int ncb, int H, int F,
+                                                        int *__restrict__ ntiles, int ncb, int H, int F,
                                                         float *__restrict__ out) {
     constexpr int K = NS * PF_KC;
     constexpr int XPT = PF_MT * PF_KC / 8 / PF_THREADS;   // 16-byte activation segments per thread per chunk
     extern __shared__ __attribute__((aligned(16))) _Float16 pf_lds[];   // [2][PF_MT][PF_LD]
     const int nitems = *ntiles * ncb;
-    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+    __shared__ int next_item;
+    for (int item = blockIdx.x; item < nitems;) {
     // item -> (tile, row block).  The tile record and its row lists are
     // loaded together.
     const int tix = item / ncb, cb = item % ncb;
@@ -349,89 +363,106 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
     xload(min(1, NS - 1));
     __syncthreads();
 
-    const int nsub = (tl.n + 31) / 32;   // 1..4, uniform over the workgroup
-    f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
     const _Float16 *xfrag = pf_lds + li * PF_LD + 64 * lh;
-    // steps 4u .. 4u + 3 of a chunk for the sub-tiles that hold pairs: one
-    // uniform branch per sub-tile, so every accumulator keeps its registers
-    // (a switch over the sub-tile count gives each arm its own allocation
-    // and costs a copy of the accumulators per chunk)
-    auto mma = [&](const f16x8 *a, const _Float16 *xb, int u) {
+    // the workgroup's next item: a ticket taken two chunks before the end of
+    // this one (its latency hidden behind them), so items go to workgroups
+    // in the order they finish work, heaviest items first
+    int nxt = 0;
+    // The chunk loop and the epilogue for a compile-time count of 32-pair
+    // sub-tiles (1..4, uniform over the workgroup): one copy per count, so
+    // no branch splits a chunk's LDS reads from its MFMAs and the compiler
+    // can issue the next operands' reads while the current MFMAs run.
+    auto body = [&](auto nsub_c) {
+        constexpr int NSUB = decltype(nsub_c)::value;
+        f32x16 acc[NSUB];
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            if (t < nsub) {
+        for (int t = 0; t < NSUB; t++) acc[t] = f32x16{};
+        // steps 4u .. 4u + 3 of a chunk for every sub-tile
+        auto mma = [&](const f16x8 *a, const _Float16 *xb, int u) {
+#pragma unroll
+            for (int t = 0; t < NSUB; t++) {
                 f16x8 bv[4];
 #pragma unroll
                 for (int ks = 0; ks < 4; ks++)
                     bv[ks] = *reinterpret_cast<const f16x8 *>(xb + 32 * t * PF_LD + 8 * (4 * u + ks));
 #pragma unroll
-                for (int ks = 0; ks < 4; ks++) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks], bv[ks], acc[t], 0, 0, 0);
+                for (int ks = 0; ks < 4; ks++)
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks], bv[ks], acc[t], 0, 0, 0);
             }
-        }
-    };
-    // chunk s: weights of chunk s + 2 into wn (ring of three named slots, so
-    // the loop need not be unrolled to keep them in registers), activations
-    // of chunk s + 2 into registers after staging chunk s + 1's into LDS.
-    // Chunks past the end reload the last one and skip the work.
-    // Every path through a chunk issues the same global loads (the compiler
-    // merges wait counts over paths, and a path with fewer loads would make
-    // it wait for the prefetches too).
-    auto chunk = [&](int s, const Q4Pair &wc, Q4Pair &wn) {
-        wload(wn, min(s + 2, NS - 1));
-        if (s < NS) {
-            const int j0 = 4 * (s & 1) + 2 * lh;
-            const _Float16 *xb = xfrag + (s & 1) * PF_MT * PF_LD;
+        };
+        // chunk s: weights of chunk s + 2 into wn (ring of three named
+        // slots, so the loop need not be unrolled to keep them in
+        // registers), activations of chunk s + 2 into registers after
+        // staging chunk s + 1's into LDS.  Chunks past the end reload the
+        // last one and skip the work.  Every path through a chunk issues the
+        // same global loads (the compiler merges wait counts over paths, and
+        // a path with fewer loads would make it wait for the prefetches too).
+        auto chunk = [&](int s, const Q4Pair &wc, Q4Pair &wn) {
+            wload(wn, min(s + 2, NS - 1));
+            if (s == NS - 2 && tid == 0) nxt = atomicAdd(ntiles + 1 + MODE, 1) + (int)gridDim.x;
+            if (s < NS) {
+                const int j0 = 4 * (s & 1) + 2 * lh;
+                const _Float16 *xb = xfrag + (s & 1) * PF_MT * PF_LD;
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                f16x8 a[4];
-                q4pair_frags(wc, j0, u, a);
-                mma(a, xb, u);
+                for (int u = 0; u < 2; u++) {
+                    f16x8 a[4];
+                    q4pair_frags(wc, j0, u, a);
+                    mma(a, xb, u);
+                }
+                // buffer last read in chunk s - 1, before the previous barrier
+                if (s + 1 < NS) xstore((s + 1) & 1);
             }
-            // buffer last read in chunk s - 1, before the previous barrier
-            if (s + 1 < NS) xstore((s + 1) & 1);
+            xload(min(s + 2, NS - 1));
+            if (s < NS) __syncthreads();
+        };
+        for (int s = 0; s < NS; s += 3) {
+            chunk(s, w0, w2);
+            chunk(s + 1, w1, w0);
+            chunk(s + 2, w2, w1);
         }
-        xload(min(s + 2, NS - 1));
-        if (s < NS) __syncthreads();
-    };
-    for (int s = 0; s < NS; s += 3) {
-        chunk(s, w0, w2);
-        chunk(s + 1, w1, w0);
-        chunk(s + 2, w2, w1);
-    }
-    // accumulator register r of lane l: row 8(r/4) + 4(l/32) + r%4 of the
-    // wave's 32, pair 32t + l%32 of the tile
+        // accumulator register r of lane l: row 8(r/4) + 4(l/32) + r%4 of
+        // the wave's 32, pair 32t + l%32 of the tile
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int pr = 32 * t + li;
-        if (t < nsub && pr < tl.n) {
-            const int p = po_s[pr];
-            const float sc = sc_s[pr];
-            if (MODE == 0) {
+        for (int t = 0; t < NSUB; t++) {
+            const int pr = 32 * t + li;
+            if (pr < tl.n) {
+                const int p = po_s[pr];
+                const float sc = sc_s[pr];
+                if (MODE == 0) {
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    float a[4];
+                    for (int h = 0; h < 2; h++) {
+                        float a[4];
 #pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        const int r = 4 * h + c;
-                        const float g = acc[t][r] * sc, u = acc[t][r + 8] * sc;
-                        a[c] = g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+                        for (int c = 0; c < 4; c++) {
+                            const int r = 4 * h + c;
+                            const float g = acc[t][r] * sc, u = acc[t][r + 8] * sc;
+                            a[c] = g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+                        }
+                        const int col = cb * PF_COLS + 16 * wave + 8 * h + 4 * lh;
+                        *reinterpret_cast<float4 *>(out + (long long)p * F + col) = make_float4(a[0], a[1], a[2], a[3]);
                     }
-                    const int col = cb * PF_COLS + 16 * wave + 8 * h + 4 * lh;
-                    *reinterpret_cast<float4 *>(out + (long long)p * F + col) = make_float4(a[0], a[1], a[2], a[3]);
-                }
-            } else {
+                } else {
 #pragma unroll
-                for (int h = 0; h < 4; h++) {
-                    const int row = cb * PF_ROWS + 32 * wave + 8 * h + 4 * lh;
-                    *reinterpret_cast<float4 *>(out + (long long)p * H + row) =
-                        make_float4(acc[t][4 * h] * sc, acc[t][4 * h + 1] * sc, acc[t][4 * h + 2] * sc,
-                                    acc[t][4 * h + 3] * sc);
+                    for (int h = 0; h < 4; h++) {
+                        const int row = cb * PF_ROWS + 32 * wave + 8 * h + 4 * lh;
+                        *reinterpret_cast<float4 *>(out + (long long)p * H + row) =
+                            make_float4(acc[t][4 * h] * sc, acc[t][4 * h + 1] * sc, acc[t][4 * h + 2] * sc,
+                                        acc[t][4 * h + 3] * sc);
+                    }
                 }
             }
         }
+    };
+    switch ((tl.n + 31) / 32) {
+    case 1: body(PfSub<1>{}); break;
+    case 2: body(PfSub<2>{}); break;
+    case 3: body(PfSub<3>{}); break;
+    default: body(PfSub<4>{}); break;
     }
     // the next item rewrites the activation buffers and the pair lists
+    if (tid == 0) next_item = nxt;
     __syncthreads();
+    item = next_item;
     }
 }
 
@@ -765,7 +796,7 @@ static unsigned pf_grid(unsigned max_items) {
 template <int MODE>
 static hipError_t launch_moe_f16(int ns, unsigned nwg, hipStream_t st, const uint8_t *W0, const uint8_t *W1,
                                  const _Float16 *X, int x_rows, const float *xinv, const int *tpair, const int *ttok,
-                                 const PfTile *tiles, const int *ntiles, int ncb, int H, int F, float *out) {
+                                 const PfTile *tiles, int *ntiles, int ncb, int H, int F, float *out) {
     // more than 64 KiB of dynamic LDS is opted into once per kernel
 #define TBQ_NS(N)                                                                                                  \
     case N: {                                                                                                      \
