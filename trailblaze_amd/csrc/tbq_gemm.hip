@@ -107,9 +107,9 @@ typedef _Float16 hg_f16x2 __attribute__((ext_vector_type(2)));
 // The piece's fp16 weights in element order (weights 2i, 2i+1 are the low
 // and high nibbles of quant byte i).  A nibble q becomes the fp16 number
 // 1 + q/16 by placing it in the mantissa (0x3C00 | q << 6, both nibbles of
-// a byte from one 24-bit multiply, an AND and an OR), minus 1 (exact) gives
-// q/16, and one packed fp16 fma with (16 S, -M) gives S q - M: 2.5 VALU
-// per weight, with the fp16 roundings of 16 S, M and the result (16 d 63
+// a byte from one 24-bit multiply and one v_bitop3 (a & b) | c), minus 1
+// (exact) gives q/16, and one packed fp16 fma with (16 S, -M) gives S q - M:
+// 2 VALU per weight, with the fp16 roundings of 16 S, M and the result (16 d 63
 // must stay below 65504).  TBQ_HG_EXACT instead rounds fl(fl(S q) - M) once
 // from fp32, as k_dequant_f16_q4k does.
 __device__ __forceinline__ void q4sub_f16(const Q4Sub &r, int j, hg_f16x8 (&o)[HG_QD]) {
@@ -136,7 +136,7 @@ __device__ __forceinline__ void q4sub_f16(const Q4Sub &r, int j, hg_f16x8 (&o)[H
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 const unsigned y = (r.q[c] >> (8 * b)) & 0xFFu;
-                const unsigned t = (__umul24(y, 0x40040u) & 0x03C003C0u) | 0x3C003C00u;
+                const unsigned t = __builtin_amdgcn_bitop3_b32(__umul24(y, 0x40040u), 0x03C003C0u, 0x3C003C00u, 0xEA);   // (a & b) | c
                 const hg_f16x2 v = __builtin_bit_cast(hg_f16x2, t) - ONE;
                 w[b] = __builtin_bit_cast(unsigned, __builtin_elementwise_fma(v, S16, NM));
             }

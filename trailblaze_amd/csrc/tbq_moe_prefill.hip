@@ -33,7 +33,8 @@
 // Dequantisation to fp16.  A nibble q becomes the fp16 number 1 + q/16 by
 // placing q in the mantissa (0x3C00 | q << 6), for two weights per dword:
 // one 24-bit multiply spreads a quant byte's two nibbles into the two
-// halves, one AND and one OR mask them and set the exponent; v_pk_add_f16
+// halves, one three-input bit operation (v_bitop3, (a & b) | c) masks them
+// and sets the exponent; v_pk_add_f16
 // with -1 (exact) gives q/16, and v_pk_fma_f16 with (16 S, -M) gives S q - M
 // with only the fp16 roundings of 16 S, M and the result.
 //
@@ -59,6 +60,9 @@ constexpr int PF_LD = PF_KC + 8;   // LDS row stride in halves (padding breaks b
 #define PF_WAVES 8
 #endif
 constexpr int PF_THREADS = 64 * PF_WAVES;   // 32 weight rows per wave
+#ifndef PF_WDEPTH
+#define PF_WDEPTH 2   // chunks of weights in flight ahead of the one in use (2 or 3)
+#endif
 constexpr int PF_ROWS = 32 * PF_WAVES;      // weight rows per workgroup
 constexpr int PF_COLS = PF_ROWS / 2;        // gate/up columns per workgroup
 constexpr size_t PF_LDS_BYTES = (size_t)2 * PF_MT * PF_LD * 2 + PF_MT * 8;   // two activation tiles, pair ids, scales
@@ -246,7 +250,7 @@ __device__ __forceinline__ f16x8 q4dword_f16(unsigned q, f16x2 S16, f16x2 NM) {
     for (int b = 0; b < 4; b++) {
         // quant byte (hi << 4 | lo) -> halves (1 + lo/16, 1 + hi/16)
         const unsigned y = (q >> (8 * b)) & 0xFFu;
-        const unsigned t = (__umul24(y, 0x40040u) & 0x03C003C0u) | 0x3C003C00u;
+        const unsigned t = __builtin_amdgcn_bitop3_b32(__umul24(y, 0x40040u), 0x03C003C0u, 0x3C003C00u, 0xEA);   // (a & b) | c
         const f16x2 v = __builtin_bit_cast(f16x2, t) - ONE;
         o[b] = __builtin_bit_cast(unsigned, __builtin_elementwise_fma(v, S16, NM));
     }
@@ -321,9 +325,16 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
         wrow = W0 + ((long long)tl.e * H + cb * PF_ROWS + 32 * wave + li) * rb;
     }
     auto wload = [&](Q4Pair &w, int s) { q4pair_load(wrow + (long long)(s >> 1) * 144, 4 * (s & 1) + 2 * lh, w); };
+#if PF_WDEPTH == 3
+    Q4Pair w0, w1, w2, w3;
+    wload(w0, 0);
+    wload(w1, min(1, NS - 1));
+    wload(w2, min(2, NS - 1));
+#else
     Q4Pair w0, w1, w2;
     wload(w0, 0);
     wload(w1, min(1, NS - 1));
+#endif
 
     // the tile's pair ids and activation-row scales, for the epilogue, in
     // LDS behind the two activation buffers
@@ -398,7 +409,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
         // same global loads (the compiler merges wait counts over paths, and
         // a path with fewer loads would make it wait for the prefetches too).
         auto chunk = [&](int s, const Q4Pair &wc, Q4Pair &wn) {
-            wload(wn, min(s + 2, NS - 1));
+            wload(wn, min(s + PF_WDEPTH, NS - 1));
             if (s == NS - 2 && tid == 0) nxt = atomicAdd(ntiles + 1 + MODE, 1) + (int)gridDim.x;
             if (s < NS) {
                 const int j0 = 4 * (s & 1) + 2 * lh;
@@ -415,11 +426,20 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
             xload(min(s + 2, NS - 1));
             if (s < NS) __syncthreads();
         };
+#if PF_WDEPTH == 3
+        for (int s = 0; s < NS; s += 4) {
+            chunk(s, w0, w3);
+            chunk(s + 1, w1, w0);
+            chunk(s + 2, w2, w1);
+            chunk(s + 3, w3, w2);
+        }
+#else
         for (int s = 0; s < NS; s += 3) {
             chunk(s, w0, w2);
             chunk(s + 1, w1, w0);
             chunk(s + 2, w2, w1);
         }
+#endif
         // accumulator register r of lane l: row 8(r/4) + 4(l/32) + r%4 of
         // the wave's 32, pair 32t + l%32 of the tile
 #pragma unroll
