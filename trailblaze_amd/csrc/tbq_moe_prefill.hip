@@ -218,21 +218,23 @@ __global__ __launch_bounds__(256) void k_rows_f16(const float *__restrict__ in, 
 // ---------------------------------------------------------------------------
 // Weight staging.
 // ---------------------------------------------------------------------------
-// One lane's weights for a 128-column chunk: the 64 weights of sub-blocks
-// j0 and j0 + 1 of a row's Q4_K super-block (j0 even) and the three header
-// dwords they need: d/dmin, and the scale and min dwords of their half of the
-// super-block (bytes 4..11 for j0 < 4; bytes 12..19 for j0 >= 4, where the
-// mins are quant bytes 0..3, layer4/tb_gguf.c:163-168).
+// One lane's loads for a 128-column chunk: the 64 weights of sub-blocks j0
+// and j0 + 1 of a row's Q4_K super-block (j0 even), and 16 header bytes.
+// The header the two chunks of a super-block need is bytes 0..19: d/dmin
+// (0..3), the scale and min dwords of sub-blocks 0..3 (4..7, 8..11), the
+// scale dword of 4..7 (12..15) and their min dword (16..19, which are quant
+// bytes 0..3, layer4/tb_gguf.c:163-168).  The even chunk (j0 < 4) loads
+// bytes 0..15 and passes d/dmin and the scale dword of 4..7 on to the odd
+// chunk, which loads bytes 16..31 for the min dword: one 16-byte load per
+// chunk instead of a dword and a dword pair (weight loads are issued per
+// lane, each to its own row's cache lines, and their count is what the
+// memory pipeline pays for).
 struct Q4Pair {
-    unsigned dd, sw, mw;
-    u32x4 q0, q1;
+    u32x4 h, q0, q1;
 };
 
 __device__ __forceinline__ void q4pair_load(const uint8_t *sb, int j0, Q4Pair &r) {
-    r.dd = *reinterpret_cast<const unsigned *>(sb);
-    const uint2 sm = *reinterpret_cast<const uint2 *>(sb + (j0 < 4 ? 4 : 12));
-    r.sw = sm.x;
-    r.mw = sm.y;
+    r.h = *reinterpret_cast<const u32x4 *>(sb + (j0 < 4 ? 0 : 16));
     r.q0 = *reinterpret_cast<const u32x4 *>(sb + 16 + 16 * j0);
     r.q1 = *reinterpret_cast<const u32x4 *>(sb + 32 + 16 * j0);
 }
@@ -259,9 +261,11 @@ __device__ __forceinline__ f16x8 q4dword_f16(unsigned q, f16x2 S16, f16x2 NM) {
 
 // The lane's four A operands of sub-block j0 + u (steps 4u .. 4u + 3 of the
 // chunk use its quant dwords 0..3).
-__device__ __forceinline__ void q4pair_frags(const Q4Pair &r, int j0, int u, f16x8 *a) {
+// dd = d/dmin, sw and mw = the scale and min dwords of j0's half.
+__device__ __forceinline__ void q4pair_frags(const Q4Pair &r, unsigned dd, unsigned sw, unsigned mw, int j0, int u,
+                                             f16x8 *a) {
     const int sh = 8 * ((j0 + u) & 3);
-    const float S = h2f(r.dd) * (float)((r.sw >> sh) & 63), Mn = h2f(r.dd >> 16) * (float)((r.mw >> sh) & 63);
+    const float S = h2f(dd) * (float)((sw >> sh) & 63), Mn = h2f(dd >> 16) * (float)((mw >> sh) & 63);
     const _Float16 s16 = (_Float16)(16.f * S), nm = (_Float16)(-Mn);
     const f16x2 S16 = {s16, s16}, NM = {nm, nm};
     const u32x4 q = u ? r.q1 : r.q0;
@@ -379,6 +383,9 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
     // this one (its latency hidden behind them), so items go to workgroups
     // in the order they finish work, heaviest items first
     int nxt = 0;
+    // d/dmin and the scale dword of sub-blocks 4..7, from the even chunk's
+    // header for the odd chunk of the same super-block
+    unsigned kdd = 0, ksw = 0;
     // The chunk loop and the epilogue for a compile-time count of 32-pair
     // sub-tiles (1..4, uniform over the workgroup): one copy per count, so
     // no branch splits a chunk's LDS reads from its MFMAs and the compiler
@@ -414,10 +421,14 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
             if (s < NS) {
                 const int j0 = 4 * (s & 1) + 2 * lh;
                 const _Float16 *xb = xfrag + (s & 1) * PF_MT * PF_LD;
+                const bool odd = s & 1;
+                const unsigned dd = odd ? kdd : wc.h.x, sw = odd ? ksw : wc.h.y, mw = odd ? wc.h.x : wc.h.z;
+                kdd = dd;
+                ksw = odd ? ksw : wc.h.w;
 #pragma unroll
                 for (int u = 0; u < 2; u++) {
                     f16x8 a[4];
-                    q4pair_frags(wc, j0, u, a);
+                    q4pair_frags(wc, dd, sw, mw, j0, u, a);
                     mma(a, xb, u);
                 }
                 // buffer last read in chunk s - 1, before the previous barrier
@@ -434,10 +445,21 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
             chunk(s + 3, w3, w2);
         }
 #else
-        for (int s = 0; s < NS; s += 3) {
-            chunk(s, w0, w2);
-            chunk(s + 1, w1, w0);
-            chunk(s + 2, w2, w1);
+        if constexpr (NS == 4) {
+            // two trips, not unrolled: unrolled, the compiler overlaps the
+            // trips past what the register file holds (spills)
+#pragma nounroll
+            for (int s = 0; s < NS; s += 3) {
+                chunk(s, w0, w2);
+                chunk(s + 1, w1, w0);
+                chunk(s + 2, w2, w1);
+            }
+        } else {
+            for (int s = 0; s < NS; s += 3) {
+                chunk(s, w0, w2);
+                chunk(s + 1, w1, w0);
+                chunk(s + 2, w2, w1);
+            }
         }
 #endif
         // accumulator register r of lane l: row 8(r/4) + 4(l/32) + r%4 of
