@@ -378,6 +378,23 @@ def test_moe_prefill_mfma_small_batches(oracle):
         assert rel_l2(out - resid, ref - resid) <= PREFILL_TOL
 
 
+@pytest.mark.parametrize("mode", ["BF16", "I8"])
+def test_moe_prefill_many_pairs(oracle, mode):
+    """More (token, slot) pairs than the dispatch keeps in LDS (8400 > 8192):
+    the permutation goes through global memory.  Routing exact for every
+    token; outputs checked on a sample (tokens are independent)."""
+    H, F, E, k, T = 512, 256, 8, 4, 2100
+    router, gate, up, down = synth.moe_layer(H, F, E, fm.Q4_K, seed=93)
+    rng = np.random.default_rng(94)
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    out, idx, w = gpu_moe(xn, resid, router, gate, up, down, F, k, fm.Q4_K, mode=getattr(tb, "TBQ_MOE_" + mode))
+    sample = np.sort(rng.choice(T, 48, replace=False))
+    ref, ridx, rw = oracle.moe(xn[sample], resid[sample], router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
+    assert np.array_equal(idx[sample], ridx)
+    assert rel_l2(out[sample] - resid[sample], ref - resid[sample]) <= PREFILL_TOL
+
+
 # ---------------------------------------------------------------------------
 # Prefill on int8 MFMA with Q8_K activations (TBQ_MOE_I8): routing exact,
 # outputs within 1e-2 rel-L2 (8-bit activations)

@@ -86,6 +86,10 @@ struct PfSub {
 // (= pair / k, the token).
 // ---------------------------------------------------------------------------
 constexpr int PF_MAX_TILES = 65536 * 8 / PF_MT + 256;
+// up to this many pairs, k_dispatch keeps the expert indices in registers
+// (read once) and the permutation in LDS: a permutation in global memory is
+// read back, after its own stores, by a loop of dependent round trips
+constexpr int PF_LDS_PAIRS = 8192;
 
 __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_idx, int T, int k, int E,
                                                    int *__restrict__ perm, PfTile *__restrict__ tiles,
@@ -95,15 +99,32 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
     __shared__ int hist[256], off[257], cur[256], scan[256];
     __shared__ int qcnt[NQ + 1], qbase[NQ + 2];
     __shared__ int t_e[PF_MAX_TILES], t_start[PF_MAX_TILES];
+    __shared__ int perm_s[PF_LDS_PAIRS];
+    constexpr int NE = PF_LDS_PAIRS / 1024;   // expert indices per thread
     const int tid = threadIdx.x, P = T * k;
+    const bool small = P <= PF_LDS_PAIRS;   // uniform
     if (tid < 256) { hist[tid] = 0; cur[tid] = 0; }
     if (tid <= NQ) qcnt[tid] = 0;
+    int es[NE];
+    if (small) {
+#pragma unroll
+        for (int m = 0; m < NE; m++) {
+            const int p = tid + 1024 * m;
+            es[m] = p < P ? sel_idx[(p / k) * 8 + p % k] : -1;
+        }
+    }
     __syncthreads();
     // a pair whose expert index is outside [0, E) (never produced by the
     // router) joins no tile; the combine skips its slot
-    for (int p = tid; p < P; p += 1024) {
-        const int e = sel_idx[(p / k) * 8 + p % k];
-        if ((unsigned)e < (unsigned)E) atomicAdd(&hist[e], 1);
+    if (small) {
+#pragma unroll
+        for (int m = 0; m < NE; m++)
+            if ((unsigned)es[m] < (unsigned)E) atomicAdd(&hist[es[m]], 1);
+    } else {
+        for (int p = tid; p < P; p += 1024) {
+            const int e = sel_idx[(p / k) * 8 + p % k];
+            if ((unsigned)e < (unsigned)E) atomicAdd(&hist[e], 1);
+        }
     }
     __syncthreads();
     // exclusive prefix sum of hist over 256 experts (Hillis-Steele in LDS);
@@ -146,9 +167,17 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
             t_start[t] = off[tid] + s0;
         }
     }
-    for (int p = tid; p < P; p += 1024) {
-        const int e = sel_idx[(p / k) * 8 + p % k];
-        if ((unsigned)e < (unsigned)E) perm[off[e] + atomicAdd(&cur[e], 1)] = p;
+    if (small) {
+#pragma unroll
+        for (int m = 0; m < NE; m++) {
+            const int e = es[m];
+            if ((unsigned)e < (unsigned)E) perm_s[off[e] + atomicAdd(&cur[e], 1)] = tid + 1024 * m;
+        }
+    } else {
+        for (int p = tid; p < P; p += 1024) {
+            const int e = sel_idx[(p / k) * 8 + p % k];
+            if ((unsigned)e < (unsigned)E) perm[off[e] + atomicAdd(&cur[e], 1)] = p;
+        }
     }
     __syncthreads();
     const int nt = qbase[0];
@@ -156,7 +185,7 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
         const int t = i / PF_MT, j = i % PF_MT, e = t_e[t];
         const int n = min(PF_MT, off[e + 1] - t_start[t]);
         if (j == 0) tiles[t] = PfTile{e, n};
-        const int p = j < n ? perm[t_start[t] + j] : -1;
+        const int p = j < n ? (small ? perm_s[t_start[t] + j] : perm[t_start[t] + j]) : -1;
         tpair[i] = p;
         ttok[i] = p >= 0 ? p / k : -1;
     }
