@@ -121,6 +121,10 @@ struct GMem {
     static __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 #endif
     static __device__ __forceinline__ uint32_t ld16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
+    // 12 bytes at a 4-byte-aligned address, one dwordx3 load
+    static __device__ __forceinline__ void ld96(const uint8_t *p, uint32_t *out) {
+        __builtin_memcpy(out, __builtin_assume_aligned(p, 4), 12);
+    }
     template <int N>
     static __device__ __forceinline__ void ldw(const uint8_t *p, uint32_t *out) { ld_dw<N>(p, out); }
 };
@@ -380,19 +384,28 @@ template <> struct KqFmt<QT_Q2_K> {
 template <> struct KqFmt<QT_Q3_K> {
     static constexpr bool PAIR = true;
     struct Unit { uint4 qs; uint2 hm; uint32_t lo; uint2 hi; };
-    // 110-byte blocks: every other block starts 2 mod 4, so runs go through
-    // ld_dw; d is a naturally aligned 16-bit load
+    // 110-byte blocks: every other block starts 2 mod 4 (sh = 2).  Five
+    // loads per unit, none past the block: the 16 quant bytes through ld_dw
+    // (two); the 8 hmask bytes as one dwordx3 from the aligned-down address;
+    // bytes 92 + sh .. 108 + sh (a 16-byte window, aligned, ending at or
+    // before the block's end) for sc[0..3] and sc[8..11], plus d as a 16-bit
+    // load (for sh = 2 the window holds d as well; the load is issued either
+    // way, so every lane issues the same loads).
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
         const uint8_t *b = row + (size_t)(u >> 2) * 110;
         const int p = u & 3;
+        const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(b) & 3u);
         uint32_t t[4];
         GMem::template ldw<4>(b + 32 + 16 * p, t);
         w.qs = make_uint4(t[0], t[1], t[2], t[3]);
-        GMem::template ldw<2>(b + 8 * p, t);
-        w.hm = make_uint2(t[0], t[1]);
-        GMem::template ldw<1>(b + 96, &w.lo);                 // sc[0..3]
-        GMem::template ldw<1>(b + 104, &w.hi.x);              // sc[8..11]
-        w.hi.y = (uint32_t)GMem::ld16(b + 108) << 16; // d in the high half
+        uint32_t h[3];
+        GMem::ld96(b + 8 * p - sh, h);
+        w.hm = make_uint2(__builtin_amdgcn_alignbyte(h[1], h[0], sh), __builtin_amdgcn_alignbyte(h[2], h[1], sh));
+        const uint4 v = GMem::ld128(b + 92 + sh);
+        const uint32_t d16 = GMem::ld16(b + 108);
+        w.lo = sh ? __builtin_amdgcn_alignbyte(v.y, v.x, 2) : v.y;    // sc[0..3]
+        w.hi.x = sh ? __builtin_amdgcn_alignbyte(v.w, v.z, 2) : v.w;  // sc[8..11]
+        w.hi.y = (sh ? v.w >> 16 : d16) << 16;                         // d in the high half
     }
     static __device__ __forceinline__ float dot(const Unit &w, const KqX &x, int u) {
         const int p1 = u & 1;   // groups 4p..4p+3 use slots 4*(p&1)..+3
