@@ -96,7 +96,8 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
                                                    int *__restrict__ ntiles, int *__restrict__ tpair,
                                                    int *__restrict__ ttok) {
     constexpr int NQ = PF_MT / 32;   // sub-tile count classes 1..NQ
-    __shared__ int hist[256], off[257], cur[256], scan[256];
+    static_assert(PF_MT == 128 && NQ == 4, "tile classes");
+    __shared__ int hist[256], off[257], cur[256], wsum[4];
     __shared__ int qcnt[NQ + 1], qbase[NQ + 2];
     __shared__ int t_e[PF_MAX_TILES], t_start[PF_MAX_TILES];
     __shared__ int perm_s[PF_LDS_PAIRS];
@@ -127,21 +128,41 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
         }
     }
     __syncthreads();
-    // exclusive prefix sum of hist over 256 experts (Hillis-Steele in LDS);
-    // tiles counted per sub-tile class
-    if (tid < 256) scan[tid] = tid < E ? hist[tid] : 0;
-    if (tid < E) {
-        const int n = hist[tid];
-        for (int s0 = 0; s0 < n; s0 += PF_MT) atomicAdd(&qcnt[(min(PF_MT, n - s0) + 31) / 32], 1);
+    // exclusive prefix sum of hist over 256 experts: a scan within each of
+    // the first four waves (shuffles, no barrier), then the wave totals.
+    // Tiles counted per sub-tile class: expert e has n >> 7 full tiles
+    // (class 4) and, if n % 128 > 0, one of class (n % 128 + 31) / 32;
+    // per wave by ballot counts, one LDS atomic per wave and class.
+    int incl = 0;
+    if (tid < 256) {   // four whole waves
+        const int lane = tid & 63, n = hist[tid];   // 0 for experts >= E
+        incl = n;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += o;
+        }
+        if (lane == 63) wsum[tid >> 6] = incl;
+        const int rem = n & (PF_MT - 1), rq = (rem + 31) >> 5;   // 0 when rem = 0
+        int c4 = (n >> 7) + (rq == NQ ? 1 : 0);
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) c4 += __shfl_xor(c4, d, 64);
+        int cq[NQ + 1];
+#pragma unroll
+        for (int q = 1; q < NQ; q++) cq[q] = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(rq == q));
+        cq[NQ] = c4;
+        if (lane == 0) {
+#pragma unroll
+            for (int q = 1; q <= NQ; q++)
+                if (cq[q]) atomicAdd(&qcnt[q], cq[q]);
+        }
     }
     __syncthreads();
-    for (int d = 1; d < 256; d <<= 1) {
-        const int v = tid < 256 && tid >= d ? scan[tid - d] : 0;
-        __syncthreads();
-        if (tid < 256) scan[tid] += v;
-        __syncthreads();
+    if (tid < 256) {
+        int add = 0;
+        for (int w = 0; w < (tid >> 6); w++) add += wsum[w];
+        off[tid + 1] = incl + add;
     }
-    if (tid < 256) off[tid + 1] = scan[tid];
     if (tid == 0) {
         off[0] = 0;
         // classes NQ (heaviest) first
@@ -163,7 +184,7 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
         for (int s0 = 0; s0 < n; s0 += PF_MT) {
             const int q = (min(PF_MT, n - s0) + 31) / 32;
             const int t = qbase[q] + atomicAdd(&qcnt[q], 1);
-            t_e[t] = tid;
+            t_e[t] = tid | min(PF_MT, n - s0) << 16;   // expert | pairs in the tile
             t_start[t] = off[tid] + s0;
         }
     }
@@ -181,11 +202,13 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int *__restrict__ sel_i
     }
     __syncthreads();
     const int nt = qbase[0];
+    // the tile's record and first pair are two independent LDS reads
+#pragma unroll 4
     for (int i = tid; i < nt * PF_MT; i += 1024) {
-        const int t = i / PF_MT, j = i % PF_MT, e = t_e[t];
-        const int n = min(PF_MT, off[e + 1] - t_start[t]);
+        const int t = i >> 7, j = i & (PF_MT - 1), te = t_e[t], st = t_start[t];
+        const int e = te & 0xFFFF, n = te >> 16;
         if (j == 0) tiles[t] = PfTile{e, n};
-        const int p = j < n ? (small ? perm_s[t_start[t] + j] : perm[t_start[t] + j]) : -1;
+        const int p = j < n ? (small ? perm_s[st + j] : perm[st + j]) : -1;
         tpair[i] = p;
         ttok[i] = p >= 0 ? p / k : -1;
     }
