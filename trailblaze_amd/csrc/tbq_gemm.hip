@@ -107,10 +107,11 @@ typedef _Float16 hg_f16x2 __attribute__((ext_vector_type(2)));
 // The piece's fp16 weights in element order (weights 2i, 2i+1 are the low
 // and high nibbles of quant byte i).  A nibble q becomes the fp16 number
 // 1 + q/16 by placing it in the mantissa (0x3C00 | q << 6, both nibbles of
-// a byte from one 24-bit multiply and one v_bitop3 (a & b) | c), minus 1
-// (exact) gives q/16, and one packed fp16 fma with (16 S, -M) gives S q - M:
-// 2 VALU per weight, with the fp16 roundings of 16 S, M and the result (16 d 63
-// must stay below 65504).  TBQ_HG_EXACT instead rounds fl(fl(S q) - M) once
+// a byte from one 24-bit multiply and one v_bitop3 (a & b) | c), and one
+// packed fp16 fma with (16 S, C = -16 S - M) gives 16 S (1 + q/16) + C =
+// S q - M (exact before its one rounding): 1.5 VALU per weight, with the
+// fp16 roundings of 16 S, C and the result (16 d 63 + dmin 63 must stay
+// below 65504).  TBQ_HG_EXACT instead rounds fl(fl(S q) - M) once
 // from fp32, as k_dequant_f16_q4k does.
 __device__ __forceinline__ void q4sub_f16(const Q4Sub &r, int j, hg_f16x8 (&o)[HG_QD]) {
     const int jb = 8 * (j & 3);
@@ -127,9 +128,8 @@ __device__ __forceinline__ void q4sub_f16(const Q4Sub &r, int j, hg_f16x8 (&o)[H
             }
         }
     } else {
-        const hg_f16x2 ONE = {(_Float16)1.f, (_Float16)1.f};
-        const _Float16 s16 = (_Float16)(16.f * S), nm = (_Float16)(-Mn);
-        const hg_f16x2 S16 = {s16, s16}, NM = {nm, nm};
+        const _Float16 s16 = (_Float16)(16.f * S), cc = (_Float16)(-(float)s16 - Mn);
+        const hg_f16x2 S16 = {s16, s16}, C = {cc, cc};
 #pragma unroll
         for (int c = 0; c < HG_QD; c++) {
             unsigned w[4];
@@ -137,8 +137,7 @@ __device__ __forceinline__ void q4sub_f16(const Q4Sub &r, int j, hg_f16x8 (&o)[H
             for (int b = 0; b < 4; b++) {
                 const unsigned y = (r.q[c] >> (8 * b)) & 0xFFu;
                 const unsigned t = __builtin_amdgcn_bitop3_b32(__umul24(y, 0x40040u), 0x03C003C0u, 0x3C003C00u, 0xEA);   // (a & b) | c
-                const hg_f16x2 v = __builtin_bit_cast(hg_f16x2, t) - ONE;
-                w[b] = __builtin_bit_cast(unsigned, __builtin_elementwise_fma(v, S16, NM));
+                w[b] = __builtin_bit_cast(unsigned, __builtin_elementwise_fma(__builtin_bit_cast(hg_f16x2, t), S16, C));
             }
             o[c] = __builtin_bit_cast(hg_f16x8, hg_u32x4{w[0], w[1], w[2], w[3]});
         }

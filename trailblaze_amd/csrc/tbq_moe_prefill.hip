@@ -34,13 +34,15 @@
 // placing q in the mantissa (0x3C00 | q << 6), for two weights per dword:
 // one 24-bit multiply spreads a quant byte's two nibbles into the two
 // halves, one three-input bit operation (v_bitop3, (a & b) | c) masks them
-// and sets the exponent; v_pk_add_f16
-// with -1 (exact) gives q/16, and v_pk_fma_f16 with (16 S, -M) gives S q - M
-// with only the fp16 roundings of 16 S, M and the result.
+// and sets the exponent; one v_pk_fma_f16 with (16 S, C = -16 S - M) gives
+// 16 S (1 + q/16) + C = S q - M: three VALU per two weights.  The fma's
+// product and sum are exact before its one rounding, so the fp16 roundings
+// are those of 16 S, of C (at most ulp(16 S + M) / 2, a per-sub-block
+// constant) and of the result.
 //
 // Accuracy: fp16 weights and activations (11-bit mantissa), fp32
 // accumulation; outputs land within 1e-2 relative L2 of the fp32 reference.
-// The weights' fp16 form needs 16 * d * 63 below 65504 (d < 64).
+// The weights' fp16 form needs 16 * 63 * d + 63 * dmin below 65504.
 #include "tbq_kernels.h"
 #include "tbq_kquant.hpp"
 
@@ -297,16 +299,14 @@ __device__ __forceinline__ float h2f(unsigned bits) {
 
 // Four quant bytes -> eight fp16 weights S q - Mn (low nibble first, the
 // reference's order), as one MFMA operand.
-__device__ __forceinline__ f16x8 q4dword_f16(unsigned q, f16x2 S16, f16x2 NM) {
-    const f16x2 ONE = {(_Float16)1.f, (_Float16)1.f};
+__device__ __forceinline__ f16x8 q4dword_f16(unsigned q, f16x2 S16, f16x2 C) {
     unsigned o[4];
 #pragma unroll
     for (int b = 0; b < 4; b++) {
         // quant byte (hi << 4 | lo) -> halves (1 + lo/16, 1 + hi/16)
         const unsigned y = (q >> (8 * b)) & 0xFFu;
         const unsigned t = __builtin_amdgcn_bitop3_b32(__umul24(y, 0x40040u), 0x03C003C0u, 0x3C003C00u, 0xEA);   // (a & b) | c
-        const f16x2 v = __builtin_bit_cast(f16x2, t) - ONE;
-        o[b] = __builtin_bit_cast(unsigned, __builtin_elementwise_fma(v, S16, NM));
+        o[b] = __builtin_bit_cast(unsigned, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, t), S16, C));
     }
     return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
@@ -318,13 +318,13 @@ __device__ __forceinline__ void q4pair_frags(const Q4Pair &r, unsigned dd, unsig
                                              f16x8 *a) {
     const int sh = 8 * ((j0 + u) & 3);
     const float S = h2f(dd) * (float)((sw >> sh) & 63), Mn = h2f(dd >> 16) * (float)((mw >> sh) & 63);
-    const _Float16 s16 = (_Float16)(16.f * S), nm = (_Float16)(-Mn);
-    const f16x2 S16 = {s16, s16}, NM = {nm, nm};
+    const _Float16 s16 = (_Float16)(16.f * S), c = (_Float16)(-(float)s16 - Mn);
+    const f16x2 S16 = {s16, s16}, C = {c, c};
     const u32x4 q = u ? r.q1 : r.q0;
-    a[0] = q4dword_f16(q.x, S16, NM);
-    a[1] = q4dword_f16(q.y, S16, NM);
-    a[2] = q4dword_f16(q.z, S16, NM);
-    a[3] = q4dword_f16(q.w, S16, NM);
+    a[0] = q4dword_f16(q.x, S16, C);
+    a[1] = q4dword_f16(q.y, S16, C);
+    a[2] = q4dword_f16(q.z, S16, C);
+    a[3] = q4dword_f16(q.w, S16, C);
 }
 
 // ---------------------------------------------------------------------------
