@@ -83,6 +83,20 @@ def test_ggml_matvec_kq(oracle, qt, M, K):
     assert rel_l2(got, oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
 
 
+@pytest.mark.parametrize("qt", [fm.Q6_K, G | fm.Q6_K])
+def test_matvec_q6k_tall(oracle, qt):
+    """Q6_K rows of 4096 above 65536 rows take their own launch shape
+    (8-wave workgroups, several per CU): a ragged row count, sampled rows."""
+    M, K = 70001, 4096
+    print("matvec tall", fm.NAMES[qt], M, K, flush=True)
+    rng = np.random.default_rng(qt + 5)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    y = gpu_matvec(W, qt, M, K, x, tb.TBQ_MV_KQ)
+    rows = np.sort(np.concatenate([rng.choice(M - 64, 2048, replace=False), np.arange(M - 64, M)]))
+    assert rel_l2(y[rows], oracle.matvec(np.ascontiguousarray(W[rows]), qt, len(rows), K, x)) <= MATVEC_TOL
+
+
 @pytest.mark.parametrize("qt", FORMATS + [G | fm.F16])
 @pytest.mark.parametrize("M,K", [(3, 256), (300, 4096)])
 def test_ggml_matvec_fma(oracle, qt, M, K):
