@@ -62,9 +62,6 @@ constexpr int PF_LD = PF_KC + 8;   // LDS row stride in halves (padding breaks b
 #define PF_WAVES 8
 #endif
 constexpr int PF_THREADS = 64 * PF_WAVES;   // 32 weight rows per wave
-#ifndef PF_WDEPTH
-#define PF_WDEPTH 2   // chunks of weights in flight ahead of the one in use (2 or 3)
-#endif
 constexpr int PF_ROWS = 32 * PF_WAVES;      // weight rows per workgroup
 constexpr int PF_COLS = PF_ROWS / 2;        // gate/up columns per workgroup
 constexpr size_t PF_LDS_BYTES = (size_t)2 * PF_MT * PF_LD * 2 + PF_MT * 8;   // two activation tiles, pair ids, scales
@@ -381,16 +378,9 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
         wrow = W0 + ((long long)tl.e * H + cb * PF_ROWS + 32 * wave + li) * rb;
     }
     auto wload = [&](Q4Pair &w, int s) { q4pair_load(wrow + (long long)(s >> 1) * 144, 4 * (s & 1) + 2 * lh, w); };
-#if PF_WDEPTH == 3
-    Q4Pair w0, w1, w2, w3;
-    wload(w0, 0);
-    wload(w1, min(1, NS - 1));
-    wload(w2, min(2, NS - 1));
-#else
     Q4Pair w0, w1, w2;
     wload(w0, 0);
     wload(w1, min(1, NS - 1));
-#endif
 
     // the tile's pair ids and activation-row scales, for the epilogue, in
     // LDS behind the two activation buffers
@@ -468,7 +458,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
         // same global loads (the compiler merges wait counts over paths, and
         // a path with fewer loads would make it wait for the prefetches too).
         auto chunk = [&](int s, const Q4Pair &wc, Q4Pair &wn) {
-            wload(wn, min(s + PF_WDEPTH, NS - 1));
+            wload(wn, min(s + 2, NS - 1));
             if (s == NS - 2 && tid == 0) nxt = atomicAdd(ntiles + 1 + MODE, 1) + (int)gridDim.x;
             if (s < NS) {
                 const int j0 = 4 * (s & 1) + 2 * lh;
@@ -489,14 +479,6 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
             xload(min(s + 2, NS - 1));
             if (s < NS) __syncthreads();
         };
-#if PF_WDEPTH == 3
-        for (int s = 0; s < NS; s += 4) {
-            chunk(s, w0, w3);
-            chunk(s + 1, w1, w0);
-            chunk(s + 2, w2, w1);
-            chunk(s + 3, w3, w2);
-        }
-#else
         if constexpr (NS == 4) {
             // two trips, not unrolled: unrolled, the compiler overlaps the
             // trips past what the register file holds (spills)
@@ -513,7 +495,6 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
                 chunk(s + 2, w2, w1);
             }
         }
-#endif
         // accumulator register r of lane l: row 8(r/4) + 4(l/32) + r%4 of
         // the wave's 32, pair 32t + l%32 of the tile
 #pragma unroll
