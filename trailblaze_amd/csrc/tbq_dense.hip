@@ -43,7 +43,6 @@ constexpr int ATT_CH = TBQ_ATT_CH;   // positions per attention workgroup
 #define TBQ_ATT_THREADS 512
 #endif
 constexpr int ATT_THREADS = TBQ_ATT_THREADS;
-constexpr int ATT_PARTS = ATT_THREADS / ATT_CH;   // threads per position in the score phase
 
 // Block-wide sum of one float per thread (blockDim.x a multiple of 64,
 // <= 1024); every thread gets the result.
@@ -92,40 +91,134 @@ __global__ __launch_bounds__(64) void k_rope_table(int pos, float theta, int D, 
     }
 }
 
-// RMSNorm with the head's norm weights then rotate-half RoPE (table rc) of
-// one head vector held by one wave: lane l has elements l and l + 64
-// (D = 128) or l (D = 64).
+// Inputs of head_norm_rope for one head vector held by one wave: lane l
+// has elements l and l + 64 (D = 128) or l (D = 64), their norm weights and
+// the cos / sin of its rotation pair.  Loading them apart from the
+// arithmetic lets a kernel issue these loads ahead of larger ones.
 template <int D>
-__device__ __forceinline__ void head_norm_rope(float (&x)[D / 64], const float *__restrict__ w,
-                                               const float *__restrict__ rc, float eps) {
+struct HeadIn {
+    float x[D / 64], w[D / 64], cs, sn;
+};
+
+template <int D>
+__device__ __forceinline__ void head_load(HeadIn<D> &h, const float *__restrict__ x, const float *__restrict__ w,
+                                          const float *__restrict__ rc) {
+    const int lane = threadIdx.x & 63, j = lane % (D / 2);
+#pragma unroll
+    for (int i = 0; i < D / 64; i++) {
+        h.x[i] = x[lane + 64 * i];
+        h.w[i] = w[lane + 64 * i];
+    }
+    h.cs = rc[j];
+    h.sn = rc[D / 2 + j];
+}
+
+// RMSNorm with the head's norm weights then rotate-half RoPE (table rc),
+// in place on h.x.
+template <int D>
+__device__ __forceinline__ void head_norm_rope(HeadIn<D> &h, float eps) {
     const int lane = threadIdx.x & 63;
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < D / 64; i++) ss += x[i] * x[i];
+    for (int i = 0; i < D / 64; i++) ss += h.x[i] * h.x[i];
     ss = group_sum<64>(ss);
     const float r = 1.0f / sqrtf(ss / (float)D + eps);
 #pragma unroll
-    for (int i = 0; i < D / 64; i++) x[i] = x[i] * r * w[lane + 64 * i];
-    const int j = lane % (D / 2);   // pair (j, j + D/2)
-    const float cs = rc[j], sn = rc[D / 2 + j];
+    for (int i = 0; i < D / 64; i++) h.x[i] = h.x[i] * r * h.w[i];
     if constexpr (D == 128) {
-        const float a = x[0], b = x[1];   // elements j and j + 64
-        x[0] = a * cs - b * sn;
-        x[1] = a * sn + b * cs;
+        const float a = h.x[0], b = h.x[1];   // elements j and j + 64
+        h.x[0] = a * h.cs - b * h.sn;
+        h.x[1] = a * h.sn + b * h.cs;
     } else {
-        const float other = __shfl_xor(x[0], 32);   // partner j +- 32
-        x[0] = lane < 32 ? x[0] * cs - other * sn : other * sn + x[0] * cs;
+        const float other = __shfl_xor(h.x[0], 32);   // partner j +- 32
+        h.x[0] = lane < 32 ? h.x[0] * h.cs - other * h.sn : other * h.sn + h.x[0] * h.cs;
     }
+}
+
+constexpr int ilog2c(int n) { return n <= 1 ? 0 : 1 + ilog2c(n / 2); }
+
+constexpr int DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;   // row_ror:4 / row_ror:8 (xor 8)
+
+// The DPP exchange that pairs lanes differing in lane bit B (B <= 3) within
+// a row of 16: xor 8 (row_ror:8), i <-> 7-i (half mirror), xor 2, xor 1.
+template <int B>
+__device__ __forceinline__ float xrow_dpp(float v) {
+    if constexpr (B == 3) return dpp_f32<DPP_ROR8>(v);
+    else if constexpr (B == 2) return dpp_f32<DPP_HALF_MIRROR>(v);
+    else if constexpr (B == 1) return dpp_f32<DPP_QXOR2>(v);
+    else return dpp_f32<DPP_QXOR1>(v);
+}
+
+// Transposing sum over the lanes of an aligned group of 2^(B+1) lanes, lane
+// bits B..0 in turn.  With C > 1 values left a step pairs the lanes that
+// differ in bit B: the lane with the bit clear keeps the sums of values
+// 0..C/2-1, its partner those of C/2..C-1, so one exchange serves two
+// values.  With one value left a step is a plain sum over the pair.  At the
+// end lane l of the group holds in a[0..] the sums of values
+// (l >> S) * C' + j, j < C' = max(1, N / 2^(B+1)), where S = log2 of the
+// number of lanes that share each value.
+template <int B, int C, int N>
+__device__ __forceinline__ void group_xsum(float (&a)[N], int lane) {
+    if constexpr (C >= 2) {
+        const bool hi = (lane >> B) & 1;
+#pragma unroll
+        for (int j = 0; j < C / 2; j++) {
+            const float x = a[j], y = a[j + C / 2];
+            if constexpr (B == 4) {   // rows of 16 lanes 0 <-> 1, 2 <-> 3
+                const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x),
+                                                                __builtin_bit_cast(uint32_t, y), false, false);
+                const uint32_t r0 = r[0], r1 = r[1];
+                a[j] = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+            } else {
+                a[j] = (hi ? y : x) + xrow_dpp<B>(hi ? x : y);
+            }
+        }
+    } else {
+        if constexpr (B == 4) a[0] = swap16_sum(a[0]);
+        else a[0] += xrow_dpp<B>(a[0]);
+    }
+    if constexpr (B > 0) group_xsum<B - 1, (C >= 2 ? C / 2 : 1), N>(a, lane);
+}
+
+// Max / sum over the 16 lanes of the wave that agree in lane bits 0 and 1;
+// every lane gets it.
+__device__ __forceinline__ float wave_max_hi4(float v) {
+    v = fmaxf(v, dpp_f32<DPP_ROR4>(v));
+    v = fmaxf(v, dpp_f32<DPP_ROR8>(v));
+    v = swap16_max(v);
+    return swap32_max(v);
+}
+__device__ __forceinline__ float wave_sum_hi4(float v) {
+    v += dpp_f32<DPP_ROR4>(v);
+    v += dpp_f32<DPP_ROR8>(v);
+    v = swap16_sum(v);
+    return swap32_sum(v);
 }
 
 // Attention for one kv head x one chunk of ATT_CH positions, all G query
 // heads of the head, with the head's QK-norm, RoPE and cache append folded
-// in.  The chunk's K and V rows are loaded first (coalesced, all in flight
-// at once) and staged in LDS; meanwhile each wave normalises and rotates its
-// query heads from qkv.  The chunk that holds `pos` also forms the new K row
-// (norm + RoPE) and V row, uses them in place of the cache's and writes them
-// to the cache.  Writes part[(qh * nsplit + chunk) * (D + 2) + {0..D-1, D:
-// max, D+1: denominator}].  grid = (NKV, nsplit), 256 threads.
+// in.  The chunk's K and V rows stay in registers: thread (row group
+// R = tid / (D/4), column c = tid % (D/4)) loads dims 4c..4c+3 of rows
+// R + RS*i, i < NL (RS = ATT_THREADS / (D/4)).  The query rows, norm weights
+// and RoPE pairs are loaded before the chunk, so they land first; the waves
+// normalise and rotate the query heads into LDS while K and V are in flight,
+// and the scores start as the K rows land.
+//   scores   each thread forms the NL x G partial dot products of its
+//            columns; a transposing sum over the D/4 lanes of the row group
+//            leaves every lane with whole scores;
+//   softmax  max and sum per wave and head over the 16 lanes that hold the
+//            head (lane bits 2..5); the weights go through a wave-private
+//            LDS slot to every lane of the row group;
+//   V        each thread sums weight x V over its rows and columns;
+//   merge    after one barrier, thread (head, dim) rescales the waves'
+//            partial sums to the chunk's max.
+// The chunk that holds `pos` also forms the new K row (norm + RoPE) and V
+// row, uses them in place of the cache's and writes them to the cache.
+// Rows past pos are loaded from row pos, then take the new row (the cache
+// row may hold anything, and a zero weight would not cancel a NaN) and are
+// scored -inf.  Writes
+// part[(qh * nsplit + chunk) * (D + 2) + {0..D-1, D: max, D+1: denominator}].
+// grid = (NKV, nsplit), ATT_THREADS threads.
 template <int D, int G>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_partial(const float *__restrict__ qkv, const float *__restrict__ qn,
                                                               const float *__restrict__ kn, int NQ, int pos,
@@ -133,147 +226,149 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_partial(const float *__res
                                                               float *__restrict__ vc, int max_ctx, int nsplit,
                                                               float *__restrict__ part) {
     static_assert(D == 64 || D == 128, "head_dim");
-    constexpr int KLD = D + 4;                        // K row stride in LDS (conflict-free row reads)
-    constexpr int NL = ATT_CH * D / 4 / ATT_THREADS;  // float4 of K (and of V) per thread
-    extern __shared__ __attribute__((aligned(16))) float at_lds[];
-    float *Ks = at_lds;                      // [ATT_CH][KLD]
-    float *Vs = Ks + ATT_CH * KLD;           // [ATT_CH][D]
-    float *qs = Vs + ATT_CH * D;             // [G][D]
-    float *sc = qs + G * D;                  // [G][ATT_CH]
-    float *pd = sc + G * ATT_CH;             // [ATT_PARTS][G][ATT_CH]
+    constexpr int LR = D / 4, LB = ilog2c(LR), RS = ATT_THREADS / LR, NL = ATT_CH / RS;
+    constexpr int NW = ATT_THREADS / 64, RPW = 64 / LR, NV = NL * G, LG = ilog2c(G);
+    constexpr int CV = NV > LR ? NV / LR : 1;           // whole scores per lane
+    constexpr int SH = NV < LR ? LB - ilog2c(NV) : 0;   // low lane bits that share a score
+    static_assert(G <= NW && (1 << LG) == G, "one query head per wave, G a power of two");
+    static_assert(ATT_CH % RS == 0 && NV % 4 == 0, "chunk layout");
+    static_assert(LB - ilog2c(NL) == 2 && SH <= 2, "score positions sit in lane bits 2..5");
+    __shared__ __attribute__((aligned(16))) float qs[G * D];                 // scaled query heads
+    __shared__ __attribute__((aligned(16))) float nrow[2 * D];               // new K | V row
+    __shared__ __attribute__((aligned(16))) float pw[NW * RPW * NV];         // weights per row group
+    __shared__ __attribute__((aligned(16))) float os[NW * RPW * G * D];      // weighted V per row group
+    __shared__ float mw[NW * G], lw[NW * G];                                 // per wave max, sum
     const int kvh = blockIdx.x, ch = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int n_pos = pos + 1, p0 = ch * ATT_CH;
     const long long hbase = (long long)kvh * max_ctx * D;
-    // K and V rows of the chunk; rows past n_pos read row n_pos - 1 (weighed 0)
+    const bool own = pos >= p0 && pos < p0 + ATT_CH;   // this chunk holds the new row
+    const bool newrow = own && wave == NW - 1;
+    HeadIn<D> hq, hk;
+    float nv[D / 64];
+    if (wave < G) head_load<D>(hq, qkv + (kvh * G + wave) * D, qn, rc);
+    if (newrow) {
+        head_load<D>(hk, qkv + (NQ + kvh) * D, kn, rc);
+#pragma unroll
+        for (int i = 0; i < D / 64; i++) nv[i] = qkv[(NQ + (int)gridDim.x + kvh) * D + lane + 64 * i];
+    }
+    asm volatile("" ::: "memory");   // the small rows are issued first
+    const int R = tid >> LB, c4 = tid & (LR - 1);
     float4 kr[NL], vr[NL];
 #pragma unroll
     for (int i = 0; i < NL; i++) {
-        const int f = tid + ATT_THREADS * i, row = f / (D / 4), c4 = f % (D / 4);
-        const int pp = p0 + row < n_pos ? p0 + row : n_pos - 1;
+        const int pp = p0 + R + RS * i < n_pos ? p0 + R + RS * i : n_pos - 1;
         kr[i] = *reinterpret_cast<const float4 *>(kc + hbase + (long long)pp * D + 4 * c4);
-        vr[i] = *reinterpret_cast<const float4 *>(vc + hbase + (long long)pp * D + 4 * c4);
     }
-    // query heads (scaled by 1/sqrt(D)); wave w takes heads w, w + 4, ...
-    const float scale = 1.0f / sqrtf((float)D);
-    for (int g = wave; g < G; g += ATT_THREADS / 64) {
-        float x[D / 64];
-#pragma unroll
-        for (int i = 0; i < D / 64; i++) x[i] = qkv[(kvh * G + g) * D + lane + 64 * i];
-        head_norm_rope<D>(x, qn, rc, eps);
-#pragma unroll
-        for (int i = 0; i < D / 64; i++) qs[g * D + lane + 64 * i] = x[i] * scale;
-    }
-    const bool own = pos >= p0 && pos < p0 + ATT_CH;   // this chunk holds the new row
+    asm volatile("" ::: "memory");   // K ahead of V
 #pragma unroll
     for (int i = 0; i < NL; i++) {
-        const int f = tid + ATT_THREADS * i, row = f / (D / 4), c4 = f % (D / 4);
-        *reinterpret_cast<float4 *>(Ks + row * KLD + 4 * c4) = kr[i];
-        *reinterpret_cast<float4 *>(Vs + row * D + 4 * c4) = vr[i];
+        const int pp = p0 + R + RS * i < n_pos ? p0 + R + RS * i : n_pos - 1;
+        vr[i] = *reinterpret_cast<const float4 *>(vc + hbase + (long long)pp * D + 4 * c4);
     }
-    __syncthreads();
-    if (own && wave == 0) {
-        float x[D / 64], v[D / 64];
+    const float scale = 1.0f / sqrtf((float)D);
+    if (wave < G) {
+        head_norm_rope<D>(hq, eps);
+#pragma unroll
+        for (int i = 0; i < D / 64; i++) qs[wave * D + lane + 64 * i] = hq.x[i] * scale;
+    }
+    if (newrow) {
+        head_norm_rope<D>(hk, eps);
 #pragma unroll
         for (int i = 0; i < D / 64; i++) {
-            x[i] = qkv[(NQ + kvh) * D + lane + 64 * i];
-            v[i] = qkv[(NQ + (int)gridDim.x + kvh) * D + lane + 64 * i];
-        }
-        head_norm_rope<D>(x, kn, rc, eps);
-        const int row = pos - p0;
-#pragma unroll
-        for (int i = 0; i < D / 64; i++) {
-            Ks[row * KLD + lane + 64 * i] = x[i];
-            Vs[row * D + lane + 64 * i] = v[i];
-            kc[hbase + (long long)pos * D + lane + 64 * i] = x[i];
-            vc[hbase + (long long)pos * D + lane + 64 * i] = v[i];
+            nrow[lane + 64 * i] = hk.x[i];
+            nrow[D + lane + 64 * i] = nv[i];
+            kc[hbase + (long long)pos * D + lane + 64 * i] = hk.x[i];
+            vc[hbase + (long long)pos * D + lane + 64 * i] = nv[i];
         }
     }
-    __syncthreads();
-    // scores: thread = (position p, part of the dims), K row from LDS
-    {
-        constexpr int DP = D / ATT_PARTS;
-        const int p = tid % ATT_CH, half = tid / ATT_CH;
-        const float *krow = Ks + p * KLD + half * DP;
-        float acc[G];
+    // LDS-only barrier: the chunk's loads stay in flight across it
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    float4 qv[G];
 #pragma unroll
-        for (int g = 0; g < G; g++) acc[g] = 0.f;
+    for (int g = 0; g < G; g++) qv[g] = *reinterpret_cast<const float4 *>(qs + g * D + 4 * c4);
+    // rows pos.. of the chunk that holds pos take the new row (rows past pos
+    // are weighed 0, and the new row is finite where the stale cache may not be)
+    if (own) {
+        const float4 k4 = *reinterpret_cast<const float4 *>(nrow + 4 * c4);
 #pragma unroll
-        for (int c = 0; c < DP / 4; c++) {
-            const float4 k4 = *reinterpret_cast<const float4 *>(krow + 4 * c);
-            const int d = half * DP + 4 * c;
-#pragma unroll
-            for (int g = 0; g < G; g++)
-                acc[g] += qs[g * D + d] * k4.x + qs[g * D + d + 1] * k4.y + qs[g * D + d + 2] * k4.z +
-                          qs[g * D + d + 3] * k4.w;
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++) pd[(half * G + g) * ATT_CH + p] = acc[g];
+        for (int i = 0; i < NL; i++)
+            if (p0 + R + RS * i >= pos) kr[i] = k4;
     }
-    __syncthreads();
-    for (int i = tid; i < G * ATT_CH; i += ATT_THREADS) {
-        const int g = i / ATT_CH, p = i % ATT_CH;
-        float t = pd[g * ATT_CH + p];
+    // scores of (row R + RS*i, head g) at value index i*G + g
+    float a[NV];
 #pragma unroll
-        for (int q = 1; q < ATT_PARTS; q++) t += pd[(q * G + g) * ATT_CH + p];
-        sc[i] = p0 + p < n_pos ? t : -__builtin_huge_valf();
-    }
-    __syncthreads();
-    // per-head max and exp; wave w takes heads w, w + 4, ...
-    for (int g = wave; g < G; g += ATT_THREADS / 64) {
-        float m = -__builtin_huge_valf();
-        for (int p = lane; p < ATT_CH; p += 64) m = fmaxf(m, sc[g * ATT_CH + p]);
-        m = wave_max(m);
-        float l = 0.f;
-        for (int p = lane; p < ATT_CH; p += 64) {
-            const float e = expf(sc[g * ATT_CH + p] - m);   // exp(-inf) = 0 past n_pos
-            sc[g * ATT_CH + p] = e;
-            l += e;
-        }
-        l = group_sum<64>(l);
-        if (lane == 0) {
-            part[((long long)(kvh * G + g) * nsplit + ch) * (D + 2) + D] = m;
-            part[((long long)(kvh * G + g) * nsplit + ch) * (D + 2) + D + 1] = l;
+    for (int i = 0; i < NL; i++)
+#pragma unroll
+        for (int g = 0; g < G; g++)
+            a[i * G + g] = fmaf(qv[g].w, kr[i].w, fmaf(qv[g].z, kr[i].z, fmaf(qv[g].y, kr[i].y, qv[g].x * kr[i].x)));
+    group_xsum<LB - 1, NV, NV>(a, lane);
+    const int li = lane & (LR - 1), rg = lane >> LB;
+    float *pr = pw + (wave * RPW + rg) * NV;
+#pragma unroll
+    for (int j = 0; j < CV; j++) {
+        const int v = (li >> SH) * CV + j, i = v >> LG, g = v & (G - 1);
+        const bool valid = p0 + R + RS * i < n_pos;
+        const float s = valid ? a[j] : -__builtin_huge_valf();
+        const float m = wave_max_hi4(s);
+        const float e = valid ? expf(s - m) : 0.f;
+        pr[v] = e;
+        const float l = wave_sum_hi4(e);
+        if ((lane & 60) == 0) {
+            mw[wave * G + g] = m;
+            lw[wave * G + g] = l;
         }
     }
-    __syncthreads();
-    // weighted V from LDS: thread = (dim d, head group), 16 positions per
-    // step with independent reads; rows past n_pos hold stale cache data and
-    // are selected to 0 (a zero weight would not cancel a NaN)
-    constexpr int HG = ATT_THREADS / D;
-    constexpr int GJ = (G + HG - 1) / HG;
-    const int d = tid % D, hg = tid / D;
-    const int np = n_pos - p0 < ATT_CH ? n_pos - p0 : ATT_CH;
-    float o[GJ];
+    if (own) {
+        const float4 v4 = *reinterpret_cast<const float4 *>(nrow + D + 4 * c4);
 #pragma unroll
-    for (int j = 0; j < GJ; j++) o[j] = 0.f;
+        for (int i = 0; i < NL; i++)
+            if (p0 + R + RS * i >= pos) vr[i] = v4;
+    }
+    // weighted V; the weights were written by lanes of this wave (LDS keeps
+    // a wave's accesses in order)
+    float4 o[G];
 #pragma unroll
-    for (int pb = 0; pb < ATT_CH; pb += 16) {
-        if (pb < np) {   // uniform
-            float vv[16];
+    for (int i = 0; i < NL; i++) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) vv[i] = pb + i < np ? Vs[(pb + i) * D + d] : 0.f;
-#pragma unroll
-            for (int j = 0; j < GJ; j++) {
-                const int g = hg + HG * j < G ? hg + HG * j : G - 1;
-                const float4 *s4 = reinterpret_cast<const float4 *>(sc + g * ATT_CH + pb);
-#pragma unroll
-                for (int q4 = 0; q4 < 4; q4++) {
-                    const float4 w = s4[q4];
-                    o[j] += w.x * vv[4 * q4] + w.y * vv[4 * q4 + 1] + w.z * vv[4 * q4 + 2] + w.w * vv[4 * q4 + 3];
-                }
+        for (int g = 0; g < G; g++) {
+            const float w = pr[i * G + g];
+            if (i == 0) {
+                o[g] = make_float4(w * vr[0].x, w * vr[0].y, w * vr[0].z, w * vr[0].w);
+            } else {
+                o[g].x = fmaf(w, vr[i].x, o[g].x);
+                o[g].y = fmaf(w, vr[i].y, o[g].y);
+                o[g].z = fmaf(w, vr[i].z, o[g].z);
+                o[g].w = fmaf(w, vr[i].w, o[g].w);
             }
         }
     }
 #pragma unroll
-    for (int j = 0; j < GJ; j++) {
-        const int g = hg + HG * j;
-        if (g < G) part[((long long)(kvh * G + g) * nsplit + ch) * (D + 2) + d] = o[j];
+    for (int g = 0; g < G; g++) *reinterpret_cast<float4 *>(os + ((wave * RPW + rg) * G + g) * D + 4 * c4) = o[g];
+    __syncthreads();
+    for (int idx = tid; idx < G * D; idx += ATT_THREADS) {
+        const int g = idx / D, d = idx % D;
+        float M = -__builtin_huge_valf();
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, mw[w * G + g]);
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = expf(mw[w * G + g] - M);   // 0 for a wave with no row below n_pos
+            float t = 0.f;
+#pragma unroll
+            for (int r = 0; r < RPW; r++) t += os[((w * RPW + r) * G + g) * D + d];
+            num += f * t;
+            den += f * lw[w * G + g];
+        }
+        float *dst = part + ((long long)(kvh * G + g) * nsplit + ch) * (D + 2);
+        dst[d] = num;
+        if (d == 0) {
+            dst[D] = M;
+            dst[D + 1] = den;
+        }
     }
-}
-
-template <int D, int G>
-constexpr size_t attn_lds_bytes() {
-    return (size_t)4 * (ATT_CH * (D + 4) + ATT_CH * D + G * D + G * ATT_CH + ATT_PARTS * G * ATT_CH);
 }
 
 // out[h][d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c.  grid = NQ,
@@ -352,12 +447,8 @@ static hipError_t launch_attn(const float *qkv, const float *qn, const float *kn
                               const float *rc, float eps, float *kc, float *vc, int max_ctx, float *part, float *out,
                               hipStream_t st) {
     const int nsplit = (pos + 1 + ATT_CH - 1) / ATT_CH;
-    constexpr size_t lds = attn_lds_bytes<D, G>();
-    static const hipError_t attr = hipFuncSetAttribute((const void *)k_attn_partial<D, G>,
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((k_attn_partial<D, G>), dim3(NKV, nsplit), dim3(ATT_THREADS), lds, st, qkv, qn, kn, NQ, pos,
-                       rc, eps, kc, vc, max_ctx, nsplit, part);
+    hipLaunchKernelGGL((k_attn_partial<D, G>), dim3(NKV, nsplit), dim3(ATT_THREADS), 0, st, qkv, qn, kn, NQ, pos, rc,
+                       eps, kc, vc, max_ctx, nsplit, part);
     hipLaunchKernelGGL((k_attn_combine<D>), dim3(NQ), dim3(D), (size_t)2 * nsplit * 4, st, part, nsplit, out);
     return hipGetLastError();
 }
