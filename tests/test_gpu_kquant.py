@@ -146,6 +146,21 @@ def test_matvec_kq_kernel(oracle, qt, M, K):
 
 
 @pytest.mark.parametrize("qt", KQ_FORMATS)
+@pytest.mark.parametrize("M,K", [(5, 2560), (26, 2304), (777, 3072), (2000, 3840), (6144, 2560)])
+def test_matvec_kq_segmented_rows(oracle, qt, M, K):
+    """Rows of 36..60 units (K = 2304 .. 3840, Qwen3-4B's hidden 2560): the
+    segmented mapping, a workgroup's lanes over consecutive units of
+    consecutive rows, partial sums meeting in LDS; ragged last row block.
+    No single-row case: one output of a 2560-term sum can cancel by 10^3
+    (sum |w x| = 2740 for a result of 1.2), where the oracle's own fp32 sum
+    is already 1.3e-5 from the exact value."""
+    rng = np.random.default_rng(M * 11 + K + 5 * qt)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, qt, M, K, x, tb.TBQ_MV_KQ), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+
+
+@pytest.mark.parametrize("qt", KQ_FORMATS)
 @pytest.mark.parametrize("M,K", [(70, 17408), (129, 24576), (33, 32768)])
 def test_matvec_long_rows(oracle, qt, M, K):
     """Rows longer than 16384 weights (FFN-down of models with FFN 17408 ..

@@ -1087,6 +1087,78 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
     }
 }
 
+// Rows of U units with 32 < U < 64, U not a power of two (K = 2560:
+// U = 40), where a 64-lane row slice would leave 64 - U lanes idle.
+// Segmented mapping instead: workgroup lane L takes unit L % U of row slot
+// L / U, RB = NT / U rows per pass, so only NT % U lanes idle; a lane's unit
+// is fixed, so its digits stay in registers as in k_mv_kq.  Row blocks of RB
+// rows are dealt to the workgroups round-robin, the next block's weights in
+// flight while the current one is reduced.  The partial sums meet in LDS
+// (double-buffered by pass parity, one barrier per pass): 8 threads per
+// row slot add every 8th partial, then a DPP sum over the 8.
+template <int QT, int NW, int PRO, bool GLU>
+__global__ __launch_bounds__(NW * 64) void k_mv_kq_seg(const uint8_t *__restrict__ W, int M, int K, long long rb,
+                                                       const float *__restrict__ x, float *__restrict__ y,
+                                                       MvPro pro) {
+    using F = KqFmt<QT>;
+    constexpr int NT = NW * 64, RP = GLU ? 2 : 1;   // RP: weight rows per lane and pass
+    constexpr int MAXT = (16 * 64 + NT - 1) / NT;   // U < 64
+    extern __shared__ uint32_t smem[];
+    const int U = K / 64, RB = NT / U;
+    uint32_t *xd = smem;
+    float *gs = reinterpret_cast<float *>(smem + U * KQ_UNIT);
+    float *red = gs + 4 * U;   // [2][RP][NT]
+    const int L = threadIdx.x, slot = L / U, u = L % U;   // slot >= RB: idle lane
+    const int nblk = (M + RB - 1) / RB;
+    const int npass = (nblk - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;   // >= 1: grid <= nblk
+    auto block_row = [&](int pass) { return ((int)blockIdx.x + pass * (int)gridDim.x) * RB; };
+    // loads are unconditional: rows past M (and idle lanes' rows) re-read row
+    // M - 1, and their results are never read
+    typename F::Unit buf[2][RP];
+    auto load = [&](typename F::Unit *dst, int pass) {
+#pragma unroll
+        for (int p = 0; p < RP; p++) {
+            const int r = min(block_row(pass) + slot, M - 1) + (GLU ? p * M : 0);
+            F::load(W + (long long)r * rb, u, dst[p]);
+        }
+    };
+    KqStager<NT, F::PAIR, MAXT, PRO> xs;
+    xs.load(x, U, pro);
+    __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
+    load(buf[0], 0);
+    xs.apply(U, pro);
+    xs.store(U, xd, gs);
+    __syncthreads();
+    KqX xr;
+    kq_xload(xd, gs, u, xr);
+    const int rs = L >> 3, part = L & 7;   // reduction: 8 threads per row slot
+    for (int pass = 0; pass < npass; ++pass) {
+        load(buf[1], pass + 1);
+        float *rbuf = red + (pass & 1) * (RP * NT);
+#pragma unroll
+        for (int p = 0; p < RP; p++) rbuf[p * NT + L] = kq_dot<QT>(buf[0][p], xr, u);
+        __syncthreads();
+        float acc[RP];
+#pragma unroll
+        for (int p = 0; p < RP; p++) {
+            float t = 0.f;
+            if (rs < RB) {
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    if (part + 8 * j < U) t += rbuf[p * NT + rs * U + part + 8 * j];
+            }
+            acc[p] = group_sum<8>(t);
+        }
+        const int r = block_row(pass) + rs;
+        if (part == 0 && rs < RB && r < M) {
+            if constexpr (GLU) y[r] = pro_swiglu(acc[0], acc[1]);
+            else y[r] = acc[0];
+        }
+#pragma unroll
+        for (int p = 0; p < RP; p++) buf[0][p] = buf[1][p];
+    }
+}
+
 template <int QT, int LPR, int S, int G, int R, int D, int PRO, bool GLU>
 static hipError_t launch_kq(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int grid,
                             int rpw, const MvPro &pro) {
@@ -1105,6 +1177,26 @@ static hipError_t launch_kq(const void *W, int M, int K, const float *x, float *
     }
     hipLaunchKernelGGL((k_mv_kq<QT, LPR, S, G, R, D, PRO, GLU>), dim3(grid), dim3(S * G * 64), lds, st,
                        (const uint8_t *)W, M, K, rb, x, y, rpw, pro);
+    return hipGetLastError();
+}
+
+#ifndef KQ_SEG_NW
+#define KQ_SEG_NW 16
+#endif
+#ifndef KQ_SEG_WPC
+#define KQ_SEG_WPC 1
+#endif
+template <int QT, int NW, int PRO, bool GLU>
+static hipError_t launch_kq_seg(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu,
+                                const MvPro &pro) {
+    constexpr int NT = NW * 64, RP = GLU ? 2 : 1;
+    const int U = K / 64, RB = NT / U;
+    const long long nblk = ((long long)M + RB - 1) / RB, cap = (long long)n_cu * KQ_SEG_WPC;
+    const int grid = (int)(nblk < cap ? nblk : cap);
+    const long long rb = (long long)(K / block_weights(QT)) * block_bytes(QT);
+    const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (size_t)2 * RP * NT * 4;
+    hipLaunchKernelGGL((k_mv_kq_seg<QT, NW, PRO, GLU>), dim3(grid), dim3(NT), lds, st, (const uint8_t *)W, M, K, rb,
+                       x, y, pro);
     return hipGetLastError();
 }
 
@@ -1136,6 +1228,11 @@ static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float
     // (151936x4096: 99.5 against 106 us with one 16-wave workgroup per CU)
     if constexpr (QT == QT_Q6_K || QT == QT_GQ6_K)
         if (U == 64 && M > 65536) return launch_kq_shape<QT, 64, 1, 8, PRO, GLU, 4>(W, M, K, x, y, st, n_cu, pro);
+    // 32 < U < 64, not a power of two: the segmented row mapping (Q8_0
+    // keeps the row slice with two passes per iteration, 7.97 against
+    // 8.47 us at 9728x2560)
+    if constexpr (QT != QT_Q8_0 && QT != QT_GQ8_0)
+        if (U < 64 && (U & (U - 1)) != 0) return launch_kq_seg<QT, KQ_SEG_NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 64) return launch_kq_shape<QT, 64, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 128) return launch_kq_shape<QT, 64, 2, NW / 2, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 192) return launch_kq_shape<QT, 64, 3, G3, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
