@@ -160,6 +160,18 @@ def test_matvec_kq_segmented_rows(oracle, qt, M, K):
     assert rel_l2(gpu_matvec(W, qt, M, K, x, tb.TBQ_MV_KQ), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
 
 
+@pytest.mark.parametrize("M", [8193, 20001])
+def test_matvec_q4k_tall_segmented(oracle, M):
+    """Q4_K rows of 40 units taller than 8192 rows: the default dispatch
+    takes the K-quant kernel's segmented mapping instead of the persistent
+    Q4_K kernel; the last row block is ragged."""
+    K = 2560
+    rng = np.random.default_rng(M + 3)
+    W = synth.kquant_matrix(fm.Q4_K, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, fm.Q4_K, M, K, x), oracle.matvec(W, fm.Q4_K, M, K, x)) <= MATVEC_TOL
+
+
 @pytest.mark.parametrize("qt", KQ_FORMATS)
 @pytest.mark.parametrize("M,K", [(70, 17408), (129, 24576), (33, 32768)])
 def test_matvec_long_rows(oracle, qt, M, K):

@@ -161,9 +161,13 @@ int tbq_matvec_variant(const void *W, int qt, int M, int K, const float *x, floa
     // The specialised Q4_K kernels keep x's digits in registers for rows of
     // up to 64 units: one pass of two rows per wave up to 8192 rows,
     // persistent waves walking the rows of taller matrices; longer rows
-    // stream through the shared K-quant kernel.
+    // stream through the shared K-quant kernel, and so do taller matrices of
+    // 33..63 units per row that are not a power of two, whose segmented
+    // mapping keeps every lane busy (151936x2560: 41.6 against 50.2 us).
+    const int U = K / 64;
+    const bool seg_rows = U > 32 && U < 64 && (U & (U - 1)) != 0 && M > 8192;
     const bool q4k_special = (qt == QT_Q4_K || qt == QT_GQ4_K) &&
-                             (variant == TBQ_MV_INTDOT || (variant == TBQ_MV_AUTO && K <= 4096));
+                             (variant == TBQ_MV_INTDOT || (variant == TBQ_MV_AUTO && K <= 4096 && !seg_rows));
     if (q4k_special) {
         hipError_t e = launch_matvec_q4k(W, M, K, x, y, S(s), g_cu, qt == QT_GQ4_K);
         if (e != hipErrorNotSupported) return hip_ok(e, "matvec launch (Q4_K int-dot)");
