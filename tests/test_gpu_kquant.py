@@ -160,6 +160,19 @@ def test_matvec_kq_segmented_rows(oracle, qt, M, K):
     assert rel_l2(gpu_matvec(W, qt, M, K, x, tb.TBQ_MV_KQ), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
 
 
+@pytest.mark.parametrize("qt", KQ_FORMATS)
+def test_matvec_tall_64_unit_rows(oracle, qt):
+    """Matrices of 64-unit rows (K = 4096) above 32768 rows: the default
+    dispatch takes the segmented mapping (16 rows per workgroup pass) for
+    every format but Q6_K; 32769 rows leave a last block of one row."""
+    M, K = 32769, 4096
+    print(f"tall rows qt={qt} M={M} K={K}", flush=True)
+    rng = np.random.default_rng(qt + 17)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, qt, M, K, x), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+
+
 @pytest.mark.parametrize("M", [8193, 20001])
 def test_matvec_q4k_tall_segmented(oracle, M):
     """Q4_K rows of 40 units taller than 8192 rows: the default dispatch

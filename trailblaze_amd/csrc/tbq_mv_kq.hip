@@ -1088,8 +1088,9 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
 }
 
 // Rows of U units with 32 < U < 64, U not a power of two (K = 2560:
-// U = 40), where a 64-lane row slice would leave 64 - U lanes idle.
-// Segmented mapping instead: workgroup lane L takes unit L % U of row slot
+// U = 40), where a 64-lane row slice would leave 64 - U lanes idle, and
+// tall matrices of 64-unit rows.  Segmented mapping: workgroup lane L takes
+// unit L % U of row slot
 // L / U, RB = NT / U rows per pass, so only NT % U lanes idle; a lane's unit
 // is fixed, so its digits stay in registers as in k_mv_kq.  Row blocks of RB
 // rows are dealt to the workgroups round-robin, the next block's weights in
@@ -1102,7 +1103,7 @@ __global__ __launch_bounds__(NW * 64) void k_mv_kq_seg(const uint8_t *__restrict
                                                        MvPro pro) {
     using F = KqFmt<QT>;
     constexpr int NT = NW * 64, RP = GLU ? 2 : 1;   // RP: weight rows per lane and pass
-    constexpr int MAXT = (16 * 64 + NT - 1) / NT;   // U < 64
+    constexpr int MAXT = (16 * 64 + NT - 1) / NT;   // U <= 64
     extern __shared__ uint32_t smem[];
     const int U = K / 64, RB = NT / U;
     uint32_t *xd = smem;
@@ -1224,6 +1225,12 @@ static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float
     if (U <= 8) return launch_kq_shape<QT, 8, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 16) return launch_kq_shape<QT, 16, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 32) return launch_kq_shape<QT, 32, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    // Tall matrices of 64-unit rows: the segmented mapping, 16 rows per
+    // workgroup pass (151936x4096: Q5_K 82.0 -> 79.5 us, Q2_K 59.4 -> 56.1,
+    // Q8_0 65536x4096 52.5 -> 51.0); Q6_K keeps the 8-wave shape below
+    // (99.3 against 104 us segmented)
+    if constexpr (QT != QT_Q6_K && QT != QT_GQ6_K)
+        if (U == 64 && M > 32768) return launch_kq_seg<QT, KQ_SEG_NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     // Q6_K's tall matrices (the lm_head): 8-wave workgroups, up to 4 per CU
     // (151936x4096: 99.5 against 106 us with one 16-wave workgroup per CU)
     if constexpr (QT == QT_Q6_K || QT == QT_GQ6_K)
