@@ -173,6 +173,16 @@ def test_matvec_tall_64_unit_rows(oracle, qt):
     assert rel_l2(gpu_matvec(W, qt, M, K, x), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
 
 
+def test_matvec_q3k_segmented_from_8193_rows(oracle):
+    """Q3_K takes the segmented mapping for 64-unit rows above 8192 rows
+    (the other formats above 32768); 12289 rows leave a last block of one."""
+    M, K = 12289, 4096
+    rng = np.random.default_rng(12289)
+    W = synth.kquant_matrix(fm.Q3_K, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, fm.Q3_K, M, K, x), oracle.matvec(W, fm.Q3_K, M, K, x)) <= MATVEC_TOL
+
+
 @pytest.mark.parametrize("M", [8193, 20001])
 def test_matvec_q4k_tall_segmented(oracle, M):
     """Q4_K rows of 40 units taller than 8192 rows: the default dispatch
