@@ -147,6 +147,26 @@ def test_dense_decode_wide_hidden(oracle, qt):
         assert rel_l2(host(logits), ref.decode(tok, pos)) <= DENSE_TOL, pos
 
 
+@pytest.mark.parametrize("qt", [fm.Q3_K, fm.Q5_K, fm.Q6_K])
+def test_dense_decode_segmented_hidden(oracle, qt):
+    """hidden 2304 (36 units per row): the q|k|v and gate|up matvecs run the
+    segmented K-quant kernel (lanes over consecutive units of consecutive
+    rows) with the add+RMSNorm prologue and, for gate|up, the SwiGLU
+    epilogue."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=1, hidden=2304, n_heads=8, n_kv_heads=2, head_dim=128, ffn=1536, vocab=256,
+                      max_ctx=64, qtype_layers=qt)
+    m = _model(cfg, 9)
+    ref = DenseOracle(oracle, cfg, m.host)
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    for pos, tok in enumerate([7, 130]):
+        print("dense segmented-hidden step", qt, pos, flush=True)
+        m.decode(tok, pos, logits)
+        assert rel_l2(host(logits), ref.decode(tok, pos)) <= DENSE_TOL, pos
+
+
 def test_dense_decode_configs2_context_4096(oracle):
     """BASELINE configs[2] at its context: two layers at the Qwen3-4B widths
     (hidden 2560, 32 query / 8 kv heads of 128, ffn 9728, max_ctx 4096)
