@@ -146,9 +146,10 @@ def test_matvec_kq_kernel(oracle, qt, M, K):
 
 
 @pytest.mark.parametrize("qt", KQ_FORMATS)
-@pytest.mark.parametrize("M,K", [(5, 2560), (26, 2304), (777, 3072), (2000, 3840), (6144, 2560)])
+@pytest.mark.parametrize("M,K", [(5, 2560), (26, 2304), (777, 3072), (2000, 3840), (6144, 2560), (300, 1280),
+                                 (8960, 1536), (43, 1792)])
 def test_matvec_kq_segmented_rows(oracle, qt, M, K):
-    """Rows of 36..60 units (K = 2304 .. 3840, Qwen3-4B's hidden 2560): the
+    """Rows of 20..60 units (K = 1280 .. 3840, Qwen3-4B's hidden 2560): the
     segmented mapping, a workgroup's lanes over consecutive units of
     consecutive rows, partial sums meeting in LDS; ragged last row block.
     No single-row case: one output of a 2560-term sum can cancel by 10^3

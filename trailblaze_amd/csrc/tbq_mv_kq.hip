@@ -1087,9 +1087,9 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
     }
 }
 
-// Rows of U units with 32 < U < 64, U not a power of two (K = 2560:
-// U = 40), where a 64-lane row slice would leave 64 - U lanes idle, and
-// tall matrices of 64-unit rows.  Segmented mapping: workgroup lane L takes
+// Rows of U units with 16 < U < 64, U not a power of two (K = 2560:
+// U = 40), where a row slice of the next power of two would leave lanes
+// idle, and tall matrices of 64-unit rows.  Segmented mapping: workgroup lane L takes
 // unit L % U of row slot
 // L / U, RB = NT / U rows per pass, so only NT % U lanes idle; a lane's unit
 // is fixed, so its digits stay in registers as in k_mv_kq.  Row blocks of RB
@@ -1221,6 +1221,13 @@ static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float
                               const MvPro &pro) {
     const int U = K / 64;
     constexpr int NW = KQ_NW, G3 = KQ_G3;
+    // 16 < U < 32, not a power of two (K = 1536: U = 24): the segmented
+    // row mapping, as for 32 < U < 64 below (8960x1536: Q3_K 6.7 -> 5.5 us,
+    // Q5_K 6.8 -> 5.8, Q2_K 5.4 -> 4.7; at U = 12 the 16-lane row slices
+    // stay faster: Q5_K 4096x768 4.4 against 5.1 us)
+    if constexpr (QT != QT_Q8_0 && QT != QT_GQ8_0)
+        if (U > 16 && U < 32 && (U & (U - 1)) != 0)
+            return launch_kq_seg<QT, KQ_SEG_NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 4) return launch_kq_shape<QT, 4, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 8) return launch_kq_shape<QT, 8, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 16) return launch_kq_shape<QT, 16, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
