@@ -184,12 +184,11 @@ def test_matvec_q3k_segmented_from_8193_rows(oracle):
     assert rel_l2(gpu_matvec(W, fm.Q3_K, M, K, x), oracle.matvec(W, fm.Q3_K, M, K, x)) <= MATVEC_TOL
 
 
-@pytest.mark.parametrize("M", [8193, 20001])
-def test_matvec_q4k_tall_segmented(oracle, M):
-    """Q4_K rows of 40 units taller than 8192 rows: the default dispatch
-    takes the K-quant kernel's segmented mapping instead of the persistent
-    Q4_K kernel; the last row block is ragged."""
-    K = 2560
+@pytest.mark.parametrize("M,K", [(8193, 2560), (20001, 2560), (9001, 1536)])
+def test_matvec_q4k_tall_segmented(oracle, M, K):
+    """Q4_K rows of 24 or 40 units taller than 8192 rows: the default
+    dispatch takes the K-quant kernel's segmented mapping instead of the
+    persistent Q4_K kernel; the last row block is ragged."""
     rng = np.random.default_rng(M + 3)
     W = synth.kquant_matrix(fm.Q4_K, M, K, rng)
     x = synth.activations(K, rng)

@@ -162,12 +162,13 @@ int tbq_matvec_variant(const void *W, int qt, int M, int K, const float *x, floa
     // up to 64 units: one pass of two rows per wave up to 8192 rows,
     // persistent waves walking the rows of taller matrices; longer rows
     // stream through the shared K-quant kernel, and so do taller matrices of
-    // 33..63 units per row that are not a power of two, whose segmented
-    // mapping keeps every lane busy (151936x2560: 41.6 against 50.2 us), and
+    // 17..63 units per row that are not a power of two, whose segmented
+    // mapping keeps every lane busy (151936x2560: 41.6 against 50.2 us,
+    // 151936x1536: 28.6 against 30.0-30.7), and
     // matrices of 64-unit rows above 32768 rows (151936x4096: 65.6-66.3
     // against 67.8 us).
     const int U = K / 64;
-    const bool seg_rows = (U > 32 && U < 64 && (U & (U - 1)) != 0 && M > 8192) || (U == 64 && M > 32768);
+    const bool seg_rows = (U > 16 && U < 64 && (U & (U - 1)) != 0 && M > 8192) || (U == 64 && M > 32768);
     const bool q4k_special = (qt == QT_Q4_K || qt == QT_GQ4_K) &&
                              (variant == TBQ_MV_INTDOT || (variant == TBQ_MV_AUTO && K <= 4096 && !seg_rows));
     if (q4k_special) {
