@@ -136,10 +136,11 @@ KQ_FORMATS = [fm.Q2_K, fm.Q3_K, fm.Q4_K, fm.Q5_K, fm.Q6_K, fm.Q8_0, fm.Q4_0, fm.
 
 @pytest.mark.parametrize("qt", KQ_FORMATS)
 @pytest.mark.parametrize("M,K", [(1, 256), (5, 512), (200, 768), (1000, 2048), (4096, 4096), (333, 8192),
-                                 (700, 12288), (65, 16384)])
+                                 (700, 12288), (65, 16384), (2560, 9728), (1281, 10240)])
 def test_matvec_kq_kernel(oracle, qt, M, K):
     """The shared integer-dot kernel for every block format: row slices of
-    4..64 units, rows split over 2..4 waves (K > 4096), ragged M."""
+    4..64 units, rows split over 2..4 waves (K > 4096), ragged M; 2560x9728
+    and 1281x10240 take five row groups of three slices."""
     rng = np.random.default_rng(M * 13 + K + 7 * qt)
     W = synth.kquant_matrix(qt, M, K, rng)
     x = synth.activations(K, rng)

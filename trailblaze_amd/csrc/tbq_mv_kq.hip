@@ -1251,7 +1251,16 @@ static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float
         if (U < 64 && (U & (U - 1)) != 0) return launch_kq_seg<QT, KQ_SEG_NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 64) return launch_kq_shape<QT, 64, 1, NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     if (U <= 128) return launch_kq_shape<QT, 64, 2, NW / 2, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
-    if (U <= 192) return launch_kq_shape<QT, 64, 3, G3, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    if (U <= 192) {
+        // three slices: 5 row groups when that takes fewer passes than G3
+        // over a workgroup's rows (2560 rows on 256 CUs: 10 rows, 2 passes
+        // instead of 3; 2560x9728 Q5_K 8.9 -> 8.5 us), else G3 (4096 rows:
+        // 4 passes either way, and 5 groups were 7-16% slower)
+        const long long rpw = ((long long)M + n_cu - 1) / n_cu;
+        if ((rpw + 4) / 5 < (rpw + G3 - 1) / G3)
+            return launch_kq_shape<QT, 64, 3, 5, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+        return launch_kq_shape<QT, 64, 3, G3, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
+    }
     if (U <= 256) return launch_kq_shape<QT, 64, 4, NW / 4, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     // K up to 32768 for plain matvecs (the fused prologue's registers do not
     // fit 8 slices): 6 or 8 slices of 64 units, two row groups
