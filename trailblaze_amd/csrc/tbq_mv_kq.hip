@@ -1235,10 +1235,11 @@ static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float
     // Tall matrices of 64-unit rows: the segmented mapping, 16 rows per
     // workgroup pass (151936x4096: Q5_K 82.0 -> 79.5 us, Q2_K 59.4 -> 56.1,
     // Q8_0 65536x4096 52.5 -> 51.0; up to 24576 rows the row slices are as
-    // fast or faster, except Q3_K: 12288x4096 10.1 -> 9.8 us); Q6_K keeps
+    // fast or faster, except Q3_K in the reference layout: 12288x4096
+    // 10.1 -> 9.5-9.8 us, ggml's 10.7 -> 11.1); Q6_K keeps
     // the 8-wave shape below (99.3 against 104 us segmented)
     if constexpr (QT != QT_Q6_K && QT != QT_GQ6_K)
-        if (U == 64 && M > (QT == QT_Q3_K || QT == QT_GQ3_K ? 8192 : 32768))
+        if (U == 64 && M > (QT == QT_Q3_K ? 8192 : 32768))
             return launch_kq_seg<QT, KQ_SEG_NW, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     // Q6_K's tall matrices (the lm_head): 8-wave workgroups, up to 4 per CU
     // (151936x4096: 99.5 against 106 us with one 16-wave workgroup per CU)
