@@ -28,7 +28,10 @@
 // <= 64 units); rows longer than 64 units are split over S waves of the
 // workgroup whose partial sums meet in LDS.  A lane keeps its unit's digits
 // in VGPRs for every row it visits; rows are grid-strided, and the weights
-// of the next pass are loaded before the current pass is reduced.
+// of the next pass are loaded before the current pass is reduced.  Rows of
+// 17..63 units that are not a power of two, and tall matrices of 64-unit
+// rows, use a segmented mapping instead (k_mv_kq_seg): workgroup lane L
+// takes unit L % U of row slot L / U, so a row slice wastes no lanes.
 #include "tbq_kernels.h"
 #include "tbq_kquant.hpp"
 
