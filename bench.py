@@ -29,7 +29,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "int8": 5000.0}   # MI355X dense, per GPU
 PMC_COPY_BYTES = 256 << 20
-PROFILES = ("q4k", "q4k_big", "sweep", "moe_b1", "moe_b16", "moe_prefill", "moe_prefill_i8")
+PROFILES = ("q4k", "q4k_big", "sweep", "seg", "moe_b1", "moe_b16", "moe_prefill", "moe_prefill_i8")
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "q4k_matvec_4096x4096_pmc.txt")
 
 
@@ -248,9 +248,12 @@ def profile_leg(name, tb, fm, synth, torch):
     one matrix is smaller, as in the timed legs."""
     rng = np.random.default_rng(0)
     reps = 3
-    if name in ("q4k", "q4k_big", "sweep"):
+    if name in ("q4k", "q4k_big", "sweep", "seg"):
+        # seg: rows the segmented mapping serves (K = 2560, Qwen3-4B's hidden)
         shapes = {"q4k": [(fm.Q4_K, 4096, 4096)], "q4k_big": [(fm.Q4_K, 151936, 4096)],
-                  "sweep": _sweep_shapes()}[name]
+                  "sweep": _sweep_shapes(),
+                  "seg": [(fm.Q4_K, 151936, 2560), (fm.Q5_K, 19456, 2560), (fm.Q3_K, 6144, 2560),
+                          (fm.Q6_K, 151936, 2560)]}[name]
         for qt, M, K in shapes:
             W = torch.from_numpy(synth.kquant_matrix(qt, M, K, rng)).cuda()
             nc = max(1, int(np.ceil(2 * 256e6 / fm.weight_bytes(qt, M, K))) + (1 if M * K < 2 ** 26 else 0))

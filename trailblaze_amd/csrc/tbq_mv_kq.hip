@@ -1116,13 +1116,16 @@ __global__ __launch_bounds__(NW * 64) void k_mv_kq_seg(const uint8_t *__restrict
     const int nblk = (M + RB - 1) / RB;
     const int npass = (nblk - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;   // >= 1: grid <= nblk
     auto block_row = [&](int pass) { return ((int)blockIdx.x + pass * (int)gridDim.x) * RB; };
-    // loads are unconditional: rows past M (and idle lanes' rows) re-read row
-    // M - 1, and their results are never read
+    // loads are unconditional and their results for rows past M or idle
+    // lanes never read: rows past M re-read row M - 1, idle lanes the
+    // block's last row (whose lines the same instruction fetches anyway; a
+    // row of the next block would be fetched twice)
+    const int lslot = min(slot, RB - 1);
     typename F::Unit buf[2][RP];
     auto load = [&](typename F::Unit *dst, int pass) {
 #pragma unroll
         for (int p = 0; p < RP; p++) {
-            const int r = min(block_row(pass) + slot, M - 1) + (GLU ? p * M : 0);
+            const int r = min(block_row(pass) + lslot, M - 1) + (GLU ? p * M : 0);
             F::load(W + (long long)r * rb, u, dst[p]);
         }
     };
