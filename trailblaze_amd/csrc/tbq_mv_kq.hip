@@ -18,6 +18,8 @@
 //   PAIR     dword 2k holds elements 8k+{0,2,4,6}, dword 2k+1 holds 8k+{1,3,5,7}
 //            (nibble-packed and 2-bit-packed formats: low/high nibbles, and
 //            v_perm of a dword with itself shifted by 4 for 2-bit fields);
+//   QUAD     dword 4g+k holds elements 16g+k+{0,4,8,12} (Q2_K: the 2-bit
+//            fields at bits 2k of a quant dword, one shift and one and);
 //   NATURAL  dword t holds elements 4t..4t+3 (int8 formats).
 // Dwords 4g..4g+3 always hold the unit's 16-element group g.  Per-group
 // integer scales multiply the digit sums in integer arithmetic
@@ -140,22 +142,27 @@ struct GMem {
 // the 4 tasks of a group are a DPP quad (group sum).  Each thread handles at
 // most MAXT tasks (MAXT * NT >= 16 * U).
 // ---------------------------------------------------------------------------
-template <int NT, bool PAIR, int MAXT, int PRO = PRO_NONE>
+template <int NT, int ORD, int MAXT, int PRO = PRO_NONE>   // ORD: 0 NATURAL, 1 PAIR, 2 QUAD
 struct KqStager {
     float e[MAXT][4];
     float p1[MAXT][4], p2[MAXT][4];   // PRO_NORM inputs: y, w
 
-    // PAIR dword t = 2k + par holds elements 8k + par + {0, 2, 4, 6}: four
+    // PAIR dword t = 2k + par holds elements 8k + par + {0, 2, 4, 6}, QUAD
+    // dword t = 4g + k elements 16g + k + {0, 4, 8, 12}: four
     // loads at a per-lane base, no selection after the data arrives.
     // Loads are unconditional (tasks past the end re-read the last one and
     // are never stored), so no branch hides them from the wait counter.
     template <typename F4>
     __device__ __forceinline__ void ld4(const float *__restrict__ src, int task, F4 &o) const {
         const int u = task >> 4, t = task & 15;
-        if constexpr (PAIR) {
+        if constexpr (ORD == 1) {
             const float *p = src + 64 * u + 8 * (t >> 1) + (t & 1);
 #pragma unroll
             for (int j = 0; j < 4; j++) o[j] = p[2 * j];
+        } else if constexpr (ORD == 2) {
+            const float *p = src + 64 * u + 16 * (t >> 2) + (t & 3);
+#pragma unroll
+            for (int j = 0; j < 4; j++) o[j] = p[4 * j];
         } else {
             const float4 a = *reinterpret_cast<const float4 *>(src + 64 * u + 4 * t);
             o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
@@ -203,10 +210,14 @@ struct KqStager {
                 }
                 if (blockIdx.x == 0 && pro.vo && task < U * 16) {
                     const int u = task >> 4, t = task & 15;
-                    if constexpr (PAIR) {
+                    if constexpr (ORD == 1) {
                         float *p = pro.vo + 64 * u + 8 * (t >> 1) + (t & 1);
 #pragma unroll
                         for (int j = 0; j < 4; j++) p[2 * j] = e[i][j];
+                    } else if constexpr (ORD == 2) {
+                        float *p = pro.vo + 64 * u + 16 * (t >> 2) + (t & 3);
+#pragma unroll
+                        for (int j = 0; j < 4; j++) p[4 * j] = e[i][j];
                     } else {
                         *reinterpret_cast<float4 *>(pro.vo + 64 * u + 4 * t) =
                             make_float4(e[i][0], e[i][1], e[i][2], e[i][3]);
@@ -349,7 +360,7 @@ template <int QT> struct KqFmt;
 // nibble per 16 weights), qs[64]@16 (weight i at bits 2(i&3) of qs[i>>2]),
 // d@80, dmin@82.  w = fl(fl(d*sc)*q) - fl(dmin*m).
 template <> struct KqFmt<QT_Q2_K> {
-    static constexpr bool PAIR = true;
+    static constexpr bool PAIR = false;   // digits in QUAD order (kq_order)
     struct Unit { uint4 qs; uint32_t sc, dd; };
     static __device__ __forceinline__ void load(const uint8_t *row, int u, Unit &w) {
         const uint8_t *b = row + (size_t)(u >> 2) * 84;
@@ -364,8 +375,11 @@ template <> struct KqFmt<QT_Q2_K> {
         float mn = 0.f;
 #pragma unroll
         for (int g = 0; g < 4; g++) {
+            // QUAD order: q[k] byte b = element 16g + 4b + k, at bits 2k of
+            // quant byte 4g + b
             uint32_t q[4];
-            unpack2(qv[g], q);
+#pragma unroll
+            for (int k = 0; k < 4; k++) q[k] = (qv[g] >> (2 * k)) & 0x03030303u;
             int ah = 0, am = 0, al = 0;
             kq_dots<4>(q, x, 4 * g, ah, am, al);
             const int s = (int)bfe(w.sc, 8 * g, 4), m = (int)bfe(w.sc, 8 * g + 4, 4);
@@ -941,6 +955,13 @@ template <> struct KqFmt<QT_GQ4_0> {
 };
 
 // Uniform entry for formats whose dot does not need the unit index.
+// Element order of a format's staged digits (see the header): QUAD for
+// Q2_K's reference layout, PAIR or NATURAL as the format declares.
+template <int QT>
+constexpr int kq_order() {
+    return QT == QT_Q2_K ? 2 : (KqFmt<QT>::PAIR ? 1 : 0);
+}
+
 template <int QT>
 __device__ __forceinline__ float kq_dot(const typename KqFmt<QT>::Unit &w, const KqX &x, int u) {
     if constexpr (QT == QT_Q2_K) return KqFmt<QT>::dot(w, x);
@@ -998,7 +1019,7 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
             F::load(W + (long long)r * rb, ul, dst[p]);
         }
     };
-    KqStager<NT, F::PAIR, MAXT, PRO> xs;
+    KqStager<NT, kq_order<QT>(), MAXT, PRO> xs;
     xs.load(x, U, pro);
     __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
 #pragma unroll
@@ -1129,7 +1150,7 @@ __global__ __launch_bounds__(NW * 64) void k_mv_kq_seg(const uint8_t *__restrict
             F::load(W + (long long)r * rb, u, dst[p]);
         }
     };
-    KqStager<NT, F::PAIR, MAXT, PRO> xs;
+    KqStager<NT, kq_order<QT>(), MAXT, PRO> xs;
     xs.load(x, U, pro);
     __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
     load(buf[0], 0);
