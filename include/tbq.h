@@ -19,7 +19,7 @@
  * ggml assigns quant bits to weights in 32-byte runs, unpacks the 6-bit
  * K-quant scales differently and decodes fp16 subnormals as IEEE.  Every
  * call that takes a qtype accepts these ids (for F32, BF16 and Q8_K the two
- * layouts are one); the prefill MFMA mode of tbq_moe_forward takes only
+ * layouts are one); the prefill MFMA modes of tbq_moe_forward take only
  * the reference's Q4_K.
  */
 #ifndef TBQ_H
@@ -96,8 +96,13 @@ int tbq_route(const float *xn, const float *router, const float *bias, int T, in
  * buffer: calls must be ordered on one stream.) */
 
 /* One MoE layer in the reference's packed expert layout
- * (layer4/tb_infer.c:780-806): gate/up are [E*F rows][H], down [E*H rows][F],
- * all in `qtype`; router is fp32 [E][H]. */
+ * (layer4/tb_infer.c:780-806): gate/up are [E*F rows][H], down [E*H rows][F];
+ * router is fp32 [E][H].  Each expert tensor has its own qtype, as the
+ * reference reads eg_t->qtype, the up tensor's and ed_t->qtype
+ * (layer4/tb_infer.c:807-816): qt_gate, qt_up and qt_down, where 0 means
+ * `qtype` (so a layer whose three tensors share one format sets only
+ * `qtype`).  Row strides follow each tensor's own format.  Expert qtypes:
+ * Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0, or TBQ_GGML | one of them. */
 typedef struct {
     int H, F, E, top_k, qtype;
     const float *router;
@@ -105,6 +110,7 @@ typedef struct {
     const void *gate;
     const void *up;
     const void *down;
+    int qt_gate, qt_up, qt_down;   /* 0 = qtype */
 } tbq_moe_layer;
 
 #define TBQ_MOE_FP32 0      /* fp32 decode kernels; outputs within 1e-5 rel-L2 */
@@ -115,6 +121,13 @@ typedef struct {
                                Q8_K blocks (d = max|x|/127 per 256), the Q4_K
                                nibbles with their 6-bit scales folded in; fp32
                                accumulate; within 1e-2 rel-L2 */
+
+/* 1 if tbq_moe_forward takes layer L in `mode`.  TBQ_MOE_FP32 takes every
+ * valid layer; the two prefill modes take layers whose gate, up and down
+ * are all Q4_K in the reference's layout, with H and F in {256, 512, 768,
+ * 1024, 1536, 2048, 3072, 4096}.  0 with tbq_last_error() for an invalid
+ * layer. */
+int tbq_moe_mode_supported(const tbq_moe_layer *L, int mode);
 
 /* Workspace bytes tbq_moe_forward needs for T tokens in `mode` (T <= 65536). */
 size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode);
@@ -149,7 +162,9 @@ int tbq_moe_forward_noalloc(const tbq_moe_layer *L, int T, const float *xn, cons
 /* Host-memory MoE block: the substitution for the MoE branch of
  * tb_layer_forward (layer4/tb_infer.c:753-833,876).  Weights in L are device
  * pointers (e.g. from tb_cuda_upload_tensor); xn, resid, out, sel_idx and
- * sel_w are host arrays.  Synchronous.  Implemented in C11 over this API. */
+ * sel_w are host arrays.  Synchronous.  A prefill mode that does not take
+ * the layer (tbq_moe_mode_supported) runs it in TBQ_MOE_FP32.  Implemented
+ * in C11 over this API. */
 int tbq_moe_block_host(const tbq_moe_layer *L, int T, const float *xn_host, const float *resid_host,
                        float *out_host, int *sel_idx_host, float *sel_w_host, int mode);
 

@@ -90,9 +90,15 @@ int tbq_gguf_set_layout(tbq_gguf *g, int layout);
 int tbq_gguf_dense_model(tbq_gguf *g, int max_ctx, tbq_dense_model *m, tbq_dense_layer *layers, int n_layers);
 
 /* MoE layer `layer` of the file (tensors blk.N.ffn_gate_inp (router, F32),
- * ffn_gate_exps, ffn_up_exps, ffn_down_exps; expert count and top-k from
- * <arch>.expert_count / expert_used_count), uploaded if needed, as the
- * reference's packed expert layout (layer4/tb_infer.c:780-806). */
+ * ffn_gate_exps, ffn_up_exps, ffn_down_exps; expert count (at most 256) and
+ * top-k from <arch>.expert_count / expert_used_count), uploaded if needed,
+ * as the reference's packed expert layout (layer4/tb_infer.c:780-806).
+ * Each expert tensor keeps its file qtype (qt_gate, qt_up, qt_down: K-quant
+ * mixes often give down a wider format than gate and up).  A file without
+ * the packed tensors may hold one tensor per expert,
+ * blk.N.ffn_{gate,up,down}.<e>.weight (the reference's fallback,
+ * layer4/tb_infer.c:783-791); those are copied into packed device matrices
+ * owned by g (the experts of one kind must share a qtype). */
 int tbq_gguf_moe_layer(tbq_gguf *g, int layer, tbq_moe_layer *L);
 
 #ifdef __cplusplus

@@ -62,7 +62,7 @@ class Oracle:
         L.tbo_route_experts.restype = C.c_int
         L.tbo_route_experts.argtypes = [_f32p, C.c_int, C.c_int, _i32p, _f32p]
         L.tbo_router_logits.argtypes = [C.c_int, C.c_int, C.c_int, _f32p, _f32p, C.c_void_p, _f32p]
-        L.tbo_moe_forward.argtypes = [C.c_int] * 6 + [_f32p, _f32p, _f32p, C.c_void_p,
+        L.tbo_moe_forward.argtypes = [C.c_int] * 8 + [_f32p, _f32p, _f32p, C.c_void_p,
                                                       _u8p, _u8p, _u8p, _f32p, C.c_void_p, C.c_void_p]
         L.tbo_quantize_q8k.argtypes = [_f32p, C.c_int, _u8p]
         L.tbo_expf_batch.argtypes = [_f32p, _f32p, C.c_size_t]
@@ -114,14 +114,17 @@ class Oracle:
                                    None if b is None else b.ctypes.data, out.reshape(-1))
         return out
 
-    def moe(self, xn, resid, router, gate, up, down, *, F, top_k, qtype, bias=None):
+    def moe(self, xn, resid, router, gate, up, down, *, F, top_k, qtype, bias=None, qt_gate=0, qt_up=0,
+            qt_down=0):
+        """The MoE block per token; qt_gate/qt_up/qt_down give a tensor its
+        own qtype (0 = qtype)."""
         T, H = xn.shape
         E = router.shape[0]
         out = np.empty((T, H), np.float32)
         idx = np.empty((T, 8), np.int32)
         w = np.empty((T, 8), np.float32)
         b = None if bias is None else np.ascontiguousarray(bias, np.float32)
-        self.lib.tbo_moe_forward(T, H, F, E, top_k, qtype,
+        self.lib.tbo_moe_forward(T, H, F, E, top_k, qt_gate or qtype, qt_up or qtype, qt_down or qtype,
                                  np.ascontiguousarray(xn, np.float32).reshape(-1),
                                  np.ascontiguousarray(resid, np.float32).reshape(-1),
                                  np.ascontiguousarray(router, np.float32).reshape(-1),
@@ -165,7 +168,7 @@ class Reference:
         L.tbref_route.argtypes = [_f32p, C.c_int, C.c_int, _i32p, _f32p]
         L.tbref_swiglu.argtypes = [_f32p, _f32p, _f32p, C.c_int]
         L.tbref_dispatch_matvec_avx512.argtypes = [_u8p, C.c_int, C.c_int, C.c_int, _f32p, _f32p]
-        L.tbref_moe_block.argtypes = [C.c_int] * 6 + [_f32p, _f32p, _f32p, _u8p, _u8p, _u8p, _f32p]
+        L.tbref_moe_block.argtypes = [C.c_int] * 8 + [_f32p, _f32p, _f32p, _u8p, _u8p, _u8p, _f32p]
 
     def dequant_rows(self, W, qtype, M, K, row_bytes):
         out = np.empty((M, K), np.float32)
@@ -188,13 +191,15 @@ class Reference:
                                               np.ascontiguousarray(x, np.float32), out)
         return out
 
-    def moe_block(self, xn, resid, router, gate, up, down, *, F, top_k, qtype):
+    def moe_block(self, xn, resid, router, gate, up, down, *, F, top_k, qtype, qt_gate=0, qt_up=0, qt_down=0):
         """The reference's MoE branch (layer4/tb_infer.c:753-833,876) composed
-        of its own functions, per token (no router bias)."""
+        of its own functions, per token (no router bias); each expert tensor
+        in its own qtype (0 = qtype)."""
         T, H = xn.shape
         E = router.shape[0]
         out = np.empty((T, H), np.float32)
-        self.lib.tbref_moe_block(T, H, F, E, top_k, qtype, np.ascontiguousarray(xn, np.float32).reshape(-1),
+        self.lib.tbref_moe_block(T, H, F, E, top_k, qt_gate or qtype, qt_up or qtype, qt_down or qtype,
+                                 np.ascontiguousarray(xn, np.float32).reshape(-1),
                                  np.ascontiguousarray(resid, np.float32).reshape(-1),
                                  np.ascontiguousarray(router, np.float32).reshape(-1),
                                  np.ascontiguousarray(gate).reshape(-1), np.ascontiguousarray(up).reshape(-1),

@@ -76,15 +76,19 @@ int tbref_sizeof_selection(void) { return (int)sizeof(TB_ExpertSelection); }
  * router (the 4-bit-compat router call at :759-763 cannot read an fp32
  * ffn_gate_inp), tb_route_experts, two tb_gguf_dequant_matvec + tb_swiglu +
  * one tb_gguf_dequant_matvec per slot on the packed expert rows (:794-820,
- * with the three mallocs per slot), the weighted accumulate (:829-831) and
- * the residual add.  The CPU baseline of the MoE block (one thread). */
-void tbref_moe_block(int T, int H, int F, int E, int top_k, int qtype, const float *xn, const float *resid,
-                     const float *router, const void *gate, const void *up, const void *down, float *out) {
+ * with the three mallocs per slot), each tensor read in its own qtype qg, qu
+ * and qd with row bytes from its own format (:807-816), the weighted
+ * accumulate (:829-831) and the residual add.  The CPU baseline of the MoE
+ * block (one thread). */
+void tbref_moe_block(int T, int H, int F, int E, int top_k, int qg, int qu, int qd, const float *xn,
+                     const float *resid, const float *router, const void *gate, const void *up, const void *down,
+                     float *out) {
     TB_GGUFModel *m = (TB_GGUFModel *)calloc(1, sizeof(TB_GGUFModel));
     TB_InferCtx *ctx = (TB_InferCtx *)calloc(1, sizeof(TB_InferCtx));
     m->n_experts_per_tok = top_k;
     ctx->model = m;
-    const size_t rb_h = (size_t)tb_gguf_row_bytes_ref(qtype, H), rb_f = (size_t)tb_gguf_row_bytes_ref(qtype, F);
+    const size_t rb_g = (size_t)tb_gguf_row_bytes_ref(qg, H), rb_u = (size_t)tb_gguf_row_bytes_ref(qu, H),
+                 rb_f = (size_t)tb_gguf_row_bytes_ref(qd, F);
     for (int t = 0; t < T; t++) {
         const float *x = xn + (size_t)t * H;
         float *lg = (float *)calloc(E, sizeof(float));
@@ -98,10 +102,10 @@ void tbref_moe_block(int T, int H, int F, int E, int top_k, int qtype, const flo
             float *g = (float *)malloc(F * sizeof(float));
             float *u = (float *)malloc(F * sizeof(float));
             float *a = (float *)malloc(F * sizeof(float));
-            tb_gguf_dequant_matvec((const char *)gate + (size_t)e * F * rb_h, qtype, F, H, x, g);
-            tb_gguf_dequant_matvec((const char *)up + (size_t)e * F * rb_h, qtype, F, H, x, u);
+            tb_gguf_dequant_matvec((const char *)gate + (size_t)e * F * rb_g, qg, F, H, x, g);
+            tb_gguf_dequant_matvec((const char *)up + (size_t)e * F * rb_u, qu, F, H, x, u);
             tb_swiglu(g, u, a, F);
-            tb_gguf_dequant_matvec((const char *)down + (size_t)e * H * rb_f, qtype, H, F, a, eo);
+            tb_gguf_dequant_matvec((const char *)down + (size_t)e * H * rb_f, qd, H, F, a, eo);
             free(g); free(u); free(a);
             const float w = sel.expert_weights[ei];
             for (int i = 0; i < H; i++) ffn[i] += w * eo[i];

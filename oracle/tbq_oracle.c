@@ -365,14 +365,15 @@ void tbo_router_logits(int T, int H, int E, const float *xn, const float *router
 }
 
 /* layer4/tb_infer.c:753-833 and :876, one token at a time.  Expert e uses
- * gate/up rows [e*F, (e+1)*F) (row bytes for K=H) and down rows
- * [e*H, (e+1)*H) (row bytes for K=F).  The weighted accumulate runs in slot
- * order into a zeroed buffer; the residual is added last. */
-void tbo_moe_forward(int T, int H, int F, int E, int top_k, int qt,
+ * gate/up rows [e*F, (e+1)*F) (row bytes for K=H in the gate's and the up
+ * tensor's own qtype, :807-812) and down rows [e*H, (e+1)*H) (row bytes for
+ * K=F in the down tensor's qtype, :815-816).  The weighted accumulate runs
+ * in slot order into a zeroed buffer; the residual is added last. */
+void tbo_moe_forward(int T, int H, int F, int E, int top_k, int qg, int qu, int qd,
                      const float *xn, const float *resid, const float *router,
                      const float *bias, const void *gate, const void *up,
                      const void *down, float *out, int *sel_idx, float *sel_w) {
-    size_t rbH = tbo_row_bytes(qt, H), rbF = tbo_row_bytes(qt, F);
+    size_t rbG = tbo_row_bytes(qg, H), rbU = tbo_row_bytes(qu, H), rbF = tbo_row_bytes(qd, F);
     float *lg = (float *)malloc((size_t)E * 4);
     float *g = (float *)malloc((size_t)F * 4);
     float *u = (float *)malloc((size_t)F * 4);
@@ -388,13 +389,13 @@ void tbo_moe_forward(int T, int H, int F, int E, int top_k, int qt,
         memset(acc, 0, (size_t)H * 4);
         for (int s = 0; s < k; s++) {
             int e = idx[s];
-            const uint8_t *gb = (const uint8_t *)gate + (size_t)e * F * rbH;
-            const uint8_t *ub = (const uint8_t *)up + (size_t)e * F * rbH;
+            const uint8_t *gb = (const uint8_t *)gate + (size_t)e * F * rbG;
+            const uint8_t *ub = (const uint8_t *)up + (size_t)e * F * rbU;
             const uint8_t *db = (const uint8_t *)down + (size_t)e * H * rbF;
-            tbo_dequant_matvec(gb, qt, F, H, x, g);
-            tbo_dequant_matvec(ub, qt, F, H, x, u);
+            tbo_dequant_matvec(gb, qg, F, H, x, g);
+            tbo_dequant_matvec(ub, qu, F, H, x, u);
             tbo_swiglu(g, u, a, F);
-            tbo_dequant_matvec(db, qt, H, F, a, y);
+            tbo_dequant_matvec(db, qd, H, F, a, y);
             for (int i = 0; i < H; i++) {
                 float p = w[s] * y[i];
                 acc[i] = acc[i] + p;

@@ -86,10 +86,11 @@ int tbo_route_experts(const float *gate_logits, int n_experts, int top_k,
  *   router  [E][H]  fp32 router weights (ffn_gate_inp, F32)
  *   bias    [E]     optional per-expert logit bias (NULL = none), added
  *                   to the logits before routing
- *   gate/up packed [E*F rows][H], down packed [E*H rows][F], qtype qt
+ *   gate/up packed [E*F rows][H] in qtypes qg/qu, down packed [E*H rows][F]
+ *           in qtype qd (each tensor's own format)
  *   out     [T][H]  resid + weighted sum of expert outputs
  *   sel_idx/sel_w [T][8] optional (may be NULL) */
-void tbo_moe_forward(int T, int H, int F, int E, int top_k, int qt,
+void tbo_moe_forward(int T, int H, int F, int E, int top_k, int qg, int qu, int qd,
                      const float *xn, const float *resid,
                      const float *router, const float *bias,
                      const void *gate, const void *up, const void *down,

@@ -12,6 +12,9 @@ Each .npz holds inputs and the reference's outputs only (no code):
                      753-833,876) assembled from the reference functions
                      above; only the weighted accumulate and the residual
                      add (one fp32 multiply and add each) run in numpy.
+  moe_mixed.npz      the same block with gate, up and down in three
+                     different qtypes, from oracle/ref_harness.c
+                     tbref_moe_block (all in the compiled reference).
 
 Run:  make -C oracle ref && python tests/golden/make_golden.py
 """
@@ -131,6 +134,21 @@ def main():
     np.savez_compressed(os.path.join(OUT, "moe.npz"), H=np.int32(H), F=np.int32(F), E=np.int32(E),
                         k=np.int32(k), qtype=np.int32(qt), router=router, gate=gate, up=up, down=down,
                         bias=bias, xn=xn, resid=resid, out=out, idx=sidx, w=sw)
+
+    # MoE block with one qtype per expert tensor (gate Q3_K, up Q4_K, down
+    # Q6_K: three block sizes, so a swapped qtype or row stride shows), as the
+    # reference reads eg_t->qtype, uqt and ed_t->qtype (tb_infer.c:807-816);
+    # its own generator, so the fixtures above do not change
+    rng = np.random.default_rng(4242)
+    H, F, E, k, T = 256, 512, 8, 3, 4
+    qg, qu, qd = fm.Q3_K, fm.Q4_K, fm.Q6_K
+    router, gate, up, down = synth.moe_layer(H, F, E, qg, seed=4243, qt_up=qu, qt_down=qd)
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    out = ref.moe_block(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=qg, qt_up=qu, qt_down=qd)
+    np.savez_compressed(os.path.join(OUT, "moe_mixed.npz"), H=np.int32(H), F=np.int32(F), E=np.int32(E),
+                        k=np.int32(k), qt=np.array([qg, qu, qd], np.int32), router=router, gate=gate, up=up,
+                        down=down, xn=xn, resid=resid, out=out)
     print("golden vectors written to", OUT)
 
 

@@ -8,7 +8,9 @@
  * workspace pointer of every call, checks that the counter area is zero on
  * entry (the contract of tbq.h), dirties the rest of the workspace and
  * leaves the counters zero, as the real router does; it writes
- * out = resid + 2 * xn so the copies can be checked.
+ * out = resid + 2 * xn so the copies can be checked.  tbq_moe_mode_supported
+ * takes the prefill modes for all-Q4_K layers only, as the real one, and the
+ * mode of the last call is recorded.
  */
 #include <stdlib.h>
 #include <string.h>
@@ -22,6 +24,7 @@ static void *g_last_ws = NULL;
 static int g_calls = 0;
 static int g_bad_counters = 0;   /* calls that found non-zero counters */
 static int g_allocs = 0;
+static int g_last_mode = -1;
 
 void *tbq_malloc(size_t bytes) {
     void *p = malloc(bytes ? bytes : 1);
@@ -54,6 +57,13 @@ int tbq_stream_sync(void *s) {
     return 1;
 }
 
+int tbq_moe_mode_supported(const tbq_moe_layer *L, int mode) {
+    if (mode == TBQ_MOE_FP32) return 1;
+    const int g = L->qt_gate ? L->qt_gate : L->qtype, u = L->qt_up ? L->qt_up : L->qtype,
+              d = L->qt_down ? L->qt_down : L->qtype;
+    return g == 12 && u == 12 && d == 12;
+}
+
 /* grows with T and with the prefill mode, like the real size */
 size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode) {
     size_t n = MOCK_COUNTER_BYTES + (size_t)T * (L->E + 16) * 4 + (size_t)T * 8 * (L->F + L->H) * 4;
@@ -66,6 +76,7 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     (void)stream;
     g_calls++;
     g_last_ws = workspace;
+    g_last_mode = mode;
     if (ws_bytes < tbq_moe_workspace_size(L, T, mode)) return 0;
     const unsigned char *c = (const unsigned char *)workspace;
     for (size_t i = 0; i < MOCK_COUNTER_BYTES; i++)
@@ -88,3 +99,4 @@ void *mock_last_ws(void) { return g_last_ws; }
 int mock_calls(void) { return g_calls; }
 int mock_bad_counters(void) { return g_bad_counters; }
 int mock_allocs(void) { return g_allocs; }
+int mock_last_mode(void) { return g_last_mode; }

@@ -141,3 +141,48 @@ def test_gguf_moe_layer(tmp_path, oracle):
         assert np.array_equal(host(idx).reshape(T, 8), ridx)
         assert bits_equal(host(w).reshape(T, 8), rw)
         assert rel_l2(host(out).reshape(T, H) - resid, ref - resid) <= 1e-5
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_gguf_moe_layer_mixed_and_split(tmp_path, oracle, split):
+    """A K-quant mix (Q4_K gate, Q5_K up, Q6_K down) read from the file with
+    each tensor's own qtype, in the packed blk.N.ffn_*_exps form and in the
+    reference's split fallback blk.N.ffn_{gate,up,down}.<e>.weight
+    (layer4/tb_infer.c:783-791), which the loader packs on the device."""
+    import torch
+    H, F, E, k = 512, 256, 16, 4
+    qg, qu, qd = fm.Q4_K, fm.Q5_K, fm.Q6_K
+    router, gate, up, down = synth.moe_layer(H, F, E, qg, seed=22, qt_up=qu, qt_down=qd)
+    kv = [("general.architecture", "str", "qwen3moe"), ("qwen3moe.embedding_length", "u32", H),
+          ("qwen3moe.expert_count", "u32", E), ("qwen3moe.expert_used_count", "u32", k),
+          ("qwen3moe.expert_feed_forward_length", "u32", F)]
+    ts = [("blk.0.ffn_gate_inp.weight", fm.F32, (H, E), router)]
+    if split:
+        for name, qt, t, d0, d1 in (("gate", qg, gate, H, F), ("up", qu, up, H, F), ("down", qd, down, F, H)):
+            per = t.reshape(E, -1)
+            ts += [(f"blk.0.ffn_{name}.{e}.weight", qt, (d0, d1), per[e]) for e in range(E)]
+    else:
+        ts += [("blk.0.ffn_gate_exps.weight", qg, (H, F, E), gate),
+               ("blk.0.ffn_up_exps.weight", qu, (H, F, E), up),
+               ("blk.0.ffn_down_exps.weight", qd, (F, H, E), down)]
+    path = tmp_path / "moe_mixed.gguf"
+    write_gguf(path, kv, ts)
+    rng = np.random.default_rng(23)
+    T = 3
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    print("gguf moe mixed split=", split, flush=True)
+    with GgufFile(path) as g:
+        L = g.moe_layer(0)
+        assert (L.H, L.F, L.E, L.top_k) == (H, F, E, k)
+        assert (L.qt_gate, L.qt_up, L.qt_down) == (qg, qu, qd)
+        out = empty(T * H, torch.float32)
+        idx = empty(T * 8, torch.int32)
+        w = empty(T * 8, torch.float32)
+        ws = torch.zeros(tb.moe_workspace_size(L, T), dtype=torch.uint8, device="cuda")
+        tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws)
+        ref, ridx, rw = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=qg, qt_up=qu,
+                                   qt_down=qd)
+        assert np.array_equal(host(idx).reshape(T, 8), ridx)
+        assert bits_equal(host(w).reshape(T, 8), rw)
+        assert rel_l2(host(out).reshape(T, H) - resid, ref - resid) <= 1e-5

@@ -32,7 +32,7 @@ REF = os.environ.get("TBQ_REFERENCE", "/root/reference")
 class MoeLayer(C.Structure):
     _fields_ = [("H", C.c_int), ("F", C.c_int), ("E", C.c_int), ("top_k", C.c_int), ("qtype", C.c_int),
                 ("router", C.c_void_p), ("bias", C.c_void_p), ("gate", C.c_void_p), ("up", C.c_void_p),
-                ("down", C.c_void_p)]
+                ("down", C.c_void_p), ("qt_gate", C.c_int), ("qt_up", C.c_int), ("qt_down", C.c_int)]
 
 
 @pytest.fixture(scope="module")
@@ -73,6 +73,25 @@ def test_moe_host_block_workspace_is_fixed_and_zeroed(host_block):
         allocs = lib.mock_allocs()
     assert lib.mock_calls() == 8
     assert allocs >= 3   # T=5, then regrown for T=16 and for the prefill mode
+
+
+def test_moe_host_block_mixed_qtypes_fall_back_to_fp32(host_block):
+    """A prefill mode that does not take the layer (a Q6_K down tensor under
+    Q4_K gate/up, as llama.cpp's K-quant mixes write) runs in TBQ_MOE_FP32;
+    an all-Q4_K layer keeps the mode it asked for."""
+    lib = host_block
+    H, F, E, k, T = 512, 256, 16, 4, 3
+    xn = np.ones((T, H), np.float32)
+    resid = np.zeros((T, H), np.float32)
+    out = np.zeros((T, H), np.float32)
+    idx = np.zeros((T, 8), np.int32)
+    w = np.zeros((T, 8), np.float32)
+    for qts, mode, ran in [((0, 0, 14), 1, 0), ((0, 0, 0), 1, 1), ((11, 11, 12), 2, 0), ((12, 12, 12), 2, 2),
+                           ((0, 0, 14), 0, 0)]:
+        L = MoeLayer(H, F, E, k, 12, 0x1000, 0, 0x2000, 0x3000, 0x4000, *qts)
+        assert lib.tbq_moe_block_host(C.byref(L), T, xn.ctypes.data, resid.ctypes.data, out.ctypes.data,
+                                      idx.ctypes.data, w.ctypes.data, mode) == 1
+        assert lib.mock_last_mode() == ran, (qts, mode)
 
 
 def _run_forced(code):

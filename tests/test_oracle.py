@@ -262,6 +262,21 @@ def test_oracle_matches_golden_moe(oracle):
     assert bits_equal(out, g["out"])
 
 
+def test_oracle_matches_golden_moe_mixed(oracle):
+    """Gate Q3_K, up Q4_K, down Q6_K: each tensor read in its own qtype and
+    row stride, as the reference's MoE branch does (tb_infer.c:807-816)."""
+    g = load_golden("moe_mixed.npz")
+    qg, qu, qd = (int(v) for v in g["qt"])
+    out, _, _ = oracle.moe(g["xn"], g["resid"], g["router"], g["gate"], g["up"], g["down"], F=int(g["F"]),
+                           top_k=int(g["k"]), qtype=qg, qt_up=qu, qt_down=qd)
+    assert bits_equal(out, g["out"])
+    # a single-qtype reading of the same bytes is not the same block
+    with np.errstate(all="ignore"):
+        wrong, _, _ = oracle.moe(g["xn"][:1], g["resid"][:1], g["router"], g["gate"], g["up"], g["up"],
+                                 F=int(g["F"]), top_k=int(g["k"]), qtype=qu, qt_gate=qu, qt_down=qu)
+    assert not bits_equal(wrong, g["out"][:1])
+
+
 # --------------------------------------------------------------------------
 # Live comparison with the compiled reference (this container only).
 # --------------------------------------------------------------------------
@@ -293,6 +308,30 @@ def test_moe_vs_compiled_reference_block(oracle, reference):
     resid = synth.activations((T, H), rng)
     out, _, _ = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
     ref = reference.moe_block(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K)
+    assert bits_equal(out, ref)
+
+
+@pytest.mark.parametrize("qts", [(fm.Q4_K, fm.Q4_K, fm.Q6_K), (fm.Q3_K, fm.Q3_K, fm.Q4_K),
+                                 (fm.Q4_K, fm.Q5_K, fm.Q6_K), (fm.Q5_K, fm.Q6_K, fm.Q8_0),
+                                 (fm.Q2_K, fm.Q3_K, fm.Q8_0)])
+def test_moe_mixed_vs_compiled_reference_block(oracle, reference, qts):
+    """Expert tensors in different qtypes (llama.cpp's K-quant mixes give down
+    a wider format): tbo_moe_forward against tbref_moe_block, bit-identical.
+    The reference's expert row-stride macro (_RB, layer4/tb_infer.c:806) has
+    no Q2_K entry and strides Q2_K rows as fp32 (K * 4 bytes), so expert e > 0
+    of a Q2_K tensor is read out of place (past the tensor's end for the last
+    experts); the Q2_K case therefore runs with one expert, whose rows start
+    at offset 0 under either stride."""
+    qg, qu, qd = qts
+    H, F, E, k, T = 512, 256, 16, 4, 3
+    if fm.Q2_K in qts:
+        E, k = 1, 1
+    router, gate, up, down = synth.moe_layer(H, F, E, qg, seed=20 + qd, qt_up=qu, qt_down=qd)
+    rng = np.random.default_rng(21 + qd)
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    out, _, _ = oracle.moe(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=qg, qt_up=qu, qt_down=qd)
+    ref = reference.moe_block(xn, resid, router, gate, up, down, F=F, top_k=k, qtype=qg, qt_up=qu, qt_down=qd)
     assert bits_equal(out, ref)
 
 

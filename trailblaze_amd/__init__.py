@@ -46,6 +46,7 @@ SYMBOLS = {
     "tbq_matvec_variant": (_i, [_vp, _i, _i, _i, _vp, _vp, _i, _vp]),
     "tbq_route": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "tbq_moe_workspace_size": (_sz, [_vp, _i, _i]),
+    "tbq_moe_mode_supported": (_i, [_vp, _i]),
     "tbq_moe_forward": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _vp]),
     "tbq_moe_block_host": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _i]),
     "tbq_moe_forward_noalloc": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
@@ -95,7 +96,7 @@ class MoeLayer(C.Structure):
     """Mirror of ``tbq_moe_layer`` (include/tbq.h)."""
     _fields_ = [("H", C.c_int), ("F", C.c_int), ("E", C.c_int), ("top_k", C.c_int), ("qtype", C.c_int),
                 ("router", C.c_void_p), ("bias", C.c_void_p), ("gate", C.c_void_p), ("up", C.c_void_p),
-                ("down", C.c_void_p)]
+                ("down", C.c_void_p), ("qt_gate", C.c_int), ("qt_up", C.c_int), ("qt_down", C.c_int)]
 
 
 _lib = None
@@ -161,11 +162,19 @@ def route(xn, router, bias, T, H, E, top_k, sel_idx, sel_w, stream=None):
                            _stream(stream)), "tbq_route")
 
 
-def moe_layer(H, F, E, top_k, qtype, router, gate, up, down, bias=None) -> MoeLayer:
+def moe_layer(H, F, E, top_k, qtype, router, gate, up, down, bias=None, qt_gate=0, qt_up=0,
+              qt_down=0) -> MoeLayer:
+    """A ``tbq_moe_layer`` over device tensors; qt_gate/qt_up/qt_down give a
+    tensor its own qtype (0 = qtype)."""
     L = MoeLayer(H, F, E, top_k, qtype, router.data_ptr(), 0 if bias is None else bias.data_ptr(),
-                 gate.data_ptr(), up.data_ptr(), down.data_ptr())
+                 gate.data_ptr(), up.data_ptr(), down.data_ptr(), qt_gate, qt_up, qt_down)
     L._keep = (router, gate, up, down, bias)   # keep the tensors alive
     return L
+
+
+def moe_mode_supported(L: MoeLayer, mode: int) -> bool:
+    """Whether tbq_moe_forward takes layer L in ``mode``."""
+    return bool(lib().tbq_moe_mode_supported(C.byref(L), mode))
 
 
 def moe_workspace_size(L: MoeLayer, T: int, mode: int = TBQ_MOE_FP32) -> int:
@@ -208,5 +217,5 @@ def expf_device(x, out, stream=None):
 
 
 __all__ = ["formats", "row_bytes", "lib", "init", "dequant", "matvec", "route", "moe_layer", "moe_forward",
-           "moe_forward_noalloc", "moe_workspace_size", "gemm", "expf_device", "MoeLayer", "TbqError", "SYMBOLS", "TBQ_MOE_FP32", "TBQ_MOE_BF16",
+           "moe_forward_noalloc", "moe_workspace_size", "moe_mode_supported", "gemm", "expf_device", "MoeLayer", "TbqError", "SYMBOLS", "TBQ_MOE_FP32", "TBQ_MOE_BF16",
            "TBQ_MOE_I8"]

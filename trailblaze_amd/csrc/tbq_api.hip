@@ -229,34 +229,69 @@ int tbq_route(const float *xn, const float *router, const float *bias, int T, in
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 
+// The qtypes of a layer's gate, up and down tensors (a zero field means
+// L->qtype, as in layer4/tb_infer.c:807-816 each tensor carries its own).
+struct MoeQts {
+    int g, u, d;
+};
+static MoeQts moe_qts(const tbq_moe_layer *L) {
+    return {L->qt_gate ? L->qt_gate : L->qtype, L->qt_up ? L->qt_up : L->qtype,
+            L->qt_down ? L->qt_down : L->qtype};
+}
+
 size_t tbq_moe_workspace_size(const tbq_moe_layer *L, int T, int mode) {
     if (!L || T <= 0) return 0;
     int k = L->top_k > 8 ? 8 : L->top_k;
+    const MoeQts q = moe_qts(L);
     size_t n = COUNTER_BYTES;
     n += align256((size_t)T * 8 * 4) * 2;                   // sel idx / w
     n += align256((size_t)T * L->E * 4);                     // router logits
     n += align256((size_t)T * k * L->F * 4);                 // act
     n += align256((size_t)T * k * L->H * 4);                 // y
     n += align256((size_t)(2 + 3 * L->E + T * k) * 4);       // decode order by expert
+    if (q.g != q.u) n += align256((size_t)T * k * L->F * 4); // up products (gate and up run apart)
     if (mode == TBQ_MOE_BF16) n += align256(prefill_workspace_bytes(T, k, L->E, L->H, L->F));
     if (mode == TBQ_MOE_I8) n += align256(prefill_i8_workspace_bytes(T, k, L->E, L->H, L->F));
     return n;
+}
+
+static bool moe_expert_qtype(int qt) {
+    switch (qt) {
+    case QT_Q2_K: case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_Q8_0:
+    case QT_GQ2_K: case QT_GQ3_K: case QT_GQ4_K: case QT_GQ5_K: case QT_GQ6_K: case QT_GQ8_0: return true;
+    default: return false;
+    }
 }
 
 static int check_moe(const tbq_moe_layer *L, int T) {
     if (!L) return fail("tbq_moe_forward: null layer");
     if (T < 0 || T > MAX_TOKENS || L->E <= 0 || L->E > 256 || L->top_k <= 0) return fail("tbq_moe_forward: bad T/E/top_k");
     if (L->H <= 0 || L->F <= 0 || L->H % 256 || L->F % 256) return fail("tbq_moe_forward: H and F must be multiples of 256");
-    switch (L->qtype) {
-    case QT_Q2_K: case QT_Q3_K: case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: case QT_Q8_0:
-    case QT_GQ2_K: case QT_GQ3_K: case QT_GQ4_K: case QT_GQ5_K: case QT_GQ6_K: case QT_GQ8_0: break;
-    default: return fail("tbq_moe_forward: expert qtype %d not supported", L->qtype);
-    }
+    const MoeQts q = moe_qts(L);
+    if (!moe_expert_qtype(q.g) || !moe_expert_qtype(q.u) || !moe_expert_qtype(q.d))
+        return fail("tbq_moe_forward: expert qtypes gate %d, up %d, down %d: each must be Q2_K, Q3_K, Q4_K, Q5_K, "
+                    "Q6_K or Q8_0 (either layout)", q.g, q.u, q.d);
     if (!L->router || !L->gate || !L->up || !L->down) return fail("tbq_moe_forward: null weight");
     if (!aligned16(L->router) || !aligned16(L->gate) || !aligned16(L->up) || !aligned16(L->down))
         return fail("tbq_moe_forward: weights must be 16-byte aligned");
     if ((size_t)L->H * 4 + (size_t)L->H / 4 > 60 * 1024) return fail("tbq_moe_forward: H too large");
     return 1;
+}
+
+// The prefill MFMA modes take layers whose three expert tensors are Q4_K in
+// the reference's layout.
+static bool moe_mode_ok(const tbq_moe_layer *L, int mode) {
+    if (mode == TBQ_MOE_FP32) return true;
+    if (mode != TBQ_MOE_BF16 && mode != TBQ_MOE_I8) return false;
+    const MoeQts q = moe_qts(L);
+    return q.g == QT_Q4_K && q.u == QT_Q4_K && q.d == QT_Q4_K && gemm_k_supported(L->H) && gemm_k_supported(L->F);
+}
+
+int tbq_moe_mode_supported(const tbq_moe_layer *L, int mode) {
+    if (!L) return 0;
+    g_err[0] = 0;
+    if (!check_moe(L, 1)) return 0;
+    return moe_mode_ok(L, mode) ? 1 : 0;
 }
 
 int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float *resid, float *out, int *sel_idx,
@@ -265,9 +300,10 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     if (!check_moe(L, T)) return 0;
     if (mode != TBQ_MOE_FP32 && mode != TBQ_MOE_BF16 && mode != TBQ_MOE_I8)
         return fail("tbq_moe_forward: unknown mode %d", mode);
-    if (mode != TBQ_MOE_FP32 && (L->qtype != QT_Q4_K || !gemm_k_supported(L->H) || !gemm_k_supported(L->F)))
-        return fail("tbq_moe_forward: the prefill MFMA paths take Q4_K experts (reference layout) with H and F "
-                    "in {256, 512, 768, 1024, 1536, 2048, 3072, 4096}");
+    if (!moe_mode_ok(L, mode))
+        return fail("tbq_moe_forward: the prefill MFMA modes take layers whose gate, up and down are all Q4_K "
+                    "(reference layout) with H and F in {256, 512, 768, 1024, 1536, 2048, 3072, 4096}; "
+                    "use TBQ_MOE_FP32 for this layer");
     if (!xn || !resid || !out || !aligned16(xn) || !aligned16(resid) || !aligned16(out))
         return fail("tbq_moe_forward: null or misaligned activation pointer");
     if (T == 0) return 1;
@@ -288,10 +324,11 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     } else if (ws_bytes < need) {
         return fail("tbq_moe_forward: workspace %zu < %zu bytes", ws_bytes, need);
     }
+    const MoeQts q = moe_qts(L);
     MoeArgs a;
     a.T = T; a.H = L->H; a.F = L->F; a.E = L->E; a.top_k = L->top_k;
     a.k = L->top_k > 8 ? 8 : L->top_k;
-    a.qtype = L->qtype;
+    a.qg = q.g; a.qu = q.u; a.qd = q.d;
     a.xn = xn; a.resid = resid; a.router = L->router; a.bias = L->bias;
     a.gate = L->gate; a.up = L->up; a.down = L->down; a.out = out;
     size_t off = 0;
@@ -302,6 +339,8 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
     a.act = (float *)(ws + off); off += align256((size_t)T * a.k * a.F * 4);
     a.y = (float *)(ws + off); off += align256((size_t)T * a.k * a.H * 4);
     a.grp = (int *)(ws + off); off += align256((size_t)(2 + 3 * a.E + T * a.k) * 4);
+    a.u = nullptr;
+    if (q.g != q.u) { a.u = (float *)(ws + off); off += align256((size_t)T * a.k * a.F * 4); }
     a.sel_idx = sel_idx ? sel_idx : ws_idx;
     a.sel_w = sel_w ? sel_w : ws_w;
     if (mode == TBQ_MOE_BF16) return hip_ok(launch_moe_bf16(a, ws + off, S(s)), "moe launch (prefill MFMA)");

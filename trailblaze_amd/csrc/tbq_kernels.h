@@ -31,7 +31,8 @@ struct MvPro {
 };
 
 struct MoeArgs {
-    int T, H, F, E, top_k, k, qtype;
+    int T, H, F, E, top_k, k;
+    int qg, qu, qd;    // qtypes of the gate, up and down expert tensors
     const float *xn, *resid, *router, *bias;
     const void *gate, *up, *down;
     float *out;
@@ -42,6 +43,7 @@ struct MoeArgs {
     float *act;        // [T*k][F]
     float *y;          // [T*k][H]
     int *grp;          // decode order by expert: 2 + 3E + T*k ints (null: the per-pair order)
+    float *u;          // [T*k][F] up products when a.qg != a.qu (null otherwise)
 };
 
 hipError_t launch_dequant(int qt, const void *W, long long nweights, float *out, hipStream_t s);
@@ -69,8 +71,14 @@ hipError_t launch_combine(const MoeArgs &a, hipStream_t st);
 hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
                          float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st,
                          _Float16 *x16 = nullptr, float *xinv = nullptr, bool *x16_done = nullptr);
-// a.qtype QT_Q4_K or QT_GQ4_K
-hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st);
+// Decode expert kernels for Q4_K tensors (tbq_moe_q4k.hip).  A batch runs in
+// expert order when moe_decode_grouped(a): launch_group writes a.grp first.
+bool moe_decode_grouped(const MoeArgs &a);
+hipError_t launch_group(const MoeArgs &a, hipStream_t st);
+// act = swiglu(gate x, up x); a.qg == a.qu, QT_Q4_K or QT_GQ4_K
+hipError_t launch_moe_q4k_gate_up(const MoeArgs &a, bool grouped, hipStream_t st);
+// out = resid + combine(down act); a.qd QT_Q4_K or QT_GQ4_K
+hipError_t launch_moe_q4k_down(const MoeArgs &a, bool grouped, hipStream_t st);
 size_t prefill_workspace_bytes(int T, int k, int E, int H, int F);
 bool gemm_k_supported(int K);
 // rows of n floats to fp16 with per-row power-of-two scales (inv = 1 / scale)

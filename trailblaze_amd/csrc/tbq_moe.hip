@@ -8,8 +8,11 @@
 //                    bit-identical to tb_route_experts (tb_infer.c:351-374).
 //   k_gate_up        g = W_gate[e] x, u = W_up[e] x, a = swiglu(g, u) for
 //                    every (token, slot) pair.
-//   k_down           y[t][s] = W_down[e] a[t][s].
+//   k_rows           y[t][s] = W_down[e] a[t][s] (and gate, up one at a
+//                    time when their qtypes differ, with k_swiglu_pairs).
 //   k_combine        out = resid + sum over slots, in slot order, of w*y.
+#include <stdlib.h>
+
 #include "tbq_kquant.hpp"
 #include "tbq_kernels.h"
 
@@ -155,29 +158,33 @@ __global__ __launch_bounds__(256) void k_gate_up(const uint8_t *__restrict__ gat
 }
 
 // ---------------------------------------------------------------------------
-// Expert down projection: y[pair][r] = W_down[e][r] . act[pair].
+// One expert matrix per (token, slot) pair: out[pair][r] = W[e][r] . x_pair
+// over R rows of K weights, x_pair = x + (pair / xdiv) * K (xdiv = k: the
+// token's input row; 1: the pair's own row).  The down projection
+// (W_down, act, R = H, K = F), and gate and up one at a time when their
+// qtypes differ (R = F, K = H).
 // ---------------------------------------------------------------------------
 template <int QT, int LPR>
-__global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, const float *__restrict__ act,
-                                              const int *__restrict__ sel_idx, int H, int F, int E, int k,
+__global__ __launch_bounds__(256) void k_rows(const uint8_t *__restrict__ W, const float *__restrict__ x,
+                                              const int *__restrict__ sel_idx, int R, int K, int E, int k, int xdiv,
                                               int rows_per_block, float *__restrict__ yout) {
     extern __shared__ float lds[];
-    float *xl = lds, *xs = lds + F;
+    float *xl = lds, *xs = lds + K;
     const int pair = blockIdx.y, t = pair / k, s = pair % k;
     const int e_sel = sel_idx[t * 8 + s];
     const bool ev = (unsigned)e_sel < (unsigned)E;
     const int e = ev ? e_sel : 0;   // out of range: y = 0
-    stage_x_swizzled<256>(act + (long long)pair * F, F, xl, xs);
+    stage_x_swizzled<256>(x + (long long)(pair / xdiv) * K, K, xl, xs);
     __syncthreads();
     constexpr int GROUPS = 256 / LPR;
-    const long long rb = (long long)(F / block_weights(QT)) * block_bytes(QT);
-    const int C = F / 32, lane = threadIdx.x % LPR, grp = threadIdx.x / LPR;
-    const uint8_t *Wb = down + (long long)e * H * rb;
+    const long long rb = (long long)(K / block_weights(QT)) * block_bytes(QT);
+    const int C = K / 32, lane = threadIdx.x % LPR, grp = threadIdx.x / LPR;
+    const uint8_t *Wb = W + (long long)e * R * rb;
     const int r_begin = blockIdx.x * rows_per_block;
     for (int r0 = r_begin; r0 < r_begin + rows_per_block; r0 += GROUPS) {
         int r = r0 + grp;
         float acc = 0.f;
-        if (r < H) {
+        if (r < R) {
             const uint8_t *row = Wb + (long long)r * rb;
             for (int c = lane; c < C; c += LPR) {
                 float xv[32];
@@ -186,7 +193,19 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, 
             }
         }
         acc = group_sum<LPR>(acc);
-        if (lane == 0 && r < H) yout[(long long)pair * H + r] = ev ? acc : 0.f;
+        if (lane == 0 && r < R) yout[(long long)pair * R + r] = ev ? acc : 0.f;
+    }
+}
+
+// act[i] = silu(act[i]) * u[i] (tb_swiglu, layer4/tb_infer.c:130-135, with
+// the router's expf), after gate and up ran separately.
+__global__ __launch_bounds__(256) void k_swiglu_pairs(float *__restrict__ act, const float *__restrict__ u,
+                                                      long long n) {
+    for (long long i = blockIdx.x * 256LL + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
+        const float g = act[i];
+        const float den = 1.0f + expf_glibc(-g);
+        const float sg = g / den;
+        act[i] = sg * u[i];
     }
 }
 
@@ -239,49 +258,123 @@ static int pick_lpr(int K) {
 }
 
 template <int QT, int LPR>
-static hipError_t launch_moe_experts_t(const MoeArgs &a, hipStream_t st) {
+static hipError_t launch_gate_up_t(const MoeArgs &a, hipStream_t st) {
     const int pairs = a.T * a.k;
-    {
-        constexpr int OUT_PER_IT = 256 / LPR / 2;
-        int rpb = OUT_PER_IT * 4;
-        dim3 grid((a.F + rpb - 1) / rpb, pairs);
-        size_t lds = (size_t)a.H * 4 + (size_t)(a.H / 16) * 4;
-        hipLaunchKernelGGL((k_gate_up<QT, LPR>), grid, dim3(256), lds, st, (const uint8_t *)a.gate,
-                           (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.E, a.k, rpb, a.act);
-    }
+    constexpr int OUT_PER_IT = 256 / LPR / 2;
+    int rpb = OUT_PER_IT * 4;
+    dim3 grid((a.F + rpb - 1) / rpb, pairs);
+    size_t lds = (size_t)a.H * 4 + (size_t)(a.H / 16) * 4;
+    hipLaunchKernelGGL((k_gate_up<QT, LPR>), grid, dim3(256), lds, st, (const uint8_t *)a.gate,
+                       (const uint8_t *)a.up, a.xn, a.sel_idx, a.H, a.F, a.E, a.k, rpb, a.act);
     return hipGetLastError();
 }
 
 template <int QT, int LPR>
-static hipError_t launch_moe_down_t(const MoeArgs &a, hipStream_t st) {
+static hipError_t launch_rows_t(const void *W, const float *x, int R, int K, int xdiv, float *out, const MoeArgs &a,
+                                hipStream_t st) {
     const int pairs = a.T * a.k;
     constexpr int OUT_PER_IT = 256 / LPR;
     int rpb = OUT_PER_IT * 2;
-    dim3 grid((a.H + rpb - 1) / rpb, pairs);
-    size_t lds = (size_t)a.F * 4 + (size_t)(a.F / 16) * 4;
-    hipLaunchKernelGGL((k_down<QT, LPR>), grid, dim3(256), lds, st, (const uint8_t *)a.down, a.act, a.sel_idx,
-                       a.H, a.F, a.E, a.k, rpb, a.y);
+    dim3 grid((R + rpb - 1) / rpb, pairs);
+    size_t lds = (size_t)K * 4 + (size_t)(K / 16) * 4;
+    hipLaunchKernelGGL((k_rows<QT, LPR>), grid, dim3(256), lds, st, (const uint8_t *)W, x, a.sel_idx, R, K, a.E, a.k,
+                       xdiv, rpb, out);
     return hipGetLastError();
 }
 
 template <int QT>
-static hipError_t launch_moe_q(const MoeArgs &a, hipStream_t st) {
-    hipError_t err;
+static hipError_t launch_gate_up_q(const MoeArgs &a, hipStream_t st) {
     switch (pick_lpr(a.H)) {
-    case 64: err = launch_moe_experts_t<QT, 64>(a, st); break;
-    case 32: err = launch_moe_experts_t<QT, 32>(a, st); break;
-    case 16: err = launch_moe_experts_t<QT, 16>(a, st); break;
-    case 8: err = launch_moe_experts_t<QT, 8>(a, st); break;
-    default: err = launch_moe_experts_t<QT, 4>(a, st); break;
+    case 64: return launch_gate_up_t<QT, 64>(a, st);
+    case 32: return launch_gate_up_t<QT, 32>(a, st);
+    case 16: return launch_gate_up_t<QT, 16>(a, st);
+    case 8: return launch_gate_up_t<QT, 8>(a, st);
+    default: return launch_gate_up_t<QT, 4>(a, st);
+    }
+}
+
+template <int QT>
+static hipError_t launch_rows_q(const void *W, const float *x, int R, int K, int xdiv, float *out, const MoeArgs &a,
+                                hipStream_t st) {
+    switch (pick_lpr(K)) {
+    case 64: return launch_rows_t<QT, 64>(W, x, R, K, xdiv, out, a, st);
+    case 32: return launch_rows_t<QT, 32>(W, x, R, K, xdiv, out, a, st);
+    case 16: return launch_rows_t<QT, 16>(W, x, R, K, xdiv, out, a, st);
+    case 8: return launch_rows_t<QT, 8>(W, x, R, K, xdiv, out, a, st);
+    default: return launch_rows_t<QT, 4>(W, x, R, K, xdiv, out, a, st);
+    }
+}
+
+// Dispatch on an expert qtype: CALL(Q) with Q the format's constant, so the
+// per-format kernel families above are instantiated for every expert qtype.
+#define TBQ_MOE_QT_SWITCH(qt, CALL)                         \
+    switch (qt) {                                           \
+    case QT_Q2_K: return CALL(QT_Q2_K);                     \
+    case QT_Q3_K: return CALL(QT_Q3_K);                     \
+    case QT_Q4_K: return CALL(QT_Q4_K);                     \
+    case QT_Q5_K: return CALL(QT_Q5_K);                     \
+    case QT_Q6_K: return CALL(QT_Q6_K);                     \
+    case QT_Q8_0: return CALL(QT_Q8_0);                     \
+    case QT_GQ2_K: return CALL(QT_GQ2_K);                   \
+    case QT_GQ3_K: return CALL(QT_GQ3_K);                   \
+    case QT_GQ4_K: return CALL(QT_GQ4_K);                   \
+    case QT_GQ5_K: return CALL(QT_GQ5_K);                   \
+    case QT_GQ6_K: return CALL(QT_GQ6_K);                   \
+    case QT_GQ8_0: return CALL(QT_GQ8_0);                   \
+    default: return hipErrorInvalidValue;                   \
+    }
+
+// act = swiglu(W_gate x, W_up x) for one qtype shared by gate and up.
+static hipError_t launch_gate_up_generic(const MoeArgs &a, hipStream_t st) {
+#define TBQ_CALL(Q) launch_gate_up_q<Q>(a, st)
+    TBQ_MOE_QT_SWITCH(a.qg, TBQ_CALL)
+#undef TBQ_CALL
+}
+
+// y[pair] = W[e] x_pair for the expert tensor W of qtype qt.
+static hipError_t launch_rows_generic(int qt, const void *W, const float *x, int R, int K, int xdiv, float *out,
+                                      const MoeArgs &a, hipStream_t st) {
+#define TBQ_CALL(Q) launch_rows_q<Q>(W, x, R, K, xdiv, out, a, st)
+    TBQ_MOE_QT_SWITCH(qt, TBQ_CALL)
+#undef TBQ_CALL
+}
+
+static bool is_q4k(int qt) { return qt == QT_Q4_K || qt == QT_GQ4_K; }
+
+// The experts of a routed batch (routing already in a.sel_idx / a.sel_w):
+// gate/up + SwiGLU into a.act, then down + the slot-ordered combine into
+// a.out.  Each phase takes the Q4_K int-dot kernels where its tensors are
+// Q4_K (and the shape fits them), else the per-format kernels; gate and up
+// of different qtypes run one at a time.
+static hipError_t launch_experts(const MoeArgs &a, hipStream_t st) {
+    const bool q4_gu = a.qg == a.qu && is_q4k(a.qg), q4_dn = is_q4k(a.qd);
+    const bool grouped = (q4_gu || q4_dn) && moe_decode_grouped(a);
+    hipError_t err;
+    if (grouped && (err = launch_group(a, st)) != hipSuccess) return err;
+    err = hipErrorNotSupported;
+    if (q4_gu) err = launch_moe_q4k_gate_up(a, grouped, st);
+    if (err == hipErrorNotSupported) {
+        if (a.qg == a.qu) {
+            err = launch_gate_up_generic(a, st);
+        } else {
+            if (!a.u) return hipErrorInvalidValue;
+            err = launch_rows_generic(a.qg, a.gate, a.xn, a.F, a.H, a.k, a.act, a, st);
+            if (err == hipSuccess) err = launch_rows_generic(a.qu, a.up, a.xn, a.F, a.H, a.k, a.u, a, st);
+            if (err == hipSuccess) {
+                const long long n = (long long)a.T * a.k * a.F;
+                const int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+                hipLaunchKernelGGL(k_swiglu_pairs, dim3(grid), dim3(256), 0, st, a.act, a.u, n);
+                err = hipGetLastError();
+            }
+        }
     }
     if (err != hipSuccess) return err;
-    switch (pick_lpr(a.F)) {
-    case 64: return launch_moe_down_t<QT, 64>(a, st);
-    case 32: return launch_moe_down_t<QT, 32>(a, st);
-    case 16: return launch_moe_down_t<QT, 16>(a, st);
-    case 8: return launch_moe_down_t<QT, 8>(a, st);
-    default: return launch_moe_down_t<QT, 4>(a, st);
-    }
+    err = hipErrorNotSupported;
+    if (q4_dn) err = launch_moe_q4k_down(a, grouped, st);
+    if (err != hipErrorNotSupported) return err;
+    err = launch_rows_generic(a.qd, a.down, a.act, a.H, a.F, 1, a.y, a, st);
+    if (err != hipSuccess) return err;
+    return launch_combine(a, st);
 }
 
 hipError_t launch_route(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
@@ -291,33 +384,44 @@ hipError_t launch_route(const float *xn, const float *router, const float *bias,
     return hipGetLastError();
 }
 
+// Tokens are independent in the MoE block (each is routed and combined on
+// its own), so a batch may run as consecutive token chunks on one stream,
+// each reusing the start of the workspace's per-token buffers.  The limit is
+// `cap` tokens, lowered by TBQ_MOE_CHUNK_TOKENS when that is set (the test
+// hook for the chunked path).
+static int chunk_tokens(int T, long long cap) {
+    if (const char *e = getenv("TBQ_MOE_CHUNK_TOKENS")) {
+        const long long v = atoll(e);
+        if (v > 0 && v < cap) cap = v;
+    }
+    return (int)(cap < T ? cap : T);
+}
+
+template <class Fn>
+static hipError_t by_token_chunks(const MoeArgs &a, long long cap, Fn fn) {
+    const int Tc = chunk_tokens(a.T, cap < 1 ? 1 : cap);
+    for (int t0 = 0; t0 < a.T; t0 += Tc) {
+        MoeArgs c = a;
+        c.T = a.T - t0 < Tc ? a.T - t0 : Tc;
+        c.xn = a.xn + (long long)t0 * a.H;
+        c.resid = a.resid + (long long)t0 * a.H;
+        c.out = a.out + (long long)t0 * a.H;
+        c.sel_idx = a.sel_idx + (long long)t0 * 8;
+        c.sel_w = a.sel_w + (long long)t0 * 8;
+        const hipError_t err = fn(c);
+        if (err != hipSuccess) return err;
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
     hipError_t err = launch_router(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.logits, a.counters, a.sel_idx,
                                    a.sel_w, st);
     if (err == hipErrorNotSupported)
         err = launch_route(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.sel_idx, a.sel_w, st);
     if (err != hipSuccess) return err;
-    if (a.qtype == QT_Q4_K || a.qtype == QT_GQ4_K) {
-        err = launch_moe_q4k_experts(a, st);
-        if (err != hipErrorNotSupported) return err;
-    }
-    switch (a.qtype) {
-    case QT_Q2_K: err = launch_moe_q<QT_Q2_K>(a, st); break;
-    case QT_Q3_K: err = launch_moe_q<QT_Q3_K>(a, st); break;
-    case QT_Q4_K: err = launch_moe_q<QT_Q4_K>(a, st); break;
-    case QT_Q5_K: err = launch_moe_q<QT_Q5_K>(a, st); break;
-    case QT_Q6_K: err = launch_moe_q<QT_Q6_K>(a, st); break;
-    case QT_Q8_0: err = launch_moe_q<QT_Q8_0>(a, st); break;
-    case QT_GQ2_K: err = launch_moe_q<QT_GQ2_K>(a, st); break;
-    case QT_GQ3_K: err = launch_moe_q<QT_GQ3_K>(a, st); break;
-    case QT_GQ4_K: err = launch_moe_q<QT_GQ4_K>(a, st); break;
-    case QT_GQ5_K: err = launch_moe_q<QT_GQ5_K>(a, st); break;
-    case QT_GQ6_K: err = launch_moe_q<QT_GQ6_K>(a, st); break;
-    case QT_GQ8_0: err = launch_moe_q<QT_GQ8_0>(a, st); break;
-    default: return hipErrorInvalidValue;
-    }
-    if (err != hipSuccess) return err;
-    return launch_combine(a, st);
+    // the per-pair kernels take a grid column per (token, slot) pair
+    return by_token_chunks(a, 65535 / a.k, [&](const MoeArgs &c) { return launch_experts(c, st); });
 }
 
 hipError_t launch_combine(const MoeArgs &a, hipStream_t st) {
@@ -333,14 +437,23 @@ hipError_t launch_combine(const MoeArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
+// The prefill kernels address a call's activation rows (fp16, or two int8
+// levels) through one buffer resource, whose byte offsets are 32-bit: T
+// tokens need T * max(H, k * F) * 2 bytes below 2^31, and larger batches run
+// in token chunks.
+static long long prefill_chunk_cap(const MoeArgs &a) {
+    const long long per_tok = a.H > (long long)a.k * a.F ? a.H : (long long)a.k * a.F;
+    return ((1LL << 30) - 1) / per_tok;
+}
+
 // Prefill: exact routing, then grouped fp16-MFMA experts and the
 // slot-ordered combine.
-hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st) {
+static hipError_t launch_moe_bf16_chunk(const MoeArgs &a, void *scratch, hipStream_t st) {
     // the batch router also writes the tokens' fp16 rows for the expert GEMMs
     _Float16 *x16 = nullptr;
     float *xinv = nullptr;
     bool x16_done = false;
-    if (a.qtype == QT_Q4_K) prefill_x16(a, scratch, &x16, &xinv);
+    prefill_x16(a, scratch, &x16, &xinv);
     hipError_t err = launch_router(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.logits,
                                    a.T >= 32 ? nullptr : a.counters, a.sel_idx, a.sel_w, st, x16, xinv, &x16_done);
     if (err == hipErrorNotSupported)
@@ -351,9 +464,13 @@ hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st) {
     return launch_combine(a, st);
 }
 
+hipError_t launch_moe_bf16(const MoeArgs &a, void *scratch, hipStream_t st) {
+    return by_token_chunks(a, prefill_chunk_cap(a), [&](const MoeArgs &c) { return launch_moe_bf16_chunk(c, scratch, st); });
+}
+
 // Prefill on int8 MFMA: exact routing, Q8_K activations, grouped int8
 // expert GEMMs, the slot-ordered combine.
-hipError_t launch_moe_i8(const MoeArgs &a, void *scratch, hipStream_t st) {
+static hipError_t launch_moe_i8_chunk(const MoeArgs &a, void *scratch, hipStream_t st) {
     hipError_t err = launch_router(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.logits,
                                    a.T >= 32 ? nullptr : a.counters, a.sel_idx, a.sel_w, st);
     if (err == hipErrorNotSupported)
@@ -362,6 +479,10 @@ hipError_t launch_moe_i8(const MoeArgs &a, void *scratch, hipStream_t st) {
     err = launch_moe_prefill_q4k_i8(a, scratch, st);
     if (err != hipSuccess) return err;
     return launch_combine(a, st);
+}
+
+hipError_t launch_moe_i8(const MoeArgs &a, void *scratch, hipStream_t st) {
+    return by_token_chunks(a, prefill_chunk_cap(a), [&](const MoeArgs &c) { return launch_moe_i8_chunk(c, scratch, st); });
 }
 
 }  // namespace tbq

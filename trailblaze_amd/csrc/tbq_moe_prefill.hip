@@ -48,6 +48,10 @@
 
 namespace tbq {
 
+// The prefill kernels decode Q4_K in the reference's layout for all three
+// expert tensors.
+static bool prefill_q4k_layer(const MoeArgs &a) { return a.qg == QT_Q4_K && a.qu == QT_Q4_K && a.qd == QT_Q4_K; }
+
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -929,7 +933,7 @@ hipError_t launch_quantize_q8k(const float *in, long long n, void *blocks, hipSt
 }
 
 hipError_t launch_moe_prefill_q4k_i8(const MoeArgs &a, void *scratch, hipStream_t st) {
-    if (a.qtype != QT_Q4_K || !gemm_k_supported(a.H) || !gemm_k_supported(a.F) || a.H % PF_ROWS ||
+    if (!prefill_q4k_layer(a) || !gemm_k_supported(a.H) || !gemm_k_supported(a.F) || a.H % PF_ROWS ||
         a.F % PF_COLS || a.T > 65536 || a.E > 256)
         return hipErrorNotSupported;
     const size_t P = (size_t)a.T * a.k;
@@ -997,7 +1001,7 @@ hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t s
         const int n = K / PF_KC;
         return K % 256 == 0 && gemm_k_supported(K);
     };
-    if (a.qtype != QT_Q4_K || !ok_k(a.H) || !ok_k(a.F) || a.H % PF_ROWS || a.F % PF_COLS || a.T > 65536 ||
+    if (!prefill_q4k_layer(a) || !ok_k(a.H) || !ok_k(a.F) || a.H % PF_ROWS || a.F % PF_COLS || a.T > 65536 ||
         a.E > 256)
         return hipErrorNotSupported;
     const size_t P = (size_t)a.T * a.k;

@@ -854,60 +854,73 @@ hipError_t launch_router(const float *xn, const float *router, const float *bias
 #define TBQ_GU_ROWS_B 4
 #endif
 
-template <int UPL_GU, int UPL_DC, bool GG>
-static hipError_t launch_experts_q4k(const MoeArgs &a, hipStream_t st) {
+// Whether a decode batch runs in expert order (k_group's pair list).
+bool moe_decode_grouped(const MoeArgs &a) {
     const int pairs = a.T * a.k;
-    const bool grouped = a.T >= TBQ_GRP_MIN_T && pairs <= 256 && a.T <= 32 && a.E <= 256 && a.H % DG_ROWS == 0 &&
-                         a.grp;
+    return a.T >= TBQ_GRP_MIN_T && pairs <= 256 && a.T <= 32 && a.E <= 256 && a.H % DG_ROWS == 0 && a.grp;
+}
+
+hipError_t launch_group(const MoeArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_group, dim3(1), dim3(256), 0, st, a.sel_idx, a.T, a.E, a.k, a.grp);
+    return hipGetLastError();
+}
+
+template <int UPL, bool GG>
+static hipError_t launch_gate_up_q4k_t(const MoeArgs &a, bool grouped, hipStream_t st) {
+    const int pairs = a.T * a.k;
     const int *order = grouped ? a.grp + 1 + 3 * a.E : nullptr, *nvalid = grouped ? order + pairs : nullptr;
-    hipError_t err;
+    // batches: more rows per workgroup, fewer workgroups
+    const int rows = grouped ? TBQ_GU_ROWS_B : GU_ROWS;
+    const int out_per_wg = (GU_THREADS / 64) * rows;
+    dim3 grid((a.F + out_per_wg - 1) / out_per_wg, pairs);
+    size_t lds = (size_t)(a.H / 32) * XD_PER_SB * 4;
+    if (rows == GU_ROWS)
+        hipLaunchKernelGGL((k_gate_up_q4k<UPL, GG>), grid, dim3(GU_THREADS), lds, st, (const uint8_t *)a.gate,
+                           (const uint8_t *)a.up, a.xn, a.sel_idx, order, nvalid, a.H, a.F, a.E, a.k, a.act);
+    else
+        hipLaunchKernelGGL((k_gate_up_q4k<UPL, GG, TBQ_GU_ROWS_B>), grid, dim3(GU_THREADS), lds, st,
+                           (const uint8_t *)a.gate, (const uint8_t *)a.up, a.xn, a.sel_idx, order, nvalid, a.H,
+                           a.F, a.E, a.k, a.act);
+    return hipGetLastError();
+}
+
+template <int UPL, bool GG>
+static hipError_t launch_down_q4k_t(const MoeArgs &a, bool grouped, hipStream_t st) {
+    const int pairs = a.T * a.k;
     if (grouped) {
-        hipLaunchKernelGGL(k_group, dim3(1), dim3(256), 0, st, a.sel_idx, a.T, a.E, a.k, a.grp);
-        if ((err = hipGetLastError()) != hipSuccess) return err;
-    }
-    {
-        // batches: more rows per workgroup, fewer workgroups
-        const int rows = grouped ? TBQ_GU_ROWS_B : GU_ROWS;
-        const int out_per_wg = (GU_THREADS / 64) * rows;
-        dim3 grid((a.F + out_per_wg - 1) / out_per_wg, pairs);
-        size_t lds = (size_t)(a.H / 32) * XD_PER_SB * 4;
-        if (rows == GU_ROWS)
-            hipLaunchKernelGGL((k_gate_up_q4k<UPL_GU, GG>), grid, dim3(GU_THREADS), lds, st, (const uint8_t *)a.gate,
-                               (const uint8_t *)a.up, a.xn, a.sel_idx, order, nvalid, a.H, a.F, a.E, a.k, a.act);
-        else
-            hipLaunchKernelGGL((k_gate_up_q4k<UPL_GU, GG, TBQ_GU_ROWS_B>), grid, dim3(GU_THREADS), lds, st,
-                               (const uint8_t *)a.gate, (const uint8_t *)a.up, a.xn, a.sel_idx, order, nvalid, a.H,
-                               a.F, a.E, a.k, a.act);
-        if ((err = hipGetLastError()) != hipSuccess) return err;
-    }
-    if (grouped) {
-        hipLaunchKernelGGL((k_down_pair_q4k<UPL_DC, GG>), dim3(a.H / DG_ROWS, pairs), dim3(DG_THREADS),
+        const int *order = a.grp + 1 + 3 * a.E, *nvalid = order + pairs;
+        hipLaunchKernelGGL((k_down_pair_q4k<UPL, GG>), dim3(a.H / DG_ROWS, pairs), dim3(DG_THREADS),
                            (size_t)(a.F / 32) * XD_PER_SB * 4, st, (const uint8_t *)a.down, a.act, a.sel_idx, order,
                            nvalid, a.H, a.F, a.E, a.k, a.y);
-        if ((err = hipGetLastError()) != hipSuccess) return err;
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
         return launch_combine(a, st);
     }
     dim3 grid(a.H / DC_ROWS, a.T);
     size_t lds = (size_t)a.k * (a.F / 32) * XD_PER_SB * 4;
-    hipLaunchKernelGGL((k_down_combine_q4k<UPL_DC, GG>), grid, dim3(DC_THREADS), lds, st, (const uint8_t *)a.down, a.act,
+    hipLaunchKernelGGL((k_down_combine_q4k<UPL, GG>), grid, dim3(DC_THREADS), lds, st, (const uint8_t *)a.down, a.act,
                        a.sel_idx, a.sel_w, a.resid, a.H, a.F, a.E, a.k, a.out);
     return hipGetLastError();
 }
 
-template <bool GG>
-static hipError_t launch_moe_q4k_experts_g(const MoeArgs &a, hipStream_t st) {
-    const int ugu = (a.H / 64 + 31) / 32, udc = (a.F / 64 + 15) / 16;
-    if (ugu == 1 && udc == 1) return launch_experts_q4k<1, 1, GG>(a, st);
-    if (ugu <= 2 && udc <= 1) return launch_experts_q4k<2, 1, GG>(a, st);
-    if (ugu <= 2 && udc <= 2) return launch_experts_q4k<2, 2, GG>(a, st);
-    return hipErrorNotSupported;
+// gate/up + SwiGLU with Q4_K gate and up (a.qg == a.qu, the reference's
+// layout or ggml's); hipErrorNotSupported for H > 4096.
+hipError_t launch_moe_q4k_gate_up(const MoeArgs &a, bool grouped, hipStream_t st) {
+    const int ugu = (a.H / 64 + 31) / 32;
+    if (ugu > 2) return hipErrorNotSupported;
+    const bool gg = a.qg == QT_GQ4_K;
+    if (ugu == 1) return gg ? launch_gate_up_q4k_t<1, true>(a, grouped, st) : launch_gate_up_q4k_t<1, false>(a, grouped, st);
+    return gg ? launch_gate_up_q4k_t<2, true>(a, grouped, st) : launch_gate_up_q4k_t<2, false>(a, grouped, st);
 }
 
-// Expert kernels for Q4_K weights, in the reference's layout or ggml's
-// (routing already in a.sel_idx / a.sel_w); hipErrorNotSupported outside
-// H <= 4096, F <= 2048.
-hipError_t launch_moe_q4k_experts(const MoeArgs &a, hipStream_t st) {
-    return a.qtype == QT_GQ4_K ? launch_moe_q4k_experts_g<true>(a, st) : launch_moe_q4k_experts_g<false>(a, st);
+// down + slot-ordered combine + residual with a Q4_K down tensor;
+// hipErrorNotSupported for F > 2048.
+hipError_t launch_moe_q4k_down(const MoeArgs &a, bool grouped, hipStream_t st) {
+    const int udc = (a.F / 64 + 15) / 16;
+    if (udc > 2) return hipErrorNotSupported;
+    const bool gg = a.qd == QT_GQ4_K;
+    if (udc == 1) return gg ? launch_down_q4k_t<1, true>(a, grouped, st) : launch_down_q4k_t<1, false>(a, grouped, st);
+    return gg ? launch_down_q4k_t<2, true>(a, grouped, st) : launch_down_q4k_t<2, false>(a, grouped, st);
 }
 
 }  // namespace tbq

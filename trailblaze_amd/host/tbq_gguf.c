@@ -564,6 +564,35 @@ int tbq_gguf_dense_model(tbq_gguf *g, int max_ctx, tbq_dense_model *m, tbq_dense
     return tbq_dense_workspace_size(m) > 0;   /* validates the shape */
 }
 
+/* One device matrix holding the rows of tensors ids[0..n) in order. */
+static void *fuse_n(tbq_gguf *g, const int *ids, int n) {
+    size_t total = 0;
+    for (int k = 0; k < n; k++) total += g->t[ids[k]].bytes;
+    unsigned char *d = (unsigned char *)own(g, total);
+    if (!d) return NULL;
+    size_t off = 0;
+    for (int k = 0; k < n; k++) {
+        const tensor_t *t = &g->t[ids[k]];
+        if (!tbq_memcpy_h2d(d + off, g->map + g->data_off + t->offset, t->bytes, NULL)) return NULL;
+        off += t->bytes;
+    }
+    return tbq_stream_sync(NULL) ? d : NULL;
+}
+
+/* The E per-expert tensors blk.<layer>.ffn_<kind>.<e>.weight (d0 x d1 each,
+ * one qtype) as one packed device matrix of E * d1 rows; *qt gets their
+ * qtype. */
+static const void *split_experts(tbq_gguf *g, int layer, const char *kind, long long E, long long d0, long long d1,
+                                 int *qt) {
+    int ids[256];
+    for (long long e = 0; e < E; e++) {
+        ids[e] = need(g, 0, e ? *qt : -1, d0, d1, "blk.%d.ffn_%s.%lld.weight", layer, kind, e);
+        if (ids[e] < 0) return NULL;
+        if (!e) *qt = g->t[ids[0]].qtype;
+    }
+    return fuse_n(g, ids, (int)E);
+}
+
 int tbq_gguf_moe_layer(tbq_gguf *g, int layer, tbq_moe_layer *Lout) {
     if (!g || !Lout) return failf("tbq_gguf_moe_layer: bad arguments");
     if (!tbq_init()) return 0;
@@ -573,26 +602,54 @@ int tbq_gguf_moe_layer(tbq_gguf *g, int layer, tbq_moe_layer *Lout) {
     if (!arch_int(g, arch, "embedding_length", &H, 0, 1) || !arch_int(g, arch, "expert_count", &E, 0, 1) ||
         !arch_int(g, arch, "expert_used_count", &K, 0, 1))
         return 0;
+    if (E <= 0 || E > 256) return failf("tbq_gguf_moe_layer: expert_count %lld outside 1..256", E);
     const int ir = need(g, 1, 0, H, E, "blk.%d.ffn_gate_inp.weight", layer);
     if (ir < 0) return 0;
-    const int ig = need(g, 1, -1, H, -1, "blk.%d.ffn_gate_exps.weight", layer);
-    if (ig < 0) return 0;
-    F = g->t[ig].dims[1];
-    const int qt = g->t[ig].qtype;
-    const int iu = need(g, 1, qt, H, F, "blk.%d.ffn_up_exps.weight", layer);
-    const int id = need(g, 1, qt, F, H, "blk.%d.ffn_down_exps.weight", layer);
-    if (iu < 0 || id < 0) return 0;
-    if (g->t[ig].dims[2] != E || g->t[iu].dims[2] != E || g->t[id].dims[2] != E)
-        return failf("tbq_gguf_moe_layer: expert tensors of layer %d do not hold %lld experts", layer, E);
+    char name[160];
+    snprintf(name, sizeof name, "blk.%d.ffn_gate_exps.weight", layer);
+    const void *dg, *du, *dd;
+    int qg, qu, qd;
+    if (tbq_gguf_find(g, name) >= 0) {
+        /* packed: blk.N.ffn_{gate,up,down}_exps, each tensor in its own qtype
+         * (layer4/tb_infer.c:780-816) */
+        const int ig = need(g, 1, -1, H, -1, "blk.%d.ffn_gate_exps.weight", layer);
+        if (ig < 0) return 0;
+        F = g->t[ig].dims[1];
+        const int iu = need(g, 1, -1, H, F, "blk.%d.ffn_up_exps.weight", layer);
+        const int id = need(g, 1, -1, F, H, "blk.%d.ffn_down_exps.weight", layer);
+        if (iu < 0 || id < 0) return 0;
+        if (g->t[ig].dims[2] != E || g->t[iu].dims[2] != E || g->t[id].dims[2] != E)
+            return failf("tbq_gguf_moe_layer: expert tensors of layer %d do not hold %lld experts", layer, E);
+        dg = g->t[ig].dev;
+        du = g->t[iu].dev;
+        dd = g->t[id].dev;
+        qg = g->t[ig].qtype;
+        qu = g->t[iu].qtype;
+        qd = g->t[id].qtype;
+    } else {
+        /* split: blk.N.ffn_{gate,up,down}.<e>.weight, the reference's
+         * fallback (layer4/tb_infer.c:783-791), packed here into the same
+         * device layout */
+        const int i0 = need(g, 0, -1, H, -1, "blk.%d.ffn_gate.0.weight", layer);
+        if (i0 < 0) return failf("tbq_gguf_moe_layer: layer %d has neither ffn_gate_exps nor ffn_gate.0", layer);
+        F = g->t[i0].dims[1];
+        if (!(dg = split_experts(g, layer, "gate", E, H, F, &qg)) || !(du = split_experts(g, layer, "up", E, H, F, &qu)) ||
+            !(dd = split_experts(g, layer, "down", E, F, H, &qd)))
+            return 0;
+    }
+    memset(Lout, 0, sizeof *Lout);
     Lout->H = (int)H;
     Lout->F = (int)F;
     Lout->E = (int)E;
     Lout->top_k = (int)K;
-    Lout->qtype = lq(g, qt);
+    Lout->qtype = lq(g, qg);
+    Lout->qt_gate = lq(g, qg);
+    Lout->qt_up = lq(g, qu);
+    Lout->qt_down = lq(g, qd);
     Lout->router = (const float *)g->t[ir].dev;
     Lout->bias = NULL;
-    Lout->gate = g->t[ig].dev;
-    Lout->up = g->t[iu].dev;
-    Lout->down = g->t[id].dev;
+    Lout->gate = dg;
+    Lout->up = du;
+    Lout->down = dd;
     return 1;
 }

@@ -4,6 +4,8 @@
  * pass that holds its activations in host memory: copy xn and the residual
  * to the device, run the gfx950 MoE layer, copy the output (and the routing)
  * back.  Device buffers are cached between calls and guarded by a mutex.
+ * A prefill mode that does not take the layer (its experts are not all
+ * reference-layout Q4_K) runs the layer on the fp32 decode kernels instead.
  *
  * Buffer layout: the tbq_moe_forward workspace first, at offset 0, so its
  * router arrival counters (the first 256 KiB, which must be zero before a
@@ -32,6 +34,7 @@ static size_t up256(size_t n) { return (n + 255) & ~(size_t)255; }
 int tbq_moe_block_host(const tbq_moe_layer *L, int T, const float *xn_host, const float *resid_host,
                        float *out_host, int *sel_idx_host, float *sel_w_host, int mode) {
     if (!L || T <= 0 || !xn_host || !resid_host || !out_host) return 0;
+    if (mode != TBQ_MOE_FP32 && !tbq_moe_mode_supported(L, mode)) mode = TBQ_MOE_FP32;
     size_t ws = up256(tbq_moe_workspace_size(L, T, mode));
     if (ws == 0) return 0;
     size_t act = up256((size_t)T * L->H * sizeof(float));

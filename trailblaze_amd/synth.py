@@ -55,12 +55,13 @@ def zipf_router_bias(E: int, s: float, c: float, rng: np.random.Generator) -> np
     return (c * np.log(p)).astype(np.float32)
 
 
-def moe_layer(H: int, F: int, E: int, qtype: int, seed: int):
+def moe_layer(H: int, F: int, E: int, qtype: int, seed: int, qt_gate: int = 0, qt_up: int = 0, qt_down: int = 0):
     """Expert tensors in the reference's packed layout: gate/up [E*F rows, H],
-    down [E*H rows, F] (layer4/tb_infer.c:780-806), plus the fp32 router."""
+    down [E*H rows, F] (layer4/tb_infer.c:780-806), plus the fp32 router.
+    qt_gate/qt_up/qt_down give a tensor its own format (0 = qtype)."""
     rng = np.random.default_rng(seed)
     router = router_weights(E, H, rng)
-    gate = kquant_matrix(qtype, E * F, H, rng)
-    up = kquant_matrix(qtype, E * F, H, rng)
-    down = kquant_matrix(qtype, E * H, F, rng)
+    gate = kquant_matrix(qt_gate or qtype, E * F, H, rng)
+    up = kquant_matrix(qt_up or qtype, E * F, H, rng)
+    down = kquant_matrix(qt_down or qtype, E * H, F, rng)
     return router, gate, up, down
