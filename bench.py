@@ -432,7 +432,7 @@ def moe_leg(tb, fm, synth, torch, rng, stream):
             us.append(len(np.unique(idx.cpu().numpy().reshape(T, 8)[:, :k])))
         return float(np.mean(us))
 
-    def decode(lx, T, name):
+    def decode(lx, T, name, expert_bytes=EXPERT_BYTES):
         # 64 different token batches per step
         ntok = 64
         xs = d(synth.activations((ntok, T, H), rng))
@@ -440,7 +440,7 @@ def moe_leg(tb, fm, synth, torch, rng, stream):
         out = torch.empty((T, H), dtype=torch.float32, device="cuda")
         ws_t = torch.zeros(tb.moe_workspace_size(lx[0], T), dtype=torch.uint8, device="cuda")
         U = distinct_experts(lx[0], xs, T)
-        nbytes = router_bytes + U * EXPERT_BYTES + 3 * T * H * 4
+        nbytes = router_bytes + U * expert_bytes + 3 * T * H * 4
         r = {}
         for temp, ls in (("cold", lx), ("warm", lx[:1])):
             def mstep():
@@ -460,6 +460,16 @@ def moe_leg(tb, fm, synth, torch, rng, stream):
     lg = [tb.moe_layer(H, F, E, k, fm.GGML | fm.Q4_K, *c) for c in keep]
     decode(lg, 1, "decode_b1_ggml_q4k")
     del lg
+    # a K-quant mix as llama.cpp writes it: Q4_K gate/up, Q6_K down (each
+    # expert tensor in its own qtype)
+    _, _, _, down6 = synth.moe_layer(H, F, E, fm.Q4_K, seed=3, qt_down=fm.Q6_K)
+    d6 = d(down6)
+    lm = [tb.moe_layer(H, F, E, k, fm.Q4_K, c[0], c[1], c[2], d6 if i == 0 else d6.clone(), qt_down=fm.Q6_K)
+          for i, c in enumerate(keep)]
+    mixed_bytes = 2 * fm.weight_bytes(fm.Q4_K, F, H) + fm.weight_bytes(fm.Q6_K, H, F)
+    for T in (1, 16):
+        decode(lm, T, f"decode_b{T}_q4k_q6k_down", mixed_bytes)
+    del lm, d6
     # prefill, Zipf-skewed routing, grouped MFMA experts
     T = 512
     bias = d(synth.zipf_router_bias(E, 1.1, 1.0, rng))
@@ -563,6 +573,44 @@ def cpu_leg(budget_s=10.0, row_budget_s=0.8):
     dt, n = _time_cpu(lambda: moe_fn(xn, rs, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K), 2 * row_budget_s)
     moe = dict(us_per_layer=round(dt * 1e6, 1), reps=n)
     log(f"CPU MoE block b=1: {dt * 1e3:.2f} ms/layer")
+    # batches: the reference's MoE branch runs token by token
+    # (layer4/tb_infer.c:1068-1075), so b=16 is timed whole and the 512-token
+    # prefill on a 32-token sample of the same Zipf-routed batch, scaled
+    x16 = synth.activations((16, H), rng)
+    r16 = synth.activations((16, H), rng)
+    dt16, n16 = _time_cpu(lambda: moe_fn(x16, r16, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K),
+                          2 * row_budget_s)
+    moe_b16 = dict(us_per_layer=round(dt16 * 1e6, 1), us_per_token=round(dt16 * 1e6 / 16, 1), reps=n16)
+    log(f"CPU MoE block b=16: {dt16 * 1e3:.2f} ms/layer")
+    x32 = synth.activations((32, H), rng)
+    r32 = synth.activations((32, H), rng)
+    dt32, n32 = _time_cpu(lambda: moe_fn(x32, r32, router, gate, up, down, F=F, top_k=k, qtype=fm.Q4_K),
+                          2 * row_budget_s)
+    moe_t512 = dict(us_per_layer=round(dt32 * 1e6 * 512 / 32, 1), us_per_token=round(dt32 * 1e6 / 32, 1),
+                    reps=n32, sample="32 of the 512 tokens (token by token, as the reference), scaled x16")
+    log(f"CPU MoE block T=512 (32-token sample): {dt32 * 512 / 32 * 1e3:.1f} ms/layer")
+    del router, gate, up, down
+    # dense Qwen3-4B decode step, the reference's CPU matvecs
+    # (tb_gguf_tensor_matvec -> tb_dispatch_matvec, layer4/tb_gguf.c:453-461):
+    # one layer's Q4_K matrices timed, x 36 layers, plus the Q6_K lm_head
+    # through the scalar matvec (the dispatch zero-fills Q6_K)
+    from trailblaze_amd.dense import QWEN3_4B as c
+    QR = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
+    lay = [(QR, c.hidden), (c.hidden, c.n_heads * c.head_dim), (2 * c.ffn, c.hidden), (c.hidden, c.ffn)]
+    mats = [(synth.kquant_matrix(fm.Q4_K, M3, K3, rng), M3, K3, synth.activations(K3, rng)) for M3, K3 in lay]
+    layer_mv = avx if avx is not None else (lambda W3, q3, M3, K3, x3: mv(W3, q3, M3, K3, x3))
+    dtl, nl = _time_cpu(lambda: [layer_mv(W3, fm.Q4_K, M3, K3, x3) for W3, M3, K3, x3 in mats], 2 * row_budget_s)
+    del mats
+    lm = synth.kquant_matrix(fm.Q6_K, c.vocab, c.hidden, rng)
+    xl = synth.activations(c.hidden, rng)
+    t0 = time.perf_counter()
+    mv(lm, fm.Q6_K, c.vocab, c.hidden, xl)
+    dt_lm = time.perf_counter() - t0
+    del lm
+    dense = dict(us_per_token=round((dtl * c.n_layers + dt_lm) * 1e6, 0), layer_ms=round(dtl * 1e3, 2),
+                 lm_head_ms=round(dt_lm * 1e3, 1), reps=nl,
+                 sample="one layer's Q4_K matvecs (qkv, o, gate|up, down) x 36 + the Q6_K lm_head, matvecs only")
+    log(f"CPU dense Qwen3-4B step (matvecs): {dense['us_per_token'] / 1e3:.0f} ms/token")
     best = max(out, key=lambda k: out[k]["gbs"])
     cpu_model = ""
     try:
@@ -575,7 +623,35 @@ def cpu_leg(budget_s=10.0, row_budget_s=0.8):
     return dict(value=out[best]["gbs"], unit="GB/s", cores=1, kind=kind,
                 sample=f"{out[best]['reps']} whole Q4_K 4096x4096 matvecs via {best}, 1 pinned thread "
                        f"({cpu_model}, nproc={os.cpu_count()})",
-                detail=out, rows=rows, moe_b1=moe)
+                detail=out, rows=rows, moe_b1=moe, moe_b16=moe_b16, moe_t512=moe_t512, dense=dense)
+
+
+def _proc_children(pid):
+    """Descendants of pid from /proc (pid, command line), for hosts without
+    psutil."""
+    kids, parent = [], {}
+    for d in os.listdir("/proc"):
+        if not d.isdigit():
+            continue
+        try:
+            with open(f"/proc/{d}/stat") as f:
+                st = f.read()
+            parent[int(d)] = int(st[st.rindex(")") + 2:].split()[1])
+        except (OSError, ValueError, IndexError):
+            pass
+    todo = [pid]
+    while todo:
+        p = todo.pop()
+        for c, pp in parent.items():
+            if pp == p:
+                try:
+                    with open(f"/proc/{c}/cmdline", "rb") as f:
+                        cmd = f.read().replace(b"\0", b" ").decode(errors="replace")[:120]
+                except OSError:
+                    cmd = "?"
+                kids.append((c, cmd))
+                todo.append(c)
+    return kids
 
 
 def _reap_children():
@@ -584,6 +660,15 @@ def _reap_children():
     try:
         import psutil
     except ImportError:
+        import signal
+        kids = _proc_children(os.getpid())
+        for pid, cmd in kids:
+            log(f"child process left at exit: pid {pid} {cmd}")
+            try:
+                os.kill(pid, signal.SIGTERM)
+            except OSError:
+                pass
+        log(f"child processes at exit: {len(kids)}")
         return
     kids = psutil.Process().children(recursive=True)
     for c in kids:
@@ -593,6 +678,7 @@ def _reap_children():
         except psutil.Error:
             pass
     psutil.wait_procs(kids, timeout=5)
+    log(f"child processes at exit: {len(kids)}")
 
 
 def main():
@@ -629,6 +715,9 @@ def main():
                    "copies_per_step": h["ncopy"]},
         "roofline": {"bound": "hbm", "achieved": round(h["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(),
+                     "traffic_source": "read from profiles/q4k_matvec_4096x4096_pmc.txt (rocprofv3 --pmc "
+                                       "FETCH_SIZE + WRITE_SIZE per dispatch, copy-calibrated), not measured in "
+                                       "this run",
                      "kernel": "k_mv_q4k_xr (Q4_K int-dot)", "us_per_launch": round(h["us_per_launch"], 3),
                      "bytes_per_launch": h["bytes_per_launch"]},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
@@ -653,11 +742,18 @@ def cpu_rows_vs_gpu(cpu, res):
         g = gpu.get((r["qt"], r["M"], r["K"]))
         rows.append(dict(r, gpu_us=None if g is None else round(g, 2),
                          gpu_speedup=None if g is None else round(r["ms"] * 1e3 / g, 1)))
-    m = (res.get("moe") or {}).get("decode_b1")
-    moe = dict(cpu["moe_b1"], gpu_us_cold=None if m is None else m["us_per_layer"])
-    if m is not None:
-        moe["gpu_speedup"] = round(moe["us_per_layer"] / m["us_per_layer"], 1)
-    return dict(matvec=rows, moe_b1=moe, cores=1, kind=cpu["kind"])
+    def beside(row, gpu_us):
+        r = dict(row, gpu_us=None if gpu_us is None else round(gpu_us, 2))
+        if gpu_us:
+            r["gpu_speedup"] = round(row["us_per_layer" if "us_per_layer" in row else "us_per_token"] / gpu_us, 1)
+        return r
+    moe_res = res.get("moe") or {}
+    g = lambda name: (moe_res.get(name) or {}).get("us_per_layer")
+    dense_gpu = (res.get("dense") or {}).get("us_per_token")
+    return dict(matvec=rows, moe_b1=beside(cpu["moe_b1"], g("decode_b1")),
+                moe_b16=beside(cpu["moe_b16"], g("decode_b16")),
+                moe_t512=beside(cpu["moe_t512"], g("prefill_512_fp16_mfma")),
+                dense_step=beside(cpu["dense"], dense_gpu), cores=1, kind=cpu["kind"])
 
 
 if __name__ == "__main__":

@@ -249,12 +249,20 @@ int tbq_dense_prefill_batched(const tbq_dense_model *m);
 int tbq_quantize_q8k(const float *x, long long n, void *blocks, void *stream);
 
 /* ---- prefill GEMM --------------------------------------------------------- */
-/* C[T][N] (row stride ldc >= N floats) = X[T][K] . W[N][K]^T with the batched
- * prefill's GEMM (hand-written fp16 MFMA, fp32 accumulate): X fp16 rows (IEEE
- * halves); W rows of IEEE fp16 halves (wqt = 1, TBQ's F16 id, taken as IEEE
- * halves here) or Q4_K in the reference's layout (wqt = 12), dequantised
- * inside the GEMM to the fp16 values the prefill's fp16 weights hold.  N a
- * multiple of 4, K of 256, T >= 1.  workspace: tbq_gemm_workspace_size()
+/* C[T][N] (row stride ldc >= N floats, ldc a multiple of 4) = X[T][K] .
+ * W[N][K]^T with the batched prefill's GEMM (hand-written fp16 MFMA, fp32
+ * accumulate): X fp16 rows (IEEE halves); W rows of IEEE fp16 halves (wqt =
+ * 1, TBQ's F16 id, taken as IEEE halves here) or Q4_K in the reference's
+ * layout (wqt = 12), dequantised inside the GEMM to fp16: per sub-block, with
+ * S = d*scale and M = dmin*min (fp32), each nibble q becomes the fp16 number
+ * 1 + q/16 and one packed fp16 fma with the fp16 roundings of 16*S and of
+ * C = -16*S - M gives 16*S*(1 + q/16) + C = S*q - M before the result's own
+ * rounding.  A weight can therefore differ from fl16(S*q - M) by up to about
+ * ulp(16*S)/2 + ulp(16*S + M)/2 (at d, dmin ~ 1e-2 that is ~4e-4 relative to
+ * the sub-block's largest weight); the products stay within 1e-3 relative L2
+ * of the fp32 dequantised weights (tests/test_gpu_gemm.py).  Weights must
+ * keep 16*d*63 + dmin*63 below 65504 (the fp16 range).  N a multiple of 4,
+ * K of 256, T >= 1, X below 2 GiB.  workspace: tbq_gemm_workspace_size()
  * bytes (split-K partial sums; may be 0).  No counterpart in the reference
  * (it prefills token by token, layer4/tb_infer.c:1068-1075). */
 size_t tbq_gemm_workspace_size(int T, int N, int K);
