@@ -200,7 +200,7 @@ __global__ __launch_bounds__(64) void k_topk(const float *__restrict__ logits, i
 // registers, and the row's last lane adds them in k order with
 // v_add_f32_dpp row_shr (one instruction per element, no LDS).  The last
 // workgroup of a token (per-token arrival counter, reset by that workgroup)
-// runs the softmax/top-k.  grid = (T, ceil(E/4)), 64 threads.
+// runs the softmax/top-k.  grid = (ceil(E/4), T), 64 threads.
 // ---------------------------------------------------------------------------
 // One 64-element block of the chain: lane j of each 16-lane row holds w and
 // x for k = 4j..4j+3 of the block; the products are formed in place, then
@@ -284,8 +284,8 @@ __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn,
     constexpr int H = 64 * M, NC = M / RD_CH;
     static_assert(M % RD_CH == 0, "H must be a multiple of 512");
     __shared__ float P[64 * NJ + 16];
-    const int t = blockIdx.x, lane = threadIdx.x, r = lane >> 4, j = lane & 15;
-    const int e = blockIdx.y * 4 + r;
+    const int t = blockIdx.y, lane = threadIdx.x, r = lane >> 4, j = lane & 15;
+    const int e = blockIdx.x * 4 + r;
     const bool ev = e < E;
     const float4 *w4 = reinterpret_cast<const float4 *>(Wr + (long long)(ev ? e : 0) * H);
     const float4 *x4 = reinterpret_cast<const float4 *>(xn + (long long)t * H);
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn,
     unsigned ticket = 0;
     if (lane == 0) ticket = __hip_atomic_fetch_add(counters + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     ticket = (unsigned)__builtin_amdgcn_readfirstlane((int)ticket);
-    if (ticket != gridDim.y - 1) return;
+    if (ticket != gridDim.x - 1) return;
     asm volatile("" ::: "memory");
     topk_wave<NJ>(logits + (long long)t * E, E, top_k, t, P, sel_idx, sel_w);
     if (lane == 0) counters[t] = 0u;
@@ -767,6 +767,125 @@ __global__ __launch_bounds__(RB_THREADS) void k_router_batch(const float *__rest
     }
 }
 
+// ---------------------------------------------------------------------------
+// Batch router, tiled (T >= 32): a workgroup of 4 waves owns 16 tokens x 16
+// experts; wave w takes tokens 8*(w&1).. and experts 8*(w>>1).., and lane l
+// runs the chain of token l&7, expert l>>3 of that 8x8 block:
+// acc = fl(acc + fl(w*x)) over k ascending, one chain per lane (one wave per
+// SIMD at T = 512, E = 128).  Both operands come from LDS 4 k at a time
+// (ds_read_b128); a wave instruction touches only 8 distinct 16-byte rows of
+// each tile, each read by 8 lanes, so the LDS serves it as broadcasts in one
+// pass instead of 64 distinct addresses, and the dependent add chain, not
+// LDS bandwidth, bounds the kernel.  Each chunk of 256 k of the 16 token and
+// 16 expert rows (32 KB) is loaded with coalesced 16-byte loads while the
+// previous chunk is summed.  Requires H % 256 == 0, E % 16 == 0.
+// grid = (ceil(T/16), E/16 (+1 row of fp16-conversion workgroups)).
+// ---------------------------------------------------------------------------
+constexpr int RTL_T = 16, RTL_E = 16, RTL_KC = 256;
+constexpr int RTL_ROW = RTL_KC + 4;   // floats per LDS row: consecutive rows 4 banks apart
+constexpr int RTL_THREADS = 256;
+constexpr int RTL_LPT = RTL_KC / 4 / 16;   // float4 of each tile row a loader thread moves per chunk
+struct RtlShared {
+    rb_f4 x[2][RTL_T][RTL_ROW / 4];
+    rb_f4 w[2][RTL_E][RTL_ROW / 4];
+};
+
+__global__ __launch_bounds__(RTL_THREADS) void k_router_tile(const float *__restrict__ xn, const float *__restrict__ Wr,
+                                                             const float *__restrict__ bias, int T, int H, int E,
+                                                             float *__restrict__ logits, _Float16 *__restrict__ x16,
+                                                             float *__restrict__ xinv) {
+    if (x16 && blockIdx.y == gridDim.y - 1) {   // uniform: the fp16 rows of this workgroup's 16 tokens
+        for (int i = (int)(threadIdx.x >> 6); i < RTL_T; i += RTL_THREADS / 64) {
+            const int t = blockIdx.x * RTL_T + i;
+            if (t < T) rb_row_f16(xn + (long long)t * H, H, x16 + (long long)t * H, xinv + t);
+        }
+        return;
+    }
+    extern __shared__ rb_f4 rtl_lds[];
+    RtlShared &sh = *reinterpret_cast<RtlShared *>(rtl_lds);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t0 = blockIdx.x * RTL_T, e0 = blockIdx.y * RTL_E;
+    // loader role: row r = tid / 16 of the x tile and of the W tile, float4
+    // q = tid % 16 + 16 i of the chunk (tokens >= T read the last token; never
+    // stored).  A chunk (256 k, 32 rows, 32 KB) is loaded while the previous
+    // one is summed: 256 dependent adds cover the loads' latency.
+    const int lr = tid >> 4, lq = tid & 15;
+    const rb_f4 *xsrc = reinterpret_cast<const rb_f4 *>(xn + (long long)(t0 + lr < T ? t0 + lr : T - 1) * H) + lq;
+    const rb_f4 *wsrc = reinterpret_cast<const rb_f4 *>(Wr + (long long)(e0 + lr) * H) + lq;
+    // chain role
+    const int tl = 8 * (wave & 1) + (lane & 7), el = 8 * (wave >> 1) + (lane >> 3);
+    const int NC = H / RTL_KC;
+    rb_f4 xr[RTL_LPT], wr[RTL_LPT];
+#pragma unroll
+    for (int i = 0; i < RTL_LPT; i++) {
+        xr[i] = xsrc[16 * i];
+        wr[i] = wsrc[16 * i];
+    }
+#pragma unroll
+    for (int i = 0; i < RTL_LPT; i++) {
+        sh.x[0][lr][lq + 16 * i] = xr[i];
+        sh.w[0][lr][lq + 16 * i] = wr[i];
+    }
+    __syncthreads();
+    float acc = 0.f;
+    for (int c = 0; c < NC; c++) {
+        const int b = c & 1;
+        if (c + 1 < NC) {
+#pragma unroll
+            for (int i = 0; i < RTL_LPT; i++) {
+                xr[i] = xsrc[(c + 1) * (RTL_KC / 4) + 16 * i];
+                wr[i] = wsrc[(c + 1) * (RTL_KC / 4) + 16 * i];
+            }
+        }
+        // 16 k per group: the next group's LDS reads are issued before the
+        // current group's arithmetic (two register slots); the empty asm
+        // statements (tied to acc) keep the compiler from hoisting more of
+        // the chunk's reads, which would need more registers than one wave has
+        rb_f4 xa[4], wa[4], xb[4], wb[4];
+        auto ld = [&](int g, rb_f4 (&xv)[4], rb_f4 (&wv)[4]) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                xv[q] = sh.x[b][tl][4 * g + q];
+                wv[q] = sh.w[b][el][4 * g + q];
+            }
+        };
+        auto sum = [&](const rb_f4 (&xv)[4], const rb_f4 (&wv)[4]) {
+            float p[16];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                p[4 * q] = wv[q].x * xv[q].x;
+                p[4 * q + 1] = wv[q].y * xv[q].y;
+                p[4 * q + 2] = wv[q].z * xv[q].z;
+                p[4 * q + 3] = wv[q].w * xv[q].w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc = acc + p[i];
+            asm volatile("" : "+v"(acc));
+        };
+        ld(0, xa, wa);
+#pragma unroll 1
+        for (int g = 0; g < RTL_KC / 16; g += 2) {
+            ld(g + 1, xb, wb);
+            sum(xa, wa);
+            if (g + 2 < RTL_KC / 16) ld(g + 2, xa, wa);
+            sum(xb, wb);
+        }
+        if (c + 1 < NC) {
+#pragma unroll
+            for (int i = 0; i < RTL_LPT; i++) {
+                sh.x[b ^ 1][lr][lq + 16 * i] = xr[i];
+                sh.w[b ^ 1][lr][lq + 16 * i] = wr[i];
+            }
+        }
+        __syncthreads();
+    }
+    const int t = t0 + tl, e = e0 + el;
+    if (t < T) {
+        if (bias) acc = acc + bias[e];
+        logits[(long long)t * E + e] = acc;
+    }
+}
+
 template <int NJ>
 static hipError_t launch_topk_t(const float *logits, int T, int E, int top_k, int *sel_idx, float *sel_w, hipStream_t st) {
     hipLaunchKernelGGL((k_topk<NJ>), dim3(T), dim3(64), 0, st, logits, E, top_k, sel_idx, sel_w);
@@ -782,7 +901,10 @@ static hipError_t launch_topk(const float *logits, int T, int E, int top_k, int 
 template <int M, int NJ>
 static hipError_t launch_router_dpp_t(const float *xn, const float *router, const float *bias, int T, int E, int top_k,
                                       float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st) {
-    dim3 grid(T, (E + 3) / 4);
+    // expert groups along x: workgroup i runs on XCD i % 8, so each XCD's L2
+    // holds one eighth of the router rows for every token of the batch
+    // (tokens along x would make every XCD read all of them)
+    dim3 grid((E + 3) / 4, T);
     hipLaunchKernelGGL((k_router_dpp<M, NJ>), grid, dim3(64), 0, st, xn, router, bias, E, top_k, logits, counters,
                        sel_idx, sel_w);
     return hipGetLastError();
@@ -810,6 +932,16 @@ hipError_t launch_router(const float *xn, const float *router, const float *bias
         if (H == 512) return launch_router_dpp<8>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
     }
     const size_t lds = (size_t)H * 4 + 2 * RT_TILE_FLOATS * 4;
+    if (T >= 32 && H % RTL_KC == 0 && E % RTL_E == 0) {
+        const bool rows = x16 && xinv && H <= 8192;
+        hipLaunchKernelGGL(k_router_tile, dim3((T + RTL_T - 1) / RTL_T, E / RTL_E + (rows ? 1 : 0)),
+                           dim3(RTL_THREADS), sizeof(RtlShared), st, xn, router, bias, T, H, E, logits,
+                           rows ? x16 : nullptr, xinv);
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        if (x16_done) *x16_done = rows;
+        return launch_topk(logits, T, E, top_k, sel_idx, sel_w, st);
+    }
     if (T >= 32 && H % RB_KC == 0 && E % 64 == 0) {
         const bool rows = x16 && xinv && H <= 8192;
         hipLaunchKernelGGL(k_router_batch, dim3((T + RB_TOK - 1) / RB_TOK, (E + 63) / 64 + (rows ? 1 : 0)),
