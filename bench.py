@@ -480,10 +480,13 @@ def moe_leg(tb, fm, synth, torch, rng, stream):
     U = distinct_experts(Lb, xs[None], T)
     nbytes = router_bytes + U * EXPERT_BYTES + 3 * T * H * 4
     flops = 2.0 * T * k * 3 * H * F + 2.0 * T * E * H
-    for name, mode, peak in (("prefill_512_fp16_mfma", tb.TBQ_MOE_BF16, MFMA_PEAK_TFLOPS["fp16"]),
-                             ("prefill_512_int8_mfma", tb.TBQ_MOE_I8, MFMA_PEAK_TFLOPS["int8"])):
-        ws_t = torch.zeros(tb.moe_workspace_size(Lb, T, mode), dtype=torch.uint8, device="cuda")
-        sec = time_region(lambda: tb.moe_forward(Lb, T, xs, rs, out, workspace=ws_t, mode=mode), 20, 3,
+    # the same expert bytes read in ggml's Q4_K layout (fp16 MFMA only)
+    Lg = tb.moe_layer(H, F, E, k, fm.GGML | fm.Q4_K, *keep[0], bias=bias)
+    for name, mode, peak, Lx in (("prefill_512_fp16_mfma", tb.TBQ_MOE_BF16, MFMA_PEAK_TFLOPS["fp16"], Lb),
+                                 ("prefill_512_int8_mfma", tb.TBQ_MOE_I8, MFMA_PEAK_TFLOPS["int8"], Lb),
+                                 ("prefill_512_fp16_mfma_ggml_q4k", tb.TBQ_MOE_BF16, MFMA_PEAK_TFLOPS["fp16"], Lg)):
+        ws_t = torch.zeros(tb.moe_workspace_size(Lx, T, mode), dtype=torch.uint8, device="cuda")
+        sec = time_region(lambda: tb.moe_forward(Lx, T, xs, rs, out, workspace=ws_t, mode=mode), 20, 3,
                           stream) / 20
         tf = flops / sec / 1e12
         moe[name] = dict(us_per_layer=round(sec * 1e6, 2), us_per_token=round(sec * 1e6 / T, 4),

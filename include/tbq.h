@@ -20,7 +20,7 @@
  * K-quant scales differently and decodes fp16 subnormals as IEEE.  Every
  * call that takes a qtype accepts these ids (for F32, BF16 and Q8_K the two
  * layouts are one); the prefill MFMA modes of tbq_moe_forward take only
- * the reference's Q4_K.
+ * Q4_K (TBQ_MOE_I8 only the reference's layout of it).
  */
 #ifndef TBQ_H
 #define TBQ_H
@@ -124,9 +124,9 @@ typedef struct {
 
 /* 1 if tbq_moe_forward takes layer L in `mode`.  TBQ_MOE_FP32 takes every
  * valid layer; the two prefill modes take layers whose gate, up and down
- * are all Q4_K in the reference's layout, with H and F in {256, 512, 768,
- * 1024, 1536, 2048, 3072, 4096}.  0 with tbq_last_error() for an invalid
- * layer. */
+ * are all Q4_K in the reference's layout (TBQ_MOE_BF16 also all three in
+ * ggml's, TBQ_GGML | 12), with H and F in {256, 512, 768, 1024, 1536, 2048,
+ * 3072, 4096}.  0 with tbq_last_error() for an invalid layer. */
 int tbq_moe_mode_supported(const tbq_moe_layer *L, int mode);
 
 /* Workspace bytes tbq_moe_forward needs for T tokens in `mode` (T <= 65536). */

@@ -23,6 +23,7 @@ from trailblaze_amd import synth
 pytestmark = pytest.mark.gpu
 MATVEC_TOL = 1e-5
 DENSE_TOL = 1e-4
+PREFILL_TOL = 1e-2
 G = fm.GGML
 FORMATS = [G | fm.Q2_K, G | fm.Q3_K, G | fm.Q4_K, G | fm.Q5_K, G | fm.Q6_K, G | fm.Q8_0, G | fm.Q4_0]
 
@@ -165,8 +166,15 @@ def test_ggml_moe_decode(oracle, qt):
     assert np.array_equal(host(idx).reshape(T, 8), ridx)
     assert bits_equal(host(w).reshape(T, 8), rw)
     assert rel_l2(host(out).reshape(T, H) - resid, ref - resid) <= MATVEC_TOL
-    with pytest.raises(tb.TbqError, match="prefill"):
-        tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws, mode=tb.TBQ_MOE_BF16)
+    if qt != G | fm.Q4_K:   # the fp16 MFMA prefill decodes Q4_K only
+        with pytest.raises(tb.TbqError, match="prefill"):
+            tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws, mode=tb.TBQ_MOE_BF16)
+    else:
+        assert not tb.moe_mode_supported(L, tb.TBQ_MOE_I8)
+        ws16 = torch.zeros(tb.moe_workspace_size(L, T, tb.TBQ_MOE_BF16), dtype=torch.uint8, device="cuda")
+        tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws16, mode=tb.TBQ_MOE_BF16)
+        assert np.array_equal(host(idx).reshape(T, 8), ridx)
+        assert rel_l2(host(out).reshape(T, H) - resid, ref - resid) <= PREFILL_TOL
 
 
 @pytest.mark.parametrize("T", [1, 5])
@@ -189,6 +197,37 @@ def test_ggml_moe_decode_config(oracle, T):
     assert np.array_equal(host(idx).reshape(T, 8), ridx)
     assert bits_equal(host(w).reshape(T, 8), rw)
     assert rel_l2(host(out).reshape(T, H) - resid, ref - resid) <= MATVEC_TOL
+
+
+@pytest.mark.parametrize("T", [40, 512])
+def test_ggml_moe_prefill_mfma(oracle, T):
+    """The fp16 MFMA prefill reading ggml's Q4_K layout (as llama.cpp files
+    hold the experts) at the Qwen3-30B-A3B shape with a Zipf(1.1)-skewed
+    router: every token routed exactly, outputs within 1e-2 of the oracle on
+    a sample of tokens (tokens are independent)."""
+    import torch
+    H, F, E, k = 2048, 768, 128, 8
+    qt = G | fm.Q4_K
+    router, gate, up, down = synth.moe_layer(H, F, E, qt, seed=33)
+    rng = np.random.default_rng(300 + T)
+    bias = synth.zipf_router_bias(E, 1.1, 1.0, rng)
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    L = tb.moe_layer(H, F, E, k, qt, dev(router), dev(gate), dev(up), dev(down), dev(bias))
+    assert tb.moe_mode_supported(L, tb.TBQ_MOE_BF16)
+    out, idx, w = empty(T * H, torch.float32), empty(T * 8, torch.int32), empty(T * 8, torch.float32)
+    ws = torch.zeros(tb.moe_workspace_size(L, T, tb.TBQ_MOE_BF16), dtype=torch.uint8, device="cuda")
+    print("ggml moe prefill T=", T, flush=True)
+    tb.moe_forward(L, T, dev(xn), dev(resid), out, idx, w, workspace=ws, mode=tb.TBQ_MOE_BF16)
+    out, idx, w = host(out).reshape(T, H), host(idx).reshape(T, 8), host(w).reshape(T, 8)
+    lg = oracle.router_logits(xn, router, bias)
+    for t in range(T):
+        ri, rw = oracle.route(lg[t], k)
+        assert np.array_equal(idx[t], ri), t
+        assert bits_equal(w[t], rw), t
+    sample = np.sort(rng.choice(T, min(T, 32), replace=False))
+    ref, _, _ = oracle.moe(xn[sample], resid[sample], router, gate, up, down, F=F, top_k=k, qtype=qt, bias=bias)
+    assert rel_l2(out[sample] - resid[sample], ref - resid[sample]) <= PREFILL_TOL
 
 
 def test_ggml_gguf_dense_file(tmp_path, oracle):

@@ -279,12 +279,14 @@ static int check_moe(const tbq_moe_layer *L, int T) {
 }
 
 // The prefill MFMA modes take layers whose three expert tensors are Q4_K in
-// the reference's layout.
+// the reference's layout, and the fp16 one also all three in ggml's.
 static bool moe_mode_ok(const tbq_moe_layer *L, int mode) {
     if (mode == TBQ_MOE_FP32) return true;
     if (mode != TBQ_MOE_BF16 && mode != TBQ_MOE_I8) return false;
     const MoeQts q = moe_qts(L);
-    return q.g == QT_Q4_K && q.u == QT_Q4_K && q.d == QT_Q4_K && gemm_k_supported(L->H) && gemm_k_supported(L->F);
+    const bool ref = q.g == QT_Q4_K && q.u == QT_Q4_K && q.d == QT_Q4_K;
+    const bool gg = mode == TBQ_MOE_BF16 && q.g == QT_GQ4_K && q.u == QT_GQ4_K && q.d == QT_GQ4_K;
+    return (ref || gg) && gemm_k_supported(L->H) && gemm_k_supported(L->F);
 }
 
 int tbq_moe_mode_supported(const tbq_moe_layer *L, int mode) {
@@ -302,8 +304,8 @@ int tbq_moe_forward(const tbq_moe_layer *L, int T, const float *xn, const float 
         return fail("tbq_moe_forward: unknown mode %d", mode);
     if (!moe_mode_ok(L, mode))
         return fail("tbq_moe_forward: the prefill MFMA modes take layers whose gate, up and down are all Q4_K "
-                    "(reference layout) with H and F in {256, 512, 768, 1024, 1536, 2048, 3072, 4096}; "
-                    "use TBQ_MOE_FP32 for this layer");
+                    "(the reference's layout; TBQ_MOE_BF16 also ggml's) with H and F in {256, 512, 768, 1024, "
+                    "1536, 2048, 3072, 4096}; use TBQ_MOE_FP32 for this layer");
     if (!xn || !resid || !out || !aligned16(xn) || !aligned16(resid) || !aligned16(out))
         return fail("tbq_moe_forward: null or misaligned activation pointer");
     if (T == 0) return 1;

@@ -48,9 +48,12 @@
 
 namespace tbq {
 
-// The prefill kernels decode Q4_K in the reference's layout for all three
-// expert tensors.
+// The int8 prefill decodes Q4_K in the reference's layout for all three
+// expert tensors; the fp16 one also takes all three in ggml's layout.
 static bool prefill_q4k_layer(const MoeArgs &a) { return a.qg == QT_Q4_K && a.qu == QT_Q4_K && a.qd == QT_Q4_K; }
+static bool prefill_gq4k_layer(const MoeArgs &a) {
+    return a.qg == QT_GQ4_K && a.qu == QT_GQ4_K && a.qd == QT_GQ4_K;
+}
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -288,8 +291,10 @@ struct Q4Pair {
     u32x4 h, q0, q1;
 };
 
+template <bool GG>
 __device__ __forceinline__ void q4pair_load(const uint8_t *sb, int j0, Q4Pair &r) {
-    r.h = *reinterpret_cast<const u32x4 *>(sb + (j0 < 4 ? 0 : 16));
+    // ggml's scales and mins of all eight sub-blocks are in bytes 4..15
+    r.h = *reinterpret_cast<const u32x4 *>(sb + (GG || j0 < 4 ? 0 : 16));
     r.q0 = *reinterpret_cast<const u32x4 *>(sb + 16 + 16 * j0);
     r.q1 = *reinterpret_cast<const u32x4 *>(sb + 32 + 16 * j0);
 }
@@ -328,6 +333,42 @@ __device__ __forceinline__ void q4pair_frags(const Q4Pair &r, unsigned dd, unsig
     a[3] = q4dword_f16(q.w, S16, C);
 }
 
+// ggml's layout (QT_GQ4_K): the 32 quant bytes of sub-blocks j0, j0 + 1 (j0
+// even) hold sub-block j0's element i in the low nibble of byte i and
+// sub-block j0 + 1's in the high nibble; the scale and min of sub-block j
+// follow ggml's get_scale_min_k4 over scale bytes 4..15; d and dmin are IEEE
+// halves.  Two quant dwords (bytes 8ks .. 8ks + 7) -> the eight fp16 weights
+// S q - Mn of step ks: a byte pair's two nibbles are spread into the two
+// halves by one 24-bit multiply (bits 6..9 and 22..25 of y * 0x4040, y the
+// pair's nibbles at bits 0..3 and 8..11) and one v_bitop3, then the packed
+// fma as in the reference's layout.
+__device__ __forceinline__ f16x8 gq4dwords_f16(unsigned d0, unsigned d1, bool hi, f16x2 S16, f16x2 C) {
+    const unsigned m0 = (hi ? d0 >> 4 : d0) & 0x0F0F0F0Fu, m1 = (hi ? d1 >> 4 : d1) & 0x0F0F0F0Fu;
+    const unsigned y[4] = {m0 & 0xFFFFu, m0 >> 16, m1 & 0xFFFFu, m1 >> 16};
+    unsigned o[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const unsigned t = __builtin_amdgcn_bitop3_b32(__umul24(y[b], 0x4040u), 0x03C003C0u, 0x3C003C00u, 0xEA);
+        o[b] = __builtin_bit_cast(unsigned, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, t), S16, C));
+    }
+    return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
+}
+
+__device__ __forceinline__ void gq4pair_frags(const Q4Pair &r, int j0, int u, f16x8 *a) {
+    const int jj = j0 + u, k = jj & 3;
+    const bool hi = jj >= 4;
+    const unsigned y = r.h.y >> (8 * k), z = r.h.z >> (8 * k), w = r.h.w >> (8 * k);
+    const int sc = hi ? (int)((w & 15u) | (((y >> 6) & 3u) << 4)) : (int)(y & 63u);
+    const int mn = hi ? (int)(((w >> 4) & 15u) | (((z >> 6) & 3u) << 4)) : (int)(z & 63u);
+    const float S = h2f(r.h.x) * (float)sc, Mn = h2f(r.h.x >> 16) * (float)mn;
+    const _Float16 s16 = (_Float16)(16.f * S), c = (_Float16)(-(float)s16 - Mn);
+    const f16x2 S16 = {s16, s16}, C = {c, c};
+    a[0] = gq4dwords_f16(r.q0.x, r.q0.y, u, S16, C);
+    a[1] = gq4dwords_f16(r.q0.z, r.q0.w, u, S16, C);
+    a[2] = gq4dwords_f16(r.q1.x, r.q1.y, u, S16, C);
+    a[3] = gq4dwords_f16(r.q1.z, r.q1.w, u, S16, C);
+}
+
 // ---------------------------------------------------------------------------
 // Expert tile GEMM.  Work items are (tile, row block) pairs, tile-major
 // (ncb = F/PF_COLS row blocks for MODE 0, H/PF_ROWS for MODE 1), the tiles
@@ -348,7 +389,7 @@ __device__ __forceinline__ void q4pair_frags(const Q4Pair &r, unsigned dd, unsig
 // 8 halves at 8*(it%16)).  Every global load is unconditional (indices
 // clamped, results selected), so the compiler's wait counts stay exact.
 // ---------------------------------------------------------------------------
-template <int MODE, int NS>
+template <int MODE, int NS, bool GG>
 __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1,
                                                         const _Float16 *__restrict__ X, int x_rows,
                                                         const float *__restrict__ xinv, const int *__restrict__ tpair,
@@ -381,7 +422,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
     } else {
         wrow = W0 + ((long long)tl.e * H + cb * PF_ROWS + 32 * wave + li) * rb;
     }
-    auto wload = [&](Q4Pair &w, int s) { q4pair_load(wrow + (long long)(s >> 1) * 144, 4 * (s & 1) + 2 * lh, w); };
+    auto wload = [&](Q4Pair &w, int s) { q4pair_load<GG>(wrow + (long long)(s >> 1) * 144, 4 * (s & 1) + 2 * lh, w); };
     Q4Pair w0, w1, w2;
     wload(w0, 0);
     wload(w1, min(1, NS - 1));
@@ -467,15 +508,24 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
             if (s < NS) {
                 const int j0 = 4 * (s & 1) + 2 * lh;
                 const _Float16 *xb = xfrag + (s & 1) * PF_MT * PF_LD;
-                const bool odd = s & 1;
-                const unsigned dd = odd ? kdd : wc.h.x, sw = odd ? ksw : wc.h.y, mw = odd ? wc.h.x : wc.h.z;
-                kdd = dd;
-                ksw = odd ? ksw : wc.h.w;
+                if constexpr (GG) {
 #pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    f16x8 a[4];
-                    q4pair_frags(wc, dd, sw, mw, j0, u, a);
-                    mma(a, xb, u);
+                    for (int u = 0; u < 2; u++) {
+                        f16x8 a[4];
+                        gq4pair_frags(wc, j0, u, a);
+                        mma(a, xb, u);
+                    }
+                } else {
+                    const bool odd = s & 1;
+                    const unsigned dd = odd ? kdd : wc.h.x, sw = odd ? ksw : wc.h.y, mw = odd ? wc.h.x : wc.h.z;
+                    kdd = dd;
+                    ksw = odd ? ksw : wc.h.w;
+#pragma unroll
+                    for (int u = 0; u < 2; u++) {
+                        f16x8 a[4];
+                        q4pair_frags(wc, dd, sw, mw, j0, u, a);
+                        mma(a, xb, u);
+                    }
                 }
                 // buffer last read in chunk s - 1, before the previous barrier
                 if (s + 1 < NS) xstore((s + 1) & 1);
@@ -872,19 +922,19 @@ static unsigned pf_grid(unsigned max_items) {
     return max_items < g ? max_items : g;
 }
 
-template <int MODE>
+template <int MODE, bool GG>
 static hipError_t launch_moe_f16(int ns, unsigned nwg, hipStream_t st, const uint8_t *W0, const uint8_t *W1,
                                  const _Float16 *X, int x_rows, const float *xinv, const int *tpair, const int *ttok,
                                  const PfTile *tiles, int *ntiles, int ncb, int H, int F, float *out) {
     // more than 64 KiB of dynamic LDS is opted into once per kernel
 #define TBQ_NS(N)                                                                                                  \
     case N: {                                                                                                      \
-        static const hipError_t attr = hipFuncSetAttribute((const void *)k_moe_f16<MODE, N>,                       \
+        static const hipError_t attr = hipFuncSetAttribute((const void *)k_moe_f16<MODE, N, GG>,                   \
                                                            hipFuncAttributeMaxDynamicSharedMemorySize,             \
                                                            (int)PF_LDS_BYTES);                                     \
         if (attr != hipSuccess) return attr;                                                                       \
-        hipLaunchKernelGGL((k_moe_f16<MODE, N>), dim3(nwg), dim3(PF_THREADS), PF_LDS_BYTES, st, W0, W1, X, x_rows, \
-                           xinv, tpair, ttok, tiles, ntiles, ncb, H, F, out);                                      \
+        hipLaunchKernelGGL((k_moe_f16<MODE, N, GG>), dim3(nwg), dim3(PF_THREADS), PF_LDS_BYTES, st, W0, W1, X,     \
+                           x_rows, xinv, tpair, ttok, tiles, ntiles, ncb, H, F, out);                              \
         break;                                                                                                     \
     }
     switch (ns) {
@@ -1001,8 +1051,9 @@ hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t s
         const int n = K / PF_KC;
         return K % 256 == 0 && gemm_k_supported(K);
     };
-    if (!prefill_q4k_layer(a) || !ok_k(a.H) || !ok_k(a.F) || a.H % PF_ROWS || a.F % PF_COLS || a.T > 65536 ||
-        a.E > 256)
+    const bool gg = prefill_gq4k_layer(a);
+    if (!(prefill_q4k_layer(a) || gg) || !ok_k(a.H) || !ok_k(a.F) || a.H % PF_ROWS || a.F % PF_COLS ||
+        a.T > 65536 || a.E > 256)
         return hipErrorNotSupported;
     const size_t P = (size_t)a.T * a.k;
     const int max_tiles = (int)((P + PF_MT - 1) / PF_MT + a.E);
@@ -1026,13 +1077,19 @@ hipError_t launch_moe_prefill_q4k(const MoeArgs &a, void *scratch, hipStream_t s
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     const int ncb0 = a.F / PF_COLS, ncb1 = a.H / PF_ROWS;
-    err = launch_moe_f16<0>(a.H / PF_KC, pf_grid((unsigned)(max_tiles * ncb0)), st, (const uint8_t *)a.gate,
-                            (const uint8_t *)a.up, x16, a.T, xinv, tpair, ttok, tiles, ntiles, ncb0, a.H, a.F, a.act);
+    const unsigned g0 = pf_grid((unsigned)(max_tiles * ncb0)), g1 = pf_grid((unsigned)(max_tiles * ncb1));
+    const uint8_t *wg = (const uint8_t *)a.gate, *wu = (const uint8_t *)a.up, *wd = (const uint8_t *)a.down;
+    err = gg ? launch_moe_f16<0, true>(a.H / PF_KC, g0, st, wg, wu, x16, a.T, xinv, tpair, ttok, tiles, ntiles, ncb0,
+                                       a.H, a.F, a.act)
+             : launch_moe_f16<0, false>(a.H / PF_KC, g0, st, wg, wu, x16, a.T, xinv, tpair, ttok, tiles, ntiles,
+                                        ncb0, a.H, a.F, a.act);
     if (err != hipSuccess) return err;
     err = launch_rows_f16(a.act, (int)P, a.F, act16, ainv, st);
     if (err != hipSuccess) return err;
-    return launch_moe_f16<1>(a.F / PF_KC, pf_grid((unsigned)(max_tiles * ncb1)), st, (const uint8_t *)a.down, nullptr,
-                             act16, (int)P, ainv, tpair, ttok, tiles, ntiles, ncb1, a.H, a.F, a.y);
+    return gg ? launch_moe_f16<1, true>(a.F / PF_KC, g1, st, wd, nullptr, act16, (int)P, ainv, tpair, ttok, tiles,
+                                        ntiles, ncb1, a.H, a.F, a.y)
+              : launch_moe_f16<1, false>(a.F / PF_KC, g1, st, wd, nullptr, act16, (int)P, ainv, tpair, ttok, tiles,
+                                         ntiles, ncb1, a.H, a.F, a.y);
 }
 
 }  // namespace tbq
