@@ -79,6 +79,13 @@ hipError_t launch_group(const MoeArgs &a, hipStream_t st);
 hipError_t launch_moe_q4k_gate_up(const MoeArgs &a, bool grouped, hipStream_t st);
 // out = resid + combine(down act); a.qd QT_Q4_K or QT_GQ4_K
 hipError_t launch_moe_q4k_down(const MoeArgs &a, bool grouped, hipStream_t st);
+// The same two phases on the K-quant int-dot units for the other expert
+// formats (tbq_mv_kq.hip; gate and up in one format); hipErrorNotSupported
+// for shapes and formats they do not cover.
+// grouped: the batch runs in expert order (a.grp written by launch_group);
+// the grouped down writes a.y and adds launch_combine.
+hipError_t launch_moe_gate_up_kq(const MoeArgs &a, bool grouped, hipStream_t st);
+hipError_t launch_moe_down_kq(const MoeArgs &a, bool grouped, hipStream_t st);
 size_t prefill_workspace_bytes(int T, int k, int E, int H, int F);
 bool gemm_k_supported(int K);
 // rows of n floats to fp16 with per-row power-of-two scales (inv = 1 / scale)

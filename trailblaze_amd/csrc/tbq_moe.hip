@@ -344,15 +344,17 @@ static bool is_q4k(int qt) { return qt == QT_Q4_K || qt == QT_GQ4_K; }
 // The experts of a routed batch (routing already in a.sel_idx / a.sel_w):
 // gate/up + SwiGLU into a.act, then down + the slot-ordered combine into
 // a.out.  Each phase takes the Q4_K int-dot kernels where its tensors are
-// Q4_K (and the shape fits them), else the per-format kernels; gate and up
-// of different qtypes run one at a time.
+// Q4_K (and the shape fits them), else the K-quant int-dot kernels
+// (tbq_mv_kq.hip), else the byte->fp32 kernels above; gate and up of
+// different qtypes run one at a time.
 static hipError_t launch_experts(const MoeArgs &a, hipStream_t st) {
     const bool q4_gu = a.qg == a.qu && is_q4k(a.qg), q4_dn = is_q4k(a.qd);
-    const bool grouped = (q4_gu || q4_dn) && moe_decode_grouped(a);
+    const bool grouped = moe_decode_grouped(a);
     hipError_t err;
     if (grouped && (err = launch_group(a, st)) != hipSuccess) return err;
     err = hipErrorNotSupported;
     if (q4_gu) err = launch_moe_q4k_gate_up(a, grouped, st);
+    if (err == hipErrorNotSupported && a.qg == a.qu) err = launch_moe_gate_up_kq(a, grouped, st);
     if (err == hipErrorNotSupported) {
         if (a.qg == a.qu) {
             err = launch_gate_up_generic(a, st);
@@ -371,6 +373,7 @@ static hipError_t launch_experts(const MoeArgs &a, hipStream_t st) {
     if (err != hipSuccess) return err;
     err = hipErrorNotSupported;
     if (q4_dn) err = launch_moe_q4k_down(a, grouped, st);
+    if (err == hipErrorNotSupported) err = launch_moe_down_kq(a, grouped, st);
     if (err != hipErrorNotSupported) return err;
     err = launch_rows_generic(a.qd, a.down, a.act, a.H, a.F, 1, a.y, a, st);
     if (err != hipSuccess) return err;

@@ -1328,6 +1328,291 @@ static hipError_t launch_matvec_kq_p(int qt, const void *W, int M, int K, const 
     }
 }
 
+// ---------------------------------------------------------------------------
+// MoE decode experts on the same int-dot units, for the K-quant formats
+// other than Q4_K (tbq_moe_q4k.hip has the Q4_K kernels).  One kernel per
+// phase, as the Q4_K ones: a layer whose tensors differ in format (llama.cpp
+// mixes give down a wider format than gate/up) runs each phase in its own.
+//
+// k_moe_gate_up_kq: act[pair][r] = silu(W_gate[e] x_t)[r] * (W_up[e] x_t)[r]
+// (layer4/tb_infer.c:810-812, tb_swiglu :130-135) for gate and up in one
+// format.  grid = (F / 8, T*k); wave w takes output row 8*bx + w, lanes
+// 0..31 its gate row and 32..63 its up row, UPL units per lane.
+// k_moe_down_kq: out[t][r] = resid[t][r] + sum over slots in slot order of
+// w_s * (W_down[e_s] act[t*k + s])[r] (:815-831, :876).  grid = (H / 4, T);
+// the token's k activation vectors (k*F contiguous floats) are staged as one
+// vector of k*F/64 units, each 16-lane row of a wave takes one (row, slot)
+// dot, and one lane per row adds the slots in slot order.
+// An expert index outside [0, E) (never produced by the router) reads expert
+// 0 and contributes 0.
+// ---------------------------------------------------------------------------
+constexpr int ME_THREADS = 512;
+constexpr int MD_ROWS = 4, MD_LPR = 16;
+constexpr int MD_MAX_UNITS = 256;   // staged units of the down kernel (k * F / 64)
+
+template <int QT, int UPL, int MAXT>
+__global__ __launch_bounds__(ME_THREADS) void k_moe_gate_up_kq(const uint8_t *__restrict__ gate,
+                                                               const uint8_t *__restrict__ up, long long rb,
+                                                               const float *__restrict__ xn,
+                                                               const int *__restrict__ sel_idx,
+                                                               const int *__restrict__ order,
+                                                               const int *__restrict__ nvalid, int H, int F, int E,
+                                                               int k, float *__restrict__ act) {
+    using Fm = KqFmt<QT>;
+    extern __shared__ uint32_t smem[];
+    const int U = H / 64;
+    uint32_t *xd = smem;
+    float *gs = reinterpret_cast<float *>(smem + U * KQ_UNIT);
+    // with an order list (expert-ordered valid pairs), column y runs pair order[y]
+    if (order && (int)blockIdx.y >= *nvalid) return;   // workgroup-uniform
+    const int pair = order ? order[blockIdx.y] : blockIdx.y, t = pair / k, s = pair % k;
+    const int e_sel = sel_idx[t * 8 + s];
+    const bool ev = (unsigned)e_sel < (unsigned)E;
+    const int e = ev ? e_sel : 0;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lr = lane & 31, half = lane >> 5;
+    const int r = blockIdx.x * (ME_THREADS / 64) + wave;   // output row (F % 8 == 0)
+    const uint8_t *row = (half ? up : gate) + ((long long)e * F + r) * rb;
+    KqStager<ME_THREADS, kq_order<QT>(), MAXT> xs;
+    xs.load(xn + (long long)t * H, U);
+    __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
+    typename Fm::Unit w[UPL];
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+        const int u = lr + 32 * i;
+        Fm::load(row, u < U ? u : 0, w[i]);
+    }
+    xs.store(U, xd, gs);
+    __syncthreads();
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+        const int u = lr + 32 * i;
+        if (u < U) {
+            KqX x;
+            kq_xload(xd, gs, u, x);
+            acc += kq_dot<QT>(w[i], x, u);
+        }
+    }
+    acc = group_sum<32>(acc);
+    const float uv = __shfl(acc, 32);
+    if (lane == 0) {
+        const float g = acc;
+        const float den = 1.0f + expf_glibc(-g);
+        const float sg = g / den;
+        act[(long long)pair * F + r] = ev ? sg * uv : 0.f;
+    }
+}
+
+template <int QT, int UPL, int MAXT>
+__global__ __launch_bounds__(ME_THREADS) void k_moe_down_kq(const uint8_t *__restrict__ down, long long rb,
+                                                            const float *__restrict__ act,
+                                                            const int *__restrict__ sel_idx,
+                                                            const float *__restrict__ sel_w,
+                                                            const float *__restrict__ resid, int H, int F, int E,
+                                                            int k, float *__restrict__ out) {
+    using Fm = KqFmt<QT>;
+    extern __shared__ uint32_t smem[];
+    const int U = F / 64, NU = k * U;
+    uint32_t *xd = smem;
+    float *gs = reinterpret_cast<float *>(smem + NU * KQ_UNIT);
+    float *yv = gs + 4 * NU;   // [slot][MD_ROWS]
+    const int t = blockIdx.y, r0 = blockIdx.x * MD_ROWS;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lr = lane & 15;
+    const int d = wave * (64 / MD_LPR) + (lane >> 4);   // dot (row r0 + d / k, slot d % k), d < 32
+    const bool dv = d < MD_ROWS * k;
+    const int rd = dv ? d / k : 0, sd = dv ? d % k : 0;
+    const int e_sel = sel_idx[t * 8 + sd];
+    const bool ev = dv && (unsigned)e_sel < (unsigned)E;
+    const int e = ev ? e_sel : 0;
+    const uint8_t *row = down + ((long long)e * H + r0 + rd) * rb;
+    KqStager<ME_THREADS, kq_order<QT>(), MAXT> xs;
+    xs.load(act + (long long)t * k * F, NU);
+    __builtin_amdgcn_sched_barrier(0);
+    typename Fm::Unit w[UPL];
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+        const int u = lr + MD_LPR * i;
+        Fm::load(row, u < U ? u : 0, w[i]);
+    }
+    xs.store(NU, xd, gs);
+    __syncthreads();
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < UPL; i++) {
+        const int u = lr + MD_LPR * i;
+        if (u < U) {
+            KqX x;
+            kq_xload(xd, gs, sd * U + u, x);
+            acc += kq_dot<QT>(w[i], x, u);
+        }
+    }
+    acc = group_sum<MD_LPR>(acc);
+    if (lr == 0 && dv) yv[sd * MD_ROWS + rd] = ev ? acc : 0.f;
+    __syncthreads();
+    if (threadIdx.x < MD_ROWS) {
+        const int rr = threadIdx.x, r = r0 + rr;
+        float a = 0.f;
+        for (int sl = 0; sl < k; sl++) {
+            if ((unsigned)sel_idx[t * 8 + sl] >= (unsigned)E) continue;   // never produced by the router
+            const float pr = sel_w[t * 8 + sl] * yv[sl * MD_ROWS + rr];
+            a = a + pr;
+        }
+        out[(long long)t * H + r] = resid[(long long)t * H + r] + a;
+    }
+}
+
+// Batches in expert order (k_group's pair list): y[pair][r] = W_down[e] .
+// act[pair] over MDP_ROWS rows per workgroup, so the workgroups of the pairs
+// that share an expert run back to back and find its rows in L2; k_combine
+// then adds the slots in slot order.  grid = (H / MDP_ROWS, T*k).
+constexpr int MDP_ROWS = 128, MDP_PASSES = MDP_ROWS / (ME_THREADS / MD_LPR);
+
+template <int QT, int UPL, int MAXT>
+__global__ __launch_bounds__(ME_THREADS) void k_moe_down_pair_kq(const uint8_t *__restrict__ down, long long rb,
+                                                                 const float *__restrict__ act,
+                                                                 const int *__restrict__ sel_idx,
+                                                                 const int *__restrict__ order,
+                                                                 const int *__restrict__ nvalid, int H, int F,
+                                                                 int E, int k, float *__restrict__ y) {
+    using Fm = KqFmt<QT>;
+    extern __shared__ uint32_t smem[];
+    const int U = F / 64;
+    uint32_t *xd = smem;
+    float *gs = reinterpret_cast<float *>(smem + U * KQ_UNIT);
+    if ((int)blockIdx.y >= *nvalid) return;   // workgroup-uniform
+    const int pair = order[blockIdx.y];
+    const int e = sel_idx[(pair / k) * 8 + pair % k];
+    if ((unsigned)e >= (unsigned)E) return;   // the list holds valid pairs only
+    const int lr = threadIdx.x & 15, rl = threadIdx.x >> 4;   // row of the pass
+    const int r0 = blockIdx.x * MDP_ROWS;
+    KqStager<ME_THREADS, kq_order<QT>(), MAXT> xs;
+    xs.load(act + (long long)pair * F, U);
+    __builtin_amdgcn_sched_barrier(0);
+    typename Fm::Unit w[MDP_PASSES][UPL];
+#pragma unroll
+    for (int p = 0; p < MDP_PASSES; p++) {
+        const uint8_t *row = down + ((long long)e * H + r0 + (ME_THREADS / MD_LPR) * p + rl) * rb;
+#pragma unroll
+        for (int i = 0; i < UPL; i++) {
+            const int u = lr + MD_LPR * i;
+            Fm::load(row, u < U ? u : 0, w[p][i]);
+        }
+    }
+    xs.store(U, xd, gs);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < MDP_PASSES; p++) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < UPL; i++) {
+            const int u = lr + MD_LPR * i;
+            if (u < U) {
+                KqX x;
+                kq_xload(xd, gs, u, x);
+                acc += kq_dot<QT>(w[p][i], x, u);
+            }
+        }
+        acc = group_sum<MD_LPR>(acc);
+        if (lr == 0) y[(long long)pair * H + r0 + (ME_THREADS / MD_LPR) * p + rl] = acc;
+    }
+}
+
+template <int QT, int UPL, int MAXT>
+static hipError_t launch_moe_gate_up_kq_t(const MoeArgs &a, bool grouped, hipStream_t st) {
+    const long long rb = (long long)(a.H / block_weights(QT)) * block_bytes(QT);
+    const int U = a.H / 64;
+    const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16;
+    const int *order = grouped ? a.grp + 1 + 3 * a.E : nullptr, *nvalid = grouped ? order + a.T * a.k : nullptr;
+    hipLaunchKernelGGL((k_moe_gate_up_kq<QT, UPL, MAXT>), dim3(a.F / (ME_THREADS / 64), a.T * a.k), dim3(ME_THREADS),
+                       lds, st, (const uint8_t *)a.gate, (const uint8_t *)a.up, rb, a.xn, a.sel_idx, order, nvalid,
+                       a.H, a.F, a.E, a.k, a.act);
+    return hipGetLastError();
+}
+
+template <int QT, int UPL, int MAXT>
+static hipError_t launch_moe_down_pair_kq_t(const MoeArgs &a, hipStream_t st) {
+    const long long rb = (long long)(a.F / block_weights(QT)) * block_bytes(QT);
+    const int U = a.F / 64;
+    const int *order = a.grp + 1 + 3 * a.E, *nvalid = order + a.T * a.k;
+    const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16;
+    hipLaunchKernelGGL((k_moe_down_pair_kq<QT, UPL, MAXT>), dim3(a.H / MDP_ROWS, a.T * a.k), dim3(ME_THREADS), lds, st,
+                       (const uint8_t *)a.down, rb, a.act, a.sel_idx, order, nvalid, a.H, a.F, a.E, a.k, a.y);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return launch_combine(a, st);
+}
+
+template <int QT, int UPL, int MAXT>
+static hipError_t launch_moe_down_kq_t(const MoeArgs &a, hipStream_t st) {
+    const long long rb = (long long)(a.F / block_weights(QT)) * block_bytes(QT);
+    const int NU = a.k * (a.F / 64);
+    const size_t lds = (size_t)NU * KQ_UNIT * 4 + (size_t)NU * 16 + 8 * MD_ROWS * 4;
+    hipLaunchKernelGGL((k_moe_down_kq<QT, UPL, MAXT>), dim3(a.H / MD_ROWS, a.T), dim3(ME_THREADS), lds, st,
+                       (const uint8_t *)a.down, rb, a.act, a.sel_idx, a.sel_w, a.resid, a.H, a.F, a.E, a.k, a.out);
+    return hipGetLastError();
+}
+
+template <int QT>
+static hipError_t launch_moe_gate_up_kq_q(const MoeArgs &a, bool grouped, hipStream_t st) {
+    const int U = a.H / 64;   // x staged in LDS: U * 16 tasks over 512 threads
+    if (U <= 32) return launch_moe_gate_up_kq_t<QT, 1, 1>(a, grouped, st);
+    if (U <= 64) return launch_moe_gate_up_kq_t<QT, 2, 2>(a, grouped, st);
+    if (U <= 128) return launch_moe_gate_up_kq_t<QT, 4, 4>(a, grouped, st);
+    return hipErrorNotSupported;
+}
+
+template <int QT>
+static hipError_t launch_moe_down_kq_q(const MoeArgs &a, bool grouped, hipStream_t st) {
+    const int U = a.F / 64, NU = a.k * U;
+    if (grouped) {   // per pair in expert order: one activation vector staged
+        if (a.H % MDP_ROWS) return hipErrorNotSupported;
+        if (U <= 16) return launch_moe_down_pair_kq_t<QT, 1, 1>(a, st);
+        if (U <= 32) return launch_moe_down_pair_kq_t<QT, 2, 1>(a, st);
+        if (U <= 64) return launch_moe_down_pair_kq_t<QT, 4, 2>(a, st);
+        return hipErrorNotSupported;
+    }
+    if (NU > MD_MAX_UNITS) return hipErrorNotSupported;
+    const int maxt = (16 * NU + ME_THREADS - 1) / ME_THREADS;
+    if (U <= 16) {
+        if (maxt <= 2) return launch_moe_down_kq_t<QT, 1, 2>(a, st);
+        if (maxt <= 4) return launch_moe_down_kq_t<QT, 1, 4>(a, st);
+        return launch_moe_down_kq_t<QT, 1, 8>(a, st);
+    }
+    if (U <= 32) {
+        if (maxt <= 4) return launch_moe_down_kq_t<QT, 2, 4>(a, st);
+        return launch_moe_down_kq_t<QT, 2, 8>(a, st);
+    }
+    return hipErrorNotSupported;
+}
+
+#define TBQ_MOE_KQ_SWITCH(qt, FN)                                             \
+    switch (qt) {                                                            \
+    case QT_Q2_K: return FN<QT_Q2_K>(a, grouped, st);                        \
+    case QT_Q3_K: return FN<QT_Q3_K>(a, grouped, st);                        \
+    case QT_Q4_K: return FN<QT_Q4_K>(a, grouped, st);                        \
+    case QT_Q5_K: return FN<QT_Q5_K>(a, grouped, st);                        \
+    case QT_Q6_K: return FN<QT_Q6_K>(a, grouped, st);                        \
+    case QT_Q8_0: return FN<QT_Q8_0>(a, grouped, st);                        \
+    case QT_GQ2_K: return FN<QT_GQ2_K>(a, grouped, st);                      \
+    case QT_GQ3_K: return FN<QT_GQ3_K>(a, grouped, st);                      \
+    case QT_GQ4_K: return FN<QT_GQ4_K>(a, grouped, st);                      \
+    case QT_GQ5_K: return FN<QT_GQ5_K>(a, grouped, st);                      \
+    case QT_GQ6_K: return FN<QT_GQ6_K>(a, grouped, st);                      \
+    case QT_GQ8_0: return FN<QT_GQ8_0>(a, grouped, st);                      \
+    default: return hipErrorNotSupported;                                    \
+    }
+
+hipError_t launch_moe_gate_up_kq(const MoeArgs &a, bool grouped, hipStream_t st) {
+    if (a.qg != a.qu || a.F % (ME_THREADS / 64)) return hipErrorNotSupported;
+    TBQ_MOE_KQ_SWITCH(a.qg, launch_moe_gate_up_kq_q)
+}
+
+hipError_t launch_moe_down_kq(const MoeArgs &a, bool grouped, hipStream_t st) {
+    if (a.H % MD_ROWS || a.k > 8) return hipErrorNotSupported;
+    TBQ_MOE_KQ_SWITCH(a.qd, launch_moe_down_kq_q)
+}
+#undef TBQ_MOE_KQ_SWITCH
+
 hipError_t launch_matvec_kq(int qt, const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu) {
     return launch_matvec_kq_p<PRO_NONE, false>(qt, W, M, K, x, y, st, n_cu, MvPro{});
 }
