@@ -67,8 +67,11 @@ int tbq_dequant(const void *W, int qtype, int nrows, int K, float *out, void *st
 /* y[M] = dequant(W[M][K]) . x[K], fp32 accumulate (tb_gguf_dequant_matvec,
  * layer4/tb_gguf.h:95-96; device-resident form of tb_cuda_matvec_device,
  * layer4/tb_gguf_dequant.h:36-37).  K a multiple of 256 for super-block
- * formats, of 32 otherwise, at most 32768 (x is staged in LDS; F32, F16 and
- * BF16 rows at most 15360); W and x 16-byte aligned. */
+ * formats, of 32 otherwise (F32, F16 and BF16 rows at most 15360); W and x
+ * 16-byte aligned.  x is staged in LDS, so rows longer than 32768 weights
+ * (K-quant formats, Q8_0, Q4_0) run as column slices of 32768 whose partial
+ * products are added in slice order; their partial sums live in a
+ * library-owned buffer, so such calls must be ordered on one stream. */
 int tbq_matvec(const void *W, int qtype, int M, int K, const float *x, float *y, void *stream);
 
 /* Kernel choice for tbq_matvec (no counterpart in the reference: it has one

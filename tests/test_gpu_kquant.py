@@ -209,13 +209,28 @@ def test_matvec_long_rows(oracle, qt, M, K):
     assert rel_l2(gpu_matvec(W, qt, M, K, x), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
 
 
-def test_matvec_rejects_rows_beyond_limit():
+@pytest.mark.parametrize("qt", [fm.Q4_K, fm.Q6_K, fm.Q3_K, fm.Q8_0, fm.GGML | fm.Q4_K])
+@pytest.mark.parametrize("M,K", [(4, 32768 + 256), (300, 53248), (17, 98304)])
+def test_matvec_rows_beyond_32768(oracle, qt, M, K):
+    """Rows longer than the LDS-staged x (53248 is a 405B-class FFN-down row):
+    column slices of 32768 weights with the full row stride, their partial
+    products added in slice order; the reference's CUDA entry point has no
+    row limit (layer4/tb_gguf_dequant.cu:422-472)."""
+    print(f"rows beyond 32768 qt={qt} M={M} K={K}", flush=True)
+    rng = np.random.default_rng(M + K + qt)
+    W = synth.kquant_matrix(qt, M, K, rng)
+    x = synth.activations(K, rng)
+    assert rel_l2(gpu_matvec(W, qt, M, K, x), oracle.matvec(W, qt, M, K, x)) <= MATVEC_TOL
+
+
+def test_matvec_rejects_fma_rows_beyond_limit():
+    """F32/F16/BF16 rows stay within the fma kernel's LDS-resident x."""
     import torch
-    W = empty(4096, torch.uint8)
-    x = empty(32768 + 256, torch.float32)
+    W = empty(16 * 16384 * 4, torch.uint8)
+    x = empty(16384, torch.float32)
     y = empty(4, torch.float32)
     with pytest.raises(tb.TbqError):
-        tb.matvec(W, fm.Q4_K, 4, 32768 + 256, x, y)
+        tb.matvec(W, fm.F32, 4, 16384, x, y)
 
 
 @pytest.mark.parametrize("qt", [fm.Q8_0, fm.Q4_0])

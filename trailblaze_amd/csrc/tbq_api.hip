@@ -28,6 +28,8 @@ void *g_ws = nullptr;
 size_t g_ws_bytes = 0;
 void *g_route = nullptr;
 size_t g_route_bytes = 0;
+void *g_part = nullptr;   // partial sums of matvecs with rows longer than TBQ_MAX_K
+size_t g_part_bytes = 0;
 
 int fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 int fail(const char *fmt, ...) {
@@ -143,7 +145,6 @@ static int check_matvec(const void *W, int qt, int M, int K, const float *x, con
     if (!known_qtype(qt)) return fail("unsupported qtype %d", qt);
     int chunk = block_weights(qt) == 256 ? 256 : 32;
     if (M < 0 || K <= 0 || K % chunk) return fail("K=%d must be a positive multiple of %d for qtype %d", K, chunk, qt);
-    if (K > TBQ_MAX_K) return fail("K=%d exceeds the LDS-resident x limit (%d)", K, TBQ_MAX_K);
     if (!W || !x || !y) return fail("null pointer");
     if (!aligned16(x)) return fail("x must be 16-byte aligned");
     if (((qt & 0xFF) == QT_Q4_K || (qt & 0xFF) == QT_Q5_K || qt == QT_F32) && !aligned16(W))
@@ -152,12 +153,48 @@ static int check_matvec(const void *W, int qt, int M, int K, const float *x, con
     return 1;
 }
 
+// Rows longer than TBQ_MAX_K (x is staged in LDS): column slices of
+// TBQ_MAX_K weights through the K-quant kernel with the full row stride,
+// the first into y, the others into a library-owned partial buffer (grown
+// on demand, so such calls must be ordered on one stream), then y plus the
+// partials in slice order.
+static int matvec_long_rows(const void *W, int qt, int M, int K, const float *x, float *y, hipStream_t st) {
+    const int S = (K + TBQ_MAX_K - 1) / TBQ_MAX_K;
+    const long long rb = (long long)tbq_row_bytes(qt, K);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    const size_t need = (size_t)(S - 1) * M * 4;
+    if (g_part_bytes < need) {
+        if (g_part && !hip_ok(hipFree(g_part), "hipFree")) return 0;
+        g_part = nullptr;
+        g_part_bytes = 0;
+        if (!hip_ok(hipMalloc(&g_part, need), "hipMalloc matvec partials")) return 0;
+        g_part_bytes = need;
+    }
+    for (int sl = 0; sl < S; sl++) {
+        const int k0 = sl * TBQ_MAX_K, ks = K - k0 < TBQ_MAX_K ? K - k0 : TBQ_MAX_K;
+        MvPro pro{};
+        pro.rb = rb;
+        const uint8_t *Ws = (const uint8_t *)W + tbq_row_bytes(qt, k0);
+        float *ys = sl == 0 ? y : (float *)g_part + (size_t)(sl - 1) * M;
+        hipError_t e = launch_matvec_kq_pro(PRO_NONE, pro, qt, Ws, M, ks, x + k0, ys, st, g_cu);
+        if (e == hipErrorNotSupported)
+            return fail("tbq_matvec: no kernel for qtype %d with rows of K=%d (slices of %d)", qt, K, TBQ_MAX_K);
+        if (!hip_ok(e, "matvec launch (long rows)")) return 0;
+    }
+    return hip_ok(launch_add_rows(y, (const float *)g_part, S - 1, M, st), "matvec slice sum");
+}
+
 int tbq_matvec_variant(const void *W, int qt, int M, int K, const float *x, float *y, int variant, void *s) {
     if (!ensure_init()) return 0;
     qt = canon_qt(qt);
     if (!check_matvec(W, qt, M, K, x, y)) return 0;
     if (variant < TBQ_MV_AUTO || variant > TBQ_MV_KQ) return fail("tbq_matvec_variant: unknown variant %d", variant);
     if (M == 0) return 1;
+    if (K > TBQ_MAX_K) {
+        if (variant != TBQ_MV_AUTO && variant != TBQ_MV_KQ)
+            return fail("tbq_matvec_variant: rows of K=%d above %d take the K-quant kernel only", K, TBQ_MAX_K);
+        return matvec_long_rows(W, qt, M, K, x, y, S(s));
+    }
     // The specialised Q4_K kernels keep x's digits in registers for rows of
     // up to 64 units: one pass of two rows per wave up to 8192 rows,
     // persistent waves walking the rows of taller matrices; longer rows

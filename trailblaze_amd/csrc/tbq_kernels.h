@@ -28,6 +28,8 @@ struct MvPro {
     const float *w;   // PRO_NORM: weights [K]
     float *vo;        // PRO_NORM: x + y for the caller (null: not stored)
     float eps;
+    long long rb;     // K-quant kernel: bytes between rows (0: K's own row bytes), for
+                      // a column slice of a matrix with longer rows
 };
 
 struct MoeArgs {
@@ -63,6 +65,9 @@ hipError_t launch_matvec_q4k_pro(int mode, const MvPro &pro, const void *W, int 
 hipError_t launch_matvec_kq_pro(int mode, const MvPro &pro, int qt, const void *W, int M, int K, const float *x,
                                 float *y, hipStream_t s, int n_cu);
 hipError_t launch_expf(const float *in, float *out, long long n, hipStream_t s);
+// y[i] = (((y[i] + part[0][i]) + part[1][i]) + ...) over nparts rows of M
+// floats: the column slices of a matvec with rows longer than TBQ_MAX_K.
+hipError_t launch_add_rows(float *y, const float *part, int nparts, int M, hipStream_t s);
 hipError_t launch_route(const float *xn, const float *router, const float *bias, int T, int H, int E,
                         int top_k, int *sel_idx, float *sel_w, hipStream_t st);
 hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st);

@@ -352,6 +352,21 @@ __global__ void k_expf(const float *__restrict__ in, float *__restrict__ out, lo
         out[i] = expf_glibc(in[i]);
 }
 
+__global__ __launch_bounds__(256) void k_add_rows(float *__restrict__ y, const float *__restrict__ part, int nparts,
+                                                  int M) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < M; i += gridDim.x * 256) {
+        float a = y[i];
+        for (int p = 0; p < nparts; p++) a = a + part[(long long)p * M + i];
+        y[i] = a;
+    }
+}
+
+hipError_t launch_add_rows(float *y, const float *part, int nparts, int M, hipStream_t s) {
+    const int blocks = (M + 255) / 256;
+    hipLaunchKernelGGL(k_add_rows, dim3(blocks < 4096 ? blocks : 4096), dim3(256), 0, s, y, part, nparts, M);
+    return hipGetLastError();
+}
+
 hipError_t launch_expf(const float *in, float *out, long long n, hipStream_t s) {
     long long blocks = (n + 255) / 256;
     int grid = (int)(blocks < 16384 ? blocks : 16384);

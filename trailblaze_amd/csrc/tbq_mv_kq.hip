@@ -1192,7 +1192,7 @@ static hipError_t launch_kq(const void *W, int M, int K, const float *x, float *
                             int rpw, const MvPro &pro) {
     constexpr int RPP = 64 / LPR;
     const int U = K / 64;
-    const long long rb = (long long)(K / block_weights(QT)) * block_bytes(QT);
+    const long long rb = pro.rb ? pro.rb : (long long)(K / block_weights(QT)) * block_bytes(QT);
     constexpr int RP = GLU ? 2 : R;
     const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (S > 1 ? (size_t)2 * G * S * RP * RPP * 4 : 0);
     if constexpr (S > 4) {
@@ -1221,7 +1221,7 @@ static hipError_t launch_kq_seg(const void *W, int M, int K, const float *x, flo
     const int U = K / 64, RB = NT / U;
     const long long nblk = ((long long)M + RB - 1) / RB, cap = (long long)n_cu * KQ_SEG_WPC;
     const int grid = (int)(nblk < cap ? nblk : cap);
-    const long long rb = (long long)(K / block_weights(QT)) * block_bytes(QT);
+    const long long rb = pro.rb ? pro.rb : (long long)(K / block_weights(QT)) * block_bytes(QT);
     const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (size_t)2 * RP * NT * 4;
     hipLaunchKernelGGL((k_mv_kq_seg<QT, NW, PRO, GLU>), dim3(grid), dim3(NT), lds, st, (const uint8_t *)W, M, K, rb,
                        x, y, pro);
