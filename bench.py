@@ -29,7 +29,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "int8": 5000.0}   # MI355X dense, per GPU
 PMC_COPY_BYTES = 256 << 20
-PROFILES = ("q4k", "q4k_big", "sweep", "seg", "moe_b1", "moe_b16", "moe_prefill", "moe_prefill_i8")
+PROFILES = ("q4k", "q4k_graph", "q4k_big", "sweep", "seg", "moe_b1", "moe_b16", "moe_prefill", "moe_prefill_i8")
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "q4k_matvec_4096x4096_pmc.txt")
 
 
@@ -248,7 +248,25 @@ def profile_leg(name, tb, fm, synth, torch):
     one matrix is smaller, as in the timed legs."""
     rng = np.random.default_rng(0)
     reps = 3
-    if name in ("q4k", "q4k_big", "sweep", "seg"):
+    if name == "q4k_graph":
+        # the headline leg as timed: the 56-launch step in a HIP graph, replayed
+        # (kernel trace: every dispatch of the timed region is a cold launch)
+        qt, M, K = fm.Q4_K, 4096, 4096
+        W = torch.from_numpy(synth.kquant_matrix(qt, M, K, rng)).cuda()
+        nc = max(2, int(np.ceil(2 * 256e6 / fm.weight_bytes(qt, M, K))) + 1)
+        cps = [W] + [W.clone() for _ in range(nc - 1)]
+        x = torch.from_numpy(synth.activations(K, rng)).cuda()
+        ys = torch.empty((nc, M), dtype=torch.float32, device="cuda")
+
+        def step():
+            for i in range(nc):
+                tb.matvec(cps[i], qt, M, K, x, ys[i])
+        steps = 20
+        secs = time_region(step, steps, 3, torch.cuda.current_stream())
+        log(f"profile {name}: Q4_K {M}x{K}, graph of {nc} launches replayed {steps} times after 3 warm-up "
+            f"replays: event-timed {secs / (steps * nc) * 1e6:.3f} us/launch")
+        del cps, W
+    elif name in ("q4k", "q4k_big", "sweep", "seg"):
         # seg: rows the segmented mapping serves (K = 2560, Qwen3-4B's hidden)
         shapes = {"q4k": [(fm.Q4_K, 4096, 4096)], "q4k_big": [(fm.Q4_K, 151936, 4096)],
                   "sweep": _sweep_shapes(),
