@@ -73,9 +73,12 @@ hipError_t launch_route(const float *xn, const float *router, const float *bias,
 hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st);
 // out = resid + sum over slots, in slot order, of sel_w * y[t*k + s]
 hipError_t launch_combine(const MoeArgs &a, hipStream_t st);
+// group: the layer call whose batch the router may also sort by expert (its
+// grp list, when moe_decode_grouped); *grouped tells whether it did.
 hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
                          float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st,
-                         _Float16 *x16 = nullptr, float *xinv = nullptr, bool *x16_done = nullptr);
+                         _Float16 *x16 = nullptr, float *xinv = nullptr, bool *x16_done = nullptr,
+                         const MoeArgs *group = nullptr, bool *grouped = nullptr);
 // Decode expert kernels for Q4_K tensors (tbq_moe_q4k.hip).  A batch runs in
 // expert order when moe_decode_grouped(a): launch_group writes a.grp first.
 bool moe_decode_grouped(const MoeArgs &a);

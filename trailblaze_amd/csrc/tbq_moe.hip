@@ -347,11 +347,12 @@ static bool is_q4k(int qt) { return qt == QT_Q4_K || qt == QT_GQ4_K; }
 // Q4_K (and the shape fits them), else the K-quant int-dot kernels
 // (tbq_mv_kq.hip), else the byte->fp32 kernels above; gate and up of
 // different qtypes run one at a time.
-static hipError_t launch_experts(const MoeArgs &a, hipStream_t st) {
+// grouped_done: the router has already written a.grp.
+static hipError_t launch_experts(const MoeArgs &a, hipStream_t st, bool grouped_done) {
     const bool q4_gu = a.qg == a.qu && is_q4k(a.qg), q4_dn = is_q4k(a.qd);
     const bool grouped = moe_decode_grouped(a);
     hipError_t err;
-    if (grouped && (err = launch_group(a, st)) != hipSuccess) return err;
+    if (grouped && !grouped_done && (err = launch_group(a, st)) != hipSuccess) return err;
     err = hipErrorNotSupported;
     if (q4_gu) err = launch_moe_q4k_gate_up(a, grouped, st);
     if (err == hipErrorNotSupported && a.qg == a.qu) err = launch_moe_gate_up_kq(a, grouped, st);
@@ -418,13 +419,17 @@ static hipError_t by_token_chunks(const MoeArgs &a, long long cap, Fn fn) {
 }
 
 hipError_t launch_moe_fp32(const MoeArgs &a, hipStream_t st) {
+    bool grouped = false;
     hipError_t err = launch_router(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.logits, a.counters, a.sel_idx,
-                                   a.sel_w, st);
+                                   a.sel_w, st, nullptr, nullptr, nullptr, &a, &grouped);
     if (err == hipErrorNotSupported)
         err = launch_route(a.xn, a.router, a.bias, a.T, a.H, a.E, a.top_k, a.sel_idx, a.sel_w, st);
     if (err != hipSuccess) return err;
-    // the per-pair kernels take a grid column per (token, slot) pair
-    return by_token_chunks(a, 65535 / a.k, [&](const MoeArgs &c) { return launch_experts(c, st); });
+    // the per-pair kernels take a grid column per (token, slot) pair; the
+    // router's grouping covers the whole batch, so a chunk uses it only when
+    // it is the whole batch
+    return by_token_chunks(a, 65535 / a.k,
+                           [&](const MoeArgs &c) { return launch_experts(c, st, grouped && c.T == a.T); });
 }
 
 hipError_t launch_combine(const MoeArgs &a, hipStream_t st) {

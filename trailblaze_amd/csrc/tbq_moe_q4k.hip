@@ -276,14 +276,120 @@ __device__ __forceinline__ float router_dpp_all(const float4 *w4, const float4 *
     return acc;
 }
 
+// ---------------------------------------------------------------------------
+// Decode batches (2 <= T <= 32) in expert order.  group_pairs sorts the
+// batch's T*k selections by expert:
+//   grp[0]                U, the number of distinct experts
+//   grp[1 + u]            expert of group u (ascending)
+//   grp[1 + E + u]        first position of group u in the pair list
+//   grp[1 + 2E + u]       number of pairs in group u
+//   grp[1 + 3E + i]       pair list (t*k + s), by expert (the pairs of one
+//                         expert in no particular order)
+//   grp[1 + 3E + T*k]     number of valid pairs in the list
+// T*k <= 256, T <= 32, E <= 256.  The per-pair expert kernels then take their
+// grid's pair column from the list, so the workgroups of the pairs that
+// share an expert run back to back on the same XCDs (a workgroup's XCD
+// follows its row block) and the later ones read the expert's rows from L2
+// instead of HBM.  Each pair's result is computed on its own and the combine
+// adds the slots in slot order, so the order within a group does not change
+// any result.
+// ---------------------------------------------------------------------------
+
+// By the NT threads of a workgroup (a multiple of 64 dividing 256).  cnt:
+// 256 ints of LDS; wsum: 2 * NT / 64 ints of LDS.  The selections are read
+// with device-scope loads (they may have been stored by another workgroup of
+// the same kernel).
+template <int NT>
+__device__ __forceinline__ void group_pairs(const int *sel_idx, int T, int E, int k, int *__restrict__ grp, int *cnt,
+                                            int *wsum) {
+    constexpr int PER = 256 / NT, NWV = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, n = T * k;
+#pragma unroll
+    for (int j = 0; j < PER; j++) cnt[tid + NT * j] = 0;
+    __syncthreads();
+    int ev[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = tid + NT * j;
+        int e = -1;
+        if (i < n) {
+            const int t = i / k, s = i - t * k;
+            e = __hip_atomic_load(sel_idx + t * 8 + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((unsigned)e >= (unsigned)E) e = -1;   // never produced by the router: left out
+        }
+        ev[j] = e;
+        if (e >= 0) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // thread tid owns experts PER*tid .. PER*tid + PER-1: exclusive scans of
+    // the pair counts (list offsets) and of the non-empty flags (group ranks)
+    int c[PER], sc = 0, sg = 0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int x = PER * tid + j;
+        c[j] = x < E ? cnt[x] : 0;
+        sc += c[j];
+        sg += c[j] > 0;
+    }
+    int ic = sc, ig = sg;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int a = __shfl_up(ic, d), b = __shfl_up(ig, d);
+        if (lane >= d) {
+            ic += a;
+            ig += b;
+        }
+    }
+    if constexpr (NWV > 1) {
+        if (lane == 63) {
+            wsum[tid >> 6] = ic;
+            wsum[NWV + (tid >> 6)] = ig;
+        }
+        __syncthreads();
+        for (int w = 0; w < (tid >> 6); w++) {
+            ic += wsum[w];
+            ig += wsum[NWV + w];
+        }
+    }
+    int off = ic - sc, rank = ig - sg;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int x = PER * tid + j;
+        if (c[j] > 0) {
+            grp[1 + rank] = x;
+            grp[1 + E + rank] = off;
+            grp[1 + 2 * E + rank] = c[j];
+            rank++;
+        }
+        if (x < E) cnt[x] = off;   // the expert's list cursor
+        off += c[j];
+    }
+    if (tid == NT - 1) {
+        grp[0] = ig;
+        grp[1 + 3 * E + n] = ic;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < PER; j++)
+        if (ev[j] >= 0) grp[1 + 3 * E + atomicAdd(&cnt[ev[j]], 1)] = tid + NT * j;
+}
+
+// With grp, the batch is also sorted by expert (group_pairs) by the
+// workgroup that finishes the last token's top-k, which saves a launch of
+// k_group: each token's top-k workgroup takes a ticket on the batch counter
+// counters[RD_GRP_CTR] after its selection stores have completed.
+constexpr int RD_GRP_CTR = 32;   // counters[0, T) are the tokens' (T < 32)
+
 template <int M, int NJ>
 __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn, const float *__restrict__ Wr,
                                                    const float *__restrict__ bias, int E, int top_k,
                                                    float *__restrict__ logits, unsigned *__restrict__ counters,
-                                                   int *__restrict__ sel_idx, float *__restrict__ sel_w) {
+                                                   int *__restrict__ sel_idx, float *__restrict__ sel_w, int k,
+                                                   int *__restrict__ grp) {
     constexpr int H = 64 * M, NC = M / RD_CH;
     static_assert(M % RD_CH == 0, "H must be a multiple of 512");
     __shared__ float P[64 * NJ + 16];
+    __shared__ int gcnt[256];
     const int t = blockIdx.y, lane = threadIdx.x, r = lane >> 4, j = lane & 15;
     const int e = blockIdx.x * 4 + r;
     const bool ev = e < E;
@@ -319,6 +425,16 @@ __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn,
     asm volatile("" ::: "memory");
     topk_wave<NJ>(logits + (long long)t * E, E, top_k, t, P, sel_idx, sel_w);
     if (lane == 0) counters[t] = 0u;
+    if (!grp) return;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the selection stores have completed
+    unsigned bt = 0;
+    if (lane == 0)
+        bt = __hip_atomic_fetch_add(counters + RD_GRP_CTR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bt = (unsigned)__builtin_amdgcn_readfirstlane((int)bt);
+    if (bt != gridDim.y - 1) return;
+    asm volatile("" ::: "memory");
+    group_pairs<64>(sel_idx, (int)gridDim.y, E, k, grp, gcnt, nullptr);
+    if (lane == 0) counters[RD_GRP_CTR] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -393,77 +509,10 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
     }
 }
 
-// ---------------------------------------------------------------------------
-// Decode batches (2 <= T <= 32) in expert order.  k_group sorts the batch's
-// T*k selections by expert:
-//   grp[0]                U, the number of distinct experts
-//   grp[1 + u]            expert of group u (ascending)
-//   grp[1 + E + u]        first position of group u in the pair list
-//   grp[1 + 2E + u]       number of pairs in group u
-//   grp[1 + 3E + i]       pair list (t*k + s), by expert, then by token
-//   grp[1 + 3E + T*k]     number of valid pairs in the list
-// One workgroup of 256 threads; T*k <= 256, T <= 32, E <= 256.
-// The per-pair expert kernels then take their grid's pair column from the
-// list, so the workgroups of the pairs that share an expert run back to
-// back on the same XCDs (a workgroup's XCD follows its row block) and the
-// later ones read the expert's rows from L2 instead of HBM.
-// ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_group(const int *__restrict__ sel_idx, int T, int E, int k,
                                                int *__restrict__ grp) {
-    __shared__ int cnt[256];
-    __shared__ unsigned tokmask[256];   // bit t: token t chose the expert (T <= 32)
-    __shared__ int wc[4], wg[4];
-    const int i = threadIdx.x, n = T * k;
-    const int t = i / k, s = i - t * k;
-    int e = -1;
-    if (i < n) {
-        e = sel_idx[t * 8 + s];
-        if ((unsigned)e >= (unsigned)E) e = -1;   // never produced by the router: left out
-    }
-    cnt[i] = 0;
-    tokmask[i] = 0u;
-    __syncthreads();
-    if (e >= 0) {
-        atomicAdd(&cnt[e], 1);
-        atomicOr(&tokmask[e], 1u << t);
-    }
-    __syncthreads();
-    // thread j = expert j: exclusive scans of the pair counts (list offsets)
-    // and of the non-empty flags (group ranks)
-    const int c = i < E ? cnt[i] : 0, g = c > 0;
-    int ic = c, ig = g;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int a = __shfl_up(ic, d), b = __shfl_up(ig, d);
-        if ((i & 63) >= d) {
-            ic += a;
-            ig += b;
-        }
-    }
-    if ((i & 63) == 63) {
-        wc[i >> 6] = ic;
-        wg[i >> 6] = ig;
-    }
-    __syncthreads();
-    int bc = 0, bg = 0;
-    for (int w = 0; w < (i >> 6); w++) {
-        bc += wc[w];
-        bg += wg[w];
-    }
-    const int off = bc + ic - c, rank = bg + ig - g;
-    if (g) {
-        grp[1 + rank] = i;
-        grp[1 + E + rank] = off;
-        grp[1 + 2 * E + rank] = c;
-    }
-    if (i == 255) {
-        grp[0] = bg + ig;
-        grp[1 + 3 * E + n] = bc + ic;
-    }
-    __syncthreads();
-    cnt[i] = off;   // list offset of expert i
-    __syncthreads();
-    if (e >= 0) grp[1 + 3 * E + cnt[e] + __popc(tokmask[e] & ((1u << t) - 1u))] = i;
+    __shared__ int cnt[256], wsum[8];
+    group_pairs<256>(sel_idx, T, E, k, grp, cnt, wsum);
 }
 
 // down for one pair: y[p][r] = W_down[e] act[p] over DG_ROWS rows, p taken
@@ -900,22 +949,26 @@ static hipError_t launch_topk(const float *logits, int T, int E, int top_k, int 
 
 template <int M, int NJ>
 static hipError_t launch_router_dpp_t(const float *xn, const float *router, const float *bias, int T, int E, int top_k,
-                                      float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st) {
+                                      float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st,
+                                      int k, int *grp) {
     // expert groups along x: workgroup i runs on XCD i % 8, so each XCD's L2
     // holds one eighth of the router rows for every token of the batch
     // (tokens along x would make every XCD read all of them)
     dim3 grid((E + 3) / 4, T);
     hipLaunchKernelGGL((k_router_dpp<M, NJ>), grid, dim3(64), 0, st, xn, router, bias, E, top_k, logits, counters,
-                       sel_idx, sel_w);
+                       sel_idx, sel_w, k, grp);
     return hipGetLastError();
 }
 
 template <int M>
 static hipError_t launch_router_dpp(const float *xn, const float *router, const float *bias, int T, int E, int top_k,
-                                    float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st) {
-    if (E <= 64) return launch_router_dpp_t<M, 1>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
-    if (E <= 128) return launch_router_dpp_t<M, 2>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
-    return launch_router_dpp_t<M, 4>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
+                                    float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st,
+                                    int k, int *grp) {
+    if (E <= 64)
+        return launch_router_dpp_t<M, 1>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st, k, grp);
+    if (E <= 128)
+        return launch_router_dpp_t<M, 2>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st, k, grp);
+    return launch_router_dpp_t<M, 4>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st, k, grp);
 }
 
 // Router: logits then softmax/top-k.  With a counter buffer (T unsigned,
@@ -924,12 +977,23 @@ static hipError_t launch_router_dpp(const float *xn, const float *router, const 
 // a top-k kernel.  hipErrorNotSupported when H does not fit either tiling.
 hipError_t launch_router(const float *xn, const float *router, const float *bias, int T, int H, int E, int top_k,
                          float *logits, unsigned *counters, int *sel_idx, float *sel_w, hipStream_t st,
-                         _Float16 *x16, float *xinv, bool *x16_done) {
+                         _Float16 *x16, float *xinv, bool *x16_done, const MoeArgs *group, bool *grouped) {
     if (x16_done) *x16_done = false;
-    if (counters && T < 32) {
-        if (H == 2048) return launch_router_dpp<32>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
-        if (H == 1024) return launch_router_dpp<16>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
-        if (H == 512) return launch_router_dpp<8>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st);
+    if (grouped) *grouped = false;
+    if (counters && T < 32 && (H == 2048 || H == 1024 || H == 512)) {
+        // the batch grouping in the same launch, when the batch runs in expert order
+        const bool g = group && moe_decode_grouped(*group);
+        int *grp = g ? group->grp : nullptr;
+        const int k = g ? group->k : 0;
+        hipError_t err;
+        if (H == 2048)
+            err = launch_router_dpp<32>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st, k, grp);
+        else if (H == 1024)
+            err = launch_router_dpp<16>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st, k, grp);
+        else
+            err = launch_router_dpp<8>(xn, router, bias, T, E, top_k, logits, counters, sel_idx, sel_w, st, k, grp);
+        if (err == hipSuccess && grouped) *grouped = g;
+        return err;
     }
     const size_t lds = (size_t)H * 4 + 2 * RT_TILE_FLOATS * 4;
     if (T >= 32 && H % RTL_KC == 0 && E % RTL_E == 0) {
@@ -1021,6 +1085,7 @@ static hipError_t launch_down_q4k_t(const MoeArgs &a, bool grouped, hipStream_t 
     const int pairs = a.T * a.k;
     if (grouped) {
         const int *order = a.grp + 1 + 3 * a.E, *nvalid = order + pairs;
+        // the combine in the kernel needs a counter per (token, row block)
         hipLaunchKernelGGL((k_down_pair_q4k<UPL, GG>), dim3(a.H / DG_ROWS, pairs), dim3(DG_THREADS),
                            (size_t)(a.F / 32) * XD_PER_SB * 4, st, (const uint8_t *)a.down, a.act, a.sel_idx, order,
                            nvalid, a.H, a.F, a.E, a.k, a.y);

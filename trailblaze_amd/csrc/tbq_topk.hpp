@@ -154,8 +154,11 @@ __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int
         } else {
             io = -1;
         }
-        sel_idx[t * 8 + lane] = io;
-        sel_w[t * 8 + lane] = wo;
+        // device-scope stores: a workgroup on another XCD may read the
+        // selection within the same kernel (the batch grouping of the DPP
+        // router)
+        __hip_atomic_store(sel_idx + t * 8 + lane, io, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sel_w + t * 8 + lane, wo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
