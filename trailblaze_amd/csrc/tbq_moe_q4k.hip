@@ -476,18 +476,29 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
 
     XStager<GU_THREADS, (1024 + GU_THREADS - 1) / GU_THREADS> xs;   // H <= 8192
     xs.load(xn + (long long)t * H, H);
+    __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
+    // Unconditional loads (rows past F re-read row F-1, units past U unit 0;
+    // their results are never used): under a branch the compiler waits for
+    // every weight load before staging x.
     Q4KUnit raw[ROWS][UPL];
 #pragma unroll
     for (int rr = 0; rr < ROWS; rr++) {
-        const int r = r0 + rr;
+        const int r = min(r0 + rr, F - 1);
 #pragma unroll
         for (int i = 0; i < UPL; i++) {
             const int u = lr + LPR * i;
-            if (r < F && u < U) q4k_load<GG>(Wb + (long long)r * rb, u, raw[rr][i]);
+            q4k_load<GG>(Wb + (long long)r * rb, u < U ? u : 0, raw[rr][i]);
         }
     }
     xs.store(xd, H);
     __syncthreads();
+    // A lane's unit is the same for all its rows: with one unit per lane
+    // its digits are read from LDS once (read per row they made the kernel
+    // LDS-bound at 4 rows); with two, per row (both in registers for 4 rows
+    // would cost a wave per SIMD).
+    constexpr bool XREG = UPL == 1 && ROWS > 1;
+    XUnit xu;
+    if constexpr (XREG) xunit_load(xd, lr < U ? lr : 0, xu);
 #pragma unroll
     for (int rr = 0; rr < ROWS; rr++) {
         const int r = r0 + rr;
@@ -496,7 +507,12 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
 #pragma unroll
         for (int i = 0; i < UPL; i++) {
             const int u = lr + LPR * i;
-            if (u < U) acc = q4k_unit_dot<GG>(raw[rr][i], u, xd, acc);
+            if (u < U) {
+                if constexpr (XREG)
+                    acc = q4k_unit_dot<GG>(raw[rr][i], u, xu, acc);
+                else
+                    acc = q4k_unit_dot<GG>(raw[rr][i], u, xd, acc);
+            }
         }
         acc = group_sum<32>(acc);
         const float u_val = __shfl(acc, 32);
@@ -543,6 +559,9 @@ __global__ __launch_bounds__(DG_THREADS) void k_down_pair_q4k(const uint8_t *__r
     const int r0 = blockIdx.x * DG_ROWS;
     XStager<DG_THREADS, 1> xs;   // F <= 4096
     xs.load(act + (long long)pair * F, F);
+    __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
+    // unconditional loads (units past U read unit 0, unused), so the
+    // staging of act does not wait for the weights
     Q4KUnit raw[PASSES][UPL];
 #pragma unroll
     for (int p = 0; p < PASSES; p++) {
@@ -550,11 +569,16 @@ __global__ __launch_bounds__(DG_THREADS) void k_down_pair_q4k(const uint8_t *__r
 #pragma unroll
         for (int i = 0; i < UPL; i++) {
             const int u = lr + LPR * i;
-            if (u < U) q4k_load<GG>(row, u, raw[p][i]);
+            q4k_load<GG>(row, u < U ? u : 0, raw[p][i]);
         }
     }
     xs.store(xd, F);
     __syncthreads();
+    // with one unit per lane its digits are read from LDS once for all
+    // passes (read per pass they made the kernel LDS-bound)
+    constexpr bool XREG = UPL == 1;
+    XUnit xu;
+    if constexpr (XREG) xunit_load(xd, lr < U ? lr : 0, xu);
 #pragma unroll
     for (int p = 0; p < PASSES; p++) {
         const int r = r0 + (DG_THREADS / LPR) * p + rl;
@@ -562,7 +586,12 @@ __global__ __launch_bounds__(DG_THREADS) void k_down_pair_q4k(const uint8_t *__r
 #pragma unroll
         for (int i = 0; i < UPL; i++) {
             const int u = lr + LPR * i;
-            if (u < U) acc = q4k_unit_dot<GG>(raw[p][i], u, xd, acc);
+            if (u < U) {
+                if constexpr (XREG)
+                    acc = q4k_unit_dot<GG>(raw[p][i], u, xu, acc);
+                else
+                    acc = q4k_unit_dot<GG>(raw[p][i], u, xd, acc);
+            }
         }
         acc = group_sum<16>(acc);
         if (lr == 0) y[(long long)pair * H + r] = acc;
@@ -597,22 +626,31 @@ __global__ __launch_bounds__(DC_THREADS) void k_down_combine_q4k(const uint8_t *
     const int lr = lane & 15, rsub = lane >> 4;
     // dot d = (row rd, slot sd), d < DC_ROWS * k; wave w pass p takes dots 4*(w + 8p) + rsub
     constexpr int PASSES = (DC_ROWS * 8 + (DC_THREADS / 64) * RPP - 1) / ((DC_THREADS / 64) * RPP);
+    // the experts of the lane's dots first: the weight addresses wait for
+    // them, and loaded after x's rows that wait would take x's loads too
+    int esel[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int d = min(RPP * (wave + (DC_THREADS / 64) * p) + rsub, DC_ROWS * k - 1);
+        esel[p] = sel_idx[t * 8 + d % k];
+    }
     XStager<DC_THREADS, 2 * UPL> xs;   // k <= 8 vectors of F <= 1024 * UPL
     xs.load(act + (long long)t * k * F, F, k);
+    __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
+    // unconditional loads (dots past DC_ROWS*k redo the last one, units past
+    // U read unit 0; unused), so the staging does not wait for the weights
     Q4KUnit raw[PASSES][UPL];
 #pragma unroll
     for (int p = 0; p < PASSES; p++) {
-        const int d = RPP * (wave + (DC_THREADS / 64) * p) + rsub;
-        if (d < DC_ROWS * k) {
-            const int rd = d / k, sd = d % k;
-            const int e_sel = sel_idx[t * 8 + sd];
-            const int e = (unsigned)e_sel < (unsigned)E ? e_sel : 0;   // out of range: contributes 0 below
-            const uint8_t *row = down + ((long long)e * H + r0 + rd) * rb;
+        const int d = min(RPP * (wave + (DC_THREADS / 64) * p) + rsub, DC_ROWS * k - 1);
+        const int rd = d / k;
+        const int e_sel = esel[p];
+        const int e = (unsigned)e_sel < (unsigned)E ? e_sel : 0;   // out of range: contributes 0 below
+        const uint8_t *row = down + ((long long)e * H + r0 + rd) * rb;
 #pragma unroll
-            for (int i = 0; i < UPL; i++) {
-                const int u = lr + LPR * i;
-                if (u < U) q4k_load<GG>(row, u, raw[p][i]);
-            }
+        for (int i = 0; i < UPL; i++) {
+            const int u = lr + LPR * i;
+            q4k_load<GG>(row, u < U ? u : 0, raw[p][i]);
         }
     }
     xs.store(xd, F, k);
