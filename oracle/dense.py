@@ -118,3 +118,48 @@ class DenseOracle:
             gu = L["wgu"] @ h
             x = x + L["wdown"] @ silu_mul(gu[:c.ffn], gu[c.ffn:])
         return self.lm @ rmsnorm(x, self.output_norm, c.norm_eps)
+
+
+def decode_layer_major(oracle, cfg, host, tokens):
+    """Logits of decode steps token[i] at position i (i = 0, 1, ...) from an
+    empty cache, computed layer by layer: a layer's matrices are dequantised
+    (float64) once, applied to every position in order, and dropped, so a
+    full-size model never holds more than one layer's weights.  The same
+    arithmetic as DenseOracle.decode (layer l of position i reads only layer
+    l's K/V of positions <= i)."""
+    c = cfg
+    D, NQ, NKV = c.head_dim, c.n_heads, c.n_kv_heads
+    QR = (NQ + 2 * NKV) * D
+    deq = lambda W, qt, M, K: oracle.dequant_rows(W, qt, M, K).astype(np.float64)
+    lm_q = host["lm_head"]
+    row_bytes = lm_q.size // c.vocab
+    xs = [oracle.dequant_rows(lm_q.reshape(c.vocab, row_bytes)[t], c.qtype_embd, 1, c.hidden)[0].astype(np.float64)
+          for t in tokens]
+    n = len(tokens)
+    for t in host["layers"]:
+        qt = c.qtype_layers
+        wqkv = deq(t["wqkv"], qt, QR, c.hidden)
+        kc = np.zeros((NKV, n, D))
+        vc = np.zeros((NKV, n, D))
+        hs = []
+        for i in range(n):
+            qkv = wqkv @ rmsnorm(xs[i], t["attn_norm"], c.norm_eps)
+            q = qkv[:NQ * D].reshape(NQ, D)
+            k = qkv[NQ * D:(NQ + NKV) * D].reshape(NKV, D)
+            v = qkv[(NQ + NKV) * D:].reshape(NKV, D)
+            q = np.stack([rope(rmsnorm(q[h], t["q_norm"], c.norm_eps), i, c.rope_theta) for h in range(NQ)])
+            kc[:, i] = np.stack([rope(rmsnorm(k[h], t["k_norm"], c.norm_eps), i, c.rope_theta) for h in range(NKV)])
+            vc[:, i] = v
+            hs.append(attention(q, kc, vc, i + 1).reshape(-1))
+        del wqkv
+        wo = deq(t["wo"], qt, c.hidden, NQ * D)
+        xs = [xs[i] + wo @ hs[i] for i in range(n)]
+        del wo
+        wgu = deq(t["wgu"], qt, 2 * c.ffn, c.hidden)
+        gus = [wgu @ rmsnorm(x, t["ffn_norm"], c.norm_eps) for x in xs]
+        del wgu
+        wdown = deq(t["wdown"], qt, c.hidden, c.ffn)
+        xs = [x + wdown @ silu_mul(gu[:c.ffn], gu[c.ffn:]) for x, gu in zip(xs, gus)]
+        del wdown
+    lm = deq(lm_q, c.qtype_embd, c.vocab, c.hidden)
+    return [lm @ rmsnorm(x, host["output_norm"], c.norm_eps) for x in xs]

@@ -204,6 +204,34 @@ def test_dense_decode_configs2_context_4096(oracle):
     assert rel_l2(vcg[:, :, P], ref.vc[:, :, P]) <= DENSE_TOL
 
 
+def test_dense_decode_qwen3_4b_all_layers(oracle):
+    """BASELINE configs[2]'s model at full depth and vocabulary: all 36
+    layers at the Qwen3-4B widths and the 151936-row Q6_K lm_head (tied
+    embedding), two steps from an empty cache, against the float64 oracle
+    run layer by layer (decode_layer_major: one layer's weights dequantised
+    at a time).  The context is short (max_ctx 8); the 4096-position
+    attention is covered at these widths by the two-layer test above."""
+    import dataclasses
+    import torch
+    from oracle.dense import decode_layer_major
+    from trailblaze_amd.dense import QWEN3_4B
+    cfg = dataclasses.replace(QWEN3_4B, max_ctx=8)
+    print("dense Qwen3-4B full depth: building the model", flush=True)
+    m = _model(cfg, 36)
+    tokens = [151935, 4096]
+    outs = []
+    for pos, tok in enumerate(tokens):
+        logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+        print("dense Qwen3-4B full depth: step", pos, flush=True)
+        m.decode(tok, pos, logits)
+        outs.append(host(logits))
+    print("dense Qwen3-4B full depth: oracle", flush=True)
+    want = decode_layer_major(oracle, cfg, m.host, tokens)
+    for pos in range(len(tokens)):
+        err = rel_l2(outs[pos], want[pos])
+        assert err <= DENSE_TOL, (pos, err)
+
+
 @pytest.mark.parametrize("qt", [fm.Q4_K, fm.Q6_K])
 def test_dense_decode_ffn_beyond_16384(oracle, qt):
     """ffn 17408 (Qwen3-14B's): the down matvec's rows are longer than 16384

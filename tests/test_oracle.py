@@ -527,3 +527,33 @@ def test_dense_attention_and_rmsnorm_closed_forms():
     x = np.full(32, 3.0)
     assert np.allclose(rmsnorm(x, np.full(32, 2.0), 0.0), 2.0)
     assert np.allclose(rmsnorm(-x, np.ones(32), 0.0), -1.0)
+
+
+def test_dense_layer_major_matches_step_by_step(oracle):
+    """decode_layer_major (one layer's weights at a time, for full-size
+    models) gives the logits of DenseOracle.decode run step by step, to
+    float64 rounding, on a small random model with GQA and tied embeddings."""
+    from oracle.dense import DenseOracle, decode_layer_major
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=3, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=300,
+                      max_ctx=8)
+    rng = np.random.default_rng(31)
+    norm = lambda n: (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    QR = (cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim
+    host = {"layers": [{"attn_norm": norm(cfg.hidden), "q_norm": norm(cfg.head_dim), "k_norm": norm(cfg.head_dim),
+                        "ffn_norm": norm(cfg.hidden),
+                        "wqkv": synth.kquant_matrix(fm.Q4_K, QR, cfg.hidden, rng),
+                        "wo": synth.kquant_matrix(fm.Q4_K, cfg.hidden, cfg.n_heads * cfg.head_dim, rng),
+                        "wgu": synth.kquant_matrix(fm.Q4_K, 2 * cfg.ffn, cfg.hidden, rng),
+                        "wdown": synth.kquant_matrix(fm.Q4_K, cfg.hidden, cfg.ffn, rng)}
+                       for _ in range(cfg.n_layers)],
+            "lm_head": synth.kquant_matrix(fm.Q6_K, cfg.vocab, cfg.hidden, rng), "output_norm": norm(cfg.hidden)}
+    tokens = [5, 299, 17, 5]
+    seq = DenseOracle(oracle, cfg, host)
+    want = [seq.decode(t, i) for i, t in enumerate(tokens)]
+    got = decode_layer_major(oracle, cfg, host, tokens)
+    for g, w in zip(got, want):
+        assert np.allclose(g, w, rtol=1e-12, atol=1e-12 * np.abs(w).max())
+    # a one-token change at position 1 changes that step and the later ones only
+    alt = decode_layer_major(oracle, cfg, host, [5, 42, 17, 5])
+    assert np.array_equal(alt[0], got[0]) and not np.allclose(alt[1], got[1]) and not np.allclose(alt[3], got[3])
