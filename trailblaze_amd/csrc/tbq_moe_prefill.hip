@@ -424,17 +424,6 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
     }
     auto wload = [&](Q4Pair &w, int s) { q4pair_load<GG>(wrow + (long long)(s >> 1) * 144, 4 * (s & 1) + 2 * lh, w); };
     Q4Pair w0, w1, w2;
-    wload(w0, 0);
-    wload(w1, min(1, NS - 1));
-
-    // the tile's pair ids and activation-row scales, for the epilogue, in
-    // LDS behind the two activation buffers
-    int *po_s = reinterpret_cast<int *>(pf_lds + 2 * PF_MT * PF_LD);
-    float *sc_s = reinterpret_cast<float *>(po_s + PF_MT);
-    if (tid < PF_MT) {
-        po_s[tid] = po;
-        sc_s[tid] = pxo >= 0 ? xinv[pxo] : 0.f;
-    }
 
     // activation rows through a range-checked buffer descriptor: rows past
     // the tile's pair count (id -1) get an offset beyond the buffer, which
@@ -460,8 +449,23 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
             *reinterpret_cast<u32x4 *>(pf_lds + (buf * PF_MT + (it >> 4)) * PF_LD + 8 * (it & 15)) = xr[m];
         }
     };
+    // Issue order: chunk 0's activations and the rows' scales, then the
+    // weights of chunks 0 and 1, so that staging the activations and
+    // storing the scales wait for their own loads only (the wait counter
+    // counts loads in issue order); the weights arrive behind them.
     xload(0);
+    const float sc = tid < PF_MT && pxo >= 0 ? xinv[pxo] : 0.f;
+    wload(w0, 0);
+    wload(w1, min(1, NS - 1));
+    // the tile's pair ids and activation-row scales, for the epilogue, in
+    // LDS behind the two activation buffers
+    int *po_s = reinterpret_cast<int *>(pf_lds + 2 * PF_MT * PF_LD);
+    float *sc_s = reinterpret_cast<float *>(po_s + PF_MT);
     xstore(0);
+    if (tid < PF_MT) {
+        po_s[tid] = po;
+        sc_s[tid] = sc;
+    }
     xload(min(1, NS - 1));
     __syncthreads();
 
