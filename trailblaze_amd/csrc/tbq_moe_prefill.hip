@@ -1021,7 +1021,54 @@ hipError_t launch_moe_prefill_q4k_i8(const MoeArgs &a, void *scratch, hipStream_
                             nullptr, a8, ad, ab, (int)P, tpair, ttok, tiles, ntiles, ncb1, a.H, a.F, a.y);
 }
 
+// Short rows (n <= 64 * 4 * RW floats): one wave per row, four rows per
+// workgroup, the row's max by a wave reduction with no LDS or barrier; the
+// same scale and conversion as k_rows_f16.
+template <int RW>
+__global__ __launch_bounds__(256) void k_rows_f16_wave(const float *__restrict__ in, int rows, int n,
+                                                       _Float16 *__restrict__ out, float *__restrict__ inv) {
+    const int lane = threadIdx.x & 63;
+    const int row = min((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), rows - 1);   // past the end: redo the last
+    const bool store = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6) < rows;
+    const int n4 = n / 4;
+    const float4 *r = reinterpret_cast<const float4 *>(in + (long long)row * n);
+    float4 v[RW];
+#pragma unroll
+    for (int i = 0; i < RW; i++) v[i] = r[min(lane + 64 * i, n4 - 1)];   // clamped: unconditional
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < RW; i++)
+        if (lane + 64 * i < n4)
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    mx = wave_max(mx);
+    int e = 0;
+    frexpf(mx, &e);
+    int sh = mx > 0.f ? 15 - e : 0;
+    sh = sh > 126 ? 126 : (sh < -126 ? -126 : sh);
+    const float s = ldexpf(1.f, sh);
+    if (!store) return;
+    uint2 *o = reinterpret_cast<uint2 *>(out + (long long)row * n);
+#pragma unroll
+    for (int i = 0; i < RW; i++) {
+        if (lane + 64 * i < n4) {
+            const f16x2 a = {(_Float16)(v[i].x * s), (_Float16)(v[i].y * s)};
+            const f16x2 b = {(_Float16)(v[i].z * s), (_Float16)(v[i].w * s)};
+            o[lane + 64 * i] = make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+        }
+    }
+    if (lane == 0) inv[row] = ldexpf(1.f, -sh);
+}
+
 hipError_t launch_rows_f16(const float *in, int rows, int n, _Float16 *out, float *inv, hipStream_t st) {
+    const int rw = (n / 4 + 63) / 64;   // float4 per lane with a wave per row
+    const unsigned wgs = (unsigned)((rows + 3) / 4);
+    if (rw <= 4) {
+        if (rw <= 1) hipLaunchKernelGGL(k_rows_f16_wave<1>, dim3(wgs), dim3(256), 0, st, in, rows, n, out, inv);
+        else if (rw <= 2) hipLaunchKernelGGL(k_rows_f16_wave<2>, dim3(wgs), dim3(256), 0, st, in, rows, n, out, inv);
+        else if (rw <= 3) hipLaunchKernelGGL(k_rows_f16_wave<3>, dim3(wgs), dim3(256), 0, st, in, rows, n, out, inv);
+        else hipLaunchKernelGGL(k_rows_f16_wave<4>, dim3(wgs), dim3(256), 0, st, in, rows, n, out, inv);
+        return hipGetLastError();
+    }
     const int rv = (n / 4 + 255) / 256;
     switch (rv) {
     case 1: hipLaunchKernelGGL(k_rows_f16<1>, dim3(rows), dim3(256), 0, st, in, n, out, inv); break;

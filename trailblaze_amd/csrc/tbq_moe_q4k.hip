@@ -191,7 +191,7 @@ template <int NJ>
 __global__ __launch_bounds__(64) void k_topk(const float *__restrict__ logits, int E, int top_k,
                                              int *__restrict__ sel_idx, float *__restrict__ sel_w) {
     __shared__ float P[64 * NJ + 16];
-    topk_wave<NJ>(logits + (long long)blockIdx.x * E, E, top_k, blockIdx.x, P, sel_idx, sel_w);
+    topk_wave<NJ, false>(logits + (long long)blockIdx.x * E, E, top_k, blockIdx.x, P, sel_idx, sel_w);
 }
 
 // ---------------------------------------------------------------------------

@@ -27,7 +27,10 @@ __device__ __forceinline__ int topk_key(float f) {
     return f != f ? (int)0x80000000 : b ^ ((b >> 31) & 0x7FFFFFFF);
 }
 __device__ __forceinline__ float topk_unkey(int k) { return __builtin_bit_cast(float, k ^ ((k >> 31) & 0x7FFFFFFF)); }
-template <int NJ>
+// DEV: the logits may have been stored by other workgroups of the same
+// kernel, and the selection may be read by them: device-scope loads and
+// stores; otherwise (logits from an earlier kernel) plain ones.
+template <int NJ, bool DEV = true>
 __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int t, float *P,
                                           int *__restrict__ sel_idx, float *__restrict__ sel_w) {
     const int lane = threadIdx.x & 63;
@@ -36,7 +39,7 @@ __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? __hip_atomic_load(lg + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : NEG;
+        v[j] = e < E ? (DEV ? __hip_atomic_load(lg + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : lg[e]) : NEG;
     }
     float m = v[0];
 #pragma unroll
@@ -154,11 +157,16 @@ __device__ __forceinline__ void topk_wave(const float *lg, int E, int top_k, int
         } else {
             io = -1;
         }
-        // device-scope stores: a workgroup on another XCD may read the
-        // selection within the same kernel (the batch grouping of the DPP
-        // router)
-        __hip_atomic_store(sel_idx + t * 8 + lane, io, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(sel_w + t * 8 + lane, wo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // device-scope stores with DEV: a workgroup on another XCD may read
+        // the selection within the same kernel (the batch grouping of the
+        // DPP router)
+        if (DEV) {
+            __hip_atomic_store(sel_idx + t * 8 + lane, io, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(sel_w + t * 8 + lane, wo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            sel_idx[t * 8 + lane] = io;
+            sel_w[t * 8 + lane] = wo;
+        }
     }
 }
 
