@@ -626,13 +626,18 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
 // (each twice) against the pair's 16-element sums of q1 and q2 (exact
 // integers in fp32).  Per super-block and output, with F_l = 8 acc_a,l +
 // acc_b,l and M_l = sum_j m_j S_j,l:
-//   y += d dx (F_1 + F_2 / 256) - dmin dx (M_1 + M_2 / 256)
+//   y += dx (d (F_1 + F_2 / 256) - dmin (M_1 + M_2 / 256))
 // with d, dmin the row's fp16 super-block scales (a1's reading of the
-// scale bytes) and dx the pair's block scale; fp32 accumulation.
+// scale bytes) and dx the pair's block scale; fp32 accumulation.  The
+// activations are the MFMAs' A operand and the weights B, so a lane's
+// accumulators all belong to its own weight row (its d and dmin, no lane
+// exchange per flush) and to 16 pairs, whose block scales are staged in LDS
+// per item.
 //
 // Items: (tile, 32-pair sub-tile, row block), otherwise the layout of
 // k_moe_f16 (8 waves x 32 weight rows, MODE 0 gate/up interleaved per wave,
-// activation tile double-buffered in LDS, one barrier per chunk).
+// activation tile double-buffered in LDS, one barrier per chunk); SwiGLU
+// takes a gate row's up partner from lane li + 16.
 // ---------------------------------------------------------------------------
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
@@ -640,7 +645,9 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int I8_MT = 32;                 // pairs per item
 constexpr int I8_LD = PF_KC + 16;         // LDS row stride in bytes (one activation level)
-constexpr size_t I8_LDS_BYTES = (size_t)2 * I8_MT * 2 * I8_LD + I8_MT * 8;
+// two activation tiles, the pair and row ids, the pairs' block scales
+// (up to 16 super-blocks: K <= 4096)
+constexpr size_t I8_LDS_BYTES = (size_t)2 * I8_MT * 2 * I8_LD + I8_MT * 8 + 16 * I8_MT * 4;
 
 // Position of element e (< 16) of a 16-element group in the stored order.
 __device__ __forceinline__ int q8_pos(int e) {
@@ -744,6 +751,8 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
     extern __shared__ __attribute__((aligned(16))) int8_t i8_lds[];   // [2][I8_MT][2][I8_LD]
     int *po_s = reinterpret_cast<int *>(i8_lds + 2 * I8_MT * 2 * I8_LD);
     int *px_s = po_s + I8_MT;
+    float *dx_s = reinterpret_cast<float *>(px_s + I8_MT);   // [NSB][I8_MT] block scale of pair slot
+    static_assert(NSB <= 16, "dx_s holds 16 super-blocks");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, lh = lane >> 5;
     const long long rb = (long long)(K / 256) * 144;
     const int xbytes = x_rows * 2 * K;
@@ -787,13 +796,22 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
         wload(w1, min(1, NS - 1));
         xload(0);
         __syncthreads();   // po_s / px_s written
+        if (tid < NSB * I8_MT) {   // ordered before the first flush by chunk 0's barrier
+            const int ps = tid % I8_MT, sbi = tid / I8_MT, xrw = px_s[ps];
+            dx_s[tid] = xrw >= 0 ? XD[(long long)xrw * NSB + sbi] : 0.f;
+        }
         xstore(0);
         xload(1);
         __syncthreads();
-        const int pa = px_s[min(li, n - 1)];   // this lane's pair's activation row
+        const int pa = px_s[min(li, n - 1)];   // activation row of the lane's pair slot (B operand)
         i32x16 aa1 = {}, ab1 = {}, aa2 = {}, ab2 = {};
         f32x16 y = {};
-        // super-block flush: y += d dx (F1 + F2/256) - dmin dx (M1 + M2/256)
+        // The MFMAs take the activations as the A operand and the weights as
+        // B, so accumulator register r of lane l holds pair slot
+        // 8(r/4) + 4(l/32) + r%4 and the lane's own weight row l%32: the
+        // row's d and dmin are the lane's, the pairs' block scales come from
+        // LDS.  Super-block flush:
+        //   y += dx (d (F1 + F2/256) - dmin (M1 + M2/256))
         auto flush = [&](const Q4I8 &w, int sb) {
             f16x8 am;   // this lane's row's mins m_{4 lh + i}, each twice
 #pragma unroll
@@ -802,23 +820,24 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
                 am[2 * i] = m;
                 am[2 * i + 1] = m;
             }
-            const float dx = XD[(long long)pa * NSB + sb];
             const _Float16 *bsr = XB + (long long)pa * 2 * (K / 16) + 16 * sb + 8 * lh;
             const f16x8 b1 = *reinterpret_cast<const f16x8 *>(bsr);
             const f16x8 b2 = *reinterpret_cast<const f16x8 *>(bsr + K / 16);
-            const f32x16 m1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, b1, f32x16{}, 0, 0, 0);
-            const f32x16 m2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, b2, f32x16{}, 0, 0, 0);
+            const f32x16 m1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b1, am, f32x16{}, 0, 0, 0);
+            const f32x16 m2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b2, am, f32x16{}, 0, 0, 0);
+            const float dw = f16_ref((uint16_t)(w.dd & 0xFFFFu)), mw = f16_ref((uint16_t)(w.dd >> 16));
+            const float4 *dxs = reinterpret_cast<const float4 *>(dx_s + sb * I8_MT);
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                // d and dmin of accumulator r's row, from the lane that loads that row
-                const int row = 8 * (r >> 2) + 4 * lh + (r & 3);
-                const unsigned ddr = (unsigned)__shfl((int)w.dd, row);
-                const float dw = f16_ref((uint16_t)(ddr & 0xFFFFu)) * dx;
-                const float mw = f16_ref((uint16_t)(ddr >> 16)) * dx;
-                const float f = fmaf((float)(8 * aa2[r] + ab2[r]), 1.0f / 256.0f, (float)(8 * aa1[r] + ab1[r]));
-                const float mm = fmaf(m2[r], 1.0f / 256.0f, m1[r]);
-                y[r] = fmaf(dw, f, y[r]);
-                y[r] = fmaf(-mw, mm, y[r]);
+            for (int c = 0; c < 4; c++) {
+                const float4 dx4 = dxs[2 * c + lh];   // pair slots 8c + 4lh + 0..3
+                const float dxv[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int r = 4 * c + q;
+                    const float f = fmaf((float)(8 * aa2[r] + ab2[r]), 1.0f / 256.0f, (float)(8 * aa1[r] + ab1[r]));
+                    const float mm = fmaf(m2[r], 1.0f / 256.0f, m1[r]);
+                    y[r] = fmaf(dxv[q], fmaf(dw, f, -mw * mm), y[r]);
+                }
             }
             aa1 = i32x16{};
             ab1 = i32x16{};
@@ -844,10 +863,10 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
                     const i32x4 Ab = {(int)mul(n0, vb), (int)mul(n1, vb), (int)mul(n2, vb), (int)mul(n3, vb)};
                     const i32x4 bv1 = *reinterpret_cast<const i32x4 *>(xb + 32 * ks);
                     const i32x4 bv2 = *reinterpret_cast<const i32x4 *>(xb + I8_LD + 32 * ks);
-                    aa1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(Aa, bv1, aa1, 0, 0, 0);
-                    ab1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ab, bv1, ab1, 0, 0, 0);
-                    aa2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(Aa, bv2, aa2, 0, 0, 0);
-                    ab2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ab, bv2, ab2, 0, 0, 0);
+                    aa1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv1, Aa, aa1, 0, 0, 0);
+                    ab1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv1, Ab, ab1, 0, 0, 0);
+                    aa2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv2, Aa, aa2, 0, 0, 0);
+                    ab2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv2, Ab, ab2, 0, 0, 0);
                 }
                 if (s & 1) flush(wc, s >> 1);
                 if (s + 1 < NS) xstore((s + 1) & 1);
@@ -860,30 +879,26 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
             chunk(s + 1, w1, w0);
             chunk(s + 2, w2, w1);
         }
-        // accumulator register r of lane l: row 8(r/4) + 4 lh + r%4 of the
-        // wave's 32, pair li of the sub-tile
-        if (li < n) {
-            const int p = po_s[li];
-            if (MODE == 0) {
+        // accumulator register r of lane l: pair slot 8(r/4) + 4 lh + r%4 of
+        // the sub-tile, the wave's weight row li
+        if (MODE == 0) {
+            // gate (rows li < 16) and up (li + 16) of column 16 wave + li%16:
+            // the up value from lane li + 16
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    float o[4];
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        const int r = 4 * h + c;
-                        const float g = y[r], u = y[r + 8];
-                        o[c] = g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
-                    }
-                    const int col = cb * PF_COLS + 16 * wave + 8 * h + 4 * lh;
-                    *reinterpret_cast<float4 *>(out + (long long)p * F + col) = make_float4(o[0], o[1], o[2], o[3]);
+            for (int r = 0; r < 16; r++) {
+                const float uv = __shfl_xor(y[r], 16);
+                const int pr = 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (li < 16 && pr < n) {
+                    const float g = y[r];
+                    const float o = g * uv * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+                    out[(long long)po_s[pr] * F + cb * PF_COLS + 16 * wave + li] = o;
                 }
-            } else {
+            }
+        } else {
 #pragma unroll
-                for (int h = 0; h < 4; h++) {
-                    const int row = cb * PF_ROWS + 32 * wave + 8 * h + 4 * lh;
-                    *reinterpret_cast<float4 *>(out + (long long)p * H + row) =
-                        make_float4(y[4 * h], y[4 * h + 1], y[4 * h + 2], y[4 * h + 3]);
-                }
+            for (int r = 0; r < 16; r++) {
+                const int pr = 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (pr < n) out[(long long)po_s[pr] * H + cb * PF_ROWS + 32 * wave + li] = y[r];
             }
         }
         __syncthreads();   // the next item rewrites the pair lists and the activation buffers
