@@ -645,9 +645,10 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int I8_MT = 32;                 // pairs per item
 constexpr int I8_LD = PF_KC + 16;         // LDS row stride in bytes (one activation level)
-// two activation tiles, the pair and row ids, the pairs' block scales
-// (up to 16 super-blocks: K <= 4096)
-constexpr size_t I8_LDS_BYTES = (size_t)2 * I8_MT * 2 * I8_LD + I8_MT * 8 + 16 * I8_MT * 4;
+// two activation tiles, the pair and row ids, the pairs' block scales (up
+// to 16 super-blocks: K <= 4096), the pairs' 16-element sums of both levels
+// (K / 8 halves per pair)
+constexpr size_t I8_LDS_BYTES = (size_t)2 * I8_MT * 2 * I8_LD + I8_MT * 8 + 16 * I8_MT * 4 + I8_MT * 4096 / 4;
 
 // Position of element e (< 16) of a 16-element group in the stored order.
 __device__ __forceinline__ int q8_pos(int e) {
@@ -752,6 +753,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
     int *po_s = reinterpret_cast<int *>(i8_lds + 2 * I8_MT * 2 * I8_LD);
     int *px_s = po_s + I8_MT;
     float *dx_s = reinterpret_cast<float *>(px_s + I8_MT);   // [NSB][I8_MT] block scale of pair slot
+    _Float16 *xb_s = reinterpret_cast<_Float16 *>(dx_s + 16 * I8_MT);   // [I8_MT][K/8] group sums
     static_assert(NSB <= 16, "dx_s holds 16 super-blocks");
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, lh = lane >> 5;
     const long long rb = (long long)(K / 256) * 144;
@@ -796,14 +798,26 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
         wload(w1, min(1, NS - 1));
         xload(0);
         __syncthreads();   // po_s / px_s written
-        if (tid < NSB * I8_MT) {   // ordered before the first flush by chunk 0's barrier
+        // the pair slots' block scales and group sums into LDS (ordered
+        // before the first flush by chunk 0's barrier): the flushes then
+        // wait for no global load
+        if (tid < NSB * I8_MT) {
             const int ps = tid % I8_MT, sbi = tid / I8_MT, xrw = px_s[ps];
             dx_s[tid] = xrw >= 0 ? XD[(long long)xrw * NSB + sbi] : 0.f;
+        }
+        {
+            constexpr int SEG = K / 64;   // 16-byte segments of a slot's K / 8 halves
+#pragma unroll
+            for (int i0 = 0; i0 < I8_MT * SEG; i0 += PF_THREADS) {
+                const int i = i0 + tid, ps = min(i / SEG, I8_MT - 1), sg = i % SEG, xrw = px_s[ps];
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(XB + (long long)(xrw >= 0 ? xrw : 0) * (K / 8) + 8 * sg);
+                if (i < I8_MT * SEG)
+                    *reinterpret_cast<u32x4 *>(xb_s + ps * (K / 8) + 8 * sg) = xrw >= 0 ? v : u32x4{0u, 0u, 0u, 0u};
+            }
         }
         xstore(0);
         xload(1);
         __syncthreads();
-        const int pa = px_s[min(li, n - 1)];   // activation row of the lane's pair slot (B operand)
         i32x16 aa1 = {}, ab1 = {}, aa2 = {}, ab2 = {};
         f32x16 y = {};
         // The MFMAs take the activations as the A operand and the weights as
@@ -820,7 +834,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
                 am[2 * i] = m;
                 am[2 * i + 1] = m;
             }
-            const _Float16 *bsr = XB + (long long)pa * 2 * (K / 16) + 16 * sb + 8 * lh;
+            const _Float16 *bsr = xb_s + li * (K / 8) + 16 * sb + 8 * lh;   // pair slot li's sums
             const f16x8 b1 = *reinterpret_cast<const f16x8 *>(bsr);
             const f16x8 b2 = *reinterpret_cast<const f16x8 *>(bsr + K / 16);
             const f32x16 m1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b1, am, f32x16{}, 0, 0, 0);
