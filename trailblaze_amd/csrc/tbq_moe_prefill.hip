@@ -725,18 +725,23 @@ __global__ __launch_bounds__(256) void k_rows_q8(const float *__restrict__ in, i
 // chunk's four scale bytes, the four mins of its half of the super-block
 // (for the min MFMA), and 8 quant bytes of each of the chunk's four
 // sub-blocks (elements 16 lh .. 16 lh + 15 of sub-block 4 (c & 1) + ks).
+// A lane's share of chunk c (half c & 1 of a super-block, sub-blocks
+// 4(c & 1) .. +3): half lh of the k range, as two whole sub-blocks, lh and
+// 2 + lh of the chunk (two 16-byte loads; MFMA step ks takes sub-block
+// 2(ks >> 1) + lh, bytes 8(ks & 1) .. +7, and the activations' groups in
+// the same order), d/dmin, the chunk's scale dword and the mins of the
+// lane's half.
 struct Q4I8 {
     unsigned dd, sw, mw;
-    uint2 q[4];
+    uint4 q[2];
 };
 
 __device__ __forceinline__ void q4i8_load(const uint8_t *sb, int c, int lh, Q4I8 &r) {
     r.dd = *reinterpret_cast<const unsigned *>(sb);
     r.sw = *reinterpret_cast<const unsigned *>(sb + ((c & 1) ? 12 : 4));
     r.mw = *reinterpret_cast<const unsigned *>(sb + (lh ? 16 : 8));   // mins 4..7 sit in quant bytes 0..3
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++)
-        r.q[ks] = *reinterpret_cast<const uint2 *>(sb + 16 + 16 * (4 * (c & 1) + ks) + 8 * lh);
+    r.q[0] = *reinterpret_cast<const uint4 *>(sb + 16 + 64 * (c & 1) + 16 * lh);
+    r.q[1] = *reinterpret_cast<const uint4 *>(sb + 16 + 64 * (c & 1) + 16 * (2 + lh));
 }
 
 template <int MODE, int NS>
@@ -861,11 +866,12 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
         auto chunk = [&](int s, const Q4I8 &wc, Q4I8 &wn) {
             wload(wn, s + 2);
             if (s < NS) {
-                const int8_t *xb = i8_lds + ((s & 1) * I8_MT + li) * 2 * I8_LD + 16 * lh;
+                const int8_t *xb = i8_lds + ((s & 1) * I8_MT + li) * 2 * I8_LD + 32 * lh;
 #pragma unroll
                 for (int ks = 0; ks < 4; ks++) {
-                    const uint2 q = wc.q[ks];
-                    const unsigned sc = (wc.sw >> (8 * ks)) & 63u;
+                    const uint4 q4 = wc.q[ks >> 1];
+                    const uint2 q = (ks & 1) ? make_uint2(q4.z, q4.w) : make_uint2(q4.x, q4.y);
+                    const unsigned sc = (wc.sw >> (8 * (2 * (ks >> 1) + lh))) & 63u;   // sub-block 2(ks>>1) + lh
                     const unsigned short a = (unsigned short)(sc >> 3), b = (unsigned short)(sc & 7u);
                     const unsigned n0 = q.x & 0x0F0F0F0Fu, n1 = (q.x >> 4) & 0x0F0F0F0Fu;
                     const unsigned n2 = q.y & 0x0F0F0F0Fu, n3 = (q.y >> 4) & 0x0F0F0F0Fu;
@@ -875,8 +881,10 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
                     };
                     const i32x4 Aa = {(int)mul(n0, va), (int)mul(n1, va), (int)mul(n2, va), (int)mul(n3, va)};
                     const i32x4 Ab = {(int)mul(n0, vb), (int)mul(n1, vb), (int)mul(n2, vb), (int)mul(n3, vb)};
-                    const i32x4 bv1 = *reinterpret_cast<const i32x4 *>(xb + 32 * ks);
-                    const i32x4 bv2 = *reinterpret_cast<const i32x4 *>(xb + I8_LD + 32 * ks);
+                    // 16-element group 4(ks >> 1) + 2 lh + (ks & 1) of the chunk
+                    const int go = 64 * (ks >> 1) + 16 * (ks & 1);
+                    const i32x4 bv1 = *reinterpret_cast<const i32x4 *>(xb + go);
+                    const i32x4 bv2 = *reinterpret_cast<const i32x4 *>(xb + I8_LD + go);
                     aa1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv1, Aa, aa1, 0, 0, 0);
                     ab1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv1, Ab, ab1, 0, 0, 0);
                     aa2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv2, Aa, aa2, 0, 0, 0);
