@@ -644,6 +644,9 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int I8_MT = 32;                 // pairs per item
+#ifndef I8_AHEAD
+#define I8_AHEAD 3                        // weight chunks in flight ahead of the one in use (2 or 3)
+#endif
 constexpr int I8_LD = PF_KC + 16;         // LDS row stride in bytes (one activation level)
 // two activation tiles, the pair and row ids, the pairs' block scales (up
 // to 16 super-blocks: K <= 4096), the pairs' 16-element sums of both levels
@@ -754,6 +757,8 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
     constexpr int K = NS * PF_KC;
     constexpr int NSB = K / 256;
     constexpr int NQ = PF_MT / I8_MT;   // sub-tiles per tile
+    // weight chunks loaded ahead: 3 for long rows (two spill at K = 768)
+    constexpr int AH = NS >= 8 ? I8_AHEAD : 2;
     extern __shared__ __attribute__((aligned(16))) int8_t i8_lds[];   // [2][I8_MT][2][I8_LD]
     int *po_s = reinterpret_cast<int *>(i8_lds + 2 * I8_MT * 2 * I8_LD);
     int *px_s = po_s + I8_MT;
@@ -798,9 +803,10 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
             *reinterpret_cast<u32x4 *>(i8_lds + ((buf * I8_MT + (tid >> 4)) * 2 + ((tid >> 3) & 1)) * I8_LD +
                                        16 * (tid & 7)) = xv;
         };
-        Q4I8 w0, w1, w2;
+        Q4I8 w0, w1, w2, w3;
         wload(w0, 0);
         wload(w1, min(1, NS - 1));
+        if constexpr (AH == 3) wload(w2, min(2, NS - 1));
         xload(0);
         __syncthreads();   // po_s / px_s written
         // the pair slots' block scales and group sums into LDS (ordered
@@ -864,7 +870,7 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
             ab2 = i32x16{};
         };
         auto chunk = [&](int s, const Q4I8 &wc, Q4I8 &wn) {
-            wload(wn, s + 2);
+            wload(wn, s + AH);
             if (s < NS) {
                 const int8_t *xb = i8_lds + ((s & 1) * I8_MT + li) * 2 * I8_LD + 32 * lh;
 #pragma unroll
@@ -896,10 +902,19 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_i8(const uint8_t *__restrict
             xload(s + 2);
             if (s < NS) __syncthreads();
         };
-        for (int s = 0; s < NS; s += 3) {
-            chunk(s, w0, w2);
-            chunk(s + 1, w1, w0);
-            chunk(s + 2, w2, w1);
+        if constexpr (AH == 3) {
+            for (int s = 0; s < NS; s += 4) {
+                chunk(s, w0, w3);
+                chunk(s + 1, w1, w0);
+                chunk(s + 2, w2, w1);
+                chunk(s + 3, w3, w2);
+            }
+        } else {
+            for (int s = 0; s < NS; s += 3) {
+                chunk(s, w0, w2);
+                chunk(s + 1, w1, w0);
+                chunk(s + 2, w2, w1);
+            }
         }
         // accumulator register r of lane l: pair slot 8(r/4) + 4 lh + r%4 of
         // the sub-tile, the wave's weight row li
