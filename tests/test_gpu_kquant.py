@@ -105,7 +105,7 @@ def test_matvec_edge_shapes(oracle, qt, M, K):
 
 @pytest.mark.parametrize("variant", [tb.TBQ_MV_FMA, tb.TBQ_MV_INTDOT])
 @pytest.mark.parametrize("M,K", [(1, 256), (7, 512), (200, 768), (1000, 2048), (4096, 4096), (6144, 4096),
-                                 (5000, 2560), (333, 8192),
+                                 (2560, 4096), (2049, 4096), (5000, 2560), (333, 8192),
                                  (4096, 12288), (65, 16384)])
 def test_matvec_q4k_kernels(oracle, variant, M, K):
     if variant == tb.TBQ_MV_FMA and K > 15360:

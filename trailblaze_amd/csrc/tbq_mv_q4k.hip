@@ -207,6 +207,11 @@ static hipError_t launch_q4k_xr_k(const void *W, int M, int K, const float *x, f
     // below two rows per lane stay faster, 4.24 against 4.31 us)
     constexpr int RW = Q4K_XR_NW * Q4K_XR_R;
     const int n_cu = tbq_cu_count() > 0 ? tbq_cu_count() : 256;
+    // 8 to 10 rows per CU (2560 rows on 256 CUs): workgroups of 10 waves of
+    // one row, one workgroup per CU, where workgroups of 16 rows left 96 CUs
+    // without one (Qwen3-4B's o projection 2560x4096: dense decode 1618 ->
+    // 1607 us/token; 5 waves of two rows: 1622)
+    if (M > 8LL * n_cu && M <= 10LL * n_cu) return launch_q4k_xr<64, 1, 10, PRO, GG>(W, M, K, x, y, s, pro);
     const long long wg = ((long long)M + RW - 1) / RW;
     if (Q4K_XR_R > 1 && wg > n_cu && wg < 2LL * n_cu)
         return launch_q4k_xr<64, 1, Q4K_XR_NW, PRO, GG>(W, M, K, x, y, s, pro);
