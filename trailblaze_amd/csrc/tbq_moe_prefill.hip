@@ -537,9 +537,9 @@ __global__ __launch_bounds__(PF_THREADS) void k_moe_f16(const uint8_t *__restric
             xload(min(s + 2, NS - 1));
             if (s < NS) __syncthreads();
         };
-        if constexpr (NS == 4) {
-            // two trips, not unrolled: unrolled, the compiler overlaps the
-            // trips past what the register file holds (spills)
+        if constexpr (NS == 4 || (GG && NS <= 8)) {
+            // two or three trips, not unrolled: unrolled, the compiler
+            // overlaps the trips past what the register file holds (spills)
 #pragma nounroll
             for (int s = 0; s < NS; s += 3) {
                 chunk(s, w0, w2);
