@@ -78,6 +78,33 @@ __global__ __launch_bounds__(1024) void k_add_rmsnorm(const float *__restrict__ 
     }
 }
 
+// h = x * rsqrt(S / n + eps) * w, S the sum of the NPART_MAX partial sums of
+// squares of x in part (PRO_NORMP's prologue as a launch of its own, where
+// the matvec that follows has none for the shape).  One workgroup; every
+// wave forms S itself.
+__global__ __launch_bounds__(1024) void k_rmsnorm_p(const float *__restrict__ x, const float *__restrict__ part,
+                                                    const float *__restrict__ w, int n, float eps,
+                                                    float *__restrict__ h) {
+    float pp[NPART_MAX / 64];
+    pro_part_load(part, pp);
+    const float r = 1.0f / sqrtf(pro_part_sum(pp) / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) h[i] = x[i] * r * w[i];
+}
+
+// res[i] += v[i] and PRO_RES's partial sums of squares (the epilogue as a
+// launch of its own).  grid = ceil(n / 256) <= NPART_MAX.
+__global__ __launch_bounds__(256) void k_res_add(float *__restrict__ res, const float *__restrict__ v, int n,
+                                                 float *__restrict__ part_out) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    float hsq = 0.f;
+    if (i < n) {
+        const float h = res[i] + v[i];
+        res[i] = h;
+        hsq = h * h;
+    }
+    pro_res_flush(hsq, part_out);
+}
+
 // RoPE table of one step: rc[j] = cos, rc[D/2 + j] = sin of pos *
 // theta^(-2j/D), formed and reduced in fp64 so the error does not grow with
 // the position.  One workgroup of D/2 threads.
@@ -406,7 +433,7 @@ __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, in
 }
 
 struct DenseWs {
-    float *x, *x2, *h, *qkv, *att, *y, *gu, *a, *part, *rope;
+    float *x, *x2, *h, *qkv, *att, *y, *gu, *a, *part, *rope, *psum;
 };
 
 static size_t up256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -432,6 +459,7 @@ static DenseWs dense_ws(const tbq_dense_model *m, void *ws, size_t *total) {
     w.a = take(m->ffn);
     w.part = take((size_t)m->n_heads * nsplit * (m->head_dim + 2));
     w.rope = take(m->head_dim);
+    w.psum = take(NPART_MAX);
     if (total) *total = off;
     return w;
 }
@@ -473,17 +501,26 @@ static hipError_t launch_attn_d(int G, const float *qkv, const float *qn, const 
 // tmp_x (K floats) and tmp_y (2M floats, MV_GLU only).
 static hipError_t dense_mv(int qt, const void *W, int M, int K, const float *x, float *out, int mode, const MvPro &pro,
                            float *tmp_x, float *tmp_y, hipStream_t st) {
-    // the register-x Q4_K kernel for plain matvecs; with the norm prologue
-    // the K-quant kernel, measured 1.3 us per layer faster at the Qwen3-4B
-    // shapes
+    // the register-x Q4_K kernel for plain matvecs and the residual
+    // epilogue; with the norm prologue the K-quant kernel, measured 1.3 us
+    // per layer faster at the Qwen3-4B shapes
     hipError_t e = hipErrorNotSupported;
-    if ((qt == QT_Q4_K || qt == QT_GQ4_K) && K <= 4096 && M <= 8192 && mode == PRO_NONE)
+    if ((qt == QT_Q4_K || qt == QT_GQ4_K) && K <= 4096 && M <= 8192 && (mode == PRO_NONE || mode == PRO_RES))
         e = launch_matvec_q4k_pro(mode, pro, W, M, K, x, out, st, qt == QT_GQ4_K);
     if (e == hipErrorNotSupported) e = launch_matvec_kq_pro(mode, pro, qt, W, M, K, x, out, st, tbq_cu_count());
     if (e != hipErrorNotSupported) return e;
+    if (mode == PRO_RES) {
+        if ((M + 255) / 256 > NPART_MAX) return hipErrorNotSupported;
+        if (!tbq_matvec(W, qt, M, K, x, tmp_y, st)) return hipErrorUnknown;
+        hipLaunchKernelGGL(k_res_add, dim3((M + 255) / 256), dim3(256), 0, st, out, tmp_y, M, pro.part_out);
+        return hipGetLastError();
+    }
     const float *xin = x;
     if (mode & PRO_NORM) {
         hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(1024), 0, st, x, pro.y, pro.w, K, pro.eps, tmp_x, pro.vo);
+        xin = tmp_x;
+    } else if (mode & PRO_NORMP) {
+        hipLaunchKernelGGL(k_rmsnorm_p, dim3(1), dim3(1024), 0, st, x, pro.part, pro.w, K, pro.eps, tmp_x);
         xin = tmp_x;
     }
     if (!(mode & MV_GLU)) return tbq_matvec(W, qt, M, K, xin, out, st) ? hipSuccess : hipErrorUnknown;
@@ -492,10 +529,12 @@ static hipError_t dense_mv(int qt, const void *W, int M, int K, const float *x, 
     return hipGetLastError();
 }
 
-// Validation happens in the C-ABI wrapper.  The residual stream alternates
-// between w.x and w.x2: the add + RMSNorm before a matvec is that matvec's
-// staging prologue, whose workgroup 0 stores x + y into the other buffer
-// (the others are still reading x).
+// Validation happens in the C-ABI wrapper.  The residual stream lives in
+// w.x: the o and down matvecs add their rows to it in place (PRO_RES) and
+// leave the partial sums of squares the next matvec's RMSNorm prologue
+// (PRO_NORMP) needs in w.psum, so that prologue neither reads the sublayer
+// output nor reduces over its workgroup.  Layer 0's prologue normalises the
+// embedding row with its own block-wide sum (PRO_NORM).
 hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,
                                hipStream_t st) {
     const int H = m->hidden, D = m->head_dim, NQ = m->n_heads, NKV = m->n_kv_heads, G = NQ / NKV, F = m->ffn;
@@ -503,26 +542,35 @@ hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, flo
     auto qt_of = [m](int q) { return canon_qt(q ? q : m->qtype_layers); };
     const DenseWs w = dense_ws(m, ws, nullptr);
     const size_t erb = tbq_row_bytes(m->qtype_embd, H);
-    float *xa = w.x, *xb = w.x2;
-    hipError_t err = launch_dequant(canon_qt(m->qtype_embd), (const uint8_t *)m->tok_embd + (size_t)token * erb, H, xa, st);
+    float *res = w.x;
+    hipError_t err = launch_dequant(canon_qt(m->qtype_embd), (const uint8_t *)m->tok_embd + (size_t)token * erb, H, res, st);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(64), 0, st, pos, m->rope_theta, D, w.rope);
-    const float *yprev = nullptr;
+    bool have_part = false;   // w.psum holds the partial sums of squares of res
+    // rmsnorm(res) * wn as the next matvec's staging prologue
+    auto norm_pro = [&](const float *wn, int *mode) {
+        *mode = have_part ? PRO_NORMP : PRO_NORM;
+        MvPro p{nullptr, wn, nullptr, m->norm_eps};
+        p.part = have_part ? w.psum : nullptr;
+        return p;
+    };
+    MvPro pres{};
+    pres.part_out = w.psum;
     for (int l = 0; l < m->n_layers; l++) {
         const tbq_dense_layer &L = m->layers[l];
         const size_t kvoff = (size_t)l * NKV * m->max_ctx * D;
-        // qkv = Wqkv rmsnorm(xa + yprev); xb = xa + yprev (stored by the first
-        // launch only when q, k and v are separate matrices)
-        const MvPro pa{yprev, L.attn_norm, xb, m->norm_eps}, pa2{yprev, L.attn_norm, nullptr, m->norm_eps};
+        // qkv = Wqkv rmsnorm(res)
+        int pm;
+        const MvPro pa = norm_pro(L.attn_norm, &pm);
         if (L.wqkv) {
-            err = dense_mv(qt_of(L.qt_qkv), L.wqkv, QKVR, H, xa, w.qkv, PRO_NORM, pa, w.h, nullptr, st);
+            err = dense_mv(qt_of(L.qt_qkv), L.wqkv, QKVR, H, res, w.qkv, pm, pa, w.h, nullptr, st);
         } else {
-            err = dense_mv(qt_of(L.qt_q), L.wq, NQ * D, H, xa, w.qkv, PRO_NORM, pa, w.h, nullptr, st);
+            err = dense_mv(qt_of(L.qt_q), L.wq, NQ * D, H, res, w.qkv, pm, pa, w.h, nullptr, st);
             if (err == hipSuccess)
-                err = dense_mv(qt_of(L.qt_k), L.wk, NKV * D, H, xa, w.qkv + NQ * D, PRO_NORM, pa2, w.h, nullptr, st);
+                err = dense_mv(qt_of(L.qt_k), L.wk, NKV * D, H, res, w.qkv + NQ * D, pm, pa, w.h, nullptr, st);
             if (err == hipSuccess)
-                err = dense_mv(qt_of(L.qt_v), L.wv, NKV * D, H, xa, w.qkv + (NQ + NKV) * D, PRO_NORM, pa2, w.h,
-                               nullptr, st);
+                err = dense_mv(qt_of(L.qt_v), L.wv, NKV * D, H, res, w.qkv + (NQ + NKV) * D, pm, pa, w.h, nullptr,
+                               st);
         }
         if (err != hipSuccess) return err;
         err = D == 128 ? launch_attn_d<128>(G, w.qkv, L.q_norm, L.k_norm, NQ, NKV, pos, w.rope, m->norm_eps,
@@ -530,31 +578,32 @@ hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, flo
                        : launch_attn_d<64>(G, w.qkv, L.q_norm, L.k_norm, NQ, NKV, pos, w.rope, m->norm_eps,
                                            m->k_cache + kvoff, m->v_cache + kvoff, m->max_ctx, w.part, w.att, st);
         if (err != hipSuccess) return err;
-        if ((err = dense_mv(qt_of(L.qt_o), L.wo, H, NQ * D, w.att, w.y, PRO_NONE, MvPro{}, nullptr, nullptr, st)) !=
+        // res += Wo att
+        if ((err = dense_mv(qt_of(L.qt_o), L.wo, H, NQ * D, w.att, res, PRO_RES, pres, nullptr, w.y, st)) !=
             hipSuccess)
             return err;
-        // a = silu(Wg h) * (Wu h) with h = rmsnorm(xb + y); xa = xb + y
-        const MvPro pf{w.y, L.ffn_norm, xa, m->norm_eps}, pf2{w.y, L.ffn_norm, nullptr, m->norm_eps};
+        have_part = true;
+        // a = silu(Wg h) * (Wu h) with h = rmsnorm(res)
+        const MvPro pf = norm_pro(L.ffn_norm, &pm);
         if (L.wgu) {
-            err = dense_mv(qt_of(L.qt_gu), L.wgu, F, H, xb, w.a, PRO_NORM | MV_GLU, pf, w.h, w.gu, st);
+            err = dense_mv(qt_of(L.qt_gu), L.wgu, F, H, res, w.a, pm | MV_GLU, pf, w.h, w.gu, st);
         } else {
-            err = dense_mv(qt_of(L.qt_gate), L.wgate, F, H, xb, w.gu, PRO_NORM, pf, w.h, nullptr, st);
-            if (err == hipSuccess)
-                err = dense_mv(qt_of(L.qt_up), L.wup, F, H, xb, w.gu + F, PRO_NORM, pf2, w.h, nullptr, st);
+            err = dense_mv(qt_of(L.qt_gate), L.wgate, F, H, res, w.gu, pm, pf, w.h, nullptr, st);
+            if (err == hipSuccess) err = dense_mv(qt_of(L.qt_up), L.wup, F, H, res, w.gu + F, pm, pf, w.h, nullptr, st);
             if (err == hipSuccess) {
                 hipLaunchKernelGGL(k_swiglu, dim3((F + 255) / 256), dim3(256), 0, st, w.gu, F, w.a);
                 err = hipGetLastError();
             }
         }
         if (err != hipSuccess) return err;
-        // y = Wdown a
-        if ((err = dense_mv(qt_of(L.qt_down), L.wdown, H, F, w.a, w.y, PRO_NONE, MvPro{}, nullptr, nullptr, st)) !=
+        // res += Wdown a
+        if ((err = dense_mv(qt_of(L.qt_down), L.wdown, H, F, w.a, res, PRO_RES, pres, nullptr, w.y, st)) !=
             hipSuccess)
             return err;
-        yprev = w.y;
     }
-    const MvPro po{yprev, m->output_norm, nullptr, m->norm_eps};
-    if ((err = dense_mv(canon_qt(m->qtype_embd), m->lm_head, m->vocab, H, xa, logits, PRO_NORM, po, w.h, nullptr, st)) !=
+    int pm;
+    const MvPro po = norm_pro(m->output_norm, &pm);
+    if ((err = dense_mv(canon_qt(m->qtype_embd), m->lm_head, m->vocab, H, res, logits, pm, po, w.h, nullptr, st)) !=
         hipSuccess)
         return err;
     return hipGetLastError();

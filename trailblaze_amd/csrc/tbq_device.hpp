@@ -251,6 +251,37 @@ __device__ __forceinline__ float pro_block_sum(float v) {
     return s;
 }
 
+// Partial sums of squares passed from a PRO_RES matvec to a PRO_NORMP one
+// (the largest grid of a PRO_RES launch).
+constexpr int NPART_MAX = 512;
+
+// PRO_RES: the workgroup's sum of squares of its new residual rows (one
+// float per thread, 0 where a thread stored none) to part_out[blockIdx.x],
+// and zeros to part_out[blockIdx.x + gridDim.x * j] below NPART_MAX, so the
+// next PRO_NORMP sums NPART_MAX values whatever this grid was.  Every
+// thread of the workgroup calls it.
+__device__ __forceinline__ void pro_res_flush(float v, float *part_out) {
+    v = pro_block_sum(v);
+    if (threadIdx.x == 0) {
+        part_out[blockIdx.x] = v;
+        for (int i = blockIdx.x + gridDim.x; i < NPART_MAX; i += gridDim.x) part_out[i] = 0.f;
+    }
+}
+
+// PRO_NORMP: the sum of the NPART_MAX partials, by each wave on its own
+// (lane l adds partials l + 64 j in j order, then a fixed-order wave sum),
+// so every wave of every workgroup gets the same value.
+__device__ __forceinline__ float pro_part_sum(const float (&pp)[NPART_MAX / 64]) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NPART_MAX / 64; j++) s += pp[j];
+    return group_sum<64>(s);
+}
+__device__ __forceinline__ void pro_part_load(const float *part, float (&pp)[NPART_MAX / 64]) {
+#pragma unroll
+    for (int j = 0; j < NPART_MAX / 64; j++) pp[j] = part[(threadIdx.x & 63) + 64 * j];
+}
+
 // An empty asm statement that takes v and gives it back and clobbers
 // memory: code that uses v stays after it, loads issued before it stay
 // before it.

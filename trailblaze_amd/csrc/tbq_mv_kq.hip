@@ -145,7 +145,8 @@ struct GMem {
 template <int NT, int ORD, int MAXT, int PRO = PRO_NONE>   // ORD: 0 NATURAL, 1 PAIR, 2 QUAD
 struct KqStager {
     float e[MAXT][4];
-    float p1[MAXT][4], p2[MAXT][4];   // PRO_NORM inputs: y, w
+    float p1[MAXT][4], p2[MAXT][4];   // PRO_NORM inputs: y, w (PRO_NORMP: w)
+    float pp[NPART_MAX / 64];         // PRO_NORMP: this lane's partial sums
 
     // PAIR dword t = 2k + par holds elements 8k + par + {0, 2, 4, 6}, QUAD
     // dword t = 4g + k elements 16g + k + {0, 4, 8, 12}: four
@@ -179,7 +180,9 @@ struct KqStager {
                 ld4(yp, task, p1[i]);
                 ld4(pro.w, task, p2[i]);
             }
+            if constexpr (PRO == PRO_NORMP) ld4(pro.w, task, p2[i]);
         }
+        if constexpr (PRO == PRO_NORMP) pro_part_load(pro.part, pp);
     }
 
     // The prologue, in registers, between load() and store(), called after
@@ -187,7 +190,7 @@ struct KqStager {
     // calls it.  Its inputs pass through pro_pin first, so the compiler
     // cannot start it (and wait for x) ahead of the weight loads.
     __device__ __forceinline__ void apply(int U, const MvPro &pro = MvPro{}) {
-        if constexpr (PRO != PRO_NONE) {
+        if constexpr (PRO == PRO_NORM) {
 #pragma unroll
             for (int i = 0; i < MAXT; i++)
 #pragma unroll
@@ -196,6 +199,22 @@ struct KqStager {
                     pro_pin(p1[i][c]);
                     pro_pin(p2[i][c]);
                 }
+        }
+        if constexpr (PRO == PRO_NORMP) {
+#pragma unroll
+            for (int i = 0; i < MAXT; i++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    pro_pin(e[i][c]);
+                    pro_pin(p2[i][c]);
+                }
+#pragma unroll
+            for (int j = 0; j < NPART_MAX / 64; j++) pro_pin(pp[j]);
+            const float r = 1.0f / sqrtf(pro_part_sum(pp) / (float)(64 * U) + pro.eps);
+#pragma unroll
+            for (int i = 0; i < MAXT; i++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) e[i][c] = e[i][c] * r * p2[i][c];
         }
         if constexpr (PRO == PRO_NORM) {
             const bool hy = pro.y != nullptr;
@@ -1019,11 +1038,30 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
             F::load(W + (long long)r * rb, ul, dst[p]);
         }
     };
-    KqStager<NT, kq_order<QT>(), MAXT, PRO> xs;
+    KqStager<NT, kq_order<QT>(), MAXT, (PRO & 3)> xs;
     xs.load(x, U, pro);
     __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
 #pragma unroll
     for (int i = 0; i < D; i++) load(buf[i], i);
+    // PRO_RES: y[r] += the row's dot, and the sum of the new y[r]^2 of the
+    // rows this lane stores.  The residual rows of a pass are loaded before
+    // the next pass's weights, so waiting for them does not wait for those.
+    float hsq = 0.f;
+    auto res_load = [&](int pass, float *rv) {
+        if constexpr ((PRO & PRO_RES) != 0) {
+#pragma unroll
+            for (int p = 0; p < RP; p++) rv[p] = y[min(orow(pass, p), rend - 1)];
+        }
+    };
+    auto put = [&](int r, float v, float rv) {
+        if constexpr ((PRO & PRO_RES) != 0) {
+            const float h = rv + v;
+            y[r] = h;
+            hsq += h * h;
+        } else {
+            y[r] = v;
+        }
+    };
     xs.apply(U, pro);
     xs.store(U, xd, gs);
     __syncthreads();
@@ -1037,7 +1075,7 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
     if constexpr (D == 1 && S == 1 &&
                   (QT == QT_Q2_K || QT == QT_GQ2_K || QT == QT_Q8_0 || QT == QT_GQ8_0)) {
         // reduce and store the rows of `cur` (pass `pass`)
-        auto pass_rows = [&](const typename F::Unit *cur, int pass) {
+        auto pass_rows = [&](const typename F::Unit *cur, int pass, const float *rv) {
             float acc[RP];
 #pragma unroll
             for (int p = 0; p < RP; p++) {
@@ -1052,22 +1090,28 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
 #pragma unroll
                 for (int p = 0; p < RP; p++) {
                     const int r = orow(pass, p);
-                    if (lr == 0 && r < rend) y[r] = acc[p];
+                    if (lr == 0 && r < rend) put(r, acc[p], rv[p]);
                 }
             }
         };
         // npass is uniform in the workgroup, so the second pass's guard is too
         for (int pass = 0; pass < npass; pass += 2) {
+            float rv0[RP], rv1[RP];
+            res_load(pass, rv0);
             load(buf[1], pass + 1);
-            pass_rows(buf[0], pass);
+            pass_rows(buf[0], pass, rv0);
             if (pass + 1 < npass) {
+                res_load(pass + 1, rv1);
                 load(buf[0], pass + 2);
-                pass_rows(buf[1], pass + 1);
+                pass_rows(buf[1], pass + 1, rv1);
             }
         }
+        if constexpr ((PRO & PRO_RES) != 0) pro_res_flush(hsq, pro.part_out);
         return;
     }
     for (int pass = 0; pass < npass; ++pass) {
+        float rv[RP];
+        res_load(pass, rv);
         load(buf[D], pass + D);
         float acc[RP];
 #pragma unroll
@@ -1100,7 +1144,7 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
 #pragma unroll
                 for (int p = 0; p < RP; p++) {
                     const int r = orow(pass, p);
-                    if (lr == 0 && r < rend) y[r] = acc[p];
+                    if (lr == 0 && r < rend) put(r, acc[p], rv[p]);
                 }
             }
         }
@@ -1109,6 +1153,7 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
 #pragma unroll
             for (int p = 0; p < RP; p++) buf[i][p] = buf[i + 1][p];
     }
+    if constexpr ((PRO & PRO_RES) != 0) pro_res_flush(hsq, pro.part_out);
 }
 
 // Rows of U units with 16 < U < 64, U not a power of two (K = 2560:
@@ -1150,7 +1195,7 @@ __global__ __launch_bounds__(NW * 64) void k_mv_kq_seg(const uint8_t *__restrict
             F::load(W + (long long)r * rb, u, dst[p]);
         }
     };
-    KqStager<NT, kq_order<QT>(), MAXT, PRO> xs;
+    KqStager<NT, kq_order<QT>(), MAXT, (PRO & 3)> xs;
     xs.load(x, U, pro);
     __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
     load(buf[0], 0);
@@ -1217,6 +1262,9 @@ static hipError_t launch_kq(const void *W, int M, int K, const float *x, float *
 template <int QT, int NW, int PRO, bool GLU>
 static hipError_t launch_kq_seg(const void *W, int M, int K, const float *x, float *y, hipStream_t st, int n_cu,
                                 const MvPro &pro) {
+    if constexpr ((PRO & PRO_RES) != 0) {
+        return hipErrorNotSupported;   // no residual epilogue in the segmented kernel
+    } else {
     constexpr int NT = NW * 64, RP = GLU ? 2 : 1;
     const int U = K / 64, RB = NT / U;
     const long long nblk = ((long long)M + RB - 1) / RB, cap = (long long)n_cu * KQ_SEG_WPC;
@@ -1226,6 +1274,7 @@ static hipError_t launch_kq_seg(const void *W, int M, int K, const float *x, flo
     hipLaunchKernelGGL((k_mv_kq_seg<QT, NW, PRO, GLU>), dim3(grid), dim3(NT), lds, st, (const uint8_t *)W, M, K, rb,
                        x, y, pro);
     return hipGetLastError();
+    }
 }
 
 // Launch shape for one row slice width: G row groups of S waves, at most
@@ -1239,6 +1288,7 @@ static hipError_t launch_kq_shape(const void *W, int M, int K, const float *x, f
     const long long cap = (long long)n_cu * WPC;
     const long long need = ((long long)M + G * RL * RPP - 1) / (G * RL * RPP);
     const int grid = (int)(need < cap ? need : cap);
+    if ((PRO & PRO_RES) != 0 && grid > NPART_MAX) return hipErrorNotSupported;
     const int rpw = (M + grid - 1) / grid;
     return launch_kq<QT, LPR, S, G, R, D, PRO, GLU>(W, M, K, x, y, st, grid, rpw, pro);
 }
@@ -1292,7 +1342,7 @@ static hipError_t launch_kq_q(const void *W, int M, int K, const float *x, float
     if (U <= 256) return launch_kq_shape<QT, 64, 4, NW / 4, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     // K up to 32768 for plain matvecs (the fused prologue's registers do not
     // fit 8 slices): 6 or 8 slices of 64 units, two row groups
-    if constexpr (PRO == PRO_NONE && !GLU) {
+    if constexpr ((PRO & 3) == PRO_NONE && !GLU) {
         if (U <= 384) return launch_kq_shape<QT, 64, 6, 2, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
         if (U <= 512) return launch_kq_shape<QT, 64, 8, 2, PRO, GLU>(W, M, K, x, y, st, n_cu, pro);
     }
@@ -1625,6 +1675,9 @@ hipError_t launch_matvec_kq_pro(int mode, const MvPro &pro, int qt, const void *
     case PRO_NONE: return launch_matvec_kq_p<PRO_NONE, false>(qt, W, M, K, x, y, st, n_cu, pro);
     case PRO_NORM: return launch_matvec_kq_p<PRO_NORM, false>(qt, W, M, K, x, y, st, n_cu, pro);
     case PRO_NORM | MV_GLU: return launch_matvec_kq_p<PRO_NORM, true>(qt, W, M, K, x, y, st, n_cu, pro);
+    case PRO_NORMP: return launch_matvec_kq_p<PRO_NORMP, false>(qt, W, M, K, x, y, st, n_cu, pro);
+    case PRO_NORMP | MV_GLU: return launch_matvec_kq_p<PRO_NORMP, true>(qt, W, M, K, x, y, st, n_cu, pro);
+    case PRO_RES: return launch_matvec_kq_p<PRO_RES, false>(qt, W, M, K, x, y, st, n_cu, pro);
     default: return hipErrorNotSupported;
     }
 }

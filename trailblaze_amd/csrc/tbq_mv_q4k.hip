@@ -98,10 +98,16 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
     const int lr = lane % LPR, rsub = lane / LPR;
     const bool lv = lr < U;
     const int ul = lv ? lr : 0;
-    XStager<NT, (4 * 128 + NT - 1) / NT, PRO> xs;   // K <= 4096
+    XStager<NT, (4 * 128 + NT - 1) / NT, (PRO & 3)> xs;   // K <= 4096
     xs.load(x, K, 1, pro);
-    __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
     const int base = (blockIdx.x * NW + wave) * R * RPP + rsub;
+    // PRO_RES: the rows' residuals, loaded ahead of the weights
+    float rv[R];
+    if constexpr ((PRO & PRO_RES) != 0) {
+#pragma unroll
+        for (int p = 0; p < R; p++) rv[p] = y[min(base + p * RPP, M - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
     // Unconditional loads (rows past M re-read row M-1, idle lanes unit 0;
     // their results are discarded): under a branch, the compiler would wait
     // for the weights before staging x.
@@ -116,13 +122,23 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
     __syncthreads();
     XUnit xu;
     xunit_load(xd, ul, xu);
+    float hsq = 0.f;
 #pragma unroll
     for (int p = 0; p < R; p++) {
         const int r = base + p * RPP;
         const float v = q4k_unit_dot<GG>(w[p], ul, xu, 0.f);
         const float acc = group_sum<LPR>((r < M && lv) ? v : 0.f);
-        if (lr == 0 && r < M) y[r] = acc;
+        if (lr == 0 && r < M) {
+            if constexpr ((PRO & PRO_RES) != 0) {
+                const float h = rv[p] + acc;
+                y[r] = h;
+                hsq += h * h;
+            } else {
+                y[r] = acc;
+            }
+        }
     }
+    if constexpr ((PRO & PRO_RES) != 0) pro_res_flush(hsq, pro.part_out);
 }
 
 // Tall matrices (rows of up to 64 units): persistent waves.  Each
@@ -186,6 +202,7 @@ static hipError_t launch_q4k_xr(const void *W, int M, int K, const float *x, flo
                                 const MvPro &pro) {
     constexpr int ROWS_PER_WG = NW * R * (64 / LPR);
     const int grid = (M + ROWS_PER_WG - 1) / ROWS_PER_WG;
+    if ((PRO & PRO_RES) != 0 && grid > NPART_MAX) return hipErrorNotSupported;
     const long long rb = (long long)(K / 256) * 144;
     const size_t lds = (size_t)(K / 32) * XD_PER_SB * 4;
     hipLaunchKernelGGL((k_mv_q4k_xr<LPR, R, NW, PRO, GG>), dim3(grid), dim3(NW * 64), lds, s, (const uint8_t *)W, M, K,
@@ -273,6 +290,9 @@ hipError_t launch_matvec_q4k_pro(int mode, const MvPro &pro, const void *W, int 
     case PRO_NORM:
         return ggml ? launch_q4k_xr_k<PRO_NORM, true>(W, M, K, x, y, s, pro)
                     : launch_q4k_xr_k<PRO_NORM, false>(W, M, K, x, y, s, pro);
+    case PRO_RES:
+        return ggml ? launch_q4k_xr_k<PRO_RES, true>(W, M, K, x, y, s, pro)
+                    : launch_q4k_xr_k<PRO_RES, false>(W, M, K, x, y, s, pro);
     default: return hipErrorNotSupported;
     }
 }
