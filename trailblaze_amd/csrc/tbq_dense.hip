@@ -95,6 +95,7 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_p(const float *__restrict__ x,
 // launch of its own).  grid = ceil(n / 256) <= NPART_MAX.
 __global__ __launch_bounds__(256) void k_res_add(float *__restrict__ res, const float *__restrict__ v, int n,
                                                  float *__restrict__ part_out) {
+    __shared__ float red[32];
     const int i = blockIdx.x * 256 + threadIdx.x;
     float hsq = 0.f;
     if (i < n) {
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(256) void k_res_add(float *__restrict__ res, const 
         res[i] = h;
         hsq = h * h;
     }
-    pro_res_flush(hsq, part_out);
+    pro_res_flush(hsq, part_out, red);
 }
 
 // RoPE table of one step: rc[j] = cos, rc[D/2 + j] = sin of pos *

@@ -259,11 +259,17 @@ constexpr int NPART_MAX = 512;
 // float per thread, 0 where a thread stored none) to part_out[blockIdx.x],
 // and zeros to part_out[blockIdx.x + gridDim.x * j] below NPART_MAX, so the
 // next PRO_NORMP sums NPART_MAX values whatever this grid was.  Every
-// thread of the workgroup calls it.
-__device__ __forceinline__ void pro_res_flush(float v, float *part_out) {
-    v = pro_block_sum(v);
+// thread of the workgroup calls it; red: 32 floats of the kernel's dynamic
+// LDS that nothing else uses at this point (a static __shared__ array beside
+// a kernel's dynamic LDS has made kernels here several times slower).
+__device__ __forceinline__ void pro_res_flush(float v, float *part_out, float *red) {
+    v = group_sum<64>(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
     if (threadIdx.x == 0) {
-        part_out[blockIdx.x] = v;
+        float s = 0.f;
+        for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += red[i];
+        part_out[blockIdx.x] = s;
         for (int i = blockIdx.x + gridDim.x; i < NPART_MAX; i += gridDim.x) part_out[i] = 0.f;
     }
 }

@@ -1044,9 +1044,11 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
 #pragma unroll
     for (int i = 0; i < D; i++) load(buf[i], i);
     // PRO_RES: y[r] += the row's dot, and the sum of the new y[r]^2 of the
-    // rows this lane stores.  The residual rows of a pass are loaded before
-    // the next pass's weights, so waiting for them does not wait for those.
+    // rows this lane stores.  A pass's residual rows are loaded one pass
+    // ahead and before the weights issued with them, so waiting for them
+    // never waits for weights.
     float hsq = 0.f;
+    float *fred = red + (S > 1 ? 2 * G * S * RWP : 0);   // pro_res_flush's 32 floats
     auto res_load = [&](int pass, float *rv) {
         if constexpr ((PRO & PRO_RES) != 0) {
 #pragma unroll
@@ -1095,23 +1097,25 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
             }
         };
         // npass is uniform in the workgroup, so the second pass's guard is too
+        float rv0[RP], rv1[RP];
+        res_load(0, rv0);   // behind pass 0's weights, which the first store waits for anyway
         for (int pass = 0; pass < npass; pass += 2) {
-            float rv0[RP], rv1[RP];
-            res_load(pass, rv0);
+            res_load(pass + 1, rv1);
             load(buf[1], pass + 1);
             pass_rows(buf[0], pass, rv0);
             if (pass + 1 < npass) {
-                res_load(pass + 1, rv1);
+                res_load(pass + 2, rv0);
                 load(buf[0], pass + 2);
                 pass_rows(buf[1], pass + 1, rv1);
             }
         }
-        if constexpr ((PRO & PRO_RES) != 0) pro_res_flush(hsq, pro.part_out);
+        if constexpr ((PRO & PRO_RES) != 0) pro_res_flush(hsq, pro.part_out, fred);
         return;
     }
+    float rv[RP], rvn[RP];
+    res_load(0, rv);   // behind pass 0's weights, which the first store waits for anyway
     for (int pass = 0; pass < npass; ++pass) {
-        float rv[RP];
-        res_load(pass, rv);
+        res_load(pass + 1, rvn);
         load(buf[D], pass + D);
         float acc[RP];
 #pragma unroll
@@ -1152,8 +1156,10 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
         for (int i = 0; i < D; i++)
 #pragma unroll
             for (int p = 0; p < RP; p++) buf[i][p] = buf[i + 1][p];
+#pragma unroll
+        for (int p = 0; p < RP; p++) rv[p] = rvn[p];
     }
-    if constexpr ((PRO & PRO_RES) != 0) pro_res_flush(hsq, pro.part_out);
+    if constexpr ((PRO & PRO_RES) != 0) pro_res_flush(hsq, pro.part_out, fred);
 }
 
 // Rows of U units with 16 < U < 64, U not a power of two (K = 2560:
@@ -1239,13 +1245,14 @@ static hipError_t launch_kq(const void *W, int M, int K, const float *x, float *
     const int U = K / 64;
     const long long rb = pro.rb ? pro.rb : (long long)(K / block_weights(QT)) * block_bytes(QT);
     constexpr int RP = GLU ? 2 : R;
-    const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (S > 1 ? (size_t)2 * G * S * RP * RPP * 4 : 0);
+    const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (S > 1 ? (size_t)2 * G * S * RP * RPP * 4 : 0) +
+                       ((PRO & PRO_RES) != 0 ? 32 * 4 : 0);
     if constexpr (S > 4) {
         // rows of more than 256 units stage more than 64 KiB of x: opted
         // into once per instantiation (gfx950 has 160 KiB of LDS per CU)
         static const hipError_t attr = hipFuncSetAttribute(
             (const void *)k_mv_kq<QT, LPR, S, G, R, D, PRO, GLU>, hipFuncAttributeMaxDynamicSharedMemorySize,
-            (int)((size_t)S * 64 * (KQ_UNIT * 4 + 16) + 2 * G * S * RP * RPP * 4));
+            (int)((size_t)S * 64 * (KQ_UNIT * 4 + 16) + 2 * G * S * RP * RPP * 4 + ((PRO & PRO_RES) != 0 ? 32 * 4 : 0)));
         if (attr != hipSuccess) return attr;
     }
     hipLaunchKernelGGL((k_mv_kq<QT, LPR, S, G, R, D, PRO, GLU>), dim3(grid), dim3(S * G * 64), lds, st,

@@ -138,7 +138,8 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
             }
         }
     }
-    if constexpr ((PRO & PRO_RES) != 0) pro_res_flush(hsq, pro.part_out);
+    if constexpr ((PRO & PRO_RES) != 0)
+        pro_res_flush(hsq, pro.part_out, reinterpret_cast<float *>(xd + (K / 32) * XD_PER_SB));
 }
 
 // Tall matrices (rows of up to 64 units): persistent waves.  Each
@@ -204,7 +205,7 @@ static hipError_t launch_q4k_xr(const void *W, int M, int K, const float *x, flo
     const int grid = (M + ROWS_PER_WG - 1) / ROWS_PER_WG;
     if ((PRO & PRO_RES) != 0 && grid > NPART_MAX) return hipErrorNotSupported;
     const long long rb = (long long)(K / 256) * 144;
-    const size_t lds = (size_t)(K / 32) * XD_PER_SB * 4;
+    const size_t lds = (size_t)(K / 32) * XD_PER_SB * 4 + ((PRO & PRO_RES) != 0 ? 32 * 4 : 0);
     hipLaunchKernelGGL((k_mv_q4k_xr<LPR, R, NW, PRO, GG>), dim3(grid), dim3(NW * 64), lds, s, (const uint8_t *)W, M, K,
                        rb, x, y, pro);
     return hipGetLastError();
