@@ -856,14 +856,17 @@ __global__ __launch_bounds__(RB_THREADS) void k_router_batch(const float *__rest
 
 // ---------------------------------------------------------------------------
 // Batch router, tiled (T >= 32): a workgroup of 4 waves owns 16 tokens x 16
-// experts; wave w takes tokens 8*(w&1).. and experts 8*(w>>1).., and lane l
-// runs the chain of token l&7, expert l>>3 of that 8x8 block:
-// acc = fl(acc + fl(w*x)) over k ascending, one chain per lane (one wave per
-// SIMD at T = 512, E = 128).  Both operands come from LDS 4 k at a time
-// (ds_read_b128); a wave instruction touches only 8 distinct 16-byte rows of
-// each tile, each read by 8 lanes, so the LDS serves it as broadcasts in one
-// pass instead of 64 distinct addresses, and the dependent add chain, not
-// LDS bandwidth, bounds the kernel.  Each chunk of 256 k of the 16 token and
+// experts; wave w takes tokens 8*(w&1).. and experts 8*(w>>1).., and each
+// quad of lanes (quad 4a + b of the wave) the 2 x 2 block of tokens 2a, 2a+1
+// and experts 2b, 2b+1: acc = fl(acc + fl(w*x)) over k ascending, one chain
+// per lane (one wave per SIMD at T = 512, E = 128).  Each lane reads ONE
+// operand from LDS, 4 k at a time (ds_read_b128): lanes 0, 1 of the quad the
+// x rows of tokens 2a, 2a+1, lanes 2, 3 the W rows of experts 2b, 2b+1; the
+// chains are (t0,e0), (t1,e1), (t1,e0), (t0,e1), so each lane's other
+// operand is one quad partner's value (DPP quad_perm [2,3,1,0], free as an
+// operand modifier).  Half the LDS reads of two operands per lane, which is
+// what bounded the kernel (the product is fl(x*w) = fl(w*x)).  Each chunk of
+// 256 k of the 16 token and
 // 16 expert rows (32 KB) is loaded with coalesced 16-byte loads while the
 // previous chunk is summed.  Requires H % 256 == 0, E % 16 == 0.
 // grid = (ceil(T/16), E/16 (+1 row of fp16-conversion workgroups)).
@@ -872,6 +875,7 @@ constexpr int RTL_T = 16, RTL_E = 16, RTL_KC = 256;
 constexpr int RTL_ROW = RTL_KC + 4;   // floats per LDS row: consecutive rows 4 banks apart
 constexpr int RTL_THREADS = 256;
 constexpr int RTL_LPT = RTL_KC / 4 / 16;   // float4 of each tile row a loader thread moves per chunk
+constexpr int RTL_PARTNER = 2 | 3 << 2 | 1 << 4 | 0 << 6;   // DPP quad_perm [2,3,1,0]
 struct RtlShared {
     rb_f4 x[2][RTL_T][RTL_ROW / 4];
     rb_f4 w[2][RTL_E][RTL_ROW / 4];
@@ -894,77 +898,87 @@ __global__ __launch_bounds__(RTL_THREADS) void k_router_tile(const float *__rest
     const int t0 = blockIdx.x * RTL_T, e0 = blockIdx.y * RTL_E;
     // loader role: row r = tid / 16 of the x tile and of the W tile, float4
     // q = tid % 16 + 16 i of the chunk (tokens >= T read the last token; never
-    // stored).  A chunk (256 k, 32 rows, 32 KB) is loaded while the previous
-    // one is summed: 256 dependent adds cover the loads' latency.
+    // stored).  A chunk (256 k, 32 rows, 32 KB) is loaded two chunks ahead
+    // of its use (below).
     const int lr = tid >> 4, lq = tid & 15;
     const rb_f4 *xsrc = reinterpret_cast<const rb_f4 *>(xn + (long long)(t0 + lr < T ? t0 + lr : T - 1) * H) + lq;
     const rb_f4 *wsrc = reinterpret_cast<const rb_f4 *>(Wr + (long long)(e0 + lr) * H) + lq;
-    // chain role
-    const int tl = 8 * (wave & 1) + (lane & 7), el = 8 * (wave >> 1) + (lane >> 3);
+    // chain role: quad qd = 4a + b, lane i of the quad (see above)
+    const int qd = lane >> 2, qi = lane & 3;
+    const int qt0 = 8 * (wave & 1) + 2 * (qd >> 2), qe0 = 8 * (wave >> 1) + 2 * (qd & 3);
+    const int tl = qt0 + ((qi == 1 || qi == 2) ? 1 : 0), el = qe0 + (qi & 1);
     const int NC = H / RTL_KC;
-    rb_f4 xr[RTL_LPT], wr[RTL_LPT];
+    // chunk j's global loads go to register set j % 2, two chunks ahead of
+    // its use: chunk c + 2 is loaded while chunk c is summed, and stored to
+    // LDS after chunk c + 1 is (its latency covers two chunks' chains)
+    struct Regs {
+        rb_f4 x[RTL_LPT], w[RTL_LPT];
+    };
+    auto gload = [&](Regs &r, int c) {   // unconditional: chunks past the end reload the last
+        c = c < NC ? c : NC - 1;
 #pragma unroll
-    for (int i = 0; i < RTL_LPT; i++) {
-        xr[i] = xsrc[16 * i];
-        wr[i] = wsrc[16 * i];
-    }
-#pragma unroll
-    for (int i = 0; i < RTL_LPT; i++) {
-        sh.x[0][lr][lq + 16 * i] = xr[i];
-        sh.w[0][lr][lq + 16 * i] = wr[i];
-    }
-    __syncthreads();
-    float acc = 0.f;
-    for (int c = 0; c < NC; c++) {
-        const int b = c & 1;
-        if (c + 1 < NC) {
-#pragma unroll
-            for (int i = 0; i < RTL_LPT; i++) {
-                xr[i] = xsrc[(c + 1) * (RTL_KC / 4) + 16 * i];
-                wr[i] = wsrc[(c + 1) * (RTL_KC / 4) + 16 * i];
-            }
+        for (int i = 0; i < RTL_LPT; i++) {
+            r.x[i] = xsrc[c * (RTL_KC / 4) + 16 * i];
+            r.w[i] = wsrc[c * (RTL_KC / 4) + 16 * i];
         }
-        // 16 k per group: the next group's LDS reads are issued before the
-        // current group's arithmetic (two register slots); the empty asm
-        // statements (tied to acc) keep the compiler from hoisting more of
-        // the chunk's reads, which would need more registers than one wave has
-        rb_f4 xa[4], wa[4], xb[4], wb[4];
-        auto ld = [&](int g, rb_f4 (&xv)[4], rb_f4 (&wv)[4]) {
+    };
+    auto lstore = [&](const Regs &r, int buf) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                xv[q] = sh.x[b][tl][4 * g + q];
-                wv[q] = sh.w[b][el][4 * g + q];
-            }
+        for (int i = 0; i < RTL_LPT; i++) {
+            sh.x[buf][lr][lq + 16 * i] = r.x[i];
+            sh.w[buf][lr][lq + 16 * i] = r.w[i];
+        }
+    };
+    float acc = 0.f;
+    // the chain over chunk c from LDS buffer c % 2: 16 k per group, the next
+    // group's LDS reads issued before the current group's arithmetic (two
+    // register slots); the empty asm statements (tied to acc) keep the
+    // compiler from hoisting more of the chunk's reads, which would need
+    // more registers than one wave has.  This lane's operand row: x of token
+    // qt0 + qi (qi < 2) or W of expert qe0 + qi - 2.
+    auto chain = [&](int c) {
+        const int b = c & 1;
+        const rb_f4 *own = qi < 2 ? &sh.x[b][qt0 + qi][0] : &sh.w[b][qe0 + qi - 2][0];
+        rb_f4 va[4], vb[4];
+        auto ld = [&](int g, rb_f4 (&v)[4]) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] = own[4 * g + q];
         };
-        auto sum = [&](const rb_f4 (&xv)[4], const rb_f4 (&wv)[4]) {
+        auto sum = [&](const rb_f4 (&v)[4]) {
             float p[16];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                p[4 * q] = wv[q].x * xv[q].x;
-                p[4 * q + 1] = wv[q].y * xv[q].y;
-                p[4 * q + 2] = wv[q].z * xv[q].z;
-                p[4 * q + 3] = wv[q].w * xv[q].w;
-            }
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) p[4 * q + j] = dpp_f32<RTL_PARTNER>(v[q][j]) * v[q][j];
 #pragma unroll
             for (int i = 0; i < 16; i++) acc = acc + p[i];
             asm volatile("" : "+v"(acc));
         };
-        ld(0, xa, wa);
+        ld(0, va);
 #pragma unroll 1
         for (int g = 0; g < RTL_KC / 16; g += 2) {
-            ld(g + 1, xb, wb);
-            sum(xa, wa);
-            if (g + 2 < RTL_KC / 16) ld(g + 2, xa, wa);
-            sum(xb, wb);
+            ld(g + 1, vb);
+            sum(va);
+            if (g + 2 < RTL_KC / 16) ld(g + 2, va);
+            sum(vb);
         }
-        if (c + 1 < NC) {
-#pragma unroll
-            for (int i = 0; i < RTL_LPT; i++) {
-                sh.x[b ^ 1][lr][lq + 16 * i] = xr[i];
-                sh.w[b ^ 1][lr][lq + 16 * i] = wr[i];
-            }
-        }
+    };
+    Regs ra, rb;
+    gload(ra, 0);
+    gload(rb, 1);
+    lstore(ra, 0);
+    __syncthreads();
+    for (int c = 0; c < NC; c += 2) {
+        gload(ra, c + 2);
+        chain(c);
+        if (c + 1 < NC) lstore(rb, (c + 1) & 1);
         __syncthreads();
+        if (c + 1 < NC) {   // uniform
+            gload(rb, c + 3);
+            chain(c + 1);
+            if (c + 2 < NC) lstore(ra, c & 1);
+            __syncthreads();
+        }
     }
     const int t = t0 + tl, e = e0 + el;
     if (t < T) {
