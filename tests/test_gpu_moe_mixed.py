@@ -92,6 +92,21 @@ def test_moe_mixed_formats(oracle, qts, T):
     check(oracle, xn, resid, layer, F, k, qts, bias=bias)
 
 
+@pytest.mark.parametrize("F", [2048, 4096])
+@pytest.mark.parametrize("qts", [(fm.Q4_K, fm.Q4_K, fm.Q6_K), (fm.Q5_K, fm.Q5_K, fm.Q3_K)])
+def test_moe_mixed_wide_expert_rows(oracle, qts, F):
+    """Down rows of 32 and 64 units (F = 2048, 4096) in a batch in expert
+    order: the per-pair down kernel holds two or four units per lane and
+    streams its passes' weights in batches (one or two passes at a time)."""
+    H, E, k, T = 256, 16, 4, 16
+    layer = synth.moe_layer(H, F, E, qts[0], seed=F + sum(qts), qt_up=qts[1], qt_down=qts[2])
+    rng = np.random.default_rng(F + 7 * sum(qts))
+    xn = synth.activations((T, H), rng)
+    resid = synth.activations((T, H), rng)
+    print("moe wide rows", qts, "F=", F, flush=True)
+    check(oracle, xn, resid, layer, F, k, qts)
+
+
 @pytest.mark.parametrize("T", [1, 16])
 def test_moe_mixed_ggml(oracle, T):
     """ggml's layouts: Q4_K gate/up with a Q6_K down, as llama.cpp writes."""

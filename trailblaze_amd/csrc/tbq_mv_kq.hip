@@ -1545,32 +1545,45 @@ __global__ __launch_bounds__(ME_THREADS) void k_moe_down_pair_kq(const uint8_t *
     KqStager<ME_THREADS, kq_order<QT>(), MAXT> xs;
     xs.load(act + (long long)pair * F, U);
     __builtin_amdgcn_sched_barrier(0);
-    typename Fm::Unit w[MDP_PASSES][UPL];
+    // PB passes' weights in registers at a time: all four at one unit per
+    // lane, fewer at more (four passes of four Q6_K units would spill)
+#ifndef MDP_PB_BIG
+#define MDP_PB_BIG 2
+#endif
+    constexpr int PB = UPL >= 4 ? 1 : (UPL >= 2 ? 2 : (sizeof(typename Fm::Unit) > 48 ? MDP_PB_BIG : MDP_PASSES));
+    typename Fm::Unit w[PB][UPL];
+    auto wload = [&](int p0) {
 #pragma unroll
-    for (int p = 0; p < MDP_PASSES; p++) {
-        const uint8_t *row = down + ((long long)e * H + r0 + (ME_THREADS / MD_LPR) * p + rl) * rb;
+        for (int p = 0; p < PB; p++) {
+            const uint8_t *row = down + ((long long)e * H + r0 + (ME_THREADS / MD_LPR) * (p0 + p) + rl) * rb;
 #pragma unroll
-        for (int i = 0; i < UPL; i++) {
-            const int u = lr + MD_LPR * i;
-            Fm::load(row, u < U ? u : 0, w[p][i]);
+            for (int i = 0; i < UPL; i++) {
+                const int u = lr + MD_LPR * i;
+                Fm::load(row, u < U ? u : 0, w[p][i]);
+            }
         }
-    }
+    };
+    wload(0);
     xs.store(U, xd, gs);
     __syncthreads();
 #pragma unroll
-    for (int p = 0; p < MDP_PASSES; p++) {
-        float acc = 0.f;
+    for (int p0 = 0; p0 < MDP_PASSES; p0 += PB) {
+        if (p0 > 0) wload(p0);
 #pragma unroll
-        for (int i = 0; i < UPL; i++) {
-            const int u = lr + MD_LPR * i;
-            if (u < U) {
-                KqX x;
-                kq_xload(xd, gs, u, x);
-                acc += kq_dot<QT>(w[p][i], x, u);
+        for (int p = 0; p < PB; p++) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < UPL; i++) {
+                const int u = lr + MD_LPR * i;
+                if (u < U) {
+                    KqX x;
+                    kq_xload(xd, gs, u, x);
+                    acc += kq_dot<QT>(w[p][i], x, u);
+                }
             }
+            acc = group_sum<MD_LPR>(acc);
+            if (lr == 0) y[(long long)pair * H + r0 + (ME_THREADS / MD_LPR) * (p0 + p) + rl] = acc;
         }
-        acc = group_sum<MD_LPR>(acc);
-        if (lr == 0) y[(long long)pair * H + r0 + (ME_THREADS / MD_LPR) * p + rl] = acc;
     }
 }
 
