@@ -30,15 +30,21 @@ constexpr int TBQ_MAX_K = 32768;
 // y[r]^2 to part_out[b] and zeros to part_out[b + grid * j] below NPART_MAX
 // (grid <= NPART_MAX), for the next matvec's PRO_NORMP.
 enum : int { PRO_NONE = 0, PRO_NORMP = 1, PRO_NORM = 2, MV_GLU = 4, PRO_RES = 8 };
+// (The fields of modes that never meet share storage: the struct is a
+// kernel argument of every matvec launch.)
 struct MvPro {
-    const float *y;   // PRO_NORM: added to x (null: nothing added)
+    union {
+        const float *y;      // PRO_NORM: added to x (null: nothing added)
+        const float *part;   // PRO_NORMP: NPART_MAX partial sums of squares
+    };
     const float *w;   // PRO_NORM, PRO_NORMP: weights [K]
-    float *vo;        // PRO_NORM: x + y for the caller (null: not stored)
+    union {
+        float *vo;         // PRO_NORM: x + y for the caller (null: not stored)
+        float *part_out;   // PRO_RES: where this launch's partial sums go
+    };
     float eps;
     long long rb;     // K-quant kernel: bytes between rows (0: K's own row bytes), for
                       // a column slice of a matrix with longer rows
-    const float *part;   // PRO_NORMP: NPART_MAX partial sums of squares
-    float *part_out;     // PRO_RES: where this launch's partial sums go
 };
 
 struct MoeArgs {
