@@ -502,11 +502,14 @@ static hipError_t launch_attn_d(int G, const float *qkv, const float *qn, const 
 // tmp_x (K floats) and tmp_y (2M floats, MV_GLU only).
 static hipError_t dense_mv(int qt, const void *W, int M, int K, const float *x, float *out, int mode, const MvPro &pro,
                            float *tmp_x, float *tmp_y, hipStream_t st) {
-    // the register-x Q4_K kernel for plain matvecs and the residual
-    // epilogue; with the norm prologue the K-quant kernel, measured 1.3 us
-    // per layer faster at the Qwen3-4B shapes
+    // the register-x Q4_K kernel for plain matvecs, the residual epilogue
+    // and the partial-sum RMSNorm prologue (q|k|v at the Qwen3-4B shapes:
+    // 1584 -> 1568 us/token against the K-quant kernel); with the block-sum
+    // prologue (PRO_NORM) the K-quant kernel, measured 1.3 us per layer
+    // faster there
     hipError_t e = hipErrorNotSupported;
-    if ((qt == QT_Q4_K || qt == QT_GQ4_K) && K <= 4096 && M <= 8192 && (mode == PRO_NONE || mode == PRO_RES))
+    if ((qt == QT_Q4_K || qt == QT_GQ4_K) && K <= 4096 && M <= 8192 &&
+        (mode == PRO_NONE || mode == PRO_RES || mode == PRO_NORMP))
         e = launch_matvec_q4k_pro(mode, pro, W, M, K, x, out, st, qt == QT_GQ4_K);
     if (e == hipErrorNotSupported) e = launch_matvec_kq_pro(mode, pro, qt, W, M, K, x, out, st, tbq_cu_count());
     if (e != hipErrorNotSupported) return e;

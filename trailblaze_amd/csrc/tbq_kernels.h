@@ -72,9 +72,9 @@ hipError_t launch_matvec_generic(int qt, const void *W, int M, int K, const floa
 hipError_t launch_matvec_q4k(const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu,
                              bool ggml = false);
 hipError_t launch_matvec_kq(int qt, const void *W, int M, int K, const float *x, float *y, hipStream_t s, int n_cu);
-// The same kernels with a staging prologue (mode = PRO_* | MV_GLU);
-// hipErrorNotSupported where they do not cover the shape or mode (the q4k
-// one: K <= 4096, no MV_GLU).
+// The same kernels with a staging prologue or epilogue (mode = PRO_* |
+// MV_GLU); hipErrorNotSupported where they do not cover the shape or mode
+// (the q4k one: K <= 4096, no MV_GLU).
 hipError_t launch_matvec_q4k_pro(int mode, const MvPro &pro, const void *W, int M, int K, const float *x, float *y,
                                  hipStream_t s, bool ggml = false);
 hipError_t launch_matvec_kq_pro(int mode, const MvPro &pro, int qt, const void *W, int M, int K, const float *x,

@@ -298,6 +298,9 @@ hipError_t launch_matvec_q4k_pro(int mode, const MvPro &pro, const void *W, int 
     case PRO_RES:
         return ggml ? launch_q4k_xr_k<PRO_RES, true>(W, M, K, x, y, s, pro)
                     : launch_q4k_xr_k<PRO_RES, false>(W, M, K, x, y, s, pro);
+    case PRO_NORMP:
+        return ggml ? launch_q4k_xr_k<PRO_NORMP, true>(W, M, K, x, y, s, pro)
+                    : launch_q4k_xr_k<PRO_NORMP, false>(W, M, K, x, y, s, pro);
     default: return hipErrorNotSupported;
     }
 }
