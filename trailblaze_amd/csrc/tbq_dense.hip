@@ -78,32 +78,10 @@ __global__ __launch_bounds__(1024) void k_add_rmsnorm(const float *__restrict__ 
     }
 }
 
-// h = x * rsqrt(S / n + eps) * w, S the sum of the NPART_MAX partial sums of
-// squares of x in part (PRO_NORMP's prologue as a launch of its own, where
-// the matvec that follows has none for the shape).  One workgroup; every
-// wave forms S itself.
-__global__ __launch_bounds__(1024) void k_rmsnorm_p(const float *__restrict__ x, const float *__restrict__ part,
-                                                    const float *__restrict__ w, int n, float eps,
-                                                    float *__restrict__ h) {
-    float pp[NPART_MAX / 64];
-    pro_part_load(part, pp);
-    const float r = 1.0f / sqrtf(pro_part_sum(pp) / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) h[i] = x[i] * r * w[i];
-}
-
-// res[i] += v[i] and PRO_RES's partial sums of squares (the epilogue as a
-// launch of its own).  grid = ceil(n / 256) <= NPART_MAX.
-__global__ __launch_bounds__(256) void k_res_add(float *__restrict__ res, const float *__restrict__ v, int n,
-                                                 float *__restrict__ part_out) {
-    __shared__ float red[32];
+// res[i] += v[i] (PRO_RES's epilogue as a launch of its own).
+__global__ __launch_bounds__(256) void k_res_add(float *__restrict__ res, const float *__restrict__ v, int n) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    float hsq = 0.f;
-    if (i < n) {
-        const float h = res[i] + v[i];
-        res[i] = h;
-        hsq = h * h;
-    }
-    pro_res_flush(hsq, part_out, red);
+    if (i < n) res[i] = res[i] + v[i];
 }
 
 // RoPE table of one step: rc[j] = cos, rc[D/2 + j] = sin of pos *
@@ -434,7 +412,7 @@ __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, in
 }
 
 struct DenseWs {
-    float *x, *x2, *h, *qkv, *att, *y, *gu, *a, *part, *rope, *psum;
+    float *x, *x2, *h, *qkv, *att, *y, *gu, *a, *part, *rope;
 };
 
 static size_t up256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -460,7 +438,6 @@ static DenseWs dense_ws(const tbq_dense_model *m, void *ws, size_t *total) {
     w.a = take(m->ffn);
     w.part = take((size_t)m->n_heads * nsplit * (m->head_dim + 2));
     w.rope = take(m->head_dim);
-    w.psum = take(NPART_MAX);
     if (total) *total = off;
     return w;
 }
@@ -503,28 +480,28 @@ static hipError_t launch_attn_d(int G, const float *qkv, const float *qn, const 
 static hipError_t dense_mv(int qt, const void *W, int M, int K, const float *x, float *out, int mode, const MvPro &pro,
                            float *tmp_x, float *tmp_y, hipStream_t st) {
     // the register-x Q4_K kernel for plain matvecs, the residual epilogue
-    // and the partial-sum RMSNorm prologue (q|k|v at the Qwen3-4B shapes:
-    // 1584 -> 1568 us/token against the K-quant kernel); with the block-sum
+    // and the deferred RMSNorm (q|k|v at the Qwen3-4B shapes: 1584 -> 1568
+    // us/token against the K-quant kernel, with the norm's sum of squares
+    // then read from partials the producer wrote); with the block-sum
     // prologue (PRO_NORM) the K-quant kernel, measured 1.3 us per layer
     // faster there
     hipError_t e = hipErrorNotSupported;
     if ((qt == QT_Q4_K || qt == QT_GQ4_K) && K <= 4096 && M <= 8192 &&
-        (mode == PRO_NONE || mode == PRO_RES || mode == PRO_NORMP))
+        (mode == PRO_NONE || mode == PRO_RES || mode == PRO_NORMD))
         e = launch_matvec_q4k_pro(mode, pro, W, M, K, x, out, st, qt == QT_GQ4_K);
     if (e == hipErrorNotSupported) e = launch_matvec_kq_pro(mode, pro, qt, W, M, K, x, out, st, tbq_cu_count());
     if (e != hipErrorNotSupported) return e;
     if (mode == PRO_RES) {
-        if ((M + 255) / 256 > NPART_MAX) return hipErrorNotSupported;
         if (!tbq_matvec(W, qt, M, K, x, tmp_y, st)) return hipErrorUnknown;
-        hipLaunchKernelGGL(k_res_add, dim3((M + 255) / 256), dim3(256), 0, st, out, tmp_y, M, pro.part_out);
+        hipLaunchKernelGGL(k_res_add, dim3((M + 255) / 256), dim3(256), 0, st, out, tmp_y, M);
         return hipGetLastError();
     }
     const float *xin = x;
     if (mode & PRO_NORM) {
         hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(1024), 0, st, x, pro.y, pro.w, K, pro.eps, tmp_x, pro.vo);
         xin = tmp_x;
-    } else if (mode & PRO_NORMP) {
-        hipLaunchKernelGGL(k_rmsnorm_p, dim3(1), dim3(1024), 0, st, x, pro.part, pro.w, K, pro.eps, tmp_x);
+    } else if (mode & PRO_NORMD) {
+        hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(1024), 0, st, x, nullptr, pro.w, K, pro.eps, tmp_x, nullptr);
         xin = tmp_x;
     }
     if (!(mode & MV_GLU)) return tbq_matvec(W, qt, M, K, xin, out, st) ? hipSuccess : hipErrorUnknown;
@@ -534,11 +511,10 @@ static hipError_t dense_mv(int qt, const void *W, int M, int K, const float *x, 
 }
 
 // Validation happens in the C-ABI wrapper.  The residual stream lives in
-// w.x: the o and down matvecs add their rows to it in place (PRO_RES) and
-// leave the partial sums of squares the next matvec's RMSNorm prologue
-// (PRO_NORMP) needs in w.psum, so that prologue neither reads the sublayer
-// output nor reduces over its workgroup.  Layer 0's prologue normalises the
-// embedding row with its own block-wide sum (PRO_NORM).
+// w.x: the o and down matvecs add their rows to it in place (PRO_RES), and
+// each RMSNorm is the next matvec's PRO_NORMD (x * w staged, the scale
+// applied to the dot products, the sum of squares taken over the staged x
+// at the staging barrier), so no launch waits on a reduction of its own.
 hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, float *logits, void *ws,
                                hipStream_t st) {
     const int H = m->hidden, D = m->head_dim, NQ = m->n_heads, NKV = m->n_kv_heads, G = NQ / NKV, F = m->ffn;
@@ -550,16 +526,12 @@ hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, flo
     hipError_t err = launch_dequant(canon_qt(m->qtype_embd), (const uint8_t *)m->tok_embd + (size_t)token * erb, H, res, st);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(k_rope_table, dim3(1), dim3(64), 0, st, pos, m->rope_theta, D, w.rope);
-    bool have_part = false;   // w.psum holds the partial sums of squares of res
-    // rmsnorm(res) * wn as the next matvec's staging prologue
+    // rmsnorm(res) * wn as the next matvec's prologue
     auto norm_pro = [&](const float *wn, int *mode) {
-        *mode = have_part ? PRO_NORMP : PRO_NORM;
-        MvPro p{nullptr, wn, nullptr, m->norm_eps};
-        p.part = have_part ? w.psum : nullptr;
-        return p;
+        *mode = PRO_NORMD;
+        return MvPro{nullptr, wn, nullptr, m->norm_eps};
     };
-    MvPro pres{};
-    pres.part_out = w.psum;
+    const MvPro pres{};
     for (int l = 0; l < m->n_layers; l++) {
         const tbq_dense_layer &L = m->layers[l];
         const size_t kvoff = (size_t)l * NKV * m->max_ctx * D;
@@ -586,7 +558,6 @@ hipError_t launch_dense_decode(const tbq_dense_model *m, int token, int pos, flo
         if ((err = dense_mv(qt_of(L.qt_o), L.wo, H, NQ * D, w.att, res, PRO_RES, pres, nullptr, w.y, st)) !=
             hipSuccess)
             return err;
-        have_part = true;
         // a = silu(Wg h) * (Wu h) with h = rmsnorm(res)
         const MvPro pf = norm_pro(L.ffn_norm, &pm);
         if (L.wgu) {

@@ -251,41 +251,23 @@ __device__ __forceinline__ float pro_block_sum(float v) {
     return s;
 }
 
-// Partial sums of squares passed from a PRO_RES matvec to a PRO_NORMP one
-// (the largest grid of a PRO_RES launch).
-constexpr int NPART_MAX = 512;
-
-// PRO_RES: the workgroup's sum of squares of its new residual rows (one
-// float per thread, 0 where a thread stored none) to part_out[blockIdx.x],
-// and zeros to part_out[blockIdx.x + gridDim.x * j] below NPART_MAX, so the
-// next PRO_NORMP sums NPART_MAX values whatever this grid was.  Every
-// thread of the workgroup calls it; red: 32 floats of the kernel's dynamic
-// LDS that nothing else uses at this point (a static __shared__ array beside
-// a kernel's dynamic LDS has made kernels here several times slower).
-__device__ __forceinline__ void pro_res_flush(float v, float *part_out, float *red) {
-    v = group_sum<64>(v);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float s = 0.f;
-        for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += red[i];
-        part_out[blockIdx.x] = s;
-        for (int i = blockIdx.x + gridDim.x; i < NPART_MAX; i += gridDim.x) part_out[i] = 0.f;
-    }
+// PRO_NORMD: this thread's sum of squares of its staged x, summed over the
+// wave (fixed order), to red[wave]; every thread of the workgroup calls it
+// before the staging barrier.  red: NW floats of the kernel's dynamic LDS
+// that nothing else uses (a static __shared__ array beside a kernel's
+// dynamic LDS has made kernels here several times slower).
+__device__ __forceinline__ void pro_ss_put(float ss, float *red) {
+    ss = group_sum<64>(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
 }
-
-// PRO_NORMP: the sum of the NPART_MAX partials, by each wave on its own
-// (lane l adds partials l + 64 j in j order, then a fixed-order wave sum),
-// so every wave of every workgroup gets the same value.
-__device__ __forceinline__ float pro_part_sum(const float (&pp)[NPART_MAX / 64]) {
-    float s = 0.f;
+// after the barrier: r = 1 / sqrt(sum / K + eps), the waves' sums added in
+// wave order, so every thread of every workgroup gets the same value
+template <int NW>
+__device__ __forceinline__ float pro_ss_scale(const float *red, int K, float eps) {
+    float s = red[0];
 #pragma unroll
-    for (int j = 0; j < NPART_MAX / 64; j++) s += pp[j];
-    return group_sum<64>(s);
-}
-__device__ __forceinline__ void pro_part_load(const float *part, float (&pp)[NPART_MAX / 64]) {
-#pragma unroll
-    for (int j = 0; j < NPART_MAX / 64; j++) pp[j] = part[(threadIdx.x & 63) + 64 * j];
+    for (int i = 1; i < NW; i++) s += red[i];
+    return 1.0f / sqrtf(s / (float)K + eps);
 }
 
 // An empty asm statement that takes v and gives it back and clobbers

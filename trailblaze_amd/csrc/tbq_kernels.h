@@ -18,30 +18,24 @@ constexpr int TBQ_MAX_K = 32768;
 //   PRO_NORM    v = x[i] + y[i] (y may be null),
 //               x'[i] = v * (1 / sqrt(mean(v^2) + eps)) * w[i] over the K
 //               elements; workgroup 0 also stores v to vo (if not null)
-//   PRO_NORMP   x'[i] = x[i] * (1 / sqrt(S / K + eps)) * w[i], S the sum of
-//               the NPART_MAX partial sums of squares in part (written by
-//               the matvec that produced x, PRO_RES below)
-// Every workgroup forms the whole normalised vector itself (one block-wide
-// sum of squares, or each wave the sum of the partials), so no workgroup
-// waits for another.  Epilogue flag MV_GLU (K-quant kernel): W holds 2M rows,
-// gate rows then up rows, and y[r] = silu(W[r] x') * (W[M + r] x'); one wave
-// computes both rows.  Epilogue PRO_RES (no prologue): y is the residual
-// stream, y[r] += W[r] x, and workgroup b stores the sum of its rows' new
-// y[r]^2 to part_out[b] and zeros to part_out[b + grid * j] below NPART_MAX
-// (grid <= NPART_MAX), for the next matvec's PRO_NORMP.
-enum : int { PRO_NONE = 0, PRO_NORMP = 1, PRO_NORM = 2, MV_GLU = 4, PRO_RES = 8 };
-// (The fields of modes that never meet share storage: the struct is a
-// kernel argument of every matvec launch.)
+//   PRO_NORMD   x'[i] = x[i] * w[i], and every output row (both rows of a
+//               GLU pair) multiplied by r = 1 / sqrt(sum(x^2) / K + eps)
+//               after its dot product: the same function as PRO_NORM with
+//               y = null, the scalar r applied after the sum instead of to
+//               every element.  The sum of squares is taken over the x the
+//               workgroup stages anyway (each wave's share to LDS before the
+//               staging barrier, then summed in wave order), so it costs
+//               neither loads nor a barrier of its own.
+// Every workgroup forms the whole normalised vector (or r) itself, so no
+// workgroup waits for another.  Epilogue flag MV_GLU (K-quant kernel): W
+// holds 2M rows, gate rows then up rows, and y[r] = silu(W[r] x') *
+// (W[M + r] x'); one wave computes both rows.  Epilogue PRO_RES (no
+// prologue): y is the residual stream, y[r] += W[r] x.
+enum : int { PRO_NONE = 0, PRO_NORMD = 1, PRO_NORM = 2, MV_GLU = 4, PRO_RES = 8 };
 struct MvPro {
-    union {
-        const float *y;      // PRO_NORM: added to x (null: nothing added)
-        const float *part;   // PRO_NORMP: NPART_MAX partial sums of squares
-    };
-    const float *w;   // PRO_NORM, PRO_NORMP: weights [K]
-    union {
-        float *vo;         // PRO_NORM: x + y for the caller (null: not stored)
-        float *part_out;   // PRO_RES: where this launch's partial sums go
-    };
+    const float *y;   // PRO_NORM: added to x (null: nothing added)
+    const float *w;   // PRO_NORM, PRO_NORMD: weights [K]
+    float *vo;        // PRO_NORM: x + y for the caller (null: not stored)
     float eps;
     long long rb;     // K-quant kernel: bytes between rows (0: K's own row bytes), for
                       // a column slice of a matrix with longer rows

@@ -145,8 +145,8 @@ struct GMem {
 template <int NT, int ORD, int MAXT, int PRO = PRO_NONE>   // ORD: 0 NATURAL, 1 PAIR, 2 QUAD
 struct KqStager {
     float e[MAXT][4];
-    float p1[MAXT][4], p2[MAXT][4];   // PRO_NORM inputs: y, w (PRO_NORMP: w)
-    float pp[NPART_MAX / 64];         // PRO_NORMP: this lane's partial sums
+    float p1[MAXT][4], p2[MAXT][4];   // PRO_NORM inputs: y, w (PRO_NORMD: w)
+    float ss;                         // PRO_NORMD: this thread's sum of x^2
 
     // PAIR dword t = 2k + par holds elements 8k + par + {0, 2, 4, 6}, QUAD
     // dword t = 4g + k elements 16g + k + {0, 4, 8, 12}: four
@@ -180,9 +180,8 @@ struct KqStager {
                 ld4(yp, task, p1[i]);
                 ld4(pro.w, task, p2[i]);
             }
-            if constexpr (PRO == PRO_NORMP) ld4(pro.w, task, p2[i]);
+            if constexpr (PRO == PRO_NORMD) ld4(pro.w, task, p2[i]);
         }
-        if constexpr (PRO == PRO_NORMP) pro_part_load(pro.part, pp);
     }
 
     // The prologue, in registers, between load() and store(), called after
@@ -200,21 +199,21 @@ struct KqStager {
                     pro_pin(p2[i][c]);
                 }
         }
-        if constexpr (PRO == PRO_NORMP) {
+        if constexpr (PRO == PRO_NORMD) {
+            // x^2 over this thread's tasks (a clamped re-read of the last
+            // task is not counted), then x' = x * w; r comes after the dots
+            ss = 0.f;
 #pragma unroll
-            for (int i = 0; i < MAXT; i++)
+            for (int i = 0; i < MAXT; i++) {
+                const bool ok = i * NT + (int)threadIdx.x < U * 16;
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     pro_pin(e[i][c]);
                     pro_pin(p2[i][c]);
+                    if (ok) ss += e[i][c] * e[i][c];
+                    e[i][c] = e[i][c] * p2[i][c];
                 }
-#pragma unroll
-            for (int j = 0; j < NPART_MAX / 64; j++) pro_pin(pp[j]);
-            const float r = 1.0f / sqrtf(pro_part_sum(pp) / (float)(64 * U) + pro.eps);
-#pragma unroll
-            for (int i = 0; i < MAXT; i++)
-#pragma unroll
-                for (int c = 0; c < 4; c++) e[i][c] = e[i][c] * r * p2[i][c];
+            }
         }
         if constexpr (PRO == PRO_NORM) {
             const bool hy = pro.y != nullptr;
@@ -1043,12 +1042,11 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
     __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
 #pragma unroll
     for (int i = 0; i < D; i++) load(buf[i], i);
-    // PRO_RES: y[r] += the row's dot, and the sum of the new y[r]^2 of the
-    // rows this lane stores.  A pass's residual rows are loaded one pass
-    // ahead and before the weights issued with them, so waiting for them
-    // never waits for weights.
-    float hsq = 0.f;
-    float *fred = red + (S > 1 ? 2 * G * S * RWP : 0);   // pro_res_flush's 32 floats
+    // PRO_RES: y[r] += the row's dot.  A pass's residual rows are loaded one
+    // pass ahead and before the weights issued with them, so waiting for
+    // them never waits for weights.
+    float *ssred = red + (S > 1 ? 2 * G * S * RWP : 0);   // PRO_NORMD: S * G floats
+    float rn = 1.f;                                       // PRO_NORMD: r
     auto res_load = [&](int pass, float *rv) {
         if constexpr ((PRO & PRO_RES) != 0) {
 #pragma unroll
@@ -1056,19 +1054,17 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
         }
     };
     auto put = [&](int r, float v, float rv) {
-        if constexpr ((PRO & PRO_RES) != 0) {
-            const float h = rv + v;
-            y[r] = h;
-            hsq += h * h;
-        } else {
-            y[r] = v;
-        }
+        if constexpr ((PRO & PRO_RES) != 0) y[r] = rv + v;
+        else if constexpr ((PRO & 3) == PRO_NORMD) y[r] = v * rn;
+        else y[r] = v;
     };
     xs.apply(U, pro);
     xs.store(U, xd, gs);
+    if constexpr ((PRO & 3) == PRO_NORMD) pro_ss_put(xs.ss, ssred);
     __syncthreads();
     KqX xr;
     kq_xload(xd, gs, ul, xr);
+    if constexpr ((PRO & 3) == PRO_NORMD) rn = pro_ss_scale<S * G>(ssred, K, pro.eps);
 
     // Q2_K and Q8_0 rows in one slice: two passes per iteration with the
     // two buffers in alternating roles, so the ring needs no register moves
@@ -1087,7 +1083,7 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
             }
             if constexpr (GLU) {
                 const int r = orow(pass, 0);
-                if (lr == 0 && r < rend) y[r] = pro_swiglu(acc[0], acc[1]);
+                if (lr == 0 && r < rend) y[r] = pro_swiglu(acc[0] * rn, acc[1] * rn);
             } else {
 #pragma unroll
                 for (int p = 0; p < RP; p++) {
@@ -1109,7 +1105,6 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
                 pass_rows(buf[1], pass + 1, rv1);
             }
         }
-        if constexpr ((PRO & PRO_RES) != 0) pro_res_flush(hsq, pro.part_out, fred);
         return;
     }
     float rv[RP], rvn[RP];
@@ -1143,7 +1138,7 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
         if (s == 0) {
             if constexpr (GLU) {
                 const int r = orow(pass, 0);
-                if (lr == 0 && r < rend) y[r] = pro_swiglu(acc[0], acc[1]);
+                if (lr == 0 && r < rend) y[r] = pro_swiglu(acc[0] * rn, acc[1] * rn);
             } else {
 #pragma unroll
                 for (int p = 0; p < RP; p++) {
@@ -1159,7 +1154,6 @@ __global__ __launch_bounds__(S * G * 64) void k_mv_kq(const uint8_t *__restrict_
 #pragma unroll
         for (int p = 0; p < RP; p++) rv[p] = rvn[p];
     }
-    if constexpr ((PRO & PRO_RES) != 0) pro_res_flush(hsq, pro.part_out, fred);
 }
 
 // Rows of U units with 16 < U < 64, U not a power of two (K = 2560:
@@ -1207,9 +1201,13 @@ __global__ __launch_bounds__(NW * 64) void k_mv_kq_seg(const uint8_t *__restrict
     load(buf[0], 0);
     xs.apply(U, pro);
     xs.store(U, xd, gs);
+    float *ssred = red + 2 * RP * NT;   // PRO_NORMD: NW floats
+    if constexpr ((PRO & 3) == PRO_NORMD) pro_ss_put(xs.ss, ssred);
     __syncthreads();
     KqX xr;
     kq_xload(xd, gs, u, xr);
+    float rn = 1.f;
+    if constexpr ((PRO & 3) == PRO_NORMD) rn = pro_ss_scale<NW>(ssred, K, pro.eps);
     const int rs = L >> 3, part = L & 7;   // reduction: 8 threads per row slot
     for (int pass = 0; pass < npass; ++pass) {
         load(buf[1], pass + 1);
@@ -1230,7 +1228,8 @@ __global__ __launch_bounds__(NW * 64) void k_mv_kq_seg(const uint8_t *__restrict
         }
         const int r = block_row(pass) + rs;
         if (part == 0 && rs < RB && r < M) {
-            if constexpr (GLU) y[r] = pro_swiglu(acc[0], acc[1]);
+            if constexpr (GLU) y[r] = pro_swiglu(acc[0] * rn, acc[1] * rn);
+            else if constexpr ((PRO & 3) == PRO_NORMD) y[r] = acc[0] * rn;
             else y[r] = acc[0];
         }
 #pragma unroll
@@ -1246,13 +1245,13 @@ static hipError_t launch_kq(const void *W, int M, int K, const float *x, float *
     const long long rb = pro.rb ? pro.rb : (long long)(K / block_weights(QT)) * block_bytes(QT);
     constexpr int RP = GLU ? 2 : R;
     const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (S > 1 ? (size_t)2 * G * S * RP * RPP * 4 : 0) +
-                       ((PRO & PRO_RES) != 0 ? 32 * 4 : 0);
+                       ((PRO & 3) == PRO_NORMD ? 32 * 4 : 0);
     if constexpr (S > 4) {
         // rows of more than 256 units stage more than 64 KiB of x: opted
         // into once per instantiation (gfx950 has 160 KiB of LDS per CU)
         static const hipError_t attr = hipFuncSetAttribute(
             (const void *)k_mv_kq<QT, LPR, S, G, R, D, PRO, GLU>, hipFuncAttributeMaxDynamicSharedMemorySize,
-            (int)((size_t)S * 64 * (KQ_UNIT * 4 + 16) + 2 * G * S * RP * RPP * 4 + ((PRO & PRO_RES) != 0 ? 32 * 4 : 0)));
+            (int)((size_t)S * 64 * (KQ_UNIT * 4 + 16) + 2 * G * S * RP * RPP * 4 + ((PRO & 3) == PRO_NORMD ? 32 * 4 : 0)));
         if (attr != hipSuccess) return attr;
     }
     hipLaunchKernelGGL((k_mv_kq<QT, LPR, S, G, R, D, PRO, GLU>), dim3(grid), dim3(S * G * 64), lds, st,
@@ -1277,7 +1276,8 @@ static hipError_t launch_kq_seg(const void *W, int M, int K, const float *x, flo
     const long long nblk = ((long long)M + RB - 1) / RB, cap = (long long)n_cu * KQ_SEG_WPC;
     const int grid = (int)(nblk < cap ? nblk : cap);
     const long long rb = pro.rb ? pro.rb : (long long)(K / block_weights(QT)) * block_bytes(QT);
-    const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (size_t)2 * RP * NT * 4;
+    const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16 + (size_t)2 * RP * NT * 4 +
+                       ((PRO & 3) == PRO_NORMD ? NW * 4 : 0);
     hipLaunchKernelGGL((k_mv_kq_seg<QT, NW, PRO, GLU>), dim3(grid), dim3(NT), lds, st, (const uint8_t *)W, M, K, rb,
                        x, y, pro);
     return hipGetLastError();
@@ -1295,7 +1295,6 @@ static hipError_t launch_kq_shape(const void *W, int M, int K, const float *x, f
     const long long cap = (long long)n_cu * WPC;
     const long long need = ((long long)M + G * RL * RPP - 1) / (G * RL * RPP);
     const int grid = (int)(need < cap ? need : cap);
-    if ((PRO & PRO_RES) != 0 && grid > NPART_MAX) return hipErrorNotSupported;
     const int rpw = (M + grid - 1) / grid;
     return launch_kq<QT, LPR, S, G, R, D, PRO, GLU>(W, M, K, x, y, st, grid, rpw, pro);
 }
@@ -1695,8 +1694,8 @@ hipError_t launch_matvec_kq_pro(int mode, const MvPro &pro, int qt, const void *
     case PRO_NONE: return launch_matvec_kq_p<PRO_NONE, false>(qt, W, M, K, x, y, st, n_cu, pro);
     case PRO_NORM: return launch_matvec_kq_p<PRO_NORM, false>(qt, W, M, K, x, y, st, n_cu, pro);
     case PRO_NORM | MV_GLU: return launch_matvec_kq_p<PRO_NORM, true>(qt, W, M, K, x, y, st, n_cu, pro);
-    case PRO_NORMP: return launch_matvec_kq_p<PRO_NORMP, false>(qt, W, M, K, x, y, st, n_cu, pro);
-    case PRO_NORMP | MV_GLU: return launch_matvec_kq_p<PRO_NORMP, true>(qt, W, M, K, x, y, st, n_cu, pro);
+    case PRO_NORMD: return launch_matvec_kq_p<PRO_NORMD, false>(qt, W, M, K, x, y, st, n_cu, pro);
+    case PRO_NORMD | MV_GLU: return launch_matvec_kq_p<PRO_NORMD, true>(qt, W, M, K, x, y, st, n_cu, pro);
     case PRO_RES: return launch_matvec_kq_p<PRO_RES, false>(qt, W, M, K, x, y, st, n_cu, pro);
     default: return hipErrorNotSupported;
     }

@@ -123,27 +123,24 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
     }
     xs.apply(K, pro);
     xs.store(xd, K);
+    float *ssred = reinterpret_cast<float *>(xd + (K / 32) * XD_PER_SB);   // PRO_NORMD: NW floats
+    if constexpr ((PRO & 3) == PRO_NORMD) pro_ss_put(xs.ss, ssred);
     __syncthreads();
     XUnit xu;
     xunit_load(xd, ul, xu);
-    float hsq = 0.f;
+    float rn = 1.f;
+    if constexpr ((PRO & 3) == PRO_NORMD) rn = pro_ss_scale<NW>(ssred, K, pro.eps);
 #pragma unroll
     for (int p = 0; p < R; p++) {
         const int r = base + p * RPP;
         const float v = q4k_unit_dot<GG>(w[p], ul, xu, 0.f);
         const float acc = group_sum<LPR>((r < M && lv) ? v : 0.f);
         if (lr == 0 && r < M) {
-            if constexpr ((PRO & PRO_RES) != 0) {
-                const float h = rv[p] + acc;
-                y[r] = h;
-                hsq += h * h;
-            } else {
-                y[r] = acc;
-            }
+            if constexpr ((PRO & PRO_RES) != 0) y[r] = rv[p] + acc;
+            else if constexpr ((PRO & 3) == PRO_NORMD) y[r] = acc * rn;
+            else y[r] = acc;
         }
     }
-    if constexpr ((PRO & PRO_RES) != 0)
-        pro_res_flush(hsq, pro.part_out, reinterpret_cast<float *>(xd + (K / 32) * XD_PER_SB));
 }
 
 // Tall matrices (rows of up to 64 units): persistent waves.  Each
@@ -207,9 +204,8 @@ static hipError_t launch_q4k_xr(const void *W, int M, int K, const float *x, flo
                                 const MvPro &pro) {
     constexpr int ROWS_PER_WG = NW * R * (64 / LPR);
     const int grid = (M + ROWS_PER_WG - 1) / ROWS_PER_WG;
-    if ((PRO & PRO_RES) != 0 && grid > NPART_MAX) return hipErrorNotSupported;
     const long long rb = (long long)(K / 256) * 144;
-    const size_t lds = (size_t)(K / 32) * XD_PER_SB * 4 + ((PRO & PRO_RES) != 0 ? 32 * 4 : 0);
+    const size_t lds = (size_t)(K / 32) * XD_PER_SB * 4 + ((PRO & 3) == PRO_NORMD ? 32 * 4 : 0);
     hipLaunchKernelGGL((k_mv_q4k_xr<LPR, R, NW, PRO, GG>), dim3(grid), dim3(NW * 64), lds, s, (const uint8_t *)W, M, K,
                        rb, x, y, pro);
     return hipGetLastError();
@@ -298,9 +294,9 @@ hipError_t launch_matvec_q4k_pro(int mode, const MvPro &pro, const void *W, int 
     case PRO_RES:
         return ggml ? launch_q4k_xr_k<PRO_RES, true>(W, M, K, x, y, s, pro)
                     : launch_q4k_xr_k<PRO_RES, false>(W, M, K, x, y, s, pro);
-    case PRO_NORMP:
-        return ggml ? launch_q4k_xr_k<PRO_NORMP, true>(W, M, K, x, y, s, pro)
-                    : launch_q4k_xr_k<PRO_NORMP, false>(W, M, K, x, y, s, pro);
+    case PRO_NORMD:
+        return ggml ? launch_q4k_xr_k<PRO_NORMD, true>(W, M, K, x, y, s, pro)
+                    : launch_q4k_xr_k<PRO_NORMD, false>(W, M, K, x, y, s, pro);
     default: return hipErrorNotSupported;
     }
 }

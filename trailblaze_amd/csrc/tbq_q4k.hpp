@@ -43,8 +43,8 @@ constexpr int XD_PER_SB = XD_UNIT / 2;   // LDS dwords per sub-block on average
 template <int NT, int MAXT, int PRO = PRO_NONE>
 struct XStager {
     float4 v[MAXT][2];
-    float4 p1[MAXT][2], p2[MAXT][2];   // PRO_NORM inputs: y, w (PRO_NORMP: w)
-    float pp[NPART_MAX / 64];          // PRO_NORMP: this lane's partial sums
+    float4 p1[MAXT][2], p2[MAXT][2];   // PRO_NORM inputs: y, w (PRO_NORMD: w)
+    float ss;                          // PRO_NORMD: this thread's sum of x^2
 
     // Unconditional loads (tasks past the end re-read the last task and are
     // never stored), so no branch makes the compiler wait for every load
@@ -67,13 +67,12 @@ struct XStager {
                 p2[i][0] = w[0];
                 p2[i][1] = w[1];
             }
-            if constexpr (PRO == PRO_NORMP) {
+            if constexpr (PRO == PRO_NORMD) {
                 const float4 *w = reinterpret_cast<const float4 *>(pro.w + 8 * t);
                 p2[i][0] = w[0];
                 p2[i][1] = w[1];
             }
         }
-        if constexpr (PRO == PRO_NORMP) pro_part_load(pro.part, pp);
     }
 
     // The prologue, in registers, between load() and store() (one vector,
@@ -83,26 +82,27 @@ struct XStager {
     // compiler computes the prologue as soon as x arrives, ahead of the
     // weight loads, and their latency then adds to x's.
     __device__ __forceinline__ void apply(int K, const MvPro &pro = MvPro{}) {
-        if constexpr (PRO == PRO_NORMP) {
+        if constexpr (PRO == PRO_NORMD) {
+            // x^2 over this thread's tasks (a clamped re-read of the last
+            // task is not counted), then x' = x * w; r comes after the dots
+            const int ntask = 4 * (K / 32);
+            ss = 0.f;
 #pragma unroll
-            for (int i = 0; i < MAXT; i++)
+            for (int i = 0; i < MAXT; i++) {
+                const bool ok = (int)threadIdx.x + i * NT < ntask;
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
                     pro_pin(v[i][h]);
                     pro_pin(p2[i][h]);
-                }
-#pragma unroll
-            for (int j = 0; j < NPART_MAX / 64; j++) pro_pin(pp[j]);
-            const float r = 1.0f / sqrtf(pro_part_sum(pp) / (float)K + pro.eps);
-#pragma unroll
-            for (int i = 0; i < MAXT; i++)
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
                     float *a = reinterpret_cast<float *>(&v[i][h]);
                     const float *w = reinterpret_cast<const float *>(&p2[i][h]);
 #pragma unroll
-                    for (int c = 0; c < 4; c++) a[c] = a[c] * r * w[c];
+                    for (int c = 0; c < 4; c++) {
+                        if (ok) ss += a[c] * a[c];
+                        a[c] = a[c] * w[c];
+                    }
                 }
+            }
         }
         if constexpr (PRO == PRO_NORM) {
 #pragma unroll
