@@ -103,15 +103,8 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
     // x's loads stay ahead of the weights'.  (The barrier's place in the
     // plain kernel is its measured one: with the base row computed ahead of
     // it, the 4096x4096 matvec took 4.36 instead of 4.22 us.)
-    if constexpr ((PRO & PRO_RES) == 0) __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);
     const int base = (blockIdx.x * NW + wave) * R * RPP + rsub;
-    // PRO_RES: the rows' residuals, loaded ahead of the weights
-    float rv[R];
-    if constexpr ((PRO & PRO_RES) != 0) {
-#pragma unroll
-        for (int p = 0; p < R; p++) rv[p] = y[min(base + p * RPP, M - 1)];
-        __builtin_amdgcn_sched_barrier(0);
-    }
     // Unconditional loads (rows past M re-read row M-1, idle lanes unit 0;
     // their results are discarded): under a branch, the compiler would wait
     // for the weights before staging x.
@@ -120,6 +113,15 @@ __global__ __launch_bounds__(NW * 64) void k_mv_q4k_xr(const uint8_t *__restrict
     for (int p = 0; p < R; p++) {
         const int r = min(base + p * RPP, M - 1);
         q4k_load<GG>(W + (long long)r * rb, ul, w[p]);
+    }
+    // PRO_RES: the rows' residuals, behind the weights (they are used after
+    // the dot products, which wait for every weight load anyway)
+    float rv[R];
+    if constexpr ((PRO & PRO_RES) != 0) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < R; p++) rv[p] = y[min(base + p * RPP, M - 1)];
+        __builtin_amdgcn_sched_barrier(0);
     }
     xs.apply(K, pro);
     xs.store(xd, K);
