@@ -79,6 +79,27 @@ def test_dense_decode_long_context(oracle, qt):
         assert err <= DENSE_TOL, (pos, err)
 
 
+@pytest.mark.parametrize("qt,qe", [(fm.F16, fm.Q6_K), (fm.BF16, fm.F16)])
+def test_dense_decode_unfused_formats(oracle, qt, qe):
+    """Layers (and, with F16 embeddings, the lm_head) in formats the fused
+    matvec kernels do not take: the RMSNorm, the SwiGLU and the residual add
+    run as launches of their own around tbq_matvec.  Three steps from an
+    empty cache."""
+    import torch
+    from oracle.dense import DenseOracle
+    from trailblaze_amd.dense import DenseConfig
+    cfg = DenseConfig(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=512,
+                      max_ctx=256, qtype_layers=qt, qtype_embd=qe)
+    m = _model(cfg, 9)
+    ref = DenseOracle(oracle, cfg, m.host)
+    logits = torch.empty(cfg.vocab, dtype=torch.float32, device="cuda")
+    for pos, tok in enumerate([11, 400, 3]):
+        print("dense unfused-format step", fm.NAMES[qt], pos, flush=True)
+        m.decode(tok, pos, logits)
+        err = rel_l2(host(logits), ref.decode(tok, pos))
+        assert err <= DENSE_TOL, (pos, err)
+
+
 @pytest.mark.parametrize("nq,nkv,D", [(4, 4, 64), (8, 1, 64), (8, 1, 128), (4, 2, 128)])
 def test_dense_decode_gqa_groups(oracle, nq, nkv, D):
     """Every query-heads-per-kv-head group the attention kernel is built for
