@@ -1137,7 +1137,8 @@ static hipError_t launch_down_q4k_t(const MoeArgs &a, bool grouped, hipStream_t 
     const int pairs = a.T * a.k;
     if (grouped) {
         const int *order = a.grp + 1 + 3 * a.E, *nvalid = order + pairs;
-        // the combine in the kernel needs a counter per (token, row block)
+        // one pair's rows per workgroup, pairs in expert order; k_combine
+        // then adds each token's slots in slot order
         hipLaunchKernelGGL((k_down_pair_q4k<UPL, GG>), dim3(a.H / DG_ROWS, pairs), dim3(DG_THREADS),
                            (size_t)(a.F / 32) * XD_PER_SB * 4, st, (const uint8_t *)a.down, a.act, a.sel_idx, order,
                            nvalid, a.H, a.F, a.E, a.k, a.y);
