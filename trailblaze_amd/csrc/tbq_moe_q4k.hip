@@ -449,11 +449,16 @@ __global__ __launch_bounds__(64) void k_router_dpp(const float *__restrict__ xn,
 #ifndef TBQ_GU_ROWS
 #define TBQ_GU_ROWS 1
 #endif
+// expert-ordered batches: 4-wave workgroups (b=16 93.0 -> 92.6 us, with a
+// Q6_K down 106.7 -> 106.2; at b=1 8 waves stay faster, 22.7 against 23.4)
+#ifndef TBQ_GU_WAVES_B
+#define TBQ_GU_WAVES_B 4
+#endif
 constexpr int GU_THREADS = 64 * TBQ_GU_WAVES;
 constexpr int GU_ROWS = TBQ_GU_ROWS;   // output rows per wave
 
-template <int UPL, bool GG, int ROWS = GU_ROWS>
-__global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
+template <int UPL, bool GG, int ROWS = GU_ROWS, int NWV = TBQ_GU_WAVES>
+__global__ __launch_bounds__(64 * NWV) void k_gate_up_q4k(const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up,
                                                             const float *__restrict__ xn, const int *__restrict__ sel_idx,
                                                             const int *__restrict__ order, const int *__restrict__ nvalid,
                                                             int H, int F, int E, int k, float *__restrict__ act) {
@@ -472,9 +477,9 @@ __global__ __launch_bounds__(GU_THREADS) void k_gate_up_q4k(const uint8_t *__res
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int lr = lane & 31, half = lane >> 5;
     const uint8_t *Wb = (half ? up : gate) + (long long)e * F * rb;
-    const int r0 = (blockIdx.x * (GU_THREADS / 64) + wave) * ROWS;
+    const int r0 = (blockIdx.x * NWV + wave) * ROWS;
 
-    XStager<GU_THREADS, (1024 + GU_THREADS - 1) / GU_THREADS> xs;   // H <= 8192
+    XStager<64 * NWV, (1024 + 64 * NWV - 1) / (64 * NWV)> xs;   // H <= 8192
     xs.load(xn + (long long)t * H, H);
     __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
     // Unconditional loads (rows past F re-read row F-1, units past U unit 0;
@@ -1119,14 +1124,15 @@ static hipError_t launch_gate_up_q4k_t(const MoeArgs &a, bool grouped, hipStream
     const int *order = grouped ? a.grp + 1 + 3 * a.E : nullptr, *nvalid = grouped ? order + pairs : nullptr;
     // batches: more rows per workgroup, fewer workgroups
     const int rows = grouped ? TBQ_GU_ROWS_B : GU_ROWS;
-    const int out_per_wg = (GU_THREADS / 64) * rows;
+    const int nwv = rows == GU_ROWS ? TBQ_GU_WAVES : TBQ_GU_WAVES_B;
+    const int out_per_wg = nwv * rows;
     dim3 grid((a.F + out_per_wg - 1) / out_per_wg, pairs);
     size_t lds = (size_t)(a.H / 32) * XD_PER_SB * 4;
     if (rows == GU_ROWS)
         hipLaunchKernelGGL((k_gate_up_q4k<UPL, GG>), grid, dim3(GU_THREADS), lds, st, (const uint8_t *)a.gate,
                            (const uint8_t *)a.up, a.xn, a.sel_idx, order, nvalid, a.H, a.F, a.E, a.k, a.act);
     else
-        hipLaunchKernelGGL((k_gate_up_q4k<UPL, GG, TBQ_GU_ROWS_B>), grid, dim3(GU_THREADS), lds, st,
+        hipLaunchKernelGGL((k_gate_up_q4k<UPL, GG, TBQ_GU_ROWS_B, TBQ_GU_WAVES_B>), grid, dim3(64 * TBQ_GU_WAVES_B), lds, st,
                            (const uint8_t *)a.gate, (const uint8_t *)a.up, a.xn, a.sel_idx, order, nvalid, a.H,
                            a.F, a.E, a.k, a.act);
     return hipGetLastError();
