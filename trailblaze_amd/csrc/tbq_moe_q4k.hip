@@ -538,12 +538,18 @@ __global__ __launch_bounds__(256) void k_group(const int *__restrict__ sel_idx, 
 
 // down for one pair: y[p][r] = W_down[e] act[p] over DG_ROWS rows, p taken
 // from the expert-ordered pair list (k_combine then adds the slots in slot
-// order).  grid = (H / DG_ROWS, T*k).
-constexpr int DG_THREADS = 512;
-#ifndef TBQ_DG_ROWS
-#define TBQ_DG_ROWS 128
+// order).  grid = (H / DG_ROWS, T*k).  4-wave workgroups of 64 rows (b=16
+// 92.4 -> 90.6 us against 8 waves of 128 rows; 4 waves of 128: 91.0; 2
+// waves of 32 or 64 rows: +1.0 / +1.5 us).
+#ifndef TBQ_DG_THREADS
+#define TBQ_DG_THREADS 256
 #endif
-constexpr int DG_ROWS = TBQ_DG_ROWS;   // rows per workgroup: passes of 32 (16 lanes per row)
+#ifndef TBQ_DG_ROWS
+#define TBQ_DG_ROWS 64
+#endif
+constexpr int DG_THREADS = TBQ_DG_THREADS;
+constexpr int DG_ROWS = TBQ_DG_ROWS;   // rows per workgroup: passes of DG_THREADS / 16 (16 lanes per row)
+static_assert(DG_ROWS % (DG_THREADS / 16) == 0, "whole passes");
 
 template <int UPL, bool GG>
 __global__ __launch_bounds__(DG_THREADS) void k_down_pair_q4k(const uint8_t *__restrict__ down,
@@ -562,7 +568,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_down_pair_q4k(const uint8_t *__r
     const int U = F / 64;
     const int lr = threadIdx.x & 15, rl = threadIdx.x >> 4;   // row of the pass
     const int r0 = blockIdx.x * DG_ROWS;
-    XStager<DG_THREADS, 1> xs;   // F <= 4096
+    XStager<DG_THREADS, (512 + DG_THREADS - 1) / DG_THREADS> xs;   // F <= 4096
     xs.load(act + (long long)pair * F, F);
     __builtin_amdgcn_sched_barrier(0);   // x's loads stay ahead of the weights'
     // unconditional loads (units past U read unit 0, unused), so the
