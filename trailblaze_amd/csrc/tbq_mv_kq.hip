@@ -1521,10 +1521,18 @@ __global__ __launch_bounds__(ME_THREADS) void k_moe_down_kq(const uint8_t *__res
 // act[pair] over MDP_ROWS rows per workgroup, so the workgroups of the pairs
 // that share an expert run back to back and find its rows in L2; k_combine
 // then adds the slots in slot order.  grid = (H / MDP_ROWS, T*k).
-constexpr int MDP_ROWS = 128, MDP_PASSES = MDP_ROWS / (ME_THREADS / MD_LPR);
+#ifndef TBQ_MDP_THREADS
+#define TBQ_MDP_THREADS 256
+#endif
+#ifndef TBQ_MDP_ROWS
+#define TBQ_MDP_ROWS 128
+#endif
+constexpr int MDP_THREADS = TBQ_MDP_THREADS, MDP_ROWS = TBQ_MDP_ROWS;
+constexpr int MDP_PASSES = MDP_ROWS / (MDP_THREADS / MD_LPR);
+static_assert(MDP_ROWS % (MDP_THREADS / MD_LPR) == 0, "whole passes");
 
 template <int QT, int UPL, int MAXT>
-__global__ __launch_bounds__(ME_THREADS) void k_moe_down_pair_kq(const uint8_t *__restrict__ down, long long rb,
+__global__ __launch_bounds__(MDP_THREADS) void k_moe_down_pair_kq(const uint8_t *__restrict__ down, long long rb,
                                                                  const float *__restrict__ act,
                                                                  const int *__restrict__ sel_idx,
                                                                  const int *__restrict__ order,
@@ -1541,7 +1549,7 @@ __global__ __launch_bounds__(ME_THREADS) void k_moe_down_pair_kq(const uint8_t *
     if ((unsigned)e >= (unsigned)E) return;   // the list holds valid pairs only
     const int lr = threadIdx.x & 15, rl = threadIdx.x >> 4;   // row of the pass
     const int r0 = blockIdx.x * MDP_ROWS;
-    KqStager<ME_THREADS, kq_order<QT>(), MAXT> xs;
+    KqStager<MDP_THREADS, kq_order<QT>(), MAXT> xs;
     xs.load(act + (long long)pair * F, U);
     __builtin_amdgcn_sched_barrier(0);
     // PB passes' weights in registers at a time: all four at one unit per
@@ -1554,7 +1562,7 @@ __global__ __launch_bounds__(ME_THREADS) void k_moe_down_pair_kq(const uint8_t *
     auto wload = [&](int p0) {
 #pragma unroll
         for (int p = 0; p < PB; p++) {
-            const uint8_t *row = down + ((long long)e * H + r0 + (ME_THREADS / MD_LPR) * (p0 + p) + rl) * rb;
+            const uint8_t *row = down + ((long long)e * H + r0 + (MDP_THREADS / MD_LPR) * (p0 + p) + rl) * rb;
 #pragma unroll
             for (int i = 0; i < UPL; i++) {
                 const int u = lr + MD_LPR * i;
@@ -1581,7 +1589,7 @@ __global__ __launch_bounds__(ME_THREADS) void k_moe_down_pair_kq(const uint8_t *
                 }
             }
             acc = group_sum<MD_LPR>(acc);
-            if (lr == 0) y[(long long)pair * H + r0 + (ME_THREADS / MD_LPR) * (p0 + p) + rl] = acc;
+            if (lr == 0) y[(long long)pair * H + r0 + (MDP_THREADS / MD_LPR) * (p0 + p) + rl] = acc;
         }
     }
 }
@@ -1604,7 +1612,7 @@ static hipError_t launch_moe_down_pair_kq_t(const MoeArgs &a, hipStream_t st) {
     const int U = a.F / 64;
     const int *order = a.grp + 1 + 3 * a.E, *nvalid = order + a.T * a.k;
     const size_t lds = (size_t)U * KQ_UNIT * 4 + (size_t)U * 16;
-    hipLaunchKernelGGL((k_moe_down_pair_kq<QT, UPL, MAXT>), dim3(a.H / MDP_ROWS, a.T * a.k), dim3(ME_THREADS), lds, st,
+    hipLaunchKernelGGL((k_moe_down_pair_kq<QT, UPL, MAXT>), dim3(a.H / MDP_ROWS, a.T * a.k), dim3(MDP_THREADS), lds, st,
                        (const uint8_t *)a.down, rb, a.act, a.sel_idx, order, nvalid, a.H, a.F, a.E, a.k, a.y);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
@@ -1635,9 +1643,10 @@ static hipError_t launch_moe_down_kq_q(const MoeArgs &a, bool grouped, hipStream
     const int U = a.F / 64, NU = a.k * U;
     if (grouped) {   // per pair in expert order: one activation vector staged
         if (a.H % MDP_ROWS) return hipErrorNotSupported;
-        if (U <= 16) return launch_moe_down_pair_kq_t<QT, 1, 1>(a, st);
-        if (U <= 32) return launch_moe_down_pair_kq_t<QT, 2, 1>(a, st);
-        if (U <= 64) return launch_moe_down_pair_kq_t<QT, 4, 2>(a, st);
+        constexpr int T = MDP_THREADS;   // x staged in LDS: U * 16 tasks
+        if (U <= 16) return launch_moe_down_pair_kq_t<QT, 1, (256 + T - 1) / T>(a, st);
+        if (U <= 32) return launch_moe_down_pair_kq_t<QT, 2, (512 + T - 1) / T>(a, st);
+        if (U <= 64) return launch_moe_down_pair_kq_t<QT, 4, (1024 + T - 1) / T>(a, st);
         return hipErrorNotSupported;
     }
     if (NU > MD_MAX_UNITS) return hipErrorNotSupported;
